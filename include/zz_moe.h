@@ -1,0 +1,148 @@
+/* zz_moe.h -- MoE-layer C ABI of libzzmoe.so (MI355X, gfx950).
+ *
+ * The whole MoE block of an engine layer runs on the GPU in one call, with every
+ * expert resident in an HBM slot table. It slots under the engines' unchanged
+ * entry points:
+ *   gemma4.c:750 moe_start(M*, li, residual, out, S, Buf*) + 792 moe_finish(...)
+ *   lfm25.c:837/891 and maple.c:738/791 moe_start/moe_finish(M*, li, X, out, S, Buf*)
+ * A zz_moe_forward() call computes what that pair computes in the default int8
+ * build: route_row for every row, the first-seen batch union, the per-expert
+ * dispatch lists, expert_apply's gated FFN on q8_0-quantised activations, the
+ * gate-weighted combine, and gemma's pre/post ffn_ln2 norms.
+ *
+ * Conventions (gpu.h:31-33): calls return 1 when done and 0 to decline, leaving
+ * outputs untouched; the engine then runs its CPU path. Single caller; calls are
+ * synchronous unless the _dev or begin/end forms are used. Device memory is owned
+ * by the library until zz_moe_layer_destroy() or gpu_shutdown().
+ * gpu_init() (zz_gpu.h) must have returned 1 first.
+ */
+#ifndef ZZ_MOE_H
+#define ZZ_MOE_H
+
+#include <stdint.h>
+#include <stddef.h>
+#include "zz_gpu.h"
+
+/* gating: how route_row turns logits into (ids, weights) */
+#define ZZ_GATE_SOFTMAX_PES  0  /* gemma4.c:581-613: rmsnorm*scale*D^-1/2, f32 logits,
+                                   top-k, softmax over k, x per-expert scale        */
+#define ZZ_GATE_SIGMOID_BIAS 1  /* lfm25.c:636-668: double logits, sigmoid, +bias for
+                                   selection only, normalise, x routed_scaling      */
+#define ZZ_GATE_SOFTMAX_TOPK 2  /* maple.c:582-601: double logits, top-k, softmax    */
+
+/* activation between gate/up and down */
+#define ZZ_ACT_GEGLU_TANH   0   /* gemma4.c:432-434, 644 */
+#define ZZ_ACT_SWIGLU       1   /* lfm25.c:456-458, 714  */
+#define ZZ_ACT_SWIGLU_CLAMP 2   /* maple.c:607-611, 672-675: silu(min(g,c))*clip(u,+-c) */
+
+typedef struct zz_moe_desc {
+    int D, MI, E, K;          /* hidden, expert intermediate, experts, top-k        */
+    int gating, act;          /* ZZ_GATE_*, ZZ_ACT_*                                  */
+    int fmt_gate, fmt_up, fmt_down;   /* GPU_FMT_Q40 / Q80 / TQ2 per tensor          */
+    int norm_topk;            /* lfm/maple norm_topk_prob                            */
+    int use_bias;             /* lfm: expert_bias on the selection score.
+                                 gemma: a per-expert logit offset added after the
+                                 dot (harness extension for skewed routing; 0 is the
+                                 reference, gemma4.c:600-601)                         */
+    float eps;                /* gemma rmsnorm epsilon                                */
+    float routed_scaling;     /* lfm                                                  */
+    float clamp;              /* maple mlp_clamp                                      */
+} zz_moe_desc;
+
+typedef struct zz_moe_weights {   /* host pointers, copied at layer creation        */
+    const float *router;          /* [E, D]                                          */
+    const float *router_scale;    /* [D] gemma router_scale                          */
+    const float *pes;             /* [E] gemma router_pes                            */
+    const float *bias;            /* [E] lfm expert_bias / gemma logit offset        */
+    const float *pre_ln;          /* [D] gemma pre_ffn_ln2                           */
+    const float *post_ln;         /* [D] gemma post_ffn_ln2                          */
+} zz_moe_weights;
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Register one MoE layer. Returns a layer id >= 0, or -1 to decline (bad shape:
+ * D, MI multiples of 64 and <= 8192, E <= 512, 1 <= K <= 16, K <= E). */
+int zz_moe_layer_create(const zz_moe_desc *d, const zz_moe_weights *w);
+void zz_moe_layer_destroy(int layer);
+
+/* Bytes of one expert record in the reference layout [gate | up | down]
+ * (gemma4.c:660 offsets 0, gate_b, 2*gate_b; per-tensor sizes q40.h:313-314,
+ * 461-462, tq2.h:84-86). The record is what experts.bin holds per expert. */
+int64_t zz_moe_record_bytes(const zz_moe_desc *d);
+
+/* Fill slot `eid` of the layer's HBM slot table from one host record
+ * (replaces slot_for/io_worker, gemma4.c:487-540: every expert stays resident). */
+int zz_moe_expert_upload(int layer, int eid, const uint8_t *rec, size_t n);
+/* Same from a device buffer (already in HBM). */
+int zz_moe_expert_upload_dev(int layer, int eid, const void *d_rec, size_t n);
+
+/* moe_start + moe_finish for S rows. in: gemma the residual [S, D], lfm/maple the
+ * normed hidden X [S, D]. out [S, D]. eidx/ewt [S*K] (may be NULL) receive the
+ * routing in route_row's order. Host pointers; synchronous. */
+int zz_moe_forward(int layer, const float *in, float *out, int S, int *eidx, float *ewt);
+
+/* Same on device pointers, enqueued on `stream` (a hipStream_t; NULL = the
+ * library's stream) and not waited for. */
+int zz_moe_forward_dev(int layer, const float *d_in, float *d_out, int S, int *d_eidx,
+                       float *d_ewt, void *stream);
+
+/* Split form for overlap (gemma runs its dense MLP between moe_start and
+ * moe_finish, gemma4.c:1012-1021): begin uploads `in` and enqueues the layer;
+ * end waits and writes out/eidx/ewt. One begin may be outstanding. */
+int zz_moe_forward_begin(int layer, const float *in, int S);
+int zz_moe_forward_end(int layer, float *out, int *eidx, float *ewt);
+
+/* Debug dump of the last forward's first chunk (any pointer may be NULL):
+ * xq/xs [S, D] / [S, D/32]: the int8 expert input; hq/hs [S*K, MI] / [S*K, MI/32]:
+ * the int8 hidden by (token, slot); dispatch: uniq[E] union order (returns nu),
+ * offs[nu+1], rows[S*K] tokens per expert ascending, slots[S*K]. */
+typedef struct zz_moe_dump {
+    int8_t *xq; float *xs;
+    int8_t *hq; float *hs;
+    int *uniq, *offs, *rows, *slots;
+    int nu;
+} zz_moe_dump;
+int zz_moe_debug(int layer, zz_moe_dump *dump);
+
+/* Exact per-block int32 dots of rows [row0, row0+nrows) of one resident expert
+ * tensor (0 gate, 1 up, 2 down) against int8 activations xq[I]:
+ * q4_0 sum (q-8)*x, q8_0 sum q*x, tq2 sum (c-1)*x; out [nrows, I/32]. */
+int zz_moe_blockdots(int layer, int eid, int tensor, int row0, int nrows,
+                     const int8_t *xq, int32_t *out);
+
+/* Device weight quantiser (the converters' q40_quant_row / q80_quant_row,
+ * q40.h:83-110, 332-348, bit-exact for finite input): n f32 values at d_w (n % 32
+ * == 0, rows laid end to end) -> n/32 blocks at d_out in the reference layout.
+ * Device pointers, enqueued on `stream` (NULL = the library's stream). */
+int zz_quantize(int fmt, const float *d_w, uint8_t *d_out, int64_t n, void *stream);
+
+/* Counters since gpu_init: [0] rmsnorm serial replays, [1] lfm/maple logit serial
+ * replays, [2] gemma tokens that needed the exact router replay, [3] lfm tokens
+ * whose selection was within the expf tolerance of a tie (contested). */
+int zz_moe_stats(unsigned *counters4);
+
+/* Per-kernel timing with HIP events recorded on the stream each kernel is
+ * launched on. zz_moe_profile(1) clears and starts recording, (0) stops.
+ * zz_moe_profile_read fills, for kernel k in the order ZZ_K_*, the summed
+ * duration in ms and the launch count; returns the number of kernels. */
+#define ZZ_K_PREP 0
+#define ZZ_K_LOGITS 1
+#define ZZ_K_TOPK 2
+#define ZZ_K_DISPATCH 3
+#define ZZ_K_FFN_UP 4
+#define ZZ_K_FFN_DOWN 5
+#define ZZ_K_COMBINE 6
+#define ZZ_K_COUNT 7
+int zz_moe_profile(int on);
+int zz_moe_profile_read(double *ms, int *launches, int n);
+
+/* Text of the last failure (a declined call), or "". */
+const char *zz_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZZ_MOE_H */

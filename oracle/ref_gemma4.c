@@ -1,0 +1,147 @@
+/* ref_gemma4.c -- drives the reference gemma4.c MoE block, unmodified.
+ *
+ * TEST INFRASTRUCTURE ONLY. Compiled by oracle/Makefile against the sources in
+ * /root/reference (never copied here) into oracle/_ref/libref_gemma4.so. The
+ * engine translation unit is included whole, so its static route_row /
+ * moe_start / moe_finish (gemma4.c:581-809) run exactly as the engine runs them.
+ * The model struct is filled by hand for one layer with every expert resident
+ * and pinned: slot_for (gemma4.c:520-540) always hits, no I/O thread is started,
+ * and g_use_gpu stays 0, so the default int8 CPU path runs.
+ */
+#define main zz_gemma4_engine_main
+#include "gemma4.c"
+#undef main
+
+static void *zz_calloc(size_t n) { return calloc(n ? n : 1, 1); }
+
+static M *g4_model(int D, int MI, int E, int K, float eps, const float *router,
+                   const float *rscale, const float *pes, const float *pre_ln,
+                   const float *post_ln, const uint8_t *experts, int64_t esz) {
+    M *m = zz_calloc(sizeof(M));
+    Cfg *c = &m->c;
+    c->hidden = D; c->n_layers = 1; c->n_experts = E; c->topk = K; c->moe_inter = MI;
+    c->eps = eps; c->slots_per_layer = E;
+    Layer *L = &m->L[0];
+    L->router_proj.O = E; L->router_proj.I = D; L->router_proj.f = router;
+    L->router_scale.f = rscale; L->router_pes.f = pes;
+    L->pre_ffn_ln2.f = pre_ln; L->post_ffn_ln2.f = post_ln;
+    m->gate_b = q40_tensor_bytes(MI, D);
+    m->down_b = q40_tensor_bytes(D, MI);
+    m->esz = esz;
+    m->slots = zz_calloc(sizeof(Slot) * (size_t)E);
+    for (int e = 0; e < E; e++) {
+        m->slots[e].eid = e;
+        m->slots[e].buf = (uint8_t *)experts + (size_t)e * (size_t)esz;
+        m->slots[e].pinned = 1;
+    }
+    m->npin = E;
+    m->ucount = zz_calloc(sizeof(int64_t) * (size_t)E);
+    pthread_mutex_init(&m->mu, NULL);
+    pthread_cond_init(&m->cv, NULL);
+    pthread_cond_init(&m->done, NULL);
+    m->qcap = E + 1;
+    m->q = zz_calloc(sizeof(*m->q) * (size_t)m->qcap);
+    return m;
+}
+
+static void g4_free_model(M *m) {
+    free(m->slots); free(m->ucount); free(m->q);
+    pthread_mutex_destroy(&m->mu);
+    pthread_cond_destroy(&m->cv);
+    pthread_cond_destroy(&m->done);
+    free(m);
+}
+
+static void g4_buf(Buf *b, int D, int MI, int E, int K, int S) {
+    memset(b, 0, sizeof *b);
+    b->S = S;
+    b->xn = zz_calloc(sizeof(float) * (size_t)D);
+    b->gate = zz_calloc(sizeof(float) * ((size_t)MI + (size_t)S * K + 64));
+    b->eout = zz_calloc(sizeof(float) * (size_t)2 * S * D);
+    b->egate = zz_calloc(sizeof(float) * (size_t)S * (MI + 64));
+    b->esx = zz_calloc(sizeof(float) * (size_t)S * (D / Q40_BLK + 8));
+    b->ehs = zz_calloc(sizeof(float) * (size_t)S * (MI / Q40_BLK + 8));
+    b->exq = zz_calloc((size_t)S * (D + 64));
+    b->ehq = zz_calloc((size_t)S * (MI + 64));
+    b->xq = zz_calloc((size_t)D + 64);
+    b->hq = zz_calloc((size_t)MI + 64);
+    b->sx = zz_calloc(sizeof(float) * (size_t)(D / Q40_BLK + 8));
+    b->hs = zz_calloc(sizeof(float) * (size_t)(MI / Q40_BLK + 8));
+    b->eidx = zz_calloc(sizeof(int) * (size_t)S * K);
+    b->ewt = zz_calloc(sizeof(float) * (size_t)S * K);
+    b->rows = zz_calloc(sizeof(int) * (size_t)S + 4);
+    b->uniq = zz_calloc(sizeof(int) * (size_t)E);
+}
+
+static void g4_free_buf(Buf *b) {
+    free(b->xn); free(b->gate); free(b->eout); free(b->egate); free(b->esx); free(b->ehs);
+    free(b->exq); free(b->ehq); free(b->xq); free(b->hq); free(b->sx); free(b->hs);
+    free(b->eidx); free(b->ewt); free(b->rows); free(b->uniq);
+}
+
+/* One MoE layer call: moe_start + moe_finish (gemma4.c:750-809). */
+int ref_g4_moe(int D, int MI, int E, int K, float eps, const float *router,
+               const float *rscale, const float *pes, const float *pre_ln,
+               const float *post_ln, const uint8_t *experts, int64_t esz,
+               const float *residual, int S, float *out, int *eidx, float *ewt,
+               int *uniq, int *nu, float *xin) {
+    if (K > MAXTOPK || K > E || E > 128) return -1;    /* moe_slots[128] in Buf */
+    M *m = g4_model(D, MI, E, K, eps, router, rscale, pes, pre_ln, post_ln, experts, esz);
+    Buf b;
+    g4_buf(&b, D, MI, E, K, S);
+    moe_start(m, 0, residual, out, S, &b);
+    moe_finish(m, 0, out, S, &b);
+    memcpy(eidx, b.eidx, sizeof(int) * (size_t)S * K);
+    memcpy(ewt, b.ewt, sizeof(float) * (size_t)S * K);
+    memcpy(uniq, b.uniq, sizeof(int) * (size_t)b.moe_nu);
+    *nu = b.moe_nu;
+    if (xin) memcpy(xin, b.eout + (size_t)S * D, sizeof(float) * (size_t)S * D);
+    g4_free_buf(&b);
+    g4_free_model(m);
+    return 0;
+}
+
+/* route_row alone (gemma4.c:581-613), one token. */
+int ref_g4_route(int D, int E, int K, float eps, const float *router, const float *rscale,
+                 const float *pes, const float *residual, int *idx, float *wts) {
+    if (K > MAXTOPK || K > E) return -1;
+    M *m = g4_model(D, 64, E, K, eps, router, rscale, pes, NULL, NULL, NULL, 0);
+    Buf b;
+    memset(&b, 0, sizeof b);
+    b.xn = zz_calloc(sizeof(float) * (size_t)D);
+    route_row(m, 0, residual, idx, wts, &b);
+    free(b.xn);
+    g4_free_model(m);
+    return 0;
+}
+
+/* expert_apply_batch_cpu for one expert and `n` rows of X (gemma4.c:618-654),
+ * dumping the int8 activations and the int8 hidden it quantised. */
+int ref_g4_expert(int D, int MI, const uint8_t *blob, const float *X, const int *rows,
+                  int n, const float *w, float *OUT, int8_t *xq, float *sx, int8_t *hq,
+                  float *hs) {
+    M *m = g4_model(D, MI, 1, 1, 1e-6f, NULL, NULL, NULL, NULL, NULL, blob, 0);
+    int S = 0;
+    for (int r = 0; r < n; r++) if (rows[r] + 1 > S) S = rows[r] + 1;
+    Buf b;
+    g4_buf(&b, D, MI, 1, 1, n > S ? n : S);
+    expert_apply_batch_cpu(m, blob, blob + m->gate_b, blob + 2 * m->gate_b,
+                           q40_row_bytes(D), q40_row_bytes(MI), X, OUT, rows, n, w, &b);
+    for (int r = 0; r < n; r++) {
+        if (xq) memcpy(xq + (size_t)r * D, b.exq + (size_t)r * (D + 64), (size_t)D);
+        if (sx) memcpy(sx + (size_t)r * (D / 32), b.esx + (size_t)r * (D / Q40_BLK + 8), sizeof(float) * (D / 32));
+        if (hq) memcpy(hq + (size_t)r * MI, b.ehq + (size_t)r * (MI + 64), (size_t)MI);
+        if (hs) memcpy(hs + (size_t)r * (MI / 32), b.ehs + (size_t)r * (MI / Q40_BLK + 8), sizeof(float) * (MI / 32));
+    }
+    g4_free_buf(&b);
+    g4_free_model(m);
+    return 0;
+}
+
+void ref_g4_set_threads(int n) {
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}

@@ -1,0 +1,381 @@
+"""GPU parity: libzzmoe.so on an MI355X against the oracle and the golden vectors
+the compiled reference wrote. Calls go through the C ABI (zunzuncito_amd is a
+ctypes binding of include/zz_moe.h and include/zz_gpu.h).
+
+Tiers:
+  bit-exact  routing ids and order, union order, dispatch lists, the int8
+             activations and scales, the per-block int32 dots;
+  fp32       layer outputs within 1e-3 relative L2, gate weights within 1e-4.
+"""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import zzref as Z
+import zunzuncito_amd as zz
+from test_oracle import CASES, load_case
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL = 1e-3          # fp32 tier: relative L2 of the layer output
+WT_RTOL = 1e-4          # gate weights (softmax/sigmoid of certified logits)
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+@pytest.fixture(scope="module")
+def dev():
+    name = zz.init()            # raises: no silent CPU path
+    return name
+
+
+def gpu_layer(L):
+    m = zz.MoeLayer(L.D, L.MI, L.E, L.K, L.gating, L.act, L.fmts, L.router, L.router_scale,
+                    L.pes, L.bias, L.pre_ln, L.post_ln, norm_topk=L.norm_topk,
+                    use_bias=L.use_bias, eps=L.eps, routed_scaling=L.routed_scaling,
+                    clamp=L.clamp)
+    m.upload_all(L.experts)
+    return m
+
+
+def check_layer(m, L, x, want, dump=False):
+    out, eidx, ewt = m.forward(x)
+    assert np.array_equal(eidx, want.eidx), "routing ids differ"
+    np.testing.assert_allclose(ewt, want.ewt, rtol=WT_RTOL, atol=1e-6)
+    err = Z.rel_l2(out, want.out)
+    assert err < OUT_TOL, err
+    return out, eidx, ewt, err
+
+
+def test_device(dev):
+    say("device:", dev)
+    assert "gfx950" in dev
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_golden_layer(dev, name, layer_cache):
+    g, kind, seed, kw, S, xseed = load_case(name)
+    say("case", name)
+    L = layer_cache(kind, seed=seed, **kw)
+    x = Z.make_input(L, S, xseed)
+    m = gpu_layer(L)
+    try:
+        want = Z.MoeResult(g["out"], g["eidx"], g["ewt"], g["uniq"])
+        out, eidx, ewt, err = check_layer(m, L, x, want)
+        say(f"  out rel L2 {err:.2e}")
+        # integer tier on the dump of that forward
+        orc = Z.oracle_moe(L, x, dump=True)
+        d = m.debug(S)
+        assert np.array_equal(d["xq"], orc.dump["xq"])
+        assert np.array_equal(d["xs"].view(np.uint32), orc.dump["xs"].view(np.uint32))
+        assert np.array_equal(d["uniq"], g["uniq"])
+        offs = np.zeros(len(g["uniq"]) + 1, np.int32)
+        rows = np.zeros(S * L.K, np.int32)
+        slots = np.zeros(S * L.K, np.int32)
+        Z.oracle().orc_dispatch(Z.ptr(orc.eidx), Z.ptr(orc.ewt), S, L.K, Z.ptr(orc.uniq),
+                                len(orc.uniq), Z.ptr(offs), Z.ptr(rows), None, Z.ptr(slots))
+        # device lists are grouped by expert id; compare per expert
+        for u, e in enumerate(g["uniq"]):
+            j = int(np.where(d["uniq"] == e)[0][0])
+            a0, a1 = d["offs"][j], d["offs"][j + 1]
+            assert np.array_equal(d["rows"][a0:a1], rows[offs[u]:offs[u + 1]])
+            assert np.array_equal(d["slots"][a0:a1], slots[offs[u]:offs[u + 1]])
+        # the hidden goes through tanhf/expf, whose device and glibc results may
+        # differ by an ulp: its int8 codes agree except for rare +-1 flips
+        diff = np.abs(d["hq"].astype(np.int32) - orc.dump["hq"].astype(np.int32))
+        assert diff.max() <= 1 and (diff > 0).mean() < 2e-3, (diff.max(), (diff > 0).mean())
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("kind,kw", [("gemma", dict(E=8)), ("lfm", dict(E=8)),
+                                     ("maple", dict(E=8, D=1024, MI=512))])
+def test_blockdots_bit_exact(dev, kind, kw, layer_cache):
+    """Per-block int32 dots of every tensor of an expert (q4_0, q8_0, tq2) against the
+    oracle's brute-force dots, on quantised activations of both signs and saturating
+    extremes."""
+    say("blockdots", kind)
+    L = layer_cache(kind, seed=31, **kw)
+    m = gpu_layer(L)
+    try:
+        rng = np.random.default_rng(31)
+        g, u, d = L.tensor_sizes()
+        for eid in (0, L.E - 1):
+            rec = L.experts[eid * L.esz:(eid + 1) * L.esz]
+            for t, (off, (O, I)) in enumerate(zip((0, g, g + u), ((L.MI, L.D), (L.MI, L.D), (L.D, L.MI)))):
+                fmt = L.fmts[t]
+                xq = rng.integers(-127, 128, I, dtype=np.int8)
+                xq[:32] = 127
+                xq[32:64] = -127
+                rows = np.arange(O)[:: max(1, O // 96)][:96]
+                got = m.blockdots(eid, t, 0, O, xq)
+                T = rec[off:off + Z.tensor_bytes(fmt, O, I)]
+                for r in rows:
+                    if fmt == Z.FMT_TQ2:
+                        row = T[O * 4 + r * (I // 4):]
+                    else:
+                        row = T[r * (I // 32) * (18 if fmt == Z.FMT_Q40 else 34):]
+                    want = np.zeros(I // 32, np.int32)
+                    Z.oracle().orc_blockdots(fmt, Z.ptr(np.ascontiguousarray(row)), Z.ptr(xq), I,
+                                             Z.ptr(want))
+                    assert np.array_equal(got[r], want), (eid, t, r)
+    finally:
+        m.close()
+
+
+_A, _C = 6364136223846793005, 1442695040888963407
+
+
+def lcg64_stream(r0, n, lanes=1 << 16):
+    """States r_1..r_n of r <- r*A + C (mod 2^64) from r_0, vectorised by jumping
+    `lanes` steps at a time: r_{i+L} = A^L r_i + C (A^L - 1)/(A - 1)."""
+    M = 2 ** 64
+    first = np.empty(min(lanes, n), np.uint64)
+    r = r0
+    for i in range(first.size):
+        r = (r * _A + _C) % M
+        first[i] = r
+    if n <= lanes:
+        return first[:n]
+    aL, cL = 1, 0
+    for _ in range(lanes):                       # compose the affine map L times
+        aL, cL = (aL * _A) % M, (cL * _A + _C) % M
+    out = np.empty(((n + lanes - 1) // lanes) * lanes, np.uint64)
+    cur = first.copy()
+    with np.errstate(over="ignore"):
+        for k in range(out.size // lanes):
+            out[k * lanes:(k + 1) * lanes] = cur
+            cur = cur * np.uint64(aL) + np.uint64(cL)
+    return out[:n]
+
+
+def _lcg_check_gpu(O, I, t):
+    """gemma4.c:2335-2343: W bytes then x from the reference's 64-bit LCG."""
+    wb = O * (I // 32) * 18
+    st = lcg64_stream((0x243f6a8885a308d3 ^ t) % 2 ** 64, wb + I)
+    W = ((st[:wb] >> np.uint64(40)) & np.uint64(0xff)).astype(np.uint8)
+    xi = (st[wb:] >> np.uint64(40)).astype(np.int64) - 8388608
+    x = (xi.astype(np.float32) / np.float32(8388608.0)).astype(np.float32)
+    return W, x
+
+
+@pytest.mark.parametrize("t,O,I", [(0, 4096, 2816), (1, 8192, 2816), (2, 2112, 2816),
+                                   (3, 2816, 2112), (4, 704, 2816), (5, 2816, 704)])
+def test_check_gpu_shapes(dev, t, O, I):
+    """gemma4.c:2315-2368 --check-gpu: gpu_q40_matmul vs q40_dot_f32 at the engine's
+    shapes, max|d| / max|ref| < 1e-4 (rows whose random fp16 scale is NaN/inf drop
+    out of the reference's comparisons, here too)."""
+    say("check_gpu", O, I)
+    W, x = _lcg_check_gpu(O, I, t)
+    Wm = zz.gpu_map(W)
+    y = np.zeros((1, O), np.float32)
+    assert zz.lib().gpu_q40_matmul(y.ctypes.data_as(zz._f32p), Wm.ctypes.data_as(zz._u8p),
+                                   x.ctypes.data_as(zz._f32p), O, I, 1) == 1
+    ref = np.zeros((1, O), np.float32)
+    Z.oracle().orc_matmul_f32(Z.FMT_Q40, Z.ptr(ref), Z.ptr(Wm), Z.ptr(x), O, I, 1)
+    fin = np.isfinite(ref[0]) & np.isfinite(y[0])
+    rel = np.abs(y[0] - ref[0])[fin].max() / (np.abs(ref[0][fin]).max() + 1e-9)
+    say(f"  max rel err {rel:.3e}")
+    assert rel < 1e-4
+
+
+@pytest.mark.parametrize("fmt", [Z.FMT_Q80, Z.FMT_TQ2])
+def test_gpu_matmul_other_formats(dev, fmt):
+    rng = np.random.default_rng(41)
+    O, I, S = 1792, 2048, 3
+    if fmt == Z.FMT_TQ2:
+        W = Z.make_expert_tq2(rng, O, I)
+    else:
+        W = Z.quant_rows(fmt, (rng.standard_normal((O, I)) * 0.02).astype(np.float32))
+    Wm = zz.gpu_map(W)
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    y = zz.gpu_matmul(fmt, Wm, x, O, I)
+    ref = np.zeros((S, O), np.float32)
+    Z.oracle().orc_matmul_f32(fmt, Z.ptr(ref), Z.ptr(Wm), Z.ptr(x), O, I, S)
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-4
+
+
+def test_gpu_matmul_declines_unmapped_and_q4a(dev):
+    x = np.ones((1, 64), np.float32)
+    y = np.full((1, 8), 5.0, np.float32)
+    W = np.zeros(8 * 2 * 18, np.uint8)               # never gpu_map'd
+    L = zz.lib()
+    assert L.gpu_matmul(1, y.ctypes.data_as(zz._f32p), W.ctypes.data_as(zz._u8p),
+                        x.ctypes.data_as(zz._f32p), 8, 64, 1) == 0
+    Wm = zz.gpu_map(np.zeros(8 * 64, np.uint8))
+    assert L.gpu_matmul(4, y.ctypes.data_as(zz._f32p), Wm.ctypes.data_as(zz._u8p),
+                        x.ctypes.data_as(zz._f32p), 8, 64, 1) == 0
+    assert np.all(y == 5.0)
+
+
+# --------------------------------------------------------------- BASELINE configs
+def test_config2_gemma_zipf_s512(dev, layer_cache):
+    """Config 2: S=512 prefill, Zipf(1.1) logit offsets (a harness extension that
+    reduces to the reference at bias 0), skewed batch union."""
+    say("config2 gemma zipf S=512")
+    L = layer_cache("gemma", seed=2, zipf=True)
+    x = Z.make_input(L, 512, 2)
+    want = Z.oracle_moe(L, x)
+    m = gpu_layer(L)
+    try:
+        out, eidx, ewt, err = check_layer(m, L, x, want)
+        cnt = np.bincount(eidx, minlength=L.E)
+        say(f"  nu {len(want.uniq)} max/min per-expert {cnt.max()}/{cnt.min()} rel L2 {err:.2e}")
+        assert len(want.uniq) > 64 and cnt.max() > 4 * max(1, np.median(cnt))
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("S", [1, 8, 256])
+def test_config3_lfm_mixed(dev, S, layer_cache):
+    """Config 3: LFM shape, gate/up q4_0 with down q8_0 (per-tensor formats)."""
+    say("config3 lfm S", S)
+    L = layer_cache("lfm", seed=3)
+    x = Z.make_input(L, S, 30 + S)
+    want = Z.oracle_moe(L, x)
+    m = gpu_layer(L)
+    try:
+        check_layer(m, L, x, want)
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("S", [1, 512])
+def test_config4_maple(dev, S, layer_cache):
+    """Config 4: Maple shape (MI=768), tq2 experts, clamped SwiGLU."""
+    say("config4 maple S", S)
+    L = layer_cache("maple", seed=4)
+    x = Z.make_input(L, S, 40 + S)
+    want = Z.oracle_moe(L, x)
+    m = gpu_layer(L)
+    try:
+        check_layer(m, L, x, want)
+    finally:
+        m.close()
+
+
+def test_config1_gemma_s1_many_tokens(dev, layer_cache):
+    """Config 1 at S=1 over 64 independent residuals (routing ids exact on each)."""
+    say("config1 gemma S=1 x64")
+    L = layer_cache("gemma", seed=1)
+    m = gpu_layer(L)
+    try:
+        for i in range(64):
+            x = Z.make_input(L, 1, 100 + i)
+            want = Z.oracle_moe(L, x)
+            check_layer(m, L, x, want)
+    finally:
+        m.close()
+
+
+# --------------------------------------------------------------- properties
+def test_batch_invariance(dev, layer_cache):
+    """Tokens do not interact in a MoE layer: one S=96 call equals three S=32 calls
+    bit for bit (the engines' --nobatch check, gemma4.c:3191-3197)."""
+    L = layer_cache("gemma", seed=2, E=16)
+    x = Z.make_input(L, 96, 50)
+    m = gpu_layer(L)
+    try:
+        a, ea, wa = m.forward(x)
+        parts = [m.forward(x[i:i + 32]) for i in (0, 32, 64)]
+        assert np.array_equal(ea, np.concatenate([p[1] for p in parts]))
+        assert np.array_equal(a.view(np.uint32), np.concatenate([p[0] for p in parts]).view(np.uint32))
+    finally:
+        m.close()
+
+
+def test_chunked_large_batch(dev, layer_cache):
+    """S beyond one dispatch chunk (8192 pairs) is split by the library; results
+    equal per-chunk calls."""
+    L = layer_cache("lfm", seed=3, E=8, fmts=(1, 1, 1), D=512, MI=256, K=4)
+    S = 2048 + 100
+    x = Z.make_input(L, S, 51)
+    m = gpu_layer(L)
+    try:
+        a, ea, _ = m.forward(x)
+        b1, e1, _ = m.forward(x[:2048])
+        b2, e2, _ = m.forward(x[2048:])
+        assert np.array_equal(ea, np.concatenate([e1, e2]))
+        assert np.array_equal(a.view(np.uint32), np.concatenate([b1, b2]).view(np.uint32))
+        want = Z.oracle_moe(L, x)
+        assert np.array_equal(ea, want.eidx) and Z.rel_l2(a, want.out) < OUT_TOL
+    finally:
+        m.close()
+
+
+def test_begin_end_and_dev_paths(dev, layer_cache):
+    import torch
+    L = layer_cache("gemma", seed=2, E=16)
+    x = Z.make_input(L, 12, 52)
+    m = gpu_layer(L)
+    try:
+        a, ea, wa = m.forward(x)
+        lib = zz.lib()
+        assert lib.zz_moe_forward_begin(m.id, x.ctypes.data_as(zz._f32p), 12) == 1
+        out = np.zeros_like(a)
+        e2 = np.zeros_like(ea)
+        w2 = np.zeros_like(wa)
+        assert lib.zz_moe_forward_end(m.id, out.ctypes.data_as(zz._f32p), e2.ctypes.data_as(zz._i32p),
+                                      w2.ctypes.data_as(zz._f32p)) == 1
+        assert np.array_equal(out.view(np.uint32), a.view(np.uint32)) and np.array_equal(e2, ea)
+        dx = torch.from_numpy(x).cuda()
+        dy = torch.zeros_like(dx)
+        de = torch.zeros(12 * L.K, dtype=torch.int32, device="cuda")
+        st = torch.cuda.current_stream()
+        m.forward_dev(dx.data_ptr(), dy.data_ptr(), 12, de.data_ptr(), 0, st.cuda_stream)
+        st.synchronize()
+        assert np.array_equal(dy.cpu().numpy().view(np.uint32), a.view(np.uint32))
+        assert np.array_equal(de.cpu().numpy(), ea)
+    finally:
+        m.close()
+
+
+def test_declines_until_all_experts_resident(dev, layer_cache):
+    L = layer_cache("gemma", seed=2, E=16)
+    m = zz.MoeLayer(L.D, L.MI, L.E, L.K, L.gating, L.act, L.fmts, L.router, L.router_scale,
+                    L.pes, None, L.pre_ln, L.post_ln)
+    try:
+        for e in range(L.E - 1):
+            m.upload(e, L.experts[e * L.esz:(e + 1) * L.esz])
+        x = Z.make_input(L, 2, 53)
+        out = np.full((2, L.D), 9.0, np.float32)
+        ok = zz.lib().zz_moe_forward(m.id, x.ctypes.data_as(zz._f32p), out.ctypes.data_as(zz._f32p),
+                                     2, None, None)
+        assert ok == 0 and np.all(out == 9.0)
+        assert "uploaded" in zz.last_error()
+        bad = np.zeros(L.esz - 1, np.uint8)
+        assert zz.lib().zz_moe_expert_upload(m.id, 0, bad.ctypes.data_as(zz._u8p), bad.nbytes) == 0
+    finally:
+        m.close()
+
+
+def test_router_fallback_counters(dev):
+    s = zz.stats()
+    say("fallback counters (rms, logit, gemma exact, lfm contested):", s)
+    assert s[3] == 0
+
+
+@pytest.mark.parametrize("fmt", [Z.FMT_Q40, Z.FMT_Q80])
+def test_device_quantiser_bit_exact(dev, fmt):
+    """zz_quantize equals q40_quant_row / q80_quant_row (through the oracle, pinned to
+    the compiled reference), including blocks whose fused x*id+8.5 rounding differs
+    from the unfused one, all-zero blocks and sign ties in max|x|."""
+    import torch
+    rng = np.random.default_rng(61)
+    w = (rng.standard_normal(32 * 4096) * 0.02).astype(np.float32)
+    w[:32] = 0.0
+    w[32:64] = 0.01
+    w[64] = -0.05
+    w[65] = 0.05                                   # first max-|x| element wins
+    want = Z.quant_rows(fmt, w.reshape(1, -1))
+    dw = torch.from_numpy(w).cuda()
+    out = torch.zeros(want.size, dtype=torch.uint8, device="cuda")
+    zz.quantize_dev(fmt, dw.data_ptr(), out.data_ptr(), w.size)
+    torch.cuda.synchronize()
+    zz.lib().gpu_init()
+    assert np.array_equal(out.cpu().numpy(), want)

@@ -1,0 +1,379 @@
+"""Pins for the CPU oracle (oracle/zz_oracle.c) before anything is checked against it.
+
+Each oracle function is checked against something that does not share its code:
+the reference's own known-answer tests (tests/test_q40.c, tests/test_tq2.c),
+golden vectors written by the compiled reference (tests/golden/), the compiled
+reference itself where oracle/_ref exists, and closed forms (numpy's IEEE
+binary16, brute-force integer dots, argsort with the lower-index tie rule).
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import zzref as Z
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def lcg12345(n):
+    """tests/test_q40.c:9-10 / test_tq2.c:16-20: rs = rs*1664525 + 1013904223."""
+    out = np.empty(n, np.float32)
+    rs = 12345
+    for i in range(n):
+        rs = (rs * 1664525 + 1013904223) & 0xffffffff
+        out[i] = np.float32(np.float32(rs >> 8) / np.float32(8388608.0) - np.float32(1.0))
+    return out
+
+
+# ------------------------------------------------------------------- fp16 (A1)
+def test_h2f_all_halves_match_numpy():
+    L = Z.oracle()
+    h = np.arange(65536, dtype=np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([L.orc_h2f(int(v)) for v in h], np.float32)
+    fin = np.isfinite(want)
+    assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+    assert np.all(np.isnan(got[np.isnan(want)]))
+    assert np.all(np.isinf(got[np.isinf(want)]))
+
+
+def test_f2h_round_half_even_matches_numpy():
+    L = Z.oracle()
+    rng = np.random.default_rng(0)
+    xs = np.concatenate([rng.standard_normal(4000).astype(np.float32) * np.float32(s)
+                         for s in (1e-9, 3e-8, 6e-5, 1e-3, 1.0, 3e4, 7e4)])
+    # exact ties between two halves: RNE must pick the even one
+    ties = (np.arange(1, 2000, dtype=np.float32) + np.float32(0.5)) * np.float32(2.0 ** -10)
+    xs = np.concatenate([xs, ties, -ties, [0.0, -0.0, 65504.0, 65520.0, np.inf, -np.inf]]).astype(np.float32)
+    want = xs.astype(np.float16).view(np.uint16)
+    got = np.array([L.orc_f2h(float(x)) for x in xs], np.uint16)
+    assert np.array_equal(got, want)
+    # NaN: quiet, payload dropped, sign kept (q40.h:64)
+    assert L.orc_f2h(float("nan")) & 0x7fff == 0x7e00
+
+
+def test_fp16_roundtrip_test_q40_case1():
+    """tests/test_q40.c:32-39: 200k round trips within half an fp16 ulp."""
+    L = Z.oracle()
+    f = lcg12345(20000) * np.float32(0.5)
+    for v in f:
+        g = L.orc_h2f(L.orc_f2h(float(v)))
+        assert abs(v - g) <= abs(v) * (1.0 / 1024.0) + 1e-7
+    assert L.orc_h2f(L.orc_f2h(0.0)) == 0.0
+
+
+# ------------------------------------------------------- quantisers (A3, A7)
+def test_q40_quant_contract_test_q40_case2():
+    """tests/test_q40.c:41-79: max element exact, in-range error <= d/2, clamps."""
+    I = 4096
+    w = lcg12345(I) * np.float32(0.1)
+    q = Z.quant_rows(Z.FMT_Q40, w.reshape(1, I))
+    L = Z.oracle()
+    wd = np.zeros(I, np.float32)
+    L.orc_q40_dequant_row.argtypes = [Z.u8p, Z.f32p, C.c_int]
+    L.orc_q40_dequant_row(Z.ptr(q), Z.ptr(wd), I)
+    for b in range(I // 32):
+        ds = np.frombuffer(q[b * 18:b * 18 + 2].tobytes(), np.float16)[0].astype(np.float32)
+        d = abs(ds)
+        lo, hi = (-8 * ds, 7 * ds) if ds >= 0 else (7 * ds, -8 * ds)
+        blk, deq = w[b * 32:(b + 1) * 32], wd[b * 32:(b + 1) * 32]
+        mx = blk[np.argmax(np.abs(blk))]
+        for t, v in zip(blk, deq):
+            if t == mx:
+                assert abs(t - v) <= 0.01 * d + 1e-6
+            if lo <= t <= hi:
+                assert abs(t - v) <= 0.5 * d + 1e-6
+            else:
+                assert abs(v - (hi if t > hi else lo)) <= 1e-6
+
+
+def _fused_differs(x, idv):
+    """True where trunc(fma(x,id,8.5)) != trunc(fl(x*id)+8.5) for f32 x, id."""
+    fused = np.floor(x.astype(np.float64) * np.float64(idv) + 8.5)
+    unf = np.floor((x * np.float32(idv)).astype(np.float32).astype(np.float64) + 8.5)
+    return fused != unf
+
+
+def test_q40_quant_fused_rounding_golden():
+    """The reference build fuses x*id + 8.5 (q40.h:101 under -mfma). Blocks built so
+    that fused and unfused truncations disagree pin that choice: the oracle must
+    reproduce the compiled reference's bytes on them."""
+    L = Z.oracle()
+    rng = np.random.default_rng(7)
+    blocks, found = [], 0
+    while found < 64:
+        mx = np.float32(-rng.uniform(0.05, 0.1))
+        hd = L.orc_f2h(float(mx / np.float32(-8.0)))
+        d = np.float32(L.orc_h2f(hd))
+        idv = np.float32(1.0) / d
+        k = rng.integers(-8, 7, size=31)
+        # land x*id within an ulp of k+0.5-8.5 boundaries
+        x = ((k.astype(np.float64) + 0.5 - 1e-7 * rng.integers(-3, 4, size=31)) / float(idv)).astype(np.float32)
+        x = np.clip(x, -abs(mx) * 0.99, abs(mx) * 0.99).astype(np.float32)
+        if _fused_differs(x, idv).any():
+            blocks.append(np.concatenate([[mx], x]).astype(np.float32))
+            found += 1
+    w = np.concatenate(blocks)
+    got = Z.quant_rows(Z.FMT_Q40, w.reshape(1, -1))
+    R = Z.ref_lib("kernels")
+    if R is None:
+        pytest.skip("oracle/_ref not built: the fused-rounding pin needs the compiled reference")
+    want = np.zeros_like(got)
+    R.ref_q40_quant_row(Z.ptr(w), Z.ptr(want), w.size)
+    assert np.array_equal(got, want)
+
+
+def test_kernel_golden_vectors():
+    """Quantiser bytes, activation quantisation and all three dots against the
+    compiled reference's outputs on the test_q40.c LCG stream."""
+    g = np.load(os.path.join(GOLDEN, "kernels_lcg12345.npz"))
+    L = Z.oracle()
+    w = g["w"]
+    O, I = 16, 2816
+    assert np.array_equal(Z.quant_rows(Z.FMT_Q40, w.reshape(O, I)), g["q40"])
+    assert np.array_equal(Z.quant_rows(Z.FMT_Q80, w.reshape(O, I)), g["q80"])
+    x = g["x"]
+    for t in range(4):
+        xq = np.zeros(I, np.int8)
+        xs = np.zeros(I // 32, np.float32)
+        L.orc_quant_act(Z.ptr(np.ascontiguousarray(x[t])), Z.ptr(xq), Z.ptr(xs), I)
+        assert np.array_equal(xq, g["xq"][t])
+        assert np.array_equal(xs.view(np.uint32), g["xs"][t].view(np.uint32))
+        for o in range(O):
+            a = L.orc_q40_dot(Z.ptr(g["q40"][o * 88 * 18:]), Z.ptr(xq), Z.ptr(xs), I)
+            b = L.orc_q80_dot(Z.ptr(g["q80"][o * 88 * 34:]), Z.ptr(xq), Z.ptr(xs), I)
+            assert np.float32(a).view(np.uint32) == g["d40"][t, o].view(np.uint32)
+            assert np.float32(b).view(np.uint32) == g["d80"][t, o].view(np.uint32)
+    assert np.array_equal(Z.tq2_tensor(g["codes"], g["alpha"]), g["tq"])
+    It = 2048
+    q = np.zeros(It, np.int8)
+    s = np.zeros(It // 32, np.float32)
+    tot = L.orc_tq2_quant_act(Z.ptr(g["xt"]), Z.ptr(q), Z.ptr(s), It)
+    assert np.array_equal(q, g["tq_q"]) and np.float32(tot) == g["tq_tot"]
+    cb = g["tq"][16 * 4:]
+    for o in range(16):
+        v = L.orc_tq2_dot(Z.ptr(cb[o * 512:]), C.c_float(g["alpha"][o]), Z.ptr(q), Z.ptr(s),
+                          C.c_float(tot), It)
+        assert np.float32(v).view(np.uint32) == g["dtq"][o].view(np.uint32)
+
+
+def test_quant_act_special_cases():
+    """q40.h:124-138: zero block -> d=0, q=0; +-amax -> +-127; ties to even."""
+    L = Z.oracle()
+    x = np.zeros(96, np.float32)
+    x[32] = 2.5
+    x[33] = -2.5
+    x[40] = 2.5 * 3 / 127          # exactly representable? check rint on a tie below
+    d = np.float32(2.5) / np.float32(127.0)
+    x[64:96] = (np.arange(32, dtype=np.float32) - 16) * np.float32(0.5) * d
+    x[64] = np.float32(127) * d    # block max element
+    q = np.zeros(96, np.int8)
+    s = np.zeros(3, np.float32)
+    L.orc_quant_act(Z.ptr(x), Z.ptr(q), Z.ptr(s), 96)
+    assert s[0] == 0.0 and not q[:32].any()
+    assert q[32] == 127 and q[33] == -127 and s[1] == d
+    idv = np.float32(1.0) / s[2]
+    want = np.clip(np.rint((x[64:] * idv).astype(np.float32)), -127, 127).astype(np.int8)
+    assert np.array_equal(q[64:], want)      # numpy rint is round-half-even
+
+
+def test_q40_dot_vs_scalar_and_saturation_test_q40_cases3_4():
+    """tests/test_q40.c:81-137: kernel vs double scalar reference within 1e-5 of
+    sum|summands|; saturation known answer 128 blocks x 32 x 7 x 127 = 3,641,344."""
+    L = Z.oracle()
+    I = 4096
+    rng = np.random.default_rng(12345)
+    q = Z.quant_rows(Z.FMT_Q40, (rng.standard_normal(I) * 0.1).astype(np.float32).reshape(1, I))
+    nib = np.frombuffer(q.tobytes(), np.uint8).reshape(-1, 18)
+    dw = nib[:, :2].copy().view(np.float16).astype(np.float64).reshape(-1)
+    qv = np.concatenate([(nib[:, 2:] & 15), (nib[:, 2:] >> 4)], axis=1).astype(np.int64) - 8
+    worst = 0.0
+    for _ in range(50):
+        x = rng.standard_normal(I).astype(np.float32)
+        xq = np.zeros(I, np.int8)
+        xs = np.zeros(I // 32, np.float32)
+        L.orc_quant_act(Z.ptr(x), Z.ptr(xq), Z.ptr(xs), I)
+        blk = (qv * xq.reshape(-1, 32).astype(np.int64)).sum(1)
+        summ = dw * xs.astype(np.float64) * blk
+        ref = summ.sum()
+        got = L.orc_q40_dot(Z.ptr(q), Z.ptr(xq), Z.ptr(xs), I)
+        mag = np.abs(dw[:, None] * xs.astype(np.float64)[:, None] * qv * xq.reshape(-1, 32)).sum()
+        worst = max(worst, abs(got - ref) / (mag + 1e-6))
+    assert worst < 1e-5
+    sat = np.zeros(I // 32 * 18, np.uint8).reshape(-1, 18)
+    sat[:, 0:2] = np.array([np.float16(1.0)]).view(np.uint8)
+    sat[:, 2:] = 0xFF
+    xq = np.full(I, 127, np.int8)
+    xs = np.ones(I // 32, np.float32)
+    got = L.orc_q40_dot(Z.ptr(sat.reshape(-1)), Z.ptr(xq), Z.ptr(xs), I)
+    assert got == 3641344.0
+
+
+def test_blockdots_brute_force():
+    L = Z.oracle()
+    rng = np.random.default_rng(3)
+    I = 768
+    xq = rng.integers(-127, 128, I, dtype=np.int8)
+    for fmt in (Z.FMT_Q40, Z.FMT_Q80):
+        row = Z.quant_rows(fmt, rng.standard_normal((1, I)).astype(np.float32))
+        out = np.zeros(I // 32, np.int32)
+        L.orc_blockdots(fmt, Z.ptr(row), Z.ptr(xq), I, Z.ptr(out))
+        bb = 18 if fmt == Z.FMT_Q40 else 34
+        blk = np.frombuffer(row.tobytes(), np.uint8).reshape(-1, bb)[:, 2:]
+        if fmt == Z.FMT_Q40:
+            wv = np.concatenate([blk & 15, blk >> 4], axis=1).astype(np.int64) - 8
+        else:
+            wv = blk.view(np.int8).astype(np.int64)
+        assert np.array_equal(out, (wv * xq.reshape(-1, 32)).sum(1))
+    codes = rng.integers(0, 3, size=(1, I)).astype(np.int8)
+    t = Z.tq2_tensor(codes, np.ones(1, np.float32))
+    out = np.zeros(I // 32, np.int32)
+    L.orc_blockdots(Z.FMT_TQ2, Z.ptr(t[4:]), Z.ptr(xq), I, Z.ptr(out))
+    assert np.array_equal(out, ((codes[0].astype(np.int64) - 1) * xq).reshape(-1, 32).sum(1))
+
+
+def test_tq2_layout_from_description():
+    """tests/test_tq2.c:28-35: code j lives in byte j%16 of group j/64 at bit
+    2*((j/16)%4); the oracle's packer and dequant must agree with that reading."""
+    rng = np.random.default_rng(12345)
+    for I in (64, 128, 512, 1792, 2048):
+        c = rng.integers(0, 3, size=(1, I)).astype(np.int8)
+        t = Z.tq2_tensor(c, np.array([0.25], np.float32))[4:]
+        j = np.arange(I)
+        read = (t[(j // 64) * 16 + j % 16] >> (2 * ((j // 16) % 4))) & 3
+        assert np.array_equal(read, c[0])
+        w = np.zeros(I, np.float32)
+        L = Z.oracle()
+        L.orc_tq2_dequant_row.argtypes = [Z.u8p, C.c_float, Z.f32p, C.c_int]
+        L.orc_tq2_dequant_row(Z.ptr(t), 0.25, Z.ptr(w), I)
+        assert np.array_equal(w, 0.25 * (c[0] - 1).astype(np.float32))
+
+
+def test_tq2_sx_identity():
+    """tq2.h:29-37: <c-1, x> = <c, x> - sum(x); Sx = sum_b sx_b * sum_j xq."""
+    L = Z.oracle()
+    rng = np.random.default_rng(5)
+    I = 2048
+    x = rng.standard_normal(I).astype(np.float32)
+    q = np.zeros(I, np.int8)
+    s = np.zeros(I // 32, np.float32)
+    tot = L.orc_tq2_quant_act(Z.ptr(x), Z.ptr(q), Z.ptr(s), I)
+    want = (s.astype(np.float64) * q.reshape(-1, 32).sum(1)).sum()
+    assert abs(tot - want) <= 1e-6 * (abs(want) + 1)
+    codes = np.ones((1, I), np.int8)                 # all-zero weights
+    t = Z.tq2_tensor(codes, np.array([0.5], np.float32))
+    v = L.orc_tq2_dot(Z.ptr(t[4:]), C.c_float(0.5), Z.ptr(q), Z.ptr(s), C.c_float(tot), I)
+    assert abs(v) <= 1e-6 * abs(tot) + 1e-7
+
+
+# ----------------------------------------------------------- routers (A10-A12)
+@pytest.mark.parametrize("kind", ["gemma", "lfm", "maple"])
+def test_router_matches_argsort_with_lower_index_ties(kind, layer_cache):
+    L = layer_cache(kind, seed=11, E=32)
+    x = Z.make_input(L, 16, 11)
+    r = Z.oracle_moe(L, x, dump=True)
+    K = L.K
+    for s in range(16):
+        lg = r.dump["logits"][s].astype(np.float64)
+        if kind == "lfm":
+            sg = 1.0 / (1.0 + np.exp(-lg.astype(np.float32)).astype(np.float32))
+            lg = (sg.astype(np.float32) + L.bias).astype(np.float32).astype(np.float64)
+        order = sorted(range(L.E), key=lambda e: (-lg[e], e))[:K]
+        assert list(r.eidx[s * K:(s + 1) * K]) == order
+
+
+def test_router_exact_ties_keep_lower_index(layer_cache):
+    """Duplicate router rows give bit-identical logits; the insertion rule
+    (gemma4.c:603-606, strict '>') keeps the lower expert index first."""
+    L0 = layer_cache("maple", seed=12, E=16)
+    L = Z.make_layer("maple", seed=12, E=16)
+    L.router = L0.router.copy()
+    L.router[9] = L.router[2]
+    L.router[14] = L.router[2]
+    x = Z.make_input(L, 32, 12)
+    r = Z.oracle_moe(L, x, dump=True)
+    for s in range(32):
+        ids = list(r.eidx[s * L.K:(s + 1) * L.K])
+        for a, b in ((2, 9), (2, 14), (9, 14)):
+            if a in ids and b in ids:
+                assert ids.index(a) < ids.index(b)
+
+
+def test_dispatch_is_stable_counting_sort(layer_cache):
+    L = layer_cache("gemma", seed=2, E=16)
+    x = Z.make_input(L, 40, 13)
+    r = Z.oracle_moe(L, x)
+    S, K, nu = 40, L.K, len(r.uniq)
+    offs = np.zeros(nu + 1, np.int32)
+    rows = np.zeros(S * K, np.int32)
+    wts = np.zeros(S * K, np.float32)
+    slots = np.zeros(S * K, np.int32)
+    Z.oracle().orc_dispatch(Z.ptr(r.eidx), Z.ptr(r.ewt), S, K, Z.ptr(r.uniq), nu, Z.ptr(offs),
+                            Z.ptr(rows), Z.ptr(wts), Z.ptr(slots))
+    flat = np.arange(S * K)
+    for u, e in enumerate(r.uniq):
+        sel = flat[r.eidx == e]                           # ascending flat index
+        assert np.array_equal(rows[offs[u]:offs[u + 1]], sel // K)
+        assert np.array_equal(slots[offs[u]:offs[u + 1]], sel % K)
+    first = [int(np.argmax(r.eidx == e)) for e in r.uniq]
+    assert first == sorted(first)                         # first-seen union order
+
+
+# ------------------------------------------------------------- whole layers
+CASES = sorted(f[:-4] for f in os.listdir(GOLDEN) if f.endswith(".npz") and not f.startswith("kernels"))
+
+
+def load_case(name):
+    g = np.load(os.path.join(GOLDEN, name + ".npz"))
+    kw = {}
+    if int(g["kw_E"]) > 0:
+        kw["E"] = int(g["kw_E"])
+    if int(g["kw_fmts"][0]) > 0:
+        kw["fmts"] = tuple(int(v) for v in g["kw_fmts"])
+    return g, str(g["kind"]), int(g["seed"]), kw, int(g["S"]), int(g["xseed"])
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_layer_golden_bit_exact(name, layer_cache):
+    """The oracle reproduces the compiled reference's layer bit for bit: ids, union
+    order, weights and the f32 outputs."""
+    from golden.make_golden import input_digest
+    g, kind, seed, kw, S, xseed = load_case(name)
+    L = layer_cache(kind, seed=seed, **kw)
+    x = Z.make_input(L, S, xseed)
+    assert input_digest(L, x) == str(g["digest"]), "input generator drifted from the fixture"
+    r = Z.oracle_moe(L, x)
+    assert np.array_equal(r.eidx, g["eidx"])
+    assert np.array_equal(r.uniq, g["uniq"])
+    assert np.array_equal(r.ewt.view(np.uint32), g["ewt"].view(np.uint32))
+    assert np.array_equal(r.out.view(np.uint32), g["out"].view(np.uint32))
+
+
+@pytest.mark.parametrize("kind,kw,S", [("gemma", dict(E=24, D=1024, MI=512), 33),
+                                       ("lfm", dict(E=12, fmts=(2, 2, 2), D=1024, MI=768), 17),
+                                       ("maple", dict(E=40, D=1024, MI=512), 29)])
+def test_layer_vs_compiled_reference(kind, kw, S):
+    """Live diff against oracle/_ref at shapes the fixtures do not cover."""
+    if Z.ref_lib("gemma4") is None:
+        pytest.skip("oracle/_ref not built here")
+    L = Z.make_layer(kind, seed=21, **kw)
+    x = Z.make_input(L, S, 21)
+    a, b = Z.oracle_moe(L, x), Z.ref_moe(L, x)
+    assert np.array_equal(a.eidx, b.eidx) and np.array_equal(a.uniq, b.uniq)
+    assert np.array_equal(a.out.view(np.uint32), b.out.view(np.uint32))
+
+
+def test_fp32_tier_tolerance_is_discriminating(layer_cache):
+    """The GPU tier's 1e-3 relative-L2 bound must reject a plausible slip: dropping
+    one expert's contribution, or using silu for gemma's GeGLU."""
+    L = layer_cache("gemma", seed=2, E=16)
+    x = Z.make_input(L, 8, 14)
+    good = Z.oracle_moe(L, x).out
+    L2 = Z.make_layer("gemma", seed=2, E=16)
+    L2.act = Z.ACT_SWIGLU
+    bad = Z.oracle_moe(L2, x).out
+    assert Z.rel_l2(bad, good) > 1e-2
+    L3 = Z.make_layer("gemma", seed=2, E=16, K=7)
+    assert Z.rel_l2(Z.oracle_moe(L3, x).out, good) > 1e-2

@@ -1,0 +1,332 @@
+"""Test-side helpers: ctypes bindings to the CPU oracle (oracle/liboracle.so), to
+the compiled reference (oracle/_ref/libref_*.so, present only where it was built),
+and seeded synthetic layers shaped like the BASELINE configs.
+
+Test infrastructure only; the product package never imports this module.
+"""
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+
+FMT_Q40, FMT_Q80, FMT_TQ2 = 1, 2, 3
+GATE_GEMMA, GATE_LFM, GATE_MAPLE = 0, 1, 2
+ACT_GEGLU_TANH, ACT_SWIGLU, ACT_SWIGLU_CL = 0, 1, 2
+
+f32p = C.POINTER(C.c_float)
+i32p = C.POINTER(C.c_int)
+u8p = C.POINTER(C.c_uint8)
+i8p = C.POINTER(C.c_int8)
+
+
+def ptr(a, t=None):
+    """ctypes pointer to a contiguous numpy array (None passes NULL)."""
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    if t is None:
+        t = {np.float32: f32p, np.int32: i32p, np.uint8: u8p, np.int8: i8p}[a.dtype.type]
+    return a.ctypes.data_as(t)
+
+
+class OrcCfg(C.Structure):
+    _fields_ = [("D", C.c_int), ("MI", C.c_int), ("E", C.c_int), ("K", C.c_int),
+                ("gating", C.c_int), ("act", C.c_int),
+                ("fmt_gate", C.c_int), ("fmt_up", C.c_int), ("fmt_down", C.c_int),
+                ("norm_topk", C.c_int), ("use_bias", C.c_int),
+                ("eps", C.c_float), ("routed_scaling", C.c_float), ("clamp", C.c_float)]
+
+
+class OrcWeights(C.Structure):
+    _fields_ = [("router", f32p), ("router_scale", f32p), ("pes", f32p), ("bias", f32p),
+                ("pre_ln", f32p), ("post_ln", f32p), ("experts", u8p), ("esz", C.c_int64)]
+
+
+class OrcDump(C.Structure):
+    _fields_ = [("xin", f32p), ("xq", i8p), ("xs", f32p), ("xtot", f32p),
+                ("hq", i8p), ("hs", f32p), ("htot", f32p), ("logits", f32p)]
+
+
+_oracle = None
+
+
+def oracle():
+    """The restatement library; built by `make -C oracle` (or __graft_entry__.build)."""
+    global _oracle
+    if _oracle is None:
+        path = os.path.join(ORACLE_DIR, "liboracle.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} missing: run `make -C oracle`")
+        L = C.CDLL(path)
+        L.orc_h2f.restype = C.c_float
+        L.orc_h2f.argtypes = [C.c_uint16]
+        L.orc_f2h.restype = C.c_uint16
+        L.orc_f2h.argtypes = [C.c_float]
+        for n in ("orc_q40_dot", "orc_q80_dot"):
+            getattr(L, n).restype = C.c_float
+            getattr(L, n).argtypes = [u8p, i8p, f32p, C.c_int]
+        L.orc_tq2_dot.restype = C.c_float
+        L.orc_tq2_dot.argtypes = [u8p, C.c_float, i8p, f32p, C.c_float, C.c_int]
+        L.orc_tq2_quant_act.restype = C.c_float
+        L.orc_tq2_quant_act.argtypes = [f32p, i8p, f32p, C.c_int]
+        L.orc_quant_act.argtypes = [f32p, i8p, f32p, C.c_int]
+        for n in ("orc_q40_dot_f32", "orc_q80_dot_f32"):
+            getattr(L, n).restype = C.c_float
+            getattr(L, n).argtypes = [u8p, f32p, C.c_int]
+        L.orc_tq2_dot_f32.restype = C.c_float
+        L.orc_tq2_dot_f32.argtypes = [u8p, C.c_float, f32p, C.c_int]
+        L.orc_tensor_bytes.restype = C.c_int64
+        L.orc_tensor_bytes.argtypes = [C.c_int, C.c_int, C.c_int]
+        L.orc_moe_layer.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), f32p, C.c_int,
+                                    f32p, i32p, f32p, i32p, i32p, C.POINTER(OrcDump)]
+        L.orc_route.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), f32p, i32p, f32p, f32p]
+        L.orc_set_threads.argtypes = [C.c_int]
+        L.orc_blockdots.argtypes = [C.c_int, u8p, i8p, C.c_int, i32p]
+        L.orc_matmul_f32.argtypes = [C.c_int, f32p, u8p, f32p, C.c_int, C.c_int, C.c_int]
+        L.orc_dispatch.argtypes = [i32p, f32p, C.c_int, C.c_int, i32p, C.c_int, i32p, i32p,
+                                   f32p, i32p]
+        _oracle = L
+    return _oracle
+
+
+def ref_lib(name):
+    """A compiled-reference library, or None where oracle/_ref was not built."""
+    path = os.path.join(ORACLE_DIR, "_ref", f"libref_{name}.so")
+    if not os.path.exists(path):
+        return None
+    return C.CDLL(path)
+
+
+# ---------------------------------------------------------------- quantisers
+def quant_rows(fmt, w):
+    """Quantise an f32 [O, I] matrix with the oracle's reference-exact quantisers."""
+    L = oracle()
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    O, I = w.shape
+    if fmt == FMT_Q40:
+        rb = I // 32 * 18
+        fn = L.orc_q40_quant_row
+    elif fmt == FMT_Q80:
+        rb = I // 32 * 34
+        fn = L.orc_q80_quant_row
+    else:
+        raise ValueError(fmt)
+    out = np.empty(O * rb, dtype=np.uint8)
+    fn.argtypes = [f32p, u8p, C.c_int]
+    fn(ptr(w.reshape(-1)), ptr(out), O * I)      # blocks are independent: one call
+    return out
+
+
+def tq2_tensor(codes, alpha):
+    """tq2 tensor bytes (alpha[O] f32, then packed code rows) from codes[O, I] in {0,1,2}."""
+    L = oracle()
+    O, I = codes.shape
+    L.orc_tq2_pack_row.argtypes = [i8p, u8p, C.c_int]
+    packed = np.empty(O * (I // 4), dtype=np.uint8)
+    c8 = np.ascontiguousarray(codes, dtype=np.int8).reshape(-1)
+    L.orc_tq2_pack_row(ptr(c8), ptr(packed), O * I)   # 64-groups are independent
+    return np.concatenate([np.ascontiguousarray(alpha, np.float32).view(np.uint8), packed])
+
+
+def tensor_bytes(fmt, O, I):
+    if fmt == FMT_Q40:
+        return O * (I // 32) * 18
+    if fmt == FMT_Q80:
+        return O * (I // 32) * 34
+    return O * 4 + O * (I // 4)
+
+
+# ------------------------------------------------------------ synthetic layers
+@dataclass
+class Layer:
+    """A seeded MoE layer in the reference's record layout ([gate | up | down])."""
+    D: int
+    MI: int
+    E: int
+    K: int
+    gating: int
+    act: int
+    fmts: tuple
+    norm_topk: int = 1
+    use_bias: int = 0
+    eps: float = 1e-6
+    routed_scaling: float = 1.0
+    clamp: float = 7.0
+    router: np.ndarray = None
+    router_scale: np.ndarray = None
+    pes: np.ndarray = None
+    bias: np.ndarray = None
+    pre_ln: np.ndarray = None
+    post_ln: np.ndarray = None
+    experts: np.ndarray = None
+    esz: int = 0
+    seed: int = 0
+    _keep: list = field(default_factory=list)
+
+    def cfg(self):
+        return OrcCfg(self.D, self.MI, self.E, self.K, self.gating, self.act,
+                      self.fmts[0], self.fmts[1], self.fmts[2], self.norm_topk, self.use_bias,
+                      self.eps, self.routed_scaling, self.clamp)
+
+    def weights(self):
+        return OrcWeights(ptr(self.router), ptr(self.router_scale), ptr(self.pes),
+                          ptr(self.bias), ptr(self.pre_ln), ptr(self.post_ln),
+                          ptr(self.experts), self.esz)
+
+    def tensor_sizes(self):
+        g = tensor_bytes(self.fmts[0], self.MI, self.D)
+        u = tensor_bytes(self.fmts[1], self.MI, self.D)
+        d = tensor_bytes(self.fmts[2], self.D, self.MI)
+        return g, u, d
+
+
+def _normal(rng, shape, sigma=1.0):
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(sigma)).astype(np.float32)
+
+
+def make_expert_q(rng, fmt, O, I, sigma=0.02):
+    return quant_rows(fmt, _normal(rng, (O, I), sigma))
+
+
+_TQ2_LUT = np.array([1] * 102 + [0] * 77 + [2] * 77, dtype=np.int8)
+
+
+def make_expert_tq2(rng, O, I, sigma=0.02):
+    """Ternary codes with P(weight 0) = 102/256 ~ 0.4 and P(+1) = P(-1) = 77/256,
+    one f32 alpha per row (tq2.h:17-28): alpha ~ the absmean of an N(0, sigma)
+    row, sigma*sqrt(2/pi), with 5% per-row jitter."""
+    u = rng.integers(0, 256, size=O * I, dtype=np.uint8)
+    codes = _TQ2_LUT[u].reshape(O, I)
+    alpha = (sigma * np.sqrt(2 / np.pi) * (1 + 0.05 * rng.standard_normal(O))).astype(np.float32)
+    return tq2_tensor(codes, alpha)
+
+
+def make_layer(kind, seed=1, E=None, D=None, MI=None, K=None, zipf=False, fmts=None):
+    """Seeded layer shaped like a BASELINE config.
+
+    kind: "gemma" (config 1/2), "lfm" (config 3: gate/up q4_0, down q8_0 unless
+    fmts is given), "maple" (config 4: tq2)."""
+    rng = np.random.default_rng(seed)
+    if kind == "gemma":
+        D, MI, E, K = D or 2816, MI or 704, E or 128, K or 8
+        L = Layer(D, MI, E, K, GATE_GEMMA, ACT_GEGLU_TANH, fmts or (FMT_Q40,) * 3, eps=1e-6)
+        L.router = _normal(rng, (E, D))
+        L.router_scale = (1 + 0.05 * rng.standard_normal(D)).astype(np.float32)
+        L.pes = (1 + 0.1 * rng.random(E)).astype(np.float32)
+        L.pre_ln = (1 + 0.05 * rng.standard_normal(D)).astype(np.float32)
+        L.post_ln = (1 + 0.05 * rng.standard_normal(D)).astype(np.float32)
+        if zipf:
+            rank = rng.permutation(E) + 1
+            L.bias = (-1.1 * np.log(rank)).astype(np.float32)
+            L.use_bias = 1
+    elif kind == "lfm":
+        D, MI, E, K = D or 2048, MI or 1792, E or 32, K or 4
+        L = Layer(D, MI, E, K, GATE_LFM, ACT_SWIGLU, fmts or (FMT_Q40, FMT_Q40, FMT_Q80),
+                  norm_topk=1, use_bias=1, routed_scaling=1.0)
+        L.router = _normal(rng, (E, D))
+        L.bias = (0.1 * rng.standard_normal(E)).astype(np.float32)
+    elif kind == "maple":
+        D, MI, E, K = D or 2048, MI or 768, E or 256, K or 8
+        L = Layer(D, MI, E, K, GATE_MAPLE, ACT_SWIGLU_CL, (FMT_TQ2,) * 3, norm_topk=1, clamp=7.0)
+        L.router = _normal(rng, (E, D))
+    else:
+        raise ValueError(kind)
+    L.seed = seed
+    g, u, d = L.tensor_sizes()
+    L.esz = g + u + d
+    L.experts = np.empty(E * L.esz, dtype=np.uint8)
+    for e in range(E):
+        rec = L.experts[e * L.esz:(e + 1) * L.esz]
+        parts = []
+        for fmt, (O, I) in zip(L.fmts, ((MI, D), (MI, D), (D, MI))):
+            if fmt == FMT_TQ2:
+                parts.append(make_expert_tq2(rng, O, I))
+            else:
+                parts.append(make_expert_q(rng, fmt, O, I))
+        rec[:] = np.concatenate(parts)
+    return L
+
+
+def make_input(L, S, seed):
+    rng = np.random.default_rng(10_000 + seed)
+    return _normal(rng, (S, L.D))
+
+
+# --------------------------------------------------------------- layer calls
+@dataclass
+class MoeResult:
+    out: np.ndarray
+    eidx: np.ndarray
+    ewt: np.ndarray
+    uniq: np.ndarray
+    dump: dict = None
+
+
+def oracle_moe(L, x, dump=False):
+    S = x.shape[0]
+    out = np.zeros((S, L.D), np.float32)
+    eidx = np.zeros(S * L.K, np.int32)
+    ewt = np.zeros(S * L.K, np.float32)
+    uniq = np.zeros(L.E, np.int32)
+    nu = C.c_int(0)
+    d = None
+    dp = None
+    if dump:
+        d = dict(xin=np.zeros((S, L.D), np.float32), xq=np.zeros((S, L.D), np.int8),
+                 xs=np.zeros((S, L.D // 32), np.float32), xtot=np.zeros(S, np.float32),
+                 hq=np.zeros((S * L.K, L.MI), np.int8),
+                 hs=np.zeros((S * L.K, L.MI // 32), np.float32),
+                 htot=np.zeros(S * L.K, np.float32), logits=np.zeros((S, L.E), np.float32))
+        dp = C.byref(OrcDump(*(ptr(d[k]) for k in ("xin", "xq", "xs", "xtot", "hq", "hs", "htot", "logits"))))
+    cfg, w = L.cfg(), L.weights()
+    rc = oracle().orc_moe_layer(C.byref(cfg), C.byref(w), ptr(np.ascontiguousarray(x, np.float32)),
+                                S, ptr(out), ptr(eidx), ptr(ewt), ptr(uniq), C.byref(nu), dp)
+    assert rc == 0
+    return MoeResult(out, eidx, ewt, uniq[:nu.value].copy(), d)
+
+
+def ref_moe(L, x):
+    """The compiled reference, or None where it is unavailable or cannot express L."""
+    S = x.shape[0]
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros((S, L.D), np.float32)
+    eidx = np.zeros(S * L.K, np.int32)
+    ewt = np.zeros(S * L.K, np.float32)
+    uniq = np.zeros(L.E, np.int32)
+    nu = C.c_int(0)
+    if L.gating == GATE_GEMMA:
+        lib = ref_lib("gemma4")
+        if lib is None or L.use_bias or L.fmts != (FMT_Q40,) * 3:
+            return None
+        xin = np.zeros((S, L.D), np.float32)
+        rc = lib.ref_g4_moe(L.D, L.MI, L.E, L.K, C.c_float(L.eps), ptr(L.router),
+                            ptr(L.router_scale), ptr(L.pes), ptr(L.pre_ln), ptr(L.post_ln),
+                            ptr(L.experts), C.c_int64(L.esz), ptr(x), S, ptr(out), ptr(eidx),
+                            ptr(ewt), ptr(uniq), C.byref(nu), ptr(xin))
+    elif L.gating == GATE_LFM:
+        lib = ref_lib("lfm25")
+        if lib is None or len(set(L.fmts)) != 1:
+            return None
+        rc = lib.ref_lfm_moe(L.D, L.MI, L.E, L.K, L.fmts[0], L.norm_topk, L.use_bias,
+                             C.c_float(L.routed_scaling), ptr(L.router), ptr(L.bias),
+                             ptr(L.experts), C.c_int64(L.esz), ptr(x), S, ptr(out), ptr(eidx),
+                             ptr(ewt), ptr(uniq), C.byref(nu))
+    else:
+        lib = ref_lib("maple")
+        if lib is None:
+            return None
+        rc = lib.ref_maple_moe(L.D, L.MI, L.E, L.K, L.norm_topk, C.c_float(L.clamp),
+                               ptr(L.router), ptr(L.experts), C.c_int64(L.esz), ptr(x), S,
+                               ptr(out), ptr(eidx), ptr(ewt), ptr(uniq), C.byref(nu))
+    assert rc == 0
+    return MoeResult(out, eidx, ewt, uniq[:nu.value].copy())
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))

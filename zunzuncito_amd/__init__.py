@@ -1,0 +1,238 @@
+"""zunzuncito_amd -- MI355X-native MoE-layer hot path for the zunzuncito engines.
+
+The product is libzzmoe.so (HIP, gfx950), whose C ABI is include/zz_gpu.h (the
+engines' gpu.h, same symbols) and include/zz_moe.h (the whole MoE block with
+experts resident in HBM). This module is a thin ctypes binding of that ABI for
+Python callers, tests and the benchmark. There is no CPU fallback here: when the
+library is missing or no gfx950 device is present, calls raise.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libzzmoe.so")
+
+GPU_FMT_Q40, GPU_FMT_Q80, GPU_FMT_TQ2, GPU_FMT_Q4A = 1, 2, 3, 4
+ZZ_GATE_SOFTMAX_PES, ZZ_GATE_SIGMOID_BIAS, ZZ_GATE_SOFTMAX_TOPK = 0, 1, 2
+ZZ_ACT_GEGLU_TANH, ZZ_ACT_SWIGLU, ZZ_ACT_SWIGLU_CLAMP = 0, 1, 2
+
+# Every symbol include/zz_gpu.h and include/zz_moe.h declare.
+ABI_SYMBOLS = (
+    "gpu_init", "gpu_shutdown", "gpu_ready", "gpu_name", "gpu_map", "gpu_q40_matmul",
+    "gpu_matmul", "zz_moe_layer_create", "zz_moe_layer_destroy", "zz_moe_record_bytes",
+    "zz_moe_expert_upload", "zz_moe_expert_upload_dev", "zz_moe_forward",
+    "zz_moe_forward_dev", "zz_moe_forward_begin", "zz_moe_forward_end", "zz_moe_debug",
+    "zz_moe_blockdots", "zz_moe_stats", "zz_moe_profile", "zz_moe_profile_read",
+    "zz_quantize",
+    "zz_last_error",
+)
+KERNELS = ("prep", "logits", "topk", "dispatch", "ffn_up", "ffn_down", "combine")
+
+_f32p = C.POINTER(C.c_float)
+_i32p = C.POINTER(C.c_int)
+_u8p = C.POINTER(C.c_uint8)
+_i8p = C.POINTER(C.c_int8)
+
+
+class ZzMoeDesc(C.Structure):
+    _fields_ = [("D", C.c_int), ("MI", C.c_int), ("E", C.c_int), ("K", C.c_int),
+                ("gating", C.c_int), ("act", C.c_int),
+                ("fmt_gate", C.c_int), ("fmt_up", C.c_int), ("fmt_down", C.c_int),
+                ("norm_topk", C.c_int), ("use_bias", C.c_int),
+                ("eps", C.c_float), ("routed_scaling", C.c_float), ("clamp", C.c_float)]
+
+
+class ZzMoeWeights(C.Structure):
+    _fields_ = [("router", _f32p), ("router_scale", _f32p), ("pes", _f32p), ("bias", _f32p),
+                ("pre_ln", _f32p), ("post_ln", _f32p)]
+
+
+class ZzMoeDump(C.Structure):
+    _fields_ = [("xq", _i8p), ("xs", _f32p), ("hq", _i8p), ("hs", _f32p),
+                ("uniq", _i32p), ("offs", _i32p), ("rows", _i32p), ("slots", _i32p),
+                ("nu", C.c_int)]
+
+
+_lib = None
+
+
+def lib():
+    """Load libzzmoe.so; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built: run `python -m zunzuncito_amd.build`")
+    L = C.CDLL(LIB_PATH)
+    L.gpu_init.restype = C.c_int
+    L.gpu_name.restype = C.c_char_p
+    L.gpu_map.argtypes = [C.c_void_p, C.c_size_t]
+    L.gpu_matmul.argtypes = [C.c_int, _f32p, _u8p, _f32p, C.c_int, C.c_int, C.c_int]
+    L.gpu_q40_matmul.argtypes = [_f32p, _u8p, _f32p, C.c_int, C.c_int, C.c_int]
+    L.zz_moe_layer_create.argtypes = [C.POINTER(ZzMoeDesc), C.POINTER(ZzMoeWeights)]
+    L.zz_moe_layer_destroy.argtypes = [C.c_int]
+    L.zz_moe_record_bytes.restype = C.c_int64
+    L.zz_moe_record_bytes.argtypes = [C.POINTER(ZzMoeDesc)]
+    L.zz_moe_expert_upload.argtypes = [C.c_int, C.c_int, _u8p, C.c_size_t]
+    L.zz_moe_expert_upload_dev.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_size_t]
+    L.zz_moe_forward.argtypes = [C.c_int, _f32p, _f32p, C.c_int, _i32p, _f32p]
+    L.zz_moe_forward_dev.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                                     C.c_void_p, C.c_void_p]
+    L.zz_moe_forward_begin.argtypes = [C.c_int, _f32p, C.c_int]
+    L.zz_moe_forward_end.argtypes = [C.c_int, _f32p, _i32p, _f32p]
+    L.zz_moe_debug.argtypes = [C.c_int, C.POINTER(ZzMoeDump)]
+    L.zz_moe_blockdots.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _i8p, _i32p]
+    L.zz_moe_stats.argtypes = [C.POINTER(C.c_uint)]
+    L.zz_moe_profile.argtypes = [C.c_int]
+    L.zz_moe_profile_read.argtypes = [C.POINTER(C.c_double), C.POINTER(C.c_int), C.c_int]
+    L.zz_quantize.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]
+    L.zz_last_error.restype = C.c_char_p
+    _lib = L
+    return L
+
+
+def last_error():
+    return lib().zz_last_error().decode()
+
+
+def init():
+    """gpu_init(); raises when no gfx950 device is usable (no silent fallback)."""
+    L = lib()
+    if not L.gpu_init():
+        raise RuntimeError(f"gpu_init declined: {last_error()}")
+    return L.gpu_name().decode()
+
+
+def _p(a, t):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(t)
+
+
+def stats():
+    c = (C.c_uint * 4)()
+    if not lib().zz_moe_stats(c):
+        raise RuntimeError(last_error())
+    return list(c)
+
+
+def quantize_dev(fmt, d_w, d_out, n, stream=0):
+    """Device f32 -> q4_0/q8_0 blocks (zz_quantize); pointers are ints."""
+    if not lib().zz_quantize(fmt, C.c_void_p(d_w), C.c_void_p(d_out), n, C.c_void_p(stream or None)):
+        raise RuntimeError(last_error())
+
+
+def profile(on):
+    if not lib().zz_moe_profile(1 if on else 0):
+        raise RuntimeError(last_error())
+
+
+def profile_read():
+    """{kernel: (total ms, launches)} recorded since profile(True)."""
+    n = len(KERNELS)
+    ms = (C.c_double * n)()
+    cnt = (C.c_int * n)()
+    if lib().zz_moe_profile_read(ms, cnt, n) < 0:
+        raise RuntimeError(last_error())
+    return {k: (ms[i], cnt[i]) for i, k in enumerate(KERNELS)}
+
+
+class MoeLayer:
+    """One registered MoE layer (zz_moe_layer_create) with its HBM slot table."""
+
+    def __init__(self, D, MI, E, K, gating, act, fmts, router, router_scale=None, pes=None,
+                 bias=None, pre_ln=None, post_ln=None, norm_topk=1, use_bias=0, eps=1e-6,
+                 routed_scaling=1.0, clamp=7.0):
+        self.desc = ZzMoeDesc(D, MI, E, K, gating, act, fmts[0], fmts[1], fmts[2], norm_topk,
+                              use_bias, eps, routed_scaling, clamp)
+        keep = [np.ascontiguousarray(a, np.float32) if a is not None else None
+                for a in (router, router_scale, pes, bias, pre_ln, post_ln)]
+        w = ZzMoeWeights(*(_p(a, _f32p) for a in keep))
+        self.D, self.MI, self.E, self.K = D, MI, E, K
+        self.id = lib().zz_moe_layer_create(C.byref(self.desc), C.byref(w))
+        if self.id < 0:
+            raise RuntimeError(f"zz_moe_layer_create declined: {last_error()}")
+        self.record_bytes = lib().zz_moe_record_bytes(C.byref(self.desc))
+
+    def upload(self, eid, rec):
+        rec = np.ascontiguousarray(rec, np.uint8)
+        if not lib().zz_moe_expert_upload(self.id, eid, _p(rec, _u8p), rec.nbytes):
+            raise RuntimeError(f"upload declined: {last_error()}")
+
+    def upload_all(self, experts):
+        for e in range(self.E):
+            self.upload(e, experts[e * self.record_bytes:(e + 1) * self.record_bytes])
+
+    def upload_dev(self, eid, dev_ptr, nbytes):
+        if not lib().zz_moe_expert_upload_dev(self.id, eid, C.c_void_p(dev_ptr), nbytes):
+            raise RuntimeError(f"upload declined: {last_error()}")
+
+    def forward(self, x):
+        """Host arrays in, (out, eidx, ewt) out; synchronous."""
+        x = np.ascontiguousarray(x, np.float32)
+        S = x.shape[0]
+        out = np.zeros((S, self.D), np.float32)
+        eidx = np.zeros(S * self.K, np.int32)
+        ewt = np.zeros(S * self.K, np.float32)
+        if not lib().zz_moe_forward(self.id, _p(x, _f32p), _p(out, _f32p), S, _p(eidx, _i32p),
+                                    _p(ewt, _f32p)):
+            raise RuntimeError(f"zz_moe_forward declined: {last_error()}")
+        return out, eidx, ewt
+
+    def forward_dev(self, d_in, d_out, S, d_eidx=0, d_ewt=0, stream=0):
+        """Device pointers (ints), enqueued on `stream` (hipStream_t as int)."""
+        ok = lib().zz_moe_forward_dev(self.id, C.c_void_p(d_in), C.c_void_p(d_out), S,
+                                      C.c_void_p(d_eidx or None), C.c_void_p(d_ewt or None),
+                                      C.c_void_p(stream or None))
+        if not ok:
+            raise RuntimeError(f"zz_moe_forward_dev declined: {last_error()}")
+
+    def debug(self, S):
+        K, D, MI = self.K, self.D, self.MI
+        d = dict(xq=np.zeros((S, D), np.int8), xs=np.zeros((S, D // 32), np.float32),
+                 hq=np.zeros((S * K, MI), np.int8), hs=np.zeros((S * K, MI // 32), np.float32),
+                 uniq=np.zeros(self.E, np.int32), offs=np.zeros(self.E + 1, np.int32),
+                 rows=np.zeros(S * K, np.int32), slots=np.zeros(S * K, np.int32))
+        dump = ZzMoeDump(_p(d["xq"], _i8p), _p(d["xs"], _f32p), _p(d["hq"], _i8p),
+                         _p(d["hs"], _f32p), _p(d["uniq"], _i32p), _p(d["offs"], _i32p),
+                         _p(d["rows"], _i32p), _p(d["slots"], _i32p), 0)
+        if not lib().zz_moe_debug(self.id, C.byref(dump)):
+            raise RuntimeError(last_error())
+        nu = dump.nu
+        d["uniq"] = d["uniq"][:nu]
+        d["offs"] = d["offs"][:nu + 1]
+        return d
+
+    def blockdots(self, eid, tensor, row0, nrows, xq):
+        xq = np.ascontiguousarray(xq, np.int8)
+        I = xq.shape[0]
+        out = np.zeros((nrows, I // 32), np.int32)
+        if not lib().zz_moe_blockdots(self.id, eid, tensor, row0, nrows, _p(xq, _i8p),
+                                      _p(out, _i32p)):
+            raise RuntimeError(last_error())
+        return out
+
+    def close(self):
+        if self.id >= 0:
+            lib().zz_moe_layer_destroy(self.id)
+            self.id = -1
+
+
+def gpu_map(arr):
+    a = np.ascontiguousarray(arr)
+    if not lib().gpu_map(C.c_void_p(a.ctypes.data), a.nbytes):
+        raise RuntimeError(f"gpu_map declined: {last_error()}")
+    return a
+
+
+def gpu_matmul(fmt, W_mapped, x, O, I):
+    """gpu.h matmul on a gpu_map'd weight array; returns y [S, O] or raises."""
+    x = np.ascontiguousarray(x, np.float32)
+    S = x.shape[0]
+    y = np.zeros((S, O), np.float32)
+    if not lib().gpu_matmul(fmt, _p(y, _f32p), _p(W_mapped, _u8p), _p(x, _f32p), O, I, S):
+        raise RuntimeError(f"gpu_matmul declined: {last_error()}")
+    return y

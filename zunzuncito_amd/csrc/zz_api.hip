@@ -1,0 +1,638 @@
+// zz_api.hip -- host side of libzzmoe.so: the gpu.h-compatible entry points
+// (include/zz_gpu.h) and the MoE-layer entry points (include/zz_moe.h).
+//
+// State is process-global and single-caller, as the reference backend's is
+// (metal.mm:289-296): one device, one library stream at default priority, a
+// registry of uploaded host ranges, and the registered MoE layers with their
+// HBM slot tables and per-layer workspaces.
+#include "zz_common.h"
+#include "zz_kernels.h"
+#include "../../include/zz_moe.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <vector>
+
+static char g_err[512];
+void zz_set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+#define ZZ_FAIL(...)               \
+    do {                           \
+        zz_set_error(__VA_ARGS__); \
+        return 0;                  \
+    } while (0)
+
+static int g_ready = 0;
+static char g_name[128] = "none";
+static hipStream_t g_stream = nullptr;
+static unsigned *g_diag = nullptr;          // device counters, see zz_moe_stats
+
+struct Mapping {
+    const uint8_t *host;
+    size_t n;
+    uint8_t *dev;
+};
+static std::vector<Mapping> g_maps;
+
+// ----------------------------------------------------------------- gpu.h ABI
+extern "C" int gpu_init(void) {
+    if (g_ready) return 1;
+    const char *off = getenv("ZZ_DISABLE");
+    if (off && off[0] == '1') ZZ_FAIL("disabled by ZZ_DISABLE");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) ZZ_FAIL("no HIP device");
+    hipDeviceProp_t p;
+    ZZ_CHECK(hipSetDevice(0));
+    ZZ_CHECK(hipGetDeviceProperties(&p, 0));
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0) ZZ_FAIL("device %s is not gfx950", p.gcnArchName);
+    snprintf(g_name, sizeof g_name, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    ZZ_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    ZZ_CHECK(hipMalloc(&g_diag, 16 * sizeof(unsigned)));
+    ZZ_CHECK(hipMemset(g_diag, 0, 16 * sizeof(unsigned)));
+    g_ready = 1;
+    return 1;
+}
+
+extern "C" int gpu_ready(void) { return g_ready; }
+extern "C" const char *gpu_name(void) { return g_name; }
+
+static const Mapping *find_map(const void *p, size_t n) {
+    const uint8_t *q = (const uint8_t *)p;
+    for (const Mapping &m : g_maps)
+        if (q >= m.host && q + n <= m.host + m.n) return &m;
+    return nullptr;
+}
+
+extern "C" int gpu_map(const void *p, size_t n) {
+    if (!g_ready || !p || !n) ZZ_FAIL("gpu_map: not ready or empty range");
+    for (Mapping &m : g_maps)
+        if (m.host == p && m.n == n) {           // refresh an existing mapping
+            ZZ_CHECK(hipMemcpy(m.dev, p, n, hipMemcpyHostToDevice));
+            return 1;
+        }
+    Mapping m{(const uint8_t *)p, n, nullptr};
+    ZZ_CHECK(hipMalloc(&m.dev, n));
+    if (hipMemcpy(m.dev, p, n, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(m.dev);
+        ZZ_FAIL("gpu_map: upload failed");
+    }
+    g_maps.push_back(m);
+    return 1;
+}
+
+static int64_t fmt_tensor_bytes(int fmt, int O, int I) {
+    if (fmt == ZZ_FMT_Q40) return (int64_t)O * (I / ZZ_BLK) * 18;
+    if (fmt == ZZ_FMT_Q80) return (int64_t)O * (I / ZZ_BLK) * 34;
+    if (fmt == ZZ_FMT_TQ2) return (int64_t)O * 4 + (int64_t)O * (I / 4);
+    return -1;
+}
+
+// scratch for the matmul path, grown on demand
+static float *g_mx = nullptr, *g_my = nullptr;
+static size_t g_mxn = 0, g_myn = 0;
+
+static int grow(float **p, size_t *cap, size_t n) {
+    if (n <= *cap) return 1;
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    ZZ_CHECK(hipMalloc(p, n * sizeof(float)));
+    *cap = n;
+    return 1;
+}
+
+extern "C" int gpu_matmul(int fmt, float *y, const uint8_t *W, const float *x, int O, int I, int S) {
+    if (!g_ready) ZZ_FAIL("gpu_matmul: not ready");
+    if (fmt != ZZ_FMT_Q40 && fmt != ZZ_FMT_Q80 && fmt != ZZ_FMT_TQ2) ZZ_FAIL("gpu_matmul: fmt %d declined", fmt);
+    if (O <= 0 || I <= 0 || S <= 0 || I % (fmt == ZZ_FMT_TQ2 ? 64 : 32)) ZZ_FAIL("gpu_matmul: bad shape");
+    const Mapping *m = find_map(W, (size_t)fmt_tensor_bytes(fmt, O, I));
+    if (!m) ZZ_FAIL("gpu_matmul: W not inside a gpu_map'd range");
+    const uint8_t *dW = m->dev + (W - m->host);
+    if (!grow(&g_mx, &g_mxn, (size_t)S * I) || !grow(&g_my, &g_myn, (size_t)S * O)) return 0;
+    ZZ_CHECK(hipMemcpyAsync(g_mx, x, sizeof(float) * (size_t)S * I, hipMemcpyHostToDevice, g_stream));
+    if (!zz_launch_matmul_f32(fmt, g_my, dW, g_mx, O, I, S, g_stream)) ZZ_FAIL("gpu_matmul: launch failed");
+    ZZ_CHECK(hipStreamSynchronize(g_stream));
+    ZZ_CHECK(hipMemcpy(y, g_my, sizeof(float) * (size_t)S * O, hipMemcpyDeviceToHost));
+    return 1;
+}
+
+extern "C" int gpu_q40_matmul(float *y, const uint8_t *W, const float *x, int O, int I, int S) {
+    return gpu_matmul(ZZ_FMT_Q40, y, W, x, O, I, S);
+}
+
+// ----------------------------------------------------------------- MoE layers
+struct Workspace {
+    int S = 0;                  // tokens per chunk this workspace holds
+    float *in = nullptr, *out = nullptr, *xn = nullptr;
+    int8_t *xq = nullptr;
+    float *xs = nullptr, *xt = nullptr;
+    int *xsum = nullptr;
+    double *cen = nullptr, *bnd = nullptr;
+    int *eidx = nullptr;
+    float *ewt = nullptr, *topv = nullptr;
+    int *contested = nullptr;
+    int *ptok = nullptr, *pslot = nullptr, *ppos = nullptr;
+    float *pwt = nullptr;
+    int *uniq = nullptr, *uoff = nullptr, *ucnt = nullptr, *meta = nullptr;
+    ZzItem *items = nullptr;
+    int8_t *hq = nullptr;
+    float *hs = nullptr;
+    int *hsum = nullptr;
+    float *y = nullptr;
+    void *block = nullptr;      // one allocation holds everything above
+};
+
+struct Layer {
+    zz_moe_desc d;
+    ZzLayout lay;
+    int64_t rec_bytes, src_gate, src_up, src_down;
+    float *router = nullptr, *rscale = nullptr, *pes = nullptr, *bias = nullptr;
+    float *pre_ln = nullptr, *post_ln = nullptr;
+    uint8_t *slots = nullptr;   // E * lay.bytes: the HBM slot table
+    uint8_t *staging = nullptr; // one reference record, for uploads
+    std::vector<char> present;
+    int n_present = 0;
+    Workspace ws;
+    int last_S = 0;             // tokens of the first chunk of the last forward
+    int pending_S = -1;         // begin/end state
+};
+static std::vector<Layer *> g_layers;
+
+static int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+static ZzTensor make_tensor(int fmt, int O, int I, int64_t *cursor) {
+    ZzTensor t;
+    t.fmt = fmt;
+    t.O = O;
+    t.I = I;
+    if (fmt == ZZ_FMT_TQ2) {
+        t.off_s = *cursor;
+        *cursor = align256(*cursor + (int64_t)O * 4);
+        t.off_q = *cursor;
+        *cursor = align256(*cursor + (int64_t)O * (I / 4));
+    } else {
+        int pb = fmt == ZZ_FMT_Q80 ? 32 : 16;
+        t.off_q = *cursor;
+        *cursor = align256(*cursor + (int64_t)O * (I / ZZ_BLK) * pb);
+        t.off_s = *cursor;
+        *cursor = align256(*cursor + (int64_t)O * (I / ZZ_BLK) * 2);
+    }
+    return t;
+}
+
+static int desc_ok(const zz_moe_desc *d) {
+    if (!d) return 0;
+    if (d->D <= 0 || d->MI <= 0 || d->D % 64 || d->MI % 64 || d->D > ZZ_MAXD || d->MI > ZZ_MAXD) return 0;
+    if (d->E <= 0 || d->E > ZZ_MAXE || d->K < 1 || d->K > ZZ_MAXK || d->K > d->E) return 0;
+    if (d->gating < 0 || d->gating > 2 || d->act < 0 || d->act > 2) return 0;
+    int f[3] = {d->fmt_gate, d->fmt_up, d->fmt_down};
+    for (int i = 0; i < 3; i++)
+        if (f[i] != ZZ_FMT_Q40 && f[i] != ZZ_FMT_Q80 && f[i] != ZZ_FMT_TQ2) return 0;
+    // the tq2 -1 offset is settled once per activation (tq2.h:29-37): gate and up
+    // share the input, so either both or neither of them is ternary
+    if ((d->fmt_gate == ZZ_FMT_TQ2) != (d->fmt_up == ZZ_FMT_TQ2)) return 0;
+    return 1;
+}
+
+extern "C" int64_t zz_moe_record_bytes(const zz_moe_desc *d) {
+    if (!desc_ok(d)) return -1;
+    return fmt_tensor_bytes(d->fmt_gate, d->MI, d->D) + fmt_tensor_bytes(d->fmt_up, d->MI, d->D) +
+           fmt_tensor_bytes(d->fmt_down, d->D, d->MI);
+}
+
+static int upload_f32(float **dst, const float *src, size_t n) {
+    if (!src) return 1;
+    ZZ_CHECK(hipMalloc(dst, n * sizeof(float)));
+    ZZ_CHECK(hipMemcpy(*dst, src, n * sizeof(float), hipMemcpyHostToDevice));
+    return 1;
+}
+
+static void free_layer(Layer *L) {
+    if (!L) return;
+    void *ps[] = {L->router, L->rscale, L->pes, L->bias, L->pre_ln, L->post_ln, L->slots,
+                  L->staging, L->ws.block};
+    for (void *p : ps)
+        if (p) (void)hipFree(p);
+    delete L;
+}
+
+extern "C" int zz_moe_layer_create(const zz_moe_desc *d, const zz_moe_weights *w) {
+    if (!g_ready) { zz_set_error("zz_moe_layer_create: gpu_init first"); return -1; }
+    if (!desc_ok(d) || !w || !w->router) { zz_set_error("zz_moe_layer_create: bad descriptor"); return -1; }
+    if (d->gating == ZZ_GATE_SOFTMAX_PES && (!w->router_scale || !w->pes || !w->pre_ln || !w->post_ln)) {
+        zz_set_error("zz_moe_layer_create: gemma gating needs scale, pes and both norms");
+        return -1;
+    }
+    if (d->use_bias && !w->bias) { zz_set_error("zz_moe_layer_create: use_bias without bias"); return -1; }
+    Layer *L = new Layer();
+    L->d = *d;
+    int64_t cur = 0;
+    L->lay.gate = make_tensor(d->fmt_gate, d->MI, d->D, &cur);
+    L->lay.up = make_tensor(d->fmt_up, d->MI, d->D, &cur);
+    L->lay.down = make_tensor(d->fmt_down, d->D, d->MI, &cur);
+    L->lay.bytes = cur;
+    L->src_gate = 0;
+    L->src_up = fmt_tensor_bytes(d->fmt_gate, d->MI, d->D);
+    L->src_down = L->src_up + fmt_tensor_bytes(d->fmt_up, d->MI, d->D);
+    L->rec_bytes = L->src_down + fmt_tensor_bytes(d->fmt_down, d->D, d->MI);
+    bool ok = upload_f32(&L->router, w->router, (size_t)d->E * d->D) &&
+              upload_f32(&L->rscale, d->gating == ZZ_GATE_SOFTMAX_PES ? w->router_scale : nullptr, d->D) &&
+              upload_f32(&L->pes, d->gating == ZZ_GATE_SOFTMAX_PES ? w->pes : nullptr, d->E) &&
+              upload_f32(&L->bias, d->use_bias ? w->bias : nullptr, d->E) &&
+              upload_f32(&L->pre_ln, d->gating == ZZ_GATE_SOFTMAX_PES ? w->pre_ln : nullptr, d->D) &&
+              upload_f32(&L->post_ln, d->gating == ZZ_GATE_SOFTMAX_PES ? w->post_ln : nullptr, d->D) &&
+              hipMalloc(&L->slots, (size_t)d->E * L->lay.bytes) == hipSuccess &&
+              hipMalloc(&L->staging, (size_t)L->rec_bytes) == hipSuccess;
+    if (!ok) {
+        zz_set_error("zz_moe_layer_create: device allocation failed");
+        free_layer(L);
+        return -1;
+    }
+    L->present.assign(d->E, 0);
+    for (size_t i = 0; i < g_layers.size(); i++)
+        if (!g_layers[i]) { g_layers[i] = L; return (int)i; }
+    g_layers.push_back(L);
+    return (int)g_layers.size() - 1;
+}
+
+static Layer *get_layer(int id) {
+    if (!g_ready || id < 0 || id >= (int)g_layers.size()) return nullptr;
+    return g_layers[id];
+}
+
+extern "C" void zz_moe_layer_destroy(int id) {
+    Layer *L = get_layer(id);
+    if (!L) return;
+    (void)hipStreamSynchronize(g_stream);
+    free_layer(L);
+    g_layers[id] = nullptr;
+}
+
+static int upload_common(Layer *L, int eid, const void *src, size_t n, hipMemcpyKind kind) {
+    if (eid < 0 || eid >= L->d.E) ZZ_FAIL("upload: expert %d out of range", eid);
+    if ((int64_t)n != L->rec_bytes) ZZ_FAIL("upload: record is %zu bytes, expected %lld", n, (long long)L->rec_bytes);
+    ZZ_CHECK(hipMemcpyAsync(L->staging, src, n, kind, g_stream));
+    ZzRepackArgs a;
+    a.src = L->staging;
+    a.src_gate = L->src_gate;
+    a.src_up = L->src_up;
+    a.src_down = L->src_down;
+    a.dst = L->slots + (size_t)eid * L->lay.bytes;
+    a.lay = L->lay;
+    if (!zz_launch_repack(a, g_stream)) ZZ_FAIL("upload: repack launch failed");
+    ZZ_CHECK(hipStreamSynchronize(g_stream));
+    if (!L->present[eid]) { L->present[eid] = 1; L->n_present++; }
+    return 1;
+}
+
+extern "C" int zz_moe_expert_upload(int id, int eid, const uint8_t *rec, size_t n) {
+    Layer *L = get_layer(id);
+    if (!L || !rec) ZZ_FAIL("zz_moe_expert_upload: bad layer or record");
+    return upload_common(L, eid, rec, n, hipMemcpyHostToDevice);
+}
+
+extern "C" int zz_moe_expert_upload_dev(int id, int eid, const void *d_rec, size_t n) {
+    Layer *L = get_layer(id);
+    if (!L || !d_rec) ZZ_FAIL("zz_moe_expert_upload_dev: bad layer or record");
+    return upload_common(L, eid, d_rec, n, hipMemcpyDeviceToDevice);
+}
+
+// largest chunk one dispatch workgroup sorts in LDS: S*K pairs <= 8192
+static int chunk_tokens(const zz_moe_desc &d) { return 8192 / d.K; }
+
+static int ensure_ws(Layer *L, int S) {
+    Workspace &w = L->ws;
+    if (S <= w.S) return 1;
+    const zz_moe_desc &d = L->d;
+    const size_t P = (size_t)S * d.K, nbD = d.D / ZZ_BLK, nbM = d.MI / ZZ_BLK;
+    const size_t nitems = (size_t)d.E + P / 8 + 8;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        size_t o = off;
+        off = (off + bytes + 255) & ~(size_t)255;
+        return o;
+    };
+    size_t o_in = take(4 * S * (size_t)d.D), o_out = take(4 * S * (size_t)d.D), o_xn = take(4 * S * (size_t)d.D);
+    size_t o_xq = take(S * (size_t)d.D), o_xs = take(4 * S * nbD), o_xsum = take(4 * S * nbD), o_xt = take(4 * (size_t)S);
+    size_t o_cen = take(8 * S * (size_t)d.E), o_bnd = take(8 * S * (size_t)d.E);
+    size_t o_eidx = take(4 * P), o_ewt = take(4 * P), o_topv = take(4 * P), o_cont = take(4 * (size_t)S);
+    size_t o_ptok = take(4 * P), o_pslot = take(4 * P), o_ppos = take(4 * P), o_pwt = take(4 * P);
+    size_t o_uniq = take(4 * (size_t)d.E), o_uoff = take(4 * (size_t)d.E), o_ucnt = take(4 * (size_t)d.E);
+    size_t o_meta = take(64), o_items = take(sizeof(ZzItem) * nitems);
+    size_t o_hq = take(P * d.MI), o_hs = take(4 * P * nbM), o_hsum = take(4 * P * nbM);
+    size_t o_y = take(4 * P * d.D);
+    void *blk = nullptr;
+    ZZ_CHECK(hipStreamSynchronize(g_stream));
+    ZZ_CHECK(hipMalloc(&blk, off));
+    if (w.block) (void)hipFree(w.block);
+    char *b = (char *)blk;
+    w.block = blk;
+    w.S = S;
+    w.in = (float *)(b + o_in); w.out = (float *)(b + o_out); w.xn = (float *)(b + o_xn);
+    w.xq = (int8_t *)(b + o_xq); w.xs = (float *)(b + o_xs); w.xsum = (int *)(b + o_xsum);
+    w.xt = (float *)(b + o_xt); w.cen = (double *)(b + o_cen); w.bnd = (double *)(b + o_bnd);
+    w.eidx = (int *)(b + o_eidx); w.ewt = (float *)(b + o_ewt); w.topv = (float *)(b + o_topv);
+    w.contested = (int *)(b + o_cont); w.ptok = (int *)(b + o_ptok); w.pslot = (int *)(b + o_pslot);
+    w.ppos = (int *)(b + o_ppos); w.pwt = (float *)(b + o_pwt); w.uniq = (int *)(b + o_uniq);
+    w.uoff = (int *)(b + o_uoff); w.ucnt = (int *)(b + o_ucnt); w.meta = (int *)(b + o_meta);
+    w.items = (ZzItem *)(b + o_items); w.hq = (int8_t *)(b + o_hq); w.hs = (float *)(b + o_hs);
+    w.hsum = (int *)(b + o_hsum); w.y = (float *)(b + o_y);
+    return 1;
+}
+
+// ----------------------------------------------------------------- profiling
+struct ProfRec {
+    int k;
+    hipEvent_t a, b;
+};
+static int g_prof = 0;
+static std::vector<ProfRec> g_prof_recs;
+static std::vector<hipEvent_t> g_event_pool;
+
+static hipEvent_t prof_event() {
+    if (!g_event_pool.empty()) {
+        hipEvent_t e = g_event_pool.back();
+        g_event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    (void)hipEventCreate(&e);
+    return e;
+}
+
+struct ProfScope {             // brackets one kernel launch with two events
+    int k;
+    hipStream_t st;
+    hipEvent_t a = nullptr;
+    ProfScope(int k_, hipStream_t st_) : k(k_), st(st_) {
+        if (g_prof) {
+            a = prof_event();
+            (void)hipEventRecord(a, st);
+        }
+    }
+    ~ProfScope() {
+        if (g_prof && a) {
+            hipEvent_t b = prof_event();
+            (void)hipEventRecord(b, st);
+            g_prof_recs.push_back({k, a, b});
+        }
+    }
+};
+
+extern "C" int zz_moe_profile(int on) {
+    if (!g_ready) ZZ_FAIL("zz_moe_profile: not ready");
+    (void)hipDeviceSynchronize();
+    for (ProfRec &r : g_prof_recs) { g_event_pool.push_back(r.a); g_event_pool.push_back(r.b); }
+    if (on) g_prof_recs.clear();
+    g_prof = on;
+    return 1;
+}
+
+extern "C" int zz_moe_profile_read(double *ms, int *launches, int n) {
+    if (!g_ready || !ms || !launches) ZZ_FAIL("zz_moe_profile_read: bad arguments");
+    ZZ_CHECK(hipDeviceSynchronize());
+    for (int k = 0; k < n; k++) { ms[k] = 0.0; launches[k] = 0; }
+    for (ProfRec &r : g_prof_recs) {
+        float t = 0.0f;
+        ZZ_CHECK(hipEventElapsedTime(&t, r.a, r.b));
+        if (r.k < n) { ms[r.k] += t; launches[r.k]++; }
+    }
+    return ZZ_K_COUNT;
+}
+
+// One chunk of S <= chunk_tokens tokens: in/out device pointers.
+static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream_t st) {
+    const zz_moe_desc &d = L->d;
+    Workspace &w = L->ws;
+    const bool gemma = d.gating == ZZ_GATE_SOFTMAX_PES;
+    const bool tq_in = d.fmt_gate == ZZ_FMT_TQ2;
+    const int P = S * d.K;
+
+    ZzPrepArgs pa;
+    pa.D = d.D; pa.gemma = gemma; pa.eps = d.eps; pa.in = d_in;
+    pa.router_scale = L->rscale; pa.pre_ln = L->pre_ln; pa.xn = w.xn;
+    pa.xq = w.xq; pa.xs = w.xs; pa.xsum = w.xsum; pa.xt = tq_in ? w.xt : nullptr; pa.diag = g_diag;
+    if (!(ProfScope(ZZ_K_PREP, st), zz_launch_prep(pa, S, st))) ZZ_FAIL("prep launch failed");
+
+    ZzLogitArgs la;
+    la.D = d.D; la.E = d.E; la.gating = d.gating; la.router = L->router; la.xn = w.xn; la.x = d_in;
+    la.bias = gemma && d.use_bias ? L->bias : nullptr; la.cen = w.cen; la.bnd = w.bnd; la.diag = g_diag;
+    if (!(ProfScope(ZZ_K_LOGITS, st), zz_launch_logits(la, S, st))) ZZ_FAIL("logits launch failed");
+
+    ZzTopkArgs ta;
+    ta.D = d.D; ta.E = d.E; ta.K = d.K; ta.gating = d.gating; ta.norm_topk = d.norm_topk;
+    ta.routed_scaling = d.routed_scaling; ta.cen = w.cen; ta.bnd = w.bnd; ta.router = L->router;
+    ta.xn = w.xn; ta.bias = d.use_bias ? L->bias : nullptr; ta.pes = L->pes; ta.eidx = w.eidx;
+    ta.ewt = w.ewt; ta.topv = w.topv; ta.contested = w.contested; ta.diag = g_diag;
+    if (!(ProfScope(ZZ_K_TOPK, st), zz_launch_topk(ta, S, st))) ZZ_FAIL("topk launch failed");
+
+    ZzDispatchArgs da;
+    da.P = P; da.E = d.E; da.K = d.K; da.tch = 8; da.eidx = w.eidx; da.ewt = w.ewt;
+    da.ptok = w.ptok; da.pslot = w.pslot; da.pwt = w.pwt; da.ppos = w.ppos; da.uniq = w.uniq;
+    da.uoff = w.uoff; da.ucnt = w.ucnt; da.items = w.items; da.meta = w.meta;
+    if (!(ProfScope(ZZ_K_DISPATCH, st), zz_launch_dispatch(da, st))) ZZ_FAIL("dispatch launch failed");
+
+    ZzFfnArgs fa;
+    fa.D = d.D; fa.MI = d.MI; fa.K = d.K; fa.act = d.act; fa.clamp = d.clamp;
+    fa.experts = L->slots; fa.estride = L->lay.bytes; fa.lay = L->lay; fa.items = w.items;
+    fa.meta = w.meta; fa.ptok = w.ptok; fa.xq = w.xq; fa.xs = w.xs; fa.xsum = w.xsum; fa.xt = w.xt;
+    fa.hq = w.hq; fa.hs = w.hs; fa.hsum = w.hsum; fa.y = w.y;
+    const int max_items = (P < d.E ? P : d.E) + (P + 7) / 8;
+    if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_ffn_up(fa, max_items, st))) ZZ_FAIL("ffn_up launch failed");
+    if (!(ProfScope(ZZ_K_FFN_DOWN, st), zz_launch_ffn_down(fa, max_items, st))) ZZ_FAIL("ffn_down launch failed");
+
+    ZzCombineArgs ca;
+    ca.D = d.D; ca.K = d.K; ca.gemma = gemma; ca.eps = d.eps; ca.y = w.y; ca.ppos = w.ppos;
+    ca.ewt = w.ewt; ca.post_ln = L->post_ln; ca.out = d_out;
+    if (!(ProfScope(ZZ_K_COMBINE, st), zz_launch_combine(ca, S, st))) ZZ_FAIL("combine launch failed");
+    return 1;
+}
+
+static int forward_dev(Layer *L, const float *d_in, float *d_out, int S, int *d_eidx, float *d_ewt,
+                       hipStream_t st) {
+    const zz_moe_desc &d = L->d;
+    if (S <= 0) ZZ_FAIL("forward: S must be positive");
+    if (L->n_present != d.E) ZZ_FAIL("forward: %d of %d experts uploaded", L->n_present, d.E);
+    const int CH = chunk_tokens(d);
+    if (!ensure_ws(L, S < CH ? S : CH)) return 0;
+    for (int s0 = 0; s0 < S; s0 += CH) {
+        int n = S - s0 < CH ? S - s0 : CH;
+        if (!run_chunk(L, d_in + (size_t)s0 * d.D, d_out + (size_t)s0 * d.D, n, st)) return 0;
+        if (d_eidx) ZZ_CHECK(hipMemcpyAsync(d_eidx + (size_t)s0 * d.K, L->ws.eidx, sizeof(int) * n * d.K, hipMemcpyDeviceToDevice, st));
+        if (d_ewt) ZZ_CHECK(hipMemcpyAsync(d_ewt + (size_t)s0 * d.K, L->ws.ewt, sizeof(float) * n * d.K, hipMemcpyDeviceToDevice, st));
+        if (s0 == 0) L->last_S = n;
+    }
+    return 1;
+}
+
+extern "C" int zz_moe_forward_dev(int id, const float *d_in, float *d_out, int S, int *d_eidx,
+                                  float *d_ewt, void *stream) {
+    Layer *L = get_layer(id);
+    if (!L || !d_in || !d_out) ZZ_FAIL("zz_moe_forward_dev: bad arguments");
+    return forward_dev(L, d_in, d_out, S, d_eidx, d_ewt, stream ? (hipStream_t)stream : g_stream);
+}
+
+// Host-pointer forward: stage through the workspace chunk by chunk.
+static int forward_host(Layer *L, const float *in, float *out, int S, int *eidx, float *ewt) {
+    const zz_moe_desc &d = L->d;
+    if (S <= 0 || !in || !out) ZZ_FAIL("forward: bad arguments");
+    if (L->n_present != d.E) ZZ_FAIL("forward: %d of %d experts uploaded", L->n_present, d.E);
+    const int CH = chunk_tokens(d);
+    if (!ensure_ws(L, S < CH ? S : CH)) return 0;
+    Workspace &w = L->ws;
+    // results go to host staging first, so a failure leaves out/eidx/ewt untouched
+    std::vector<float> o((size_t)S * d.D), wt((size_t)S * d.K);
+    std::vector<int> ix((size_t)S * d.K);
+    for (int s0 = 0; s0 < S; s0 += CH) {
+        int n = S - s0 < CH ? S - s0 : CH;
+        ZZ_CHECK(hipMemcpyAsync(w.in, in + (size_t)s0 * d.D, sizeof(float) * n * d.D, hipMemcpyHostToDevice, g_stream));
+        if (!run_chunk(L, w.in, w.out, n, g_stream)) return 0;
+        ZZ_CHECK(hipMemcpyAsync(o.data() + (size_t)s0 * d.D, w.out, sizeof(float) * n * d.D, hipMemcpyDeviceToHost, g_stream));
+        ZZ_CHECK(hipMemcpyAsync(ix.data() + (size_t)s0 * d.K, w.eidx, sizeof(int) * n * d.K, hipMemcpyDeviceToHost, g_stream));
+        ZZ_CHECK(hipMemcpyAsync(wt.data() + (size_t)s0 * d.K, w.ewt, sizeof(float) * n * d.K, hipMemcpyDeviceToHost, g_stream));
+        ZZ_CHECK(hipStreamSynchronize(g_stream));
+        if (s0 == 0) L->last_S = n;
+    }
+    memcpy(out, o.data(), sizeof(float) * o.size());
+    if (eidx) memcpy(eidx, ix.data(), sizeof(int) * ix.size());
+    if (ewt) memcpy(ewt, wt.data(), sizeof(float) * wt.size());
+    return 1;
+}
+
+extern "C" int zz_moe_forward(int id, const float *in, float *out, int S, int *eidx, float *ewt) {
+    Layer *L = get_layer(id);
+    if (!L) ZZ_FAIL("zz_moe_forward: no such layer");
+    return forward_host(L, in, out, S, eidx, ewt);
+}
+
+extern "C" int zz_moe_forward_begin(int id, const float *in, int S) {
+    Layer *L = get_layer(id);
+    if (!L || !in || S <= 0) ZZ_FAIL("zz_moe_forward_begin: bad arguments");
+    const zz_moe_desc &d = L->d;
+    if (S > chunk_tokens(d)) ZZ_FAIL("zz_moe_forward_begin: S > %d", chunk_tokens(d));
+    if (L->pending_S >= 0) ZZ_FAIL("zz_moe_forward_begin: a forward is already pending");
+    if (L->n_present != d.E) ZZ_FAIL("forward: %d of %d experts uploaded", L->n_present, d.E);
+    if (!ensure_ws(L, S)) return 0;
+    ZZ_CHECK(hipMemcpyAsync(L->ws.in, in, sizeof(float) * S * d.D, hipMemcpyHostToDevice, g_stream));
+    if (!run_chunk(L, L->ws.in, L->ws.out, S, g_stream)) return 0;
+    L->pending_S = S;
+    L->last_S = S;
+    return 1;
+}
+
+extern "C" int zz_moe_forward_end(int id, float *out, int *eidx, float *ewt) {
+    Layer *L = get_layer(id);
+    if (!L || L->pending_S < 0 || !out) ZZ_FAIL("zz_moe_forward_end: nothing pending");
+    const zz_moe_desc &d = L->d;
+    int S = L->pending_S;
+    L->pending_S = -1;
+    ZZ_CHECK(hipStreamSynchronize(g_stream));
+    ZZ_CHECK(hipMemcpy(out, L->ws.out, sizeof(float) * S * d.D, hipMemcpyDeviceToHost));
+    if (eidx) ZZ_CHECK(hipMemcpy(eidx, L->ws.eidx, sizeof(int) * S * d.K, hipMemcpyDeviceToHost));
+    if (ewt) ZZ_CHECK(hipMemcpy(ewt, L->ws.ewt, sizeof(float) * S * d.K, hipMemcpyDeviceToHost));
+    return 1;
+}
+
+extern "C" int zz_moe_debug(int id, zz_moe_dump *dp) {
+    Layer *L = get_layer(id);
+    if (!L || !dp || L->last_S <= 0) ZZ_FAIL("zz_moe_debug: no forward to dump");
+    const zz_moe_desc &d = L->d;
+    Workspace &w = L->ws;
+    const int S = L->last_S, P = S * d.K;
+    ZZ_CHECK(hipStreamSynchronize(g_stream));
+    if (dp->xq) ZZ_CHECK(hipMemcpy(dp->xq, w.xq, (size_t)S * d.D, hipMemcpyDeviceToHost));
+    if (dp->xs) ZZ_CHECK(hipMemcpy(dp->xs, w.xs, sizeof(float) * S * (d.D / ZZ_BLK), hipMemcpyDeviceToHost));
+    std::vector<int> ptok(P), pslot(P), ppos(P), meta(2), uniq(d.E), uoff(d.E), ucnt(d.E);
+    ZZ_CHECK(hipMemcpy(ptok.data(), w.ptok, sizeof(int) * P, hipMemcpyDeviceToHost));
+    ZZ_CHECK(hipMemcpy(pslot.data(), w.pslot, sizeof(int) * P, hipMemcpyDeviceToHost));
+    ZZ_CHECK(hipMemcpy(ppos.data(), w.ppos, sizeof(int) * P, hipMemcpyDeviceToHost));
+    ZZ_CHECK(hipMemcpy(meta.data(), w.meta, sizeof(int) * 2, hipMemcpyDeviceToHost));
+    ZZ_CHECK(hipMemcpy(uniq.data(), w.uniq, sizeof(int) * d.E, hipMemcpyDeviceToHost));
+    ZZ_CHECK(hipMemcpy(uoff.data(), w.uoff, sizeof(int) * d.E, hipMemcpyDeviceToHost));
+    ZZ_CHECK(hipMemcpy(ucnt.data(), w.ucnt, sizeof(int) * d.E, hipMemcpyDeviceToHost));
+    const int nu = meta[0];
+    dp->nu = nu;
+    if (dp->uniq) memcpy(dp->uniq, uniq.data(), sizeof(int) * nu);
+    if (dp->offs) {
+        for (int u = 0; u < nu; u++) dp->offs[u] = uoff[u];
+        dp->offs[nu] = P;
+    }
+    if (dp->rows) memcpy(dp->rows, ptok.data(), sizeof(int) * P);
+    if (dp->slots) memcpy(dp->slots, pslot.data(), sizeof(int) * P);
+    const int nbM = d.MI / ZZ_BLK;
+    if (dp->hq || dp->hs) {
+        std::vector<int8_t> hq((size_t)P * d.MI);
+        std::vector<float> hs((size_t)P * nbM);
+        ZZ_CHECK(hipMemcpy(hq.data(), w.hq, hq.size(), hipMemcpyDeviceToHost));
+        ZZ_CHECK(hipMemcpy(hs.data(), w.hs, sizeof(float) * hs.size(), hipMemcpyDeviceToHost));
+        for (int f = 0; f < P; f++) {              // (token, slot) order
+            int p = ppos[f];
+            if (dp->hq) memcpy(dp->hq + (size_t)f * d.MI, hq.data() + (size_t)p * d.MI, d.MI);
+            if (dp->hs) memcpy(dp->hs + (size_t)f * nbM, hs.data() + (size_t)p * nbM, sizeof(float) * nbM);
+        }
+    }
+    return 1;
+}
+
+extern "C" int zz_moe_blockdots(int id, int eid, int tensor, int row0, int nrows, const int8_t *xq,
+                                int32_t *out) {
+    Layer *L = get_layer(id);
+    if (!L || eid < 0 || eid >= L->d.E || tensor < 0 || tensor > 2 || !xq || !out) ZZ_FAIL("blockdots: bad arguments");
+    ZzTensor t = tensor == 0 ? L->lay.gate : tensor == 1 ? L->lay.up : L->lay.down;
+    if (row0 < 0 || nrows <= 0 || row0 + nrows > t.O) ZZ_FAIL("blockdots: rows out of range");
+    int8_t *dx = nullptr;
+    int32_t *dout = nullptr;
+    size_t nout = (size_t)nrows * (t.I / ZZ_BLK);
+    ZZ_CHECK(hipMalloc(&dx, t.I));
+    if (hipMalloc(&dout, sizeof(int32_t) * nout) != hipSuccess) { (void)hipFree(dx); ZZ_FAIL("blockdots: alloc"); }
+    int ok = hipMemcpy(dx, xq, t.I, hipMemcpyHostToDevice) == hipSuccess &&
+             zz_launch_blockdots(L->slots + (size_t)eid * L->lay.bytes, t, row0, nrows, dx, dout, g_stream) &&
+             hipStreamSynchronize(g_stream) == hipSuccess &&
+             hipMemcpy(out, dout, sizeof(int32_t) * nout, hipMemcpyDeviceToHost) == hipSuccess;
+    (void)hipFree(dx);
+    (void)hipFree(dout);
+    if (!ok) ZZ_FAIL("blockdots: failed");
+    return 1;
+}
+
+extern "C" int zz_quantize(int fmt, const float *d_w, uint8_t *d_out, int64_t n, void *stream) {
+    if (!g_ready || !d_w || !d_out || n <= 0 || n % ZZ_BLK) ZZ_FAIL("zz_quantize: bad arguments");
+    if (fmt != ZZ_FMT_Q40 && fmt != ZZ_FMT_Q80) ZZ_FAIL("zz_quantize: fmt %d declined", fmt);
+    if (!zz_launch_quantize(fmt, d_w, d_out, n / ZZ_BLK, stream ? (hipStream_t)stream : g_stream))
+        ZZ_FAIL("zz_quantize: launch failed");
+    return 1;
+}
+
+extern "C" int zz_moe_stats(unsigned *c) {
+    if (!g_ready || !c) ZZ_FAIL("zz_moe_stats: not ready");
+    ZZ_CHECK(hipStreamSynchronize(g_stream));
+    ZZ_CHECK(hipMemcpy(c, g_diag, 4 * sizeof(unsigned), hipMemcpyDeviceToHost));
+    return 1;
+}
+
+extern "C" const char *zz_last_error(void) { return g_err; }
+
+extern "C" void gpu_shutdown(void) {
+    if (!g_ready) return;
+    (void)hipStreamSynchronize(g_stream);
+    for (Layer *&L : g_layers) { free_layer(L); L = nullptr; }
+    g_layers.clear();
+    for (Mapping &m : g_maps) (void)hipFree(m.dev);
+    g_maps.clear();
+    if (g_mx) (void)hipFree(g_mx);
+    if (g_my) (void)hipFree(g_my);
+    g_mx = g_my = nullptr;
+    g_mxn = g_myn = 0;
+    (void)hipFree(g_diag);
+    g_diag = nullptr;
+    (void)hipStreamDestroy(g_stream);
+    g_stream = nullptr;
+    g_ready = 0;
+    snprintf(g_name, sizeof g_name, "none");
+}

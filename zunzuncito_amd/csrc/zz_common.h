@@ -1,0 +1,116 @@
+// zz_common.h -- shared device/host definitions for the MI355X MoE library.
+//
+// Everything here is gfx950-only HIP. Files are compiled with -ffp-contract=off:
+// every fused multiply-add is written as fmaf(), so bit-level behaviour is
+// explicit wherever it matters (activation quantisation, router logits).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#define ZZ_BLK 32              // q4_0 / q8_0 / activation block (q40.h:41)
+#define ZZ_MAXK 16             // top-k limit (gemma4.c:53 MAXTOPK)
+#define ZZ_MAXE 512            // experts per layer (maple.c:67 MAXEXPERTS)
+#define ZZ_MAXD 8192           // hidden / intermediate limit of one call
+
+// formats: gpu.h:49-52
+#define ZZ_FMT_Q40 1
+#define ZZ_FMT_Q80 2
+#define ZZ_FMT_TQ2 3
+
+// gating and activation kinds, mirrored in include/zz_moe.h
+#define ZZ_GATE_SOFTMAX_PES 0   // gemma4.c:581-613
+#define ZZ_GATE_SIGMOID_BIAS 1  // lfm25.c:636-668
+#define ZZ_GATE_SOFTMAX_TOPK 2  // maple.c:582-601
+
+#define ZZ_ACT_GEGLU_TANH 0     // gemma4.c:432-434
+#define ZZ_ACT_SWIGLU 1         // lfm25.c:456-458
+#define ZZ_ACT_SWIGLU_CLAMP 2   // maple.c:607-611
+
+#define ZZ_CHECK(x)                                                            \
+    do {                                                                       \
+        hipError_t e_ = (x);                                                   \
+        if (e_ != hipSuccess) {                                                \
+            zz_set_error("%s:%d %s: %s", __FILE__, __LINE__, #x,                 \
+                         hipGetErrorString(e_));                               \
+            return 0;                                                          \
+        }                                                                      \
+    } while (0)
+
+void zz_set_error(const char *fmt, ...);
+
+// Device view of one expert tensor inside the HBM slot table. q4_0 and q8_0
+// tensors are stored repacked as two planes so every block's payload is 16-byte
+// aligned: qs[O][nb][16|32] then scales[O][nb] (fp16). tq2 keeps its reference
+// layout: alpha[O] f32 then codes[O][I/4].
+struct ZzTensor {
+    int fmt, O, I;
+    int64_t off_q;       // byte offset of the payload plane inside the expert
+    int64_t off_s;       // byte offset of the scale plane (alpha for tq2)
+};
+
+struct ZzLayout {        // byte layout of one repacked expert, all 256-aligned
+    ZzTensor gate, up, down;
+    int64_t bytes;       // stride between experts in the slot table
+};
+
+// ---------------------------------------------------------------- device helpers
+__device__ __forceinline__ float zz_h2f(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float)v;     // v_cvt_f32_f16: exact for every binary16 value
+}
+
+// distance from |x| to the next float away from zero
+__device__ __forceinline__ float ulp_of(float x) {
+    float a = fabsf(x);
+    return __uint_as_float(__float_as_uint(a) + 1u) - a;
+}
+
+__device__ __forceinline__ int zz_dot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);   // v_dot4_i32_i8
+}
+
+template <typename T>
+__device__ __forceinline__ T zz_wave_sum(T v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float zz_wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// q40.h:124-138 activation quantisation of one 32-value block held one value per
+// lane of a 32-lane group (lanes 0..31 or 32..63 of a wave). d = amax/127 (IEEE
+// division), q = rint(v * (1/d)) clamped to +-127. Bit-exact with the reference.
+__device__ __forceinline__ int zz_quant_lane(float v, float *d_out) {
+    float a = fabsf(v);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+    float d = a / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    float q = rintf(v * id);
+    q = fminf(fmaxf(q, -127.0f), 127.0f);
+    *d_out = d;
+    return (int)q;
+}
+
+__device__ __forceinline__ float zz_gelu_tanh(float x) {
+    float inner = fmaf((0.044715f * x) * x, x, x);
+    return (0.5f * x) * (1.0f + tanhf(0.7978845608028654f * inner));
+}
+
+__device__ __forceinline__ float zz_silu(float x) { return x / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float zz_act(int act, float g, float u, float clamp) {
+    if (act == ZZ_ACT_GEGLU_TANH) return zz_gelu_tanh(g) * u;
+    if (act == ZZ_ACT_SWIGLU_CLAMP) {           // maple.c:672-675
+        if (g > clamp) g = clamp;
+        u = u < -clamp ? -clamp : (u > clamp ? clamp : u);
+    }
+    return zz_silu(g) * u;
+}

@@ -1,0 +1,329 @@
+// zz_ffn.hip -- expert FFN on gfx950: slot-table repack, gate/up GEMV with the
+// fused activation and int8 re-quantisation of the hidden, down GEMV, and the
+// gate-weighted combine (+ gemma's post-norm).
+//
+// The per-block integer dots are exact int32 (v_dot4_i32_i8): q4_0 uses the
+// unsigned nibbles and subtracts 8*sum(x) (q40.h:30-32), tq2 uses the unsigned
+// codes and subtracts Sx once per row (tq2.h:29-37), q8_0 is signed x signed.
+// Across blocks the fp32 accumulation order is this kernel's own; the layer
+// output matches the reference within the fp32 tolerance, the integers exactly.
+#include "zz_common.h"
+#include "zz_kernels.h"
+
+#define ZZ_TCH 8   // pairs (token, expert) per FFN work item
+
+// ------------------------------------------------------------------ block dots
+__device__ __forceinline__ int zz_dot_q40(uint4 w, uint4 x0, uint4 x1) {
+    const unsigned m = 0x0F0F0F0Fu;
+    int s = zz_dot4(w.x & m, x0.x, 0);
+    s = zz_dot4(w.y & m, x0.y, s);
+    s = zz_dot4(w.z & m, x0.z, s);
+    s = zz_dot4(w.w & m, x0.w, s);
+    s = zz_dot4((w.x >> 4) & m, x1.x, s);
+    s = zz_dot4((w.y >> 4) & m, x1.y, s);
+    s = zz_dot4((w.z >> 4) & m, x1.z, s);
+    s = zz_dot4((w.w >> 4) & m, x1.w, s);
+    return s;                      // sum q*x with q in 0..15
+}
+
+__device__ __forceinline__ int zz_dot_q80(uint4 w0, uint4 w1, uint4 x0, uint4 x1) {
+    int s = zz_dot4(w0.x, x0.x, 0);
+    s = zz_dot4(w0.y, x0.y, s);
+    s = zz_dot4(w0.z, x0.z, s);
+    s = zz_dot4(w0.w, x0.w, s);
+    s = zz_dot4(w1.x, x1.x, s);
+    s = zz_dot4(w1.y, x1.y, s);
+    s = zz_dot4(w1.z, x1.z, s);
+    s = zz_dot4(w1.w, x1.w, s);
+    return s;
+}
+
+// half h of a tq2 group: weights 32h..32h+31 are bit planes 2h (weights 32h+k) and
+// 2h+1 (weights 32h+16+k) of the 16 code bytes (tq2.h:46-51)
+__device__ __forceinline__ int zz_dot_tq2(uint4 c, int h, uint4 xa, uint4 xb) {
+    const unsigned m = 0x03030303u;
+    const int sa = 4 * h, sb = 4 * h + 2;
+    int s = zz_dot4((c.x >> sa) & m, xa.x, 0);
+    s = zz_dot4((c.y >> sa) & m, xa.y, s);
+    s = zz_dot4((c.z >> sa) & m, xa.z, s);
+    s = zz_dot4((c.w >> sa) & m, xa.w, s);
+    s = zz_dot4((c.x >> sb) & m, xb.x, s);
+    s = zz_dot4((c.y >> sb) & m, xb.y, s);
+    s = zz_dot4((c.z >> sb) & m, xb.z, s);
+    s = zz_dot4((c.w >> sb) & m, xb.w, s);
+    return s;                      // sum c*x with c in {0,1,2}
+}
+
+__device__ __forceinline__ uint4 ld16(const void *p) { return *(const uint4 *)p; }
+
+// Partial row dot of one lane: blocks b = sub, sub+4, ... of row `row` of tensor T
+// against the int8 activations of up to ZZ_TCH tokens. Returns per-token partial
+// sums of d_w * d_x * int32 (q4_0 / q8_0) or d_x * int32 (tq2, alpha applied later).
+template <int NT>
+__device__ __forceinline__ void zz_row_partial(const uint8_t *E, const ZzTensor &T, int row, int sub,
+                                               int nt, const int8_t *const *xq,
+                                               const float *const *xs, const int *const *xsum,
+                                               float (&acc)[NT]) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = 0.0f;
+    if (T.fmt == ZZ_FMT_TQ2) {
+        const int ng = T.I / 64;
+        const uint8_t *codes = E + T.off_q + (size_t)row * (T.I / 4);
+        for (int g = sub; g < ng; g += 4) {
+            uint4 c = ld16(codes + (size_t)g * 16);
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                if (t < nt) {
+                    const int8_t *x = xq[t] + g * 64;
+                    uint4 x0 = ld16(x), x1 = ld16(x + 16), x2 = ld16(x + 32), x3 = ld16(x + 48);
+                    int d0 = zz_dot_tq2(c, 0, x0, x1), d1 = zz_dot_tq2(c, 1, x2, x3);
+                    acc[t] = fmaf(xs[t][2 * g], (float)d0, acc[t]);
+                    acc[t] = fmaf(xs[t][2 * g + 1], (float)d1, acc[t]);
+                }
+            }
+        }
+        return;
+    }
+    const int nb = T.I / ZZ_BLK;
+    const bool q8 = T.fmt == ZZ_FMT_Q80;
+    const int pb = q8 ? 32 : 16;
+    const uint8_t *qs = E + T.off_q + (size_t)row * nb * pb;
+    const uint16_t *sc = (const uint16_t *)(E + T.off_s) + (size_t)row * nb;
+    for (int b = sub; b < nb; b += 4) {
+        float dw = zz_h2f(sc[b]);
+        uint4 w0 = ld16(qs + (size_t)b * pb), w1 = make_uint4(0, 0, 0, 0);
+        if (q8) w1 = ld16(qs + (size_t)b * pb + 16);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (t < nt) {
+                const int8_t *x = xq[t] + b * ZZ_BLK;
+                uint4 x0 = ld16(x), x1 = ld16(x + 16);
+                int d = q8 ? zz_dot_q80(w0, w1, x0, x1) : zz_dot_q40(w0, x0, x1) - 8 * xsum[t][b];
+                acc[t] = fmaf(dw * xs[t][b], (float)d, acc[t]);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ repack
+// Reference record [gate | up | down] (18/34-byte blocks, tq2 alpha+codes) into
+// the slot-table layout. One thread per block; grid.y selects the tensor.
+__global__ void zz_repack_kernel(ZzRepackArgs a) {
+    const ZzTensor &T = blockIdx.y == 0 ? a.lay.gate : (blockIdx.y == 1 ? a.lay.up : a.lay.down);
+    const int64_t so = blockIdx.y == 0 ? a.src_gate : (blockIdx.y == 1 ? a.src_up : a.src_down);
+    const uint8_t *src = a.src + so;
+    uint8_t *dst = a.dst;
+    if (T.fmt == ZZ_FMT_TQ2) {
+        int64_t n = (int64_t)T.O * 4 + (int64_t)T.O * (T.I / 4);
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+             i += (int64_t)gridDim.x * blockDim.x) {
+            if (i < (int64_t)T.O * 4) dst[T.off_s + i] = src[i];
+            else dst[T.off_q + (i - (int64_t)T.O * 4)] = src[i];
+        }
+        return;
+    }
+    const int nb = T.I / ZZ_BLK, pb = T.fmt == ZZ_FMT_Q80 ? 32 : 16, bb = pb + 2;
+    const int64_t n = (int64_t)T.O * nb;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const uint8_t *s = src + i * bb;
+        uint8_t *q = dst + T.off_q + i * pb;
+        for (int k = 0; k < pb; k++) q[k] = s[2 + k];
+        dst[T.off_s + 2 * i] = s[0];
+        dst[T.off_s + 2 * i + 1] = s[1];
+    }
+}
+
+// ------------------------------------------------------------------ gate / up
+// grid (MI/32, items). Waves 0,1 compute gate rows rb*32 + 0..31, waves 2,3 the
+// same up rows; 4 lanes per row. Then one lane per (token, row) forms
+// h = act(g, u) and the 32 lanes of a token quantise the 32-block of h
+// (gemma4.c:642-645, lfm25.c:712-723, maple.c:665-684).
+__global__ __launch_bounds__(256) void zz_ffn_up_kernel(ZzFfnArgs a) {
+    const int it = blockIdx.y;
+    if (it >= a.meta[1]) return;
+    const ZzItem item = a.items[it];
+    const int rb = blockIdx.x, w = threadIdx.x >> 6, l = threadIdx.x & 63, sub = l & 3;
+    const ZzTensor &T = w < 2 ? a.lay.gate : a.lay.up;
+    const int rloc = (w & 1) * 16 + (l >> 2), row = rb * 32 + rloc;
+    const uint8_t *E = a.experts + (size_t)item.e * a.estride;
+    const int D = a.D, nb = D / ZZ_BLK;
+    const int8_t *xq[ZZ_TCH];
+    const float *xs[ZZ_TCH];
+    const int *xsum[ZZ_TCH];
+    int tok[ZZ_TCH];
+#pragma unroll
+    for (int t = 0; t < ZZ_TCH; t++) {
+        tok[t] = t < item.n ? a.ptok[item.p0 + t] : 0;
+        xq[t] = a.xq + (size_t)tok[t] * D;
+        xs[t] = a.xs + (size_t)tok[t] * nb;
+        xsum[t] = a.xsum + (size_t)tok[t] * nb;
+    }
+    float acc[ZZ_TCH];
+    zz_row_partial<ZZ_TCH>(E, T, row, sub, item.n, xq, xs, xsum, acc);
+    __shared__ float gu[ZZ_TCH][64];
+#pragma unroll
+    for (int t = 0; t < ZZ_TCH; t++) {
+        float v = acc[t];
+        v += __shfl_xor(v, 1, 64);
+        v += __shfl_xor(v, 2, 64);
+        if (T.fmt == ZZ_FMT_TQ2) {
+            const float alpha = ((const float *)(E + T.off_s))[row];
+            v = alpha * (v - a.xt[tok[t]]);                   // tq2.h:154
+        }
+        if (sub == 0) gu[t][w * 16 + (l >> 2)] = v;
+    }
+    __syncthreads();
+    const int t = threadIdx.x >> 5, r = threadIdx.x & 31;
+    float h = 0.0f;
+    if (t < item.n) h = zz_act(a.act, gu[t][r], gu[t][32 + r], a.clamp);
+    float d;
+    int q = zz_quant_lane(h, &d);
+    int qs = q;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) qs += __shfl_xor(qs, o, 64);
+    if (t < item.n) {
+        const size_t p = (size_t)item.p0 + t;
+        a.hq[p * a.MI + rb * 32 + r] = (int8_t)q;
+        if (r == 0) {
+            a.hs[p * (a.MI / ZZ_BLK) + rb] = d;
+            a.hsum[p * (a.MI / ZZ_BLK) + rb] = qs;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ down
+// grid (D/64, items): 64 output rows per workgroup, 4 lanes per row. Writes the
+// unweighted expert output y[pair][row]; the combine applies the gate weights.
+__global__ __launch_bounds__(256) void zz_ffn_down_kernel(ZzFfnArgs a) {
+    const int it = blockIdx.y;
+    if (it >= a.meta[1]) return;
+    const ZzItem item = a.items[it];
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, sub = l & 3;
+    const int row = blockIdx.x * 64 + w * 16 + (l >> 2);
+    const ZzTensor &T = a.lay.down;
+    const uint8_t *E = a.experts + (size_t)item.e * a.estride;
+    const int MI = a.MI, nb = MI / ZZ_BLK;
+    __shared__ float htot[ZZ_TCH];
+    if (T.fmt == ZZ_FMT_TQ2 && threadIdx.x < item.n) {
+        const size_t p = (size_t)item.p0 + threadIdx.x;   // tq2.h:101-106, serial
+        double tot = 0.0;
+        for (int b = 0; b < nb; b++)
+            tot += (double)a.hs[p * nb + b] * (double)a.hsum[p * nb + b];
+        htot[threadIdx.x] = (float)tot;
+    }
+    __syncthreads();
+    if (row >= a.D) return;
+    const int8_t *xq[ZZ_TCH];
+    const float *xs[ZZ_TCH];
+    const int *xsum[ZZ_TCH];
+#pragma unroll
+    for (int t = 0; t < ZZ_TCH; t++) {
+        const size_t p = (size_t)item.p0 + (t < item.n ? t : 0);
+        xq[t] = a.hq + p * MI;
+        xs[t] = a.hs + p * nb;
+        xsum[t] = a.hsum + p * nb;
+    }
+    float acc[ZZ_TCH];
+    zz_row_partial<ZZ_TCH>(E, T, row, sub, item.n, xq, xs, xsum, acc);
+#pragma unroll
+    for (int t = 0; t < ZZ_TCH; t++) {
+        float v = acc[t];
+        v += __shfl_xor(v, 1, 64);
+        v += __shfl_xor(v, 2, 64);
+        if (T.fmt == ZZ_FMT_TQ2) {
+            const float alpha = ((const float *)(E + T.off_s))[row];
+            v = alpha * (v - htot[t]);
+        }
+        if (sub == 0 && t < item.n) a.y[((size_t)item.p0 + t) * a.D + row] = v;
+    }
+}
+
+// ------------------------------------------------------------------ combine
+// out[s] = sum_j w[s,j] * y[pair(s,j)] in slot order, fused multiply-add as the
+// reference's `out[o] += ww * dot` (gemma4.c:652); gemma then applies
+// rmsnorm(out, post_ffn_ln2) (gemma4.c:807-808). One workgroup per token.
+__global__ __launch_bounds__(256) void zz_combine_kernel(ZzCombineArgs a) {
+    const int s = blockIdx.x, D = a.D, K = a.K;
+    __shared__ float row[ZZ_MAXD];
+    __shared__ double red[4];
+    __shared__ int pos[ZZ_MAXK];
+    __shared__ float wt[ZZ_MAXK];
+    if (threadIdx.x < K) {
+        pos[threadIdx.x] = a.ppos[(size_t)s * K + threadIdx.x];
+        wt[threadIdx.x] = a.ewt[(size_t)s * K + threadIdx.x];
+    }
+    __syncthreads();
+    double ss = 0.0;
+    for (int o = threadIdx.x; o < D; o += 256) {
+        float v = 0.0f;
+        for (int j = 0; j < K; j++) v = fmaf(wt[j], a.y[(size_t)pos[j] * D + o], v);
+        row[o] = v;
+        ss += (double)v * (double)v;
+    }
+    float r = 1.0f;
+    if (a.gemma) {
+        ss = zz_wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        double tot = red[0] + red[1] + red[2] + red[3];
+        r = 1.0f / sqrtf((float)(tot / D) + a.eps);
+    }
+    for (int o = threadIdx.x; o < D; o += 256) {
+        float v = row[o];
+        a.out[(size_t)s * D + o] = a.gemma ? (v * r) * a.post_ln[o] : v;
+    }
+}
+
+// ------------------------------------------------------------------ debug dots
+__global__ void zz_blockdots_kernel(const uint8_t *E, ZzTensor T, int row0, int nrows,
+                                    const int8_t *xq, int32_t *out) {
+    const int nb = T.I / ZZ_BLK;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nrows * nb) return;
+    const int r = row0 + i / nb, b = i % nb;
+    const int8_t *x = xq + b * ZZ_BLK;
+    uint4 x0 = ld16(x), x1 = ld16(x + 16);
+    int xs = 0;
+    for (int j = 0; j < ZZ_BLK; j++) xs += x[j];
+    int d;
+    if (T.fmt == ZZ_FMT_Q40) {
+        d = zz_dot_q40(ld16(E + T.off_q + ((size_t)r * nb + b) * 16), x0, x1) - 8 * xs;
+    } else if (T.fmt == ZZ_FMT_Q80) {
+        const uint8_t *q = E + T.off_q + ((size_t)r * nb + b) * 32;
+        d = zz_dot_q80(ld16(q), ld16(q + 16), x0, x1);
+    } else {
+        const uint4 c = ld16(E + T.off_q + (size_t)r * (T.I / 4) + (size_t)(b / 2) * 16);
+        d = zz_dot_tq2(c, b & 1, x0, x1) - xs;
+    }
+    out[i] = d;
+}
+
+// ------------------------------------------------------------------ launchers
+int zz_launch_repack(const ZzRepackArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(zz_repack_kernel, dim3(256, 3), dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess;
+}
+
+int zz_launch_ffn_up(const ZzFfnArgs &a, int max_items, hipStream_t st) {
+    hipLaunchKernelGGL(zz_ffn_up_kernel, dim3(a.MI / 32, max_items), dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess;
+}
+
+int zz_launch_ffn_down(const ZzFfnArgs &a, int max_items, hipStream_t st) {
+    hipLaunchKernelGGL(zz_ffn_down_kernel, dim3((a.D + 63) / 64, max_items), dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess;
+}
+
+int zz_launch_combine(const ZzCombineArgs &a, int S, hipStream_t st) {
+    hipLaunchKernelGGL(zz_combine_kernel, dim3(S), dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess;
+}
+
+int zz_launch_blockdots(const uint8_t *expert, ZzTensor t, int row0, int nrows,
+                        const int8_t *xq, int32_t *out, hipStream_t st) {
+    int n = nrows * (t.I / ZZ_BLK);
+    hipLaunchKernelGGL(zz_blockdots_kernel, dim3((n + 255) / 256), dim3(256), 0, st, expert, t,
+                       row0, nrows, xq, out);
+    return hipGetLastError() == hipSuccess;
+}

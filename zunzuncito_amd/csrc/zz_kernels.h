@@ -1,0 +1,111 @@
+// zz_kernels.h -- kernel argument blocks and launchers shared by the HIP sources
+// and the C-ABI host layer. Plain structs passed by value to each kernel.
+#pragma once
+#include "zz_common.h"
+
+struct ZzPrepArgs {
+    int D, gemma;
+    float eps;
+    const float *in;            // [S, D]
+    const float *router_scale;  // [D]   gemma
+    const float *pre_ln;        // [D]   gemma
+    float *xn;                  // [S, D] gemma router input
+    int8_t *xq;                 // [S, D]
+    float *xs;                  // [S, D/32]
+    int *xsum;                  // [S, D/32]
+    float *xt;                  // [S] tq2 Sx, or null
+    unsigned *diag;             // diagnostics counters
+};
+
+struct ZzLogitArgs {
+    int D, E, gating;
+    const float *router;        // [E, D]
+    const float *xn;            // [S, D] gemma
+    const float *x;             // [S, D] lfm / maple
+    const float *bias;          // [E] gemma Zipf offset, or null
+    double *cen, *bnd;          // [S, E]
+    unsigned *diag;
+};
+
+struct ZzTopkArgs {
+    int D, E, K, gating, norm_topk;
+    float routed_scaling;
+    const double *cen, *bnd;    // [S, E]
+    const float *router, *xn;   // gemma refinement
+    const float *bias;          // gemma Zipf offset / lfm expert_bias
+    const float *pes;           // gemma
+    int *eidx;                  // [S, K]
+    float *ewt;                 // [S, K]
+    float *topv;                // [S, K] selected scores (debug), or null
+    int *contested;             // [S] lfm near-tie flags, or null
+    unsigned *diag;
+};
+
+struct ZzItem {                 // one FFN work unit: <= tch pairs of one expert
+    int e, u, p0, n;
+};
+
+struct ZzDispatchArgs {
+    int P, E, K, tch;
+    const int *eidx;            // [P]
+    const float *ewt;           // [P]
+    int *ptok, *pslot;          // [P] sorted pair -> token, slot
+    float *pwt;                 // [P] sorted pair -> weight
+    int *ppos;                  // [P] flat (token*K + slot) -> sorted position
+    int *uniq, *uoff, *ucnt;    // [E] union order
+    ZzItem *items;              // [<= E + P/tch]
+    int *meta;                  // [0] = nu, [1] = n_items
+};
+
+struct ZzFfnArgs {
+    int D, MI, K, act;
+    float clamp;
+    const uint8_t *experts;     // slot table base of this layer
+    int64_t estride;            // bytes per expert
+    ZzLayout lay;
+    const ZzItem *items;
+    const int *meta;
+    const int *ptok;            // sorted pair -> token
+    const int8_t *xq;           // [S, D]
+    const float *xs;            // [S, D/32]
+    const int *xsum;            // [S, D/32]
+    const float *xt;            // [S]
+    int8_t *hq;                 // [P, MI] by sorted pair
+    float *hs;                  // [P, MI/32]
+    int *hsum;                  // [P, MI/32]
+    float *y;                   // [P, D] expert outputs before weighting
+};
+
+struct ZzCombineArgs {
+    int D, K, gemma;
+    float eps;
+    const float *y;             // [P, D]
+    const int *ppos;            // [S*K]
+    const float *ewt;           // [S, K]
+    const float *post_ln;       // [D] gemma
+    float *out;                 // [S, D]
+};
+
+struct ZzRepackArgs {
+    const uint8_t *src;         // reference record [gate | up | down]
+    int64_t src_gate, src_up, src_down;   // byte offsets in the record
+    uint8_t *dst;               // repacked expert
+    ZzLayout lay;
+};
+
+int zz_launch_prep(const ZzPrepArgs &a, int S, hipStream_t st);
+int zz_launch_logits(const ZzLogitArgs &a, int S, hipStream_t st);
+int zz_launch_topk(const ZzTopkArgs &a, int S, hipStream_t st);
+int zz_launch_dispatch(const ZzDispatchArgs &a, hipStream_t st);
+int zz_launch_ffn_up(const ZzFfnArgs &a, int max_items, hipStream_t st);
+int zz_launch_ffn_down(const ZzFfnArgs &a, int max_items, hipStream_t st);
+int zz_launch_combine(const ZzCombineArgs &a, int S, hipStream_t st);
+int zz_launch_repack(const ZzRepackArgs &a, hipStream_t st);
+// y[S,O] = W[O,I] x[S,I] with f32 activations (gpu.h matmul contract)
+int zz_launch_matmul_f32(int fmt, float *y, const uint8_t *W, const float *x, int O, int I,
+                         int S, hipStream_t st);
+// f32 -> q4_0 / q8_0 blocks in the reference layout (nblk blocks of 32 values)
+int zz_launch_quantize(int fmt, const float *w, uint8_t *dst, int64_t nblk, hipStream_t st);
+// per-block exact int32 dots of n rows of a repacked tensor against one int8 vector
+int zz_launch_blockdots(const uint8_t *expert, ZzTensor t, int row0, int nrows,
+                        const int8_t *xq, int32_t *out, hipStream_t st);
