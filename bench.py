@@ -217,6 +217,9 @@ def main():
     layers, host = build_layers(zz, torch, args.layers, args.seed)
     log(f"built {len(layers)} layers ({len(layers) * E * REC_B / 1e9:.1f} GB experts) in {time.time() - t0:.1f}s")
 
+    # a stream of our own: handle 0 would mean "the library's stream" to the ABI
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
     res = {}
     for S, steps, warm in ((args.tokens, args.steps, args.warmup), (1, args.steps * 4, args.warmup)):
         g = torch.Generator(device="cuda")
@@ -234,6 +237,7 @@ def main():
             f"-> {ev / steps * 1e6:.1f} us/step, nu {nu:.1f}; kernels (us): "
             + ", ".join(f"{k} {v:.1f}" for k, v in kern.items()))
 
+    log("router fallback counters (rms, logit, gemma exact, lfm contested):", zz.stats())
     S = args.tokens
     r = res[S]
     step_s = r["ev"] / r["steps"]

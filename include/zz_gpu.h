@@ -9,9 +9,10 @@
  *
  * Differences forced by a discrete GPU, all inside the same contract:
  *  - gpu_map() cannot wrap host pages without a copy (gpu.h:66-69 "NO copy" is a
- *    unified-memory property). It uploads the range into HBM once; calling it again
- *    on the same range re-uploads (the refresh an engine needs after rewriting a
- *    mapped buffer, e.g. an expert slot filled by pread).
+ *    unified-memory property). It uploads the range into HBM once. Mapping a range
+ *    inside an existing mapping re-uploads those bytes (the refresh an engine needs
+ *    after rewriting a mapped buffer, e.g. an expert slot filled by pread); a range
+ *    that only overlaps older mappings replaces them (the host memory was reused).
  *  - gpu_matmul() copies x in and y out per call (PCIe), then runs a dequantising
  *    GEMV with f32 activations: the *_dot_f32 semantics (gpu.h:25-27), checked to
  *    < 1e-4 relative like gemma4.c:2315-2368.

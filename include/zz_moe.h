@@ -96,8 +96,9 @@ int zz_moe_forward_end(int layer, float *out, int *eidx, float *ewt);
 
 /* Debug dump of the last forward's first chunk (any pointer may be NULL):
  * xq/xs [S, D] / [S, D/32]: the int8 expert input; hq/hs [S*K, MI] / [S*K, MI/32]:
- * the int8 hidden by (token, slot); dispatch: uniq[E] union order (returns nu),
- * offs[nu+1], rows[S*K] tokens per expert ascending, slots[S*K]. */
+ * the int8 hidden by (token, slot); dispatch: uniq[E] union order (nu is set),
+ * and for union entry u the tokens rows[offs[u] .. offs[u+1]) ascending with
+ * their top-k slots (offs[nu+1], rows[S*K], slots[S*K]). */
 typedef struct zz_moe_dump {
     int8_t *xq; float *xs;
     int8_t *hq; float *hs;

@@ -65,6 +65,13 @@ def lib():
         return _lib
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(f"{LIB_PATH} is not built: run `python -m zunzuncito_amd.build`")
+    # torch ships its own libamdhip64.so.7 (same SONAME as /opt/rocm's): load it
+    # first where torch is installed, so one HIP runtime serves both and device
+    # pointers and streams can be shared with torch tensors
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = C.CDLL(LIB_PATH)
     L.gpu_init.restype = C.c_int
     L.gpu_name.restype = C.c_char_p

@@ -14,7 +14,7 @@ CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libzzmoe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["zz_api.hip", "zz_route.hip", "zz_ffn.hip", "zz_matmul.hip", "zz_quant.hip", "zz_prefill.hip"]
+SOURCES = ["zz_api.hip", "zz_route.hip", "zz_ffn.hip", "zz_matmul.hip", "zz_quant.hip", "zz_prefill.hip", "zz_decode.hip"]
 
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
@@ -23,6 +23,8 @@ FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     # no packed-fp32 instructions from the compiler
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # matrix-core results straight into VGPRs (no v_accvgpr_read per element)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-function",
 ]
 

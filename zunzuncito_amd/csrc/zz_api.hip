@@ -29,6 +29,8 @@ void zz_set_error(const char *fmt, ...) {
     } while (0)
 
 static int g_ready = 0;
+// batches of at least this many tokens take the matrix-core FFN (ZZ_MFMA_MIN_S)
+static int g_mfma_min_s = 16;
 static char g_name[128] = "none";
 static hipStream_t g_stream = nullptr;
 static unsigned *g_diag = nullptr;          // device counters, see zz_moe_stats
@@ -55,6 +57,8 @@ extern "C" int gpu_init(void) {
     ZZ_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     ZZ_CHECK(hipMalloc(&g_diag, 16 * sizeof(unsigned)));
     ZZ_CHECK(hipMemset(g_diag, 0, 16 * sizeof(unsigned)));
+    const char *ms = getenv("ZZ_MFMA_MIN_S");
+    if (ms && atoi(ms) > 0) g_mfma_min_s = atoi(ms);
     g_ready = 1;
     return 1;
 }
@@ -64,19 +68,35 @@ extern "C" const char *gpu_name(void) { return g_name; }
 
 static const Mapping *find_map(const void *p, size_t n) {
     const uint8_t *q = (const uint8_t *)p;
-    for (const Mapping &m : g_maps)
+    for (size_t i = g_maps.size(); i-- > 0;) {
+        const Mapping &m = g_maps[i];
         if (q >= m.host && q + n <= m.host + m.n) return &m;
+    }
     return nullptr;
 }
 
+// A range inside an existing mapping is re-uploaded in place (the refresh an
+// engine does after rewriting a mapped buffer). A range that only overlaps older
+// mappings means that host memory was released and reused: those mappings are
+// dropped so a lookup can never return bytes from the previous owner.
 extern "C" int gpu_map(const void *p, size_t n) {
     if (!g_ready || !p || !n) ZZ_FAIL("gpu_map: not ready or empty range");
-    for (Mapping &m : g_maps)
-        if (m.host == p && m.n == n) {           // refresh an existing mapping
-            ZZ_CHECK(hipMemcpy(m.dev, p, n, hipMemcpyHostToDevice));
+    const uint8_t *q = (const uint8_t *)p;
+    for (size_t i = g_maps.size(); i-- > 0;) {
+        Mapping &m = g_maps[i];
+        if (q >= m.host && q + n <= m.host + m.n) {
+            ZZ_CHECK(hipMemcpy(m.dev + (q - m.host), p, n, hipMemcpyHostToDevice));
             return 1;
         }
-    Mapping m{(const uint8_t *)p, n, nullptr};
+    }
+    for (size_t i = g_maps.size(); i-- > 0;) {
+        Mapping &m = g_maps[i];
+        if (q < m.host + m.n && m.host < q + n) {
+            (void)hipFree(m.dev);
+            g_maps.erase(g_maps.begin() + i);
+        }
+    }
+    Mapping m{q, n, nullptr};
     ZZ_CHECK(hipMalloc(&m.dev, n));
     if (hipMemcpy(m.dev, p, n, hipMemcpyHostToDevice) != hipSuccess) {
         (void)hipFree(m.dev);
@@ -177,9 +197,8 @@ static ZzTensor make_tensor(int fmt, int O, int I, int64_t *cursor) {
         t.off_q = *cursor;
         *cursor = align256(*cursor + (int64_t)O * (I / 4));
     } else {
-        int pb = fmt == ZZ_FMT_Q80 ? 32 : 16;
         t.off_q = *cursor;
-        *cursor = align256(*cursor + (int64_t)O * (I / ZZ_BLK) * pb);
+        *cursor = align256(*cursor + (int64_t)O * (I / ZZ_BLK) * zz_pbytes(t));
         t.off_s = *cursor;
         *cursor = align256(*cursor + (int64_t)O * (I / ZZ_BLK) * 2);
     }
@@ -303,8 +322,13 @@ extern "C" int zz_moe_expert_upload_dev(int id, int eid, const void *d_rec, size
     return upload_common(L, eid, d_rec, n, hipMemcpyDeviceToDevice);
 }
 
-// largest chunk one dispatch workgroup sorts in LDS: S*K pairs <= 8192
-static int chunk_tokens(const zz_moe_desc &d) { return 8192 / d.K; }
+// largest chunk one dispatch workgroup handles: S*K <= 8192 pairs and the two
+// per-expert token bitmasks (2 * E * ceil(S/32) words) within 48 KB of LDS
+static int chunk_tokens(const zz_moe_desc &d) {
+    int by_pairs = 8192 / d.K;
+    int by_masks = 32 * (6144 / d.E);
+    return by_pairs < by_masks ? by_pairs : by_masks;
+}
 
 static int ensure_ws(Layer *L, int S) {
     Workspace &w = L->ws;
@@ -421,7 +445,7 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
     if (!(ProfScope(ZZ_K_PREP, st), zz_launch_prep(pa, S, st))) ZZ_FAIL("prep launch failed");
 
     ZzLogitArgs la;
-    la.D = d.D; la.E = d.E; la.gating = d.gating; la.router = L->router; la.xn = w.xn; la.x = d_in;
+    la.D = d.D; la.E = d.E; la.gating = d.gating; la.S = S; la.router = L->router; la.xn = w.xn; la.x = d_in;
     la.bias = gemma && d.use_bias ? L->bias : nullptr; la.cen = w.cen; la.bnd = w.bnd; la.diag = g_diag;
     if (!(ProfScope(ZZ_K_LOGITS, st), zz_launch_logits(la, S, st))) ZZ_FAIL("logits launch failed");
 
@@ -432,8 +456,12 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
     ta.ewt = w.ewt; ta.topv = w.topv; ta.contested = w.contested; ta.diag = g_diag;
     if (!(ProfScope(ZZ_K_TOPK, st), zz_launch_topk(ta, S, st))) ZZ_FAIL("topk launch failed");
 
+    // many tokens per expert: 64-token items on the matrix cores; decode-sized
+    // batches: 8-token items on the dot4 GEMV
+    const bool mfma = S >= g_mfma_min_s && d.fmt_gate == d.fmt_up;
+    const int tch = mfma ? 64 : 8;
     ZzDispatchArgs da;
-    da.P = P; da.E = d.E; da.K = d.K; da.tch = 8; da.eidx = w.eidx; da.ewt = w.ewt;
+    da.P = P; da.E = d.E; da.K = d.K; da.tch = tch; da.eidx = w.eidx; da.ewt = w.ewt;
     da.ptok = w.ptok; da.pslot = w.pslot; da.pwt = w.pwt; da.ppos = w.ppos; da.uniq = w.uniq;
     da.uoff = w.uoff; da.ucnt = w.ucnt; da.items = w.items; da.meta = w.meta;
     if (!(ProfScope(ZZ_K_DISPATCH, st), zz_launch_dispatch(da, st))) ZZ_FAIL("dispatch launch failed");
@@ -443,9 +471,14 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
     fa.experts = L->slots; fa.estride = L->lay.bytes; fa.lay = L->lay; fa.items = w.items;
     fa.meta = w.meta; fa.ptok = w.ptok; fa.xq = w.xq; fa.xs = w.xs; fa.xsum = w.xsum; fa.xt = w.xt;
     fa.hq = w.hq; fa.hs = w.hs; fa.hsum = w.hsum; fa.y = w.y;
-    const int max_items = (P < d.E ? P : d.E) + (P + 7) / 8;
-    if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_ffn_up(fa, max_items, st))) ZZ_FAIL("ffn_up launch failed");
-    if (!(ProfScope(ZZ_K_FFN_DOWN, st), zz_launch_ffn_down(fa, max_items, st))) ZZ_FAIL("ffn_down launch failed");
+    const int max_items = (P < d.E ? P : d.E) + (P + tch - 1) / tch;
+    if (mfma) {
+        if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_up_mfma(fa, max_items, st))) ZZ_FAIL("ffn_up launch failed");
+        if (!(ProfScope(ZZ_K_FFN_DOWN, st), zz_launch_down_mfma(fa, max_items, st))) ZZ_FAIL("ffn_down launch failed");
+    } else {
+        if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_ffn_up(fa, max_items, st))) ZZ_FAIL("ffn_up launch failed");
+        if (!(ProfScope(ZZ_K_FFN_DOWN, st), zz_launch_ffn_down(fa, max_items, st))) ZZ_FAIL("ffn_down launch failed");
+    }
 
     ZzCombineArgs ca;
     ca.D = d.D; ca.K = d.K; ca.gemma = gemma; ca.eps = d.eps; ca.y = w.y; ca.ppos = w.ppos;
@@ -559,12 +592,16 @@ extern "C" int zz_moe_debug(int id, zz_moe_dump *dp) {
     const int nu = meta[0];
     dp->nu = nu;
     if (dp->uniq) memcpy(dp->uniq, uniq.data(), sizeof(int) * nu);
-    if (dp->offs) {
-        for (int u = 0; u < nu; u++) dp->offs[u] = uoff[u];
-        dp->offs[nu] = P;
+    // lists in union order, as moe_apply_chunk walks them (gemma4.c:776-790)
+    int n = 0;
+    for (int u = 0; u < nu; u++) {
+        if (dp->offs) dp->offs[u] = n;
+        for (int i = 0; i < ucnt[u]; i++, n++) {
+            if (dp->rows) dp->rows[n] = ptok[uoff[u] + i];
+            if (dp->slots) dp->slots[n] = pslot[uoff[u] + i];
+        }
     }
-    if (dp->rows) memcpy(dp->rows, ptok.data(), sizeof(int) * P);
-    if (dp->slots) memcpy(dp->slots, pslot.data(), sizeof(int) * P);
+    if (dp->offs) dp->offs[nu] = n;
     const int nbM = d.MI / ZZ_BLK;
     if (dp->hq || dp->hs) {
         std::vector<int8_t> hq((size_t)P * d.MI);

@@ -39,15 +39,35 @@
 
 void zz_set_error(const char *fmt, ...);
 
-// Device view of one expert tensor inside the HBM slot table. q4_0 and q8_0
-// tensors are stored repacked as two planes so every block's payload is 16-byte
-// aligned: qs[O][nb][16|32] then scales[O][nb] (fp16). tq2 keeps its reference
-// layout: alpha[O] f32 then codes[O][I/4].
+// Device view of one expert tensor inside the HBM slot table. Rows are stored in
+// groups of 16: for each (16-row group, block) the 16 rows' payloads are one
+// contiguous chunk, so a wave reading one block of 16 rows reads 256 (q4_0, tq2)
+// or 512 (q8_0) contiguous bytes, in the order the 16x16x32 int8 MFMA wants them.
+//   q4_0: payload [O/16][I/32][16][16 B nibbles], scales [O/16][I/32][16] fp16
+//   q8_0: payload [O/16][I/32][16][32 B int8],    scales as q4_0
+//   tq2:  codes   [O/16][I/64][16][16 B],         alpha [O] f32 (row order)
+// The block contents are the reference's bytes unchanged (q40.h:12-17, 320-329;
+// tq2.h:46-51); only their placement differs.
 struct ZzTensor {
     int fmt, O, I;
     int64_t off_q;       // byte offset of the payload plane inside the expert
     int64_t off_s;       // byte offset of the scale plane (alpha for tq2)
 };
+
+// blocks per row: 32-weight blocks (q4_0, q8_0) or 64-weight groups (tq2)
+__host__ __device__ __forceinline__ int zz_nblk(const ZzTensor &T) {
+    return T.fmt == ZZ_FMT_TQ2 ? T.I / 64 : T.I / ZZ_BLK;
+}
+__host__ __device__ __forceinline__ int zz_pbytes(const ZzTensor &T) {
+    return T.fmt == ZZ_FMT_Q80 ? 32 : 16;
+}
+// byte offset of row `row`, block `b` payload; of its fp16 scale (q4_0/q8_0)
+__host__ __device__ __forceinline__ int64_t zz_qoff(const ZzTensor &T, int row, int b) {
+    return T.off_q + (((int64_t)(row >> 4) * zz_nblk(T) + b) * 16 + (row & 15)) * zz_pbytes(T);
+}
+__host__ __device__ __forceinline__ int64_t zz_soff(const ZzTensor &T, int row, int b) {
+    return T.off_s + (((int64_t)(row >> 4) * zz_nblk(T) + b) * 16 + (row & 15)) * 2;
+}
 
 struct ZzLayout {        // byte layout of one repacked expert, all 256-aligned
     ZzTensor gate, up, down;
@@ -97,6 +117,29 @@ __device__ __forceinline__ int zz_quant_lane(float v, float *d_out) {
     q = fminf(fmaxf(q, -127.0f), 127.0f);
     *d_out = d;
     return (int)q;
+}
+
+// q40.h:124-138 for one whole 32-block held by a single thread: no cross-lane
+// traffic. Writes 32 int8 to q (16-byte aligned), returns d; *sum = sum of q.
+__device__ __forceinline__ float zz_quant_block(const float (&v)[ZZ_BLK], int8_t *q, int *sum) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < ZZ_BLK; j++) amax = fmaxf(amax, fabsf(v[j]));
+    const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+    unsigned w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < ZZ_BLK; j++) {
+        float f = rintf(v[j] * id);
+        f = fminf(fmaxf(f, -127.0f), 127.0f);
+        const int qi = (int)f;
+        s += qi;
+        w[j >> 2] |= (unsigned)(qi & 0xff) << (8 * (j & 3));
+    }
+    ((uint4 *)q)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    ((uint4 *)q)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    *sum = s;
+    return d;
 }
 
 __device__ __forceinline__ float zz_gelu_tanh(float x) {

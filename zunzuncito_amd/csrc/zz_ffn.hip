@@ -68,9 +68,8 @@ __device__ __forceinline__ void zz_row_partial(const uint8_t *E, const ZzTensor 
     for (int t = 0; t < NT; t++) acc[t] = 0.0f;
     if (T.fmt == ZZ_FMT_TQ2) {
         const int ng = T.I / 64;
-        const uint8_t *codes = E + T.off_q + (size_t)row * (T.I / 4);
         for (int g = sub; g < ng; g += 4) {
-            uint4 c = ld16(codes + (size_t)g * 16);
+            uint4 c = ld16(E + zz_qoff(T, row, g));
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 if (t < nt) {
@@ -86,13 +85,11 @@ __device__ __forceinline__ void zz_row_partial(const uint8_t *E, const ZzTensor 
     }
     const int nb = T.I / ZZ_BLK;
     const bool q8 = T.fmt == ZZ_FMT_Q80;
-    const int pb = q8 ? 32 : 16;
-    const uint8_t *qs = E + T.off_q + (size_t)row * nb * pb;
-    const uint16_t *sc = (const uint16_t *)(E + T.off_s) + (size_t)row * nb;
     for (int b = sub; b < nb; b += 4) {
-        float dw = zz_h2f(sc[b]);
-        uint4 w0 = ld16(qs + (size_t)b * pb), w1 = make_uint4(0, 0, 0, 0);
-        if (q8) w1 = ld16(qs + (size_t)b * pb + 16);
+        const uint8_t *qs = E + zz_qoff(T, row, b);
+        float dw = zz_h2f(*(const uint16_t *)(E + zz_soff(T, row, b)));
+        uint4 w0 = ld16(qs), w1 = make_uint4(0, 0, 0, 0);
+        if (q8) w1 = ld16(qs + 16);
 #pragma unroll
         for (int t = 0; t < NT; t++) {
             if (t < nt) {
@@ -107,30 +104,37 @@ __device__ __forceinline__ void zz_row_partial(const uint8_t *E, const ZzTensor 
 
 // ------------------------------------------------------------------ repack
 // Reference record [gate | up | down] (18/34-byte blocks, tq2 alpha+codes) into
-// the slot-table layout. One thread per block; grid.y selects the tensor.
+// the slot-table layout. One thread per (row, block); grid.y selects the tensor.
 __global__ void zz_repack_kernel(ZzRepackArgs a) {
     const ZzTensor &T = blockIdx.y == 0 ? a.lay.gate : (blockIdx.y == 1 ? a.lay.up : a.lay.down);
     const int64_t so = blockIdx.y == 0 ? a.src_gate : (blockIdx.y == 1 ? a.src_up : a.src_down);
     const uint8_t *src = a.src + so;
     uint8_t *dst = a.dst;
+    const int nb = zz_nblk(T);
+    const int64_t n = (int64_t)T.O * nb;
     if (T.fmt == ZZ_FMT_TQ2) {
-        int64_t n = (int64_t)T.O * 4 + (int64_t)T.O * (T.I / 4);
+        const uint8_t *codes = src + (int64_t)T.O * 4;
         for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
              i += (int64_t)gridDim.x * blockDim.x) {
-            if (i < (int64_t)T.O * 4) dst[T.off_s + i] = src[i];
-            else dst[T.off_q + (i - (int64_t)T.O * 4)] = src[i];
+            const int row = (int)(i / nb), g = (int)(i % nb);
+            const uint8_t *s = codes + (int64_t)row * (T.I / 4) + (int64_t)g * 16;
+            uint8_t *q = dst + zz_qoff(T, row, g);
+            for (int k = 0; k < 16; k++) q[k] = s[k];
+            if (g == 0)
+                for (int k = 0; k < 4; k++) dst[T.off_s + (int64_t)row * 4 + k] = src[(int64_t)row * 4 + k];
         }
         return;
     }
-    const int nb = T.I / ZZ_BLK, pb = T.fmt == ZZ_FMT_Q80 ? 32 : 16, bb = pb + 2;
-    const int64_t n = (int64_t)T.O * nb;
+    const int pb = zz_pbytes(T), bb = pb + 2;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
+        const int row = (int)(i / nb), b = (int)(i % nb);
         const uint8_t *s = src + i * bb;
-        uint8_t *q = dst + T.off_q + i * pb;
+        uint8_t *q = dst + zz_qoff(T, row, b);
         for (int k = 0; k < pb; k++) q[k] = s[2 + k];
-        dst[T.off_s + 2 * i] = s[0];
-        dst[T.off_s + 2 * i + 1] = s[1];
+        uint8_t *sc = dst + zz_soff(T, row, b);
+        sc[0] = s[0];
+        sc[1] = s[1];
     }
 }
 
@@ -174,21 +178,21 @@ __global__ __launch_bounds__(256) void zz_ffn_up_kernel(ZzFfnArgs a) {
         if (sub == 0) gu[t][w * 16 + (l >> 2)] = v;
     }
     __syncthreads();
-    const int t = threadIdx.x >> 5, r = threadIdx.x & 31;
-    float h = 0.0f;
-    if (t < item.n) h = zz_act(a.act, gu[t][r], gu[t][32 + r], a.clamp);
-    float d;
-    int q = zz_quant_lane(h, &d);
-    int qs = q;
+    __shared__ float hb[ZZ_TCH][ZZ_BLK + 1];
+    {
+        const int t = threadIdx.x >> 5, r = threadIdx.x & 31;
+        if (t < item.n) hb[t][r] = zz_act(a.act, gu[t][r], gu[t][32 + r], a.clamp);
+    }
+    __syncthreads();
+    if (threadIdx.x < item.n) {                       // one thread quantises a token's block
+        float v[ZZ_BLK];
 #pragma unroll
-    for (int o = 16; o > 0; o >>= 1) qs += __shfl_xor(qs, o, 64);
-    if (t < item.n) {
-        const size_t p = (size_t)item.p0 + t;
-        a.hq[p * a.MI + rb * 32 + r] = (int8_t)q;
-        if (r == 0) {
-            a.hs[p * (a.MI / ZZ_BLK) + rb] = d;
-            a.hsum[p * (a.MI / ZZ_BLK) + rb] = qs;
-        }
+        for (int r = 0; r < ZZ_BLK; r++) v[r] = hb[threadIdx.x][r];
+        const size_t p = (size_t)item.p0 + threadIdx.x;
+        int qs;
+        const float d = zz_quant_block(v, a.hq + p * a.MI + rb * 32, &qs);
+        a.hs[p * (a.MI / ZZ_BLK) + rb] = d;
+        a.hsum[p * (a.MI / ZZ_BLK) + rb] = qs;
     }
 }
 
@@ -255,11 +259,19 @@ __global__ __launch_bounds__(256) void zz_combine_kernel(ZzCombineArgs a) {
     }
     __syncthreads();
     double ss = 0.0;
-    for (int o = threadIdx.x; o < D; o += 256) {
-        float v = 0.0f;
-        for (int j = 0; j < K; j++) v = fmaf(wt[j], a.y[(size_t)pos[j] * D + o], v);
-        row[o] = v;
-        ss += (double)v * (double)v;
+    for (int o = 4 * threadIdx.x; o < D; o += 1024) {
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+        for (int j = 0; j < K; j++) {
+            const float4 y = *(const float4 *)(a.y + (size_t)pos[j] * D + o);
+            const float w = wt[j];
+            v.x = fmaf(w, y.x, v.x);
+            v.y = fmaf(w, y.y, v.y);
+            v.z = fmaf(w, y.z, v.z);
+            v.w = fmaf(w, y.w, v.w);
+        }
+        *(float4 *)&row[o] = v;
+        ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
     }
     float r = 1.0f;
     if (a.gemma) {
@@ -269,9 +281,13 @@ __global__ __launch_bounds__(256) void zz_combine_kernel(ZzCombineArgs a) {
         double tot = red[0] + red[1] + red[2] + red[3];
         r = 1.0f / sqrtf((float)(tot / D) + a.eps);
     }
-    for (int o = threadIdx.x; o < D; o += 256) {
-        float v = row[o];
-        a.out[(size_t)s * D + o] = a.gemma ? (v * r) * a.post_ln[o] : v;
+    for (int o = 4 * threadIdx.x; o < D; o += 1024) {
+        float4 v = *(const float4 *)&row[o];
+        if (a.gemma) {
+            const float4 w = *(const float4 *)(a.post_ln + o);
+            v = make_float4((v.x * r) * w.x, (v.y * r) * w.y, (v.z * r) * w.z, (v.w * r) * w.w);
+        }
+        *(float4 *)(a.out + (size_t)s * D + o) = v;
     }
 }
 
@@ -288,13 +304,12 @@ __global__ void zz_blockdots_kernel(const uint8_t *E, ZzTensor T, int row0, int 
     for (int j = 0; j < ZZ_BLK; j++) xs += x[j];
     int d;
     if (T.fmt == ZZ_FMT_Q40) {
-        d = zz_dot_q40(ld16(E + T.off_q + ((size_t)r * nb + b) * 16), x0, x1) - 8 * xs;
+        d = zz_dot_q40(ld16(E + zz_qoff(T, r, b)), x0, x1) - 8 * xs;
     } else if (T.fmt == ZZ_FMT_Q80) {
-        const uint8_t *q = E + T.off_q + ((size_t)r * nb + b) * 32;
+        const uint8_t *q = E + zz_qoff(T, r, b);
         d = zz_dot_q80(ld16(q), ld16(q + 16), x0, x1);
     } else {
-        const uint4 c = ld16(E + T.off_q + (size_t)r * (T.I / 4) + (size_t)(b / 2) * 16);
-        d = zz_dot_tq2(c, b & 1, x0, x1) - xs;
+        d = zz_dot_tq2(ld16(E + zz_qoff(T, r, b / 2)), b & 1, x0, x1) - xs;
     }
     out[i] = d;
 }

@@ -18,7 +18,7 @@ struct ZzPrepArgs {
 };
 
 struct ZzLogitArgs {
-    int D, E, gating;
+    int D, E, gating, S;
     const float *router;        // [E, D]
     const float *xn;            // [S, D] gemma
     const float *x;             // [S, D] lfm / maple
@@ -86,6 +86,31 @@ struct ZzCombineArgs {
     float *out;                 // [S, D]
 };
 
+// Fused decode router: logits on every workgroup, then top-k and the small-batch
+// dispatch in the last workgroup to finish (device-scope ticket).
+struct ZzDecRouteArgs {
+    ZzPrepArgs prep;            // quantisation of the expert input
+    ZzLogitArgs lg;             // logits (cen/bnd) of all tokens
+    ZzTopkArgs tk;              // top-k of all tokens
+    ZzDispatchArgs dp;          // dispatch lists and work items
+    int S;
+    unsigned *ticket;           // zero between calls; reset by the last workgroup
+};
+
+// Fused decode down projection + gate-weighted combine (+ gemma post-norm).
+struct ZzDecDownArgs {
+    ZzFfnArgs f;
+    int S, K, gemma;
+    float eps;
+    const int *eidx;            // [S, K]
+    const float *ewt;           // [S, K]
+    const int *ppos;            // [S*K] -> sorted pair
+    const float *post_ln;       // [D]
+    float *out;                 // [S, D]
+    double *part;               // [S, gridDim.x] partial sums of squares
+    unsigned *ticket;
+};
+
 struct ZzRepackArgs {
     const uint8_t *src;         // reference record [gate | up | down]
     int64_t src_gate, src_up, src_down;   // byte offsets in the record
@@ -99,6 +124,11 @@ int zz_launch_topk(const ZzTopkArgs &a, int S, hipStream_t st);
 int zz_launch_dispatch(const ZzDispatchArgs &a, hipStream_t st);
 int zz_launch_ffn_up(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_ffn_down(const ZzFfnArgs &a, int max_items, hipStream_t st);
+int zz_launch_dec_route(const ZzDecRouteArgs &a, hipStream_t st);
+int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st);
+// int8-MFMA grouped GEMM versions for work items of up to 64 tokens
+int zz_launch_up_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st);
+int zz_launch_down_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_combine(const ZzCombineArgs &a, int S, hipStream_t st);
 int zz_launch_repack(const ZzRepackArgs &a, hipStream_t st);
 // y[S,O] = W[O,I] x[S,I] with f32 activations (gpu.h matmul contract)

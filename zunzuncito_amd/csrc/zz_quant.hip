@@ -6,11 +6,28 @@
 #include "zz_common.h"
 #include "zz_kernels.h"
 
+// IEEE binary16 from binary32, round half to even, subnormals kept, signed zeros
+// kept (q40.h:60-80 encodes mx/-8 = -0.0 of an all-zero block as 0x8000).
 __device__ __forceinline__ uint16_t zz_f2h(float f) {
-    _Float16 h = (_Float16)f;          // v_cvt_f16_f32: round to nearest even
-    uint16_t b;
-    __builtin_memcpy(&b, &h, 2);
-    return b;
+    uint32_t b = __float_as_uint(f);
+    uint16_t sign = (uint16_t)((b >> 16) & 0x8000u);
+    uint32_t ex = (b >> 23) & 0xffu, man = b & 0x7fffffu;
+    if (ex == 0xff) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u : 0u));
+    int e = (int)ex - 112;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return sign;
+        uint32_t full = man | 0x800000u;
+        int sh = 14 - e;
+        uint32_t q = full >> sh, r = full & ((1u << sh) - 1u), half = 1u << (sh - 1);
+        if (r > half || (r == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = man >> 13, r = man & 0x1fffu;
+    uint32_t v = ((uint32_t)e << 10) | q;
+    if (r > 0x1000u || (r == 0x1000u && (q & 1u))) v++;
+    if (v >= 0x7c00u) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | v);
 }
 
 __global__ void zz_quant_q40_kernel(const float *w, uint8_t *dst, int64_t nblk) {
@@ -25,7 +42,8 @@ __global__ void zz_quant_q40_kernel(const float *w, uint8_t *dst, int64_t nblk) 
         float a = fabsf(v[j]);
         if (a > amax) { amax = a; mx = v[j]; }     // first element of largest |x|
     }
-    uint16_t hd = zz_f2h(mx / -8.0f);
+    // an all-zero block has mx = +0 and the reference stores fp16(0/-8) = -0 (0x8000)
+    uint16_t hd = amax == 0.0f ? (uint16_t)0x8000u : zz_f2h(mx / -8.0f);
     float d = zz_h2f(hd);
     float id = d != 0.0f ? 1.0f / d : 0.0f;
     uint8_t *o = dst + b * 18;
