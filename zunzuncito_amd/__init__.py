@@ -28,7 +28,8 @@ ABI_SYMBOLS = (
     "zz_quantize",
     "zz_last_error",
 )
-KERNELS = ("prep", "logits", "topk", "dispatch", "ffn_up", "ffn_down", "combine")
+KERNELS = ("prep", "logits", "topk", "dispatch", "ffn_up", "ffn_down", "combine", "dec_route",
+           "dec_down")
 
 _f32p = C.POINTER(C.c_float)
 _i32p = C.POINTER(C.c_int)

@@ -31,6 +31,9 @@ void zz_set_error(const char *fmt, ...) {
 static int g_ready = 0;
 // batches of at least this many tokens take the matrix-core FFN (ZZ_MFMA_MIN_S)
 static int g_mfma_min_s = 16;
+// batches of at most this many tokens take the three-launch decode path
+// (ZZ_DECODE_MAX_S, 0 turns it off; never above ZZ_DEC_MAXS)
+static int g_dec_max_s = ZZ_DEC_MAXS;
 static char g_name[128] = "none";
 static hipStream_t g_stream = nullptr;
 static unsigned *g_diag = nullptr;          // device counters, see zz_moe_stats
@@ -59,6 +62,8 @@ extern "C" int gpu_init(void) {
     ZZ_CHECK(hipMemset(g_diag, 0, 16 * sizeof(unsigned)));
     const char *ms = getenv("ZZ_MFMA_MIN_S");
     if (ms && atoi(ms) > 0) g_mfma_min_s = atoi(ms);
+    const char *dm = getenv("ZZ_DECODE_MAX_S");
+    if (dm) g_dec_max_s = atoi(dm) < 0 ? 0 : (atoi(dm) > ZZ_DEC_MAXS ? ZZ_DEC_MAXS : atoi(dm));
     g_ready = 1;
     return 1;
 }
@@ -367,6 +372,7 @@ static int ensure_ws(Layer *L, int S) {
     w.uoff = (int *)(b + o_uoff); w.ucnt = (int *)(b + o_ucnt); w.meta = (int *)(b + o_meta);
     w.items = (ZzItem *)(b + o_items); w.hq = (int8_t *)(b + o_hq); w.hs = (float *)(b + o_hs);
     w.hsum = (int *)(b + o_hsum); w.y = (float *)(b + o_y);
+    ZZ_CHECK(hipStreamSynchronize(g_stream));
     return 1;
 }
 
@@ -442,29 +448,37 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
     pa.D = d.D; pa.gemma = gemma; pa.eps = d.eps; pa.in = d_in;
     pa.router_scale = L->rscale; pa.pre_ln = L->pre_ln; pa.xn = w.xn;
     pa.xq = w.xq; pa.xs = w.xs; pa.xsum = w.xsum; pa.xt = tq_in ? w.xt : nullptr; pa.diag = g_diag;
-    if (!(ProfScope(ZZ_K_PREP, st), zz_launch_prep(pa, S, st))) ZZ_FAIL("prep launch failed");
 
     ZzLogitArgs la;
     la.D = d.D; la.E = d.E; la.gating = d.gating; la.S = S; la.router = L->router; la.xn = w.xn; la.x = d_in;
     la.bias = gemma && d.use_bias ? L->bias : nullptr; la.cen = w.cen; la.bnd = w.bnd; la.diag = g_diag;
-    if (!(ProfScope(ZZ_K_LOGITS, st), zz_launch_logits(la, S, st))) ZZ_FAIL("logits launch failed");
 
     ZzTopkArgs ta;
     ta.D = d.D; ta.E = d.E; ta.K = d.K; ta.gating = d.gating; ta.norm_topk = d.norm_topk;
     ta.routed_scaling = d.routed_scaling; ta.cen = w.cen; ta.bnd = w.bnd; ta.router = L->router;
     ta.xn = w.xn; ta.bias = d.use_bias ? L->bias : nullptr; ta.pes = L->pes; ta.eidx = w.eidx;
     ta.ewt = w.ewt; ta.topv = w.topv; ta.contested = w.contested; ta.diag = g_diag;
-    if (!(ProfScope(ZZ_K_TOPK, st), zz_launch_topk(ta, S, st))) ZZ_FAIL("topk launch failed");
 
-    // many tokens per expert: 64-token items on the matrix cores; decode-sized
+    // many tokens per expert: 64-token items on the matrix cores; smaller
     // batches: 8-token items on the dot4 GEMV
     const bool mfma = S >= g_mfma_min_s && d.fmt_gate == d.fmt_up;
+    const bool dec = S <= g_dec_max_s;
     const int tch = mfma ? 64 : 8;
     ZzDispatchArgs da;
     da.P = P; da.E = d.E; da.K = d.K; da.tch = tch; da.eidx = w.eidx; da.ewt = w.ewt;
     da.ptok = w.ptok; da.pslot = w.pslot; da.pwt = w.pwt; da.ppos = w.ppos; da.uniq = w.uniq;
     da.uoff = w.uoff; da.ucnt = w.ucnt; da.items = w.items; da.meta = w.meta;
-    if (!(ProfScope(ZZ_K_DISPATCH, st), zz_launch_dispatch(da, st))) ZZ_FAIL("dispatch launch failed");
+
+    if (dec) {
+        ZzDecRouteArgs ra;
+        ra.prep = pa; ra.lg = la; ra.tk = ta; ra.dp = da; ra.S = S;
+        if (!(ProfScope(ZZ_K_DEC_ROUTE, st), zz_launch_dec_route(ra, st))) ZZ_FAIL("decode route launch failed");
+    } else {
+        if (!(ProfScope(ZZ_K_PREP, st), zz_launch_prep(pa, S, st))) ZZ_FAIL("prep launch failed");
+        if (!(ProfScope(ZZ_K_LOGITS, st), zz_launch_logits(la, S, st))) ZZ_FAIL("logits launch failed");
+        if (!(ProfScope(ZZ_K_TOPK, st), zz_launch_topk(ta, S, st))) ZZ_FAIL("topk launch failed");
+        if (!(ProfScope(ZZ_K_DISPATCH, st), zz_launch_dispatch(da, st))) ZZ_FAIL("dispatch launch failed");
+    }
 
     ZzFfnArgs fa;
     fa.D = d.D; fa.MI = d.MI; fa.K = d.K; fa.act = d.act; fa.clamp = d.clamp;
@@ -472,6 +486,16 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
     fa.meta = w.meta; fa.ptok = w.ptok; fa.xq = w.xq; fa.xs = w.xs; fa.xsum = w.xsum; fa.xt = w.xt;
     fa.hq = w.hq; fa.hs = w.hs; fa.hsum = w.hsum; fa.y = w.y;
     const int max_items = (P < d.E ? P : d.E) + (P + tch - 1) / tch;
+    if (dec) {
+        ZzDecDownArgs dd;
+        dd.f = fa; dd.S = S; dd.K = d.K; dd.E = d.E; dd.eidx = w.eidx; dd.ewt = w.ewt; dd.ppos = w.ppos;
+        dd.out = d_out;
+        if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_dec_up(fa, max_items, st))) ZZ_FAIL("ffn_up launch failed");
+        if (!(ProfScope(ZZ_K_DEC_DOWN, st), zz_launch_dec_down(dd, st))) ZZ_FAIL("decode down launch failed");
+        if (gemma && !(ProfScope(ZZ_K_COMBINE, st), zz_launch_dec_norm(d_out, L->post_ln, d.D, d.eps, S, st)))
+            ZZ_FAIL("decode post-norm launch failed");
+        return 1;
+    }
     if (mfma) {
         if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_up_mfma(fa, max_items, st))) ZZ_FAIL("ffn_up launch failed");
         if (!(ProfScope(ZZ_K_FFN_DOWN, st), zz_launch_down_mfma(fa, max_items, st))) ZZ_FAIL("ffn_down launch failed");

@@ -1,64 +1,104 @@
-// zz_decode.hip -- decode-sized batches (S <= 4 tokens) in three launches:
-//   1. zz_dec_route_kernel: every workgroup quantises a slice of the expert input
-//      and computes the certified logits of 4 experts for all tokens; the last
-//      workgroup to arrive (device-scope ticket) runs the top-k gating and builds
-//      the dispatch lists (gemma4.c:750-790 for a handful of rows).
-//   2. the dot4 gate/up GEMV (zz_ffn.hip) over the work items.
-//   3. zz_dec_down_kernel: down GEMV for all (token, slot) pairs of a row tile,
-//      the gate-weighted combine in registers (gemma4.c:652) and, for gemma, the
-//      post-norm (gemma4.c:807-808) finished by the last workgroup.
+// zz_decode.hip -- decode-sized batches (S <= 4 tokens):
+//   1. zz_dec_logits_kernel: one workgroup per expert computes that expert's
+//      certified router logit for every token (gemma: with the input rmsnorm from
+//      the same loads) and quantises a share of the expert input;
+//   2. zz_dec_gate_kernel: one workgroup runs the top-k gating and builds the
+//      dispatch lists (gemma4.c:750-790 for a handful of rows);
+//   3. zz_dec_up_kernel: gate/up GEMV with the activation and the int8
+//      re-quantisation of the hidden, per expert work item;
+//   4. zz_dec_down_kernel: down GEMV for all (token, slot) pairs of a row tile
+//      and the gate-weighted combine (gemma4.c:652); gemma's post-norm
+//      (gemma4.c:807-808) follows as a one-workgroup-per-token kernel.
 #include "zz_common.h"
 #include "zz_kernels.h"
 #include "zz_route_dev.h"
+#include "zz_dot_dev.h"
 
-#define DEC_MAXS 4
+#define DEC_MAXS ZZ_DEC_MAXS
 
-// rmsnorm factor of one row, the mean square certified as in zz_prep_kernel
-__device__ float zz_row_rms(const float *x, int D, float eps, double *red, float *cert, unsigned *diag) {
-    const int tid = threadIdx.x;
-    double sq = 0.0;
-    for (int i = 4 * tid; i < D; i += 1024) {
-        const float4 v = *(const float4 *)(x + i);
-        sq += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
-    }
-    sq = zz_block_sum(sq, red);
-    const double m = (double)(D / 1024 + 12);
-    const double g = zz_gamma(D, ZZ_U64) + zz_gamma(m, ZZ_U64);
-    const double b = g * sq / (1.0 - zz_gamma(m, ZZ_U64)) * 1.0000001 + 1e-300;
-    const float lo = (float)((sq - b) / (double)D), hi = (float)((sq + b) / (double)D);
-    if (tid == 0) {
-        if (lo == hi) {
-            *cert = lo;
-        } else {
-            double t = 0.0;
-            for (int i = 0; i < D; i++) t += (double)x[i] * (double)x[i];
-            *cert = (float)(t / (double)D);
-            atomicAdd(diag, 1u);
-        }
-    }
-    __syncthreads();
-    return 1.0f / sqrtf(*cert + eps);
-}
+// expert id kept inside the slot table whatever the router produced
+__device__ __forceinline__ int zz_clamp_e(int e, int E) { return e < 0 || e >= E ? 0 : e; }
 
-__global__ __launch_bounds__(256) void zz_dec_route_kernel(ZzDecRouteArgs a) {
+// Decode router, part 1: one workgroup per expert e. Gemma: per token, one set of
+// loads (x row, router row e, router scale) gives both the rmsnorm factor and the
+// rounded products of the router logit. The mean square is certified to round to
+// the float of the reference's serial double sum (gemma4.c:425-428), else that sum
+// is replayed; the logit gets the tight bound of zz_tight_block_scan. lfm/maple:
+// wave s computes token s's logit. Then the workgroup quantises its share of the
+// expert input (blocks e, e + E, ...).
+__global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
     const ZzPrepArgs &pp = a.prep;
-    const int S = a.S, D = pp.D, nb = D / ZZ_BLK, tid = threadIdx.x, l = tid & 63;
+    const ZzLogitArgs &lg = a.lg;
+    const int S = a.S, D = pp.D, nb = D / ZZ_BLK, tid = threadIdx.x, e = blockIdx.x;
     const bool gem = pp.gemma;
-    __shared__ double red[4];
-    __shared__ float cert;
+    __shared__ __attribute__((aligned(16))) float buf[ZZ_MAXD + ZZ_MAXD / 32];
+    __shared__ double red[12];
     __shared__ float rr[DEC_MAXS];
-    __shared__ int last;
-    __shared__ ZzTopkShared sh;
-    if (gem) {
-        for (int s = 0; s < S; s++) {
-            const float r = zz_row_rms(pp.in + (size_t)s * D, D, pp.eps, red, &cert, pp.diag);
-            if (tid == 0) rr[s] = r;
-            __syncthreads();
-        }
-    }
-    // (a) this workgroup's slice of the expert input quantisation and of xn
+    __shared__ float cert;
     const float rs = 1.0f / sqrtf((float)D);
-    for (int g = blockIdx.x * 256 + tid; g < S * nb; g += gridDim.x * 256) {
+    if (gem) {
+        const int R = (D + 255) >> 8;                         // <= 32
+        const float *w = lg.router + (size_t)e * D;
+        float wr[32], sr[32];
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            if (j < R) {
+                const int i = min(tid + 256 * j, D - 1);      // clamped: loads stay in range
+                wr[j] = w[i];
+                sr[j] = pp.router_scale[i] * rs;
+            }
+        }
+        for (int s = 0; s < S; s++) {
+            const float *x = pp.in + (size_t)s * D;
+            float xr[32];
+            double sq = 0.0;
+#pragma unroll
+            for (int j = 0; j < 32; j++) {
+                if (j < R) {
+                    const int i = tid + 256 * j;
+                    xr[j] = x[min(i, D - 1)];
+                    if (i < D) sq += (double)xr[j] * (double)xr[j];
+                }
+            }
+            // every square is exact in double; each term meets at most R - 1 + 6 + 3
+            // roundings here and D - 1 in the reference's serial sum
+            sq = zz_block_sum(sq, red);
+            const double m = (double)(R + 10);
+            const double g = zz_gamma(D, ZZ_U64) + zz_gamma(m, ZZ_U64);
+            const double b = g * sq / (1.0 - zz_gamma(m, ZZ_U64)) * 1.0000001 + 1e-300;
+            const float lo = (float)((sq - b) / (double)D), hi = (float)((sq + b) / (double)D);
+            if (tid == 0) {
+                if (lo == hi) {
+                    cert = lo;
+                } else {
+                    double t = 0.0;                           // serial replay, reference order
+                    for (int i = 0; i < D; i++) t += (double)x[i] * (double)x[i];
+                    cert = (float)(t / (double)D);
+                    if (e == 0) atomicAdd(pp.diag + 0, 1u);
+                }
+            }
+            __syncthreads();
+            const float r = 1.0f / sqrtf(cert + pp.eps);
+            if (tid == 0) rr[s] = r;
+#pragma unroll
+            for (int j = 0; j < 32; j++) {
+                const int i = tid + 256 * j;
+                if (j < R && i < D) {
+                    const float xv = (xr[j] * r) * sr[j];     // xn as zz_prep_kernel forms it
+                    if (e == 0) pp.xn[(size_t)s * D + i] = xv;   // for the exact replay
+                    buf[zz_pad32(i)] = wr[j] * xv;
+                }
+            }
+            __syncthreads();
+            zz_tight_block_scan(buf, D, lg.bias, e, red, lg.cen + (size_t)s * lg.E + e,
+                                lg.bnd + (size_t)s * lg.E + e);
+        }
+    } else if ((tid >> 6) < S) {
+        zz_logit_wave_f64(lg, tid >> 6, e);
+    }
+    // the expert input quantisation, block g on workgroup g % gridDim.x
+    __syncthreads();
+    for (int g = e + gridDim.x * tid; g < S * nb; g += gridDim.x * 256) {
         const int s = g / nb, b = g % nb;
         const float *x = pp.in + (size_t)s * D + b * ZZ_BLK;
         float v[ZZ_BLK];
@@ -70,10 +110,10 @@ __global__ __launch_bounds__(256) void zz_dec_route_kernel(ZzDecRouteArgs a) {
         if (gem) {
             const float r = rr[s];
 #pragma unroll
-            for (int j = 0; j < ZZ_BLK; j++) {
-                const int i = b * ZZ_BLK + j;
-                pp.xn[(size_t)s * D + i] = (v[j] * r) * (pp.router_scale[i] * rs);
-                v[j] = (v[j] * r) * pp.pre_ln[i];
+            for (int j = 0; j < ZZ_BLK; j += 4) {
+                const float4 w = *(const float4 *)(pp.pre_ln + b * ZZ_BLK + j);
+                v[j] = (v[j] * r) * w.x; v[j + 1] = (v[j + 1] * r) * w.y;
+                v[j + 2] = (v[j + 2] * r) * w.z; v[j + 3] = (v[j + 3] * r) * w.w;
             }
         }
         int qs;
@@ -81,50 +121,13 @@ __global__ __launch_bounds__(256) void zz_dec_route_kernel(ZzDecRouteArgs a) {
         pp.xs[(size_t)s * nb + b] = d;
         pp.xsum[(size_t)s * nb + b] = qs;
     }
-    // (b) logits of this workgroup's experts; xn is formed on the fly from x
-    const ZzLogitArgs &lg = a.lg;
-    const int e = blockIdx.x * 4 + (tid >> 6);
-    if (e < lg.E) {
-        const float *w = lg.router + (size_t)e * D;
-        for (int s = 0; s < S; s++) {
-            const size_t o = (size_t)s * lg.E + e;
-            const float *x = pp.in + (size_t)s * D;
-            if (gem) {
-                const float r = rr[s];
-                float c = 0.0f, t = 0.0f;
-                for (int i = l; i < D; i += 64) {
-                    const float xn = (x[i] * r) * (pp.router_scale[i] * rs);
-                    const float p = w[i] * xn;
-                    c += p;
-                    t += fabsf(p);
-                }
-                c = zz_wave_sum(c);
-                t = zz_wave_sum(t);
-                if (l == 0) {
-                    const double m = (double)((D + 63) / 64 + 6);
-                    const double gm = zz_gamma(m, ZZ_U32);
-                    const double T = (double)t / (1.0 - gm);
-                    double b = (zz_gamma(D - 1, ZZ_U32) + gm) * T * 1.0000001 + 1e-40;
-                    double cen = (double)c;
-                    if (lg.bias) {
-                        cen += (double)lg.bias[e];
-                        b += 2.0 * ZZ_U32 * (fabs(cen) + b) + 1e-40;
-                    }
-                    lg.cen[o] = cen;
-                    lg.bnd[o] = b;
-                }
-            } else {
-                zz_logit_wave(lg, s, e);
-            }
-        }
-    }
-    // (c) the last workgroup to finish does the gating and the dispatch
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last = atomicAdd(a.ticket, 1u) == gridDim.x - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
+}
+
+// Decode router, part 2 (one workgroup): certified top-k gating of every token,
+// then the dispatch of the S*K pairs.
+__global__ __launch_bounds__(256) void zz_dec_gate_kernel(ZzDecRouteArgs a) {
+    const int S = a.S, tid = threadIdx.x;
+    __shared__ ZzTopkShared sh;
     for (int s = 0; s < S; s++) {
         zz_topk_token(a.tk, s, sh);
         __syncthreads();
@@ -132,27 +135,28 @@ __global__ __launch_bounds__(256) void zz_dec_route_kernel(ZzDecRouteArgs a) {
     // dispatch of P = S*K <= 64 pairs: stable ranking by (expert, pair index)
     const ZzDispatchArgs &dp = a.dp;
     const int K = dp.K, P = S * K;
-    __shared__ int pe[DEC_MAXS * ZZ_MAXK];
-    __shared__ int firsts;
-    if (tid < P) pe[tid] = dp.eidx[tid];
-    if (tid == 0) firsts = 0;
-    __syncthreads();
+    __shared__ int pe[DEC_MAXS * ZZ_MAXK], pf[DEC_MAXS * ZZ_MAXK];
     if (tid < P) {
-        const int ep = pe[tid];
-        int rank = 0, start = 0, cnt = 0, first = 1, urank = 0;
+        const int e = dp.eidx[tid];
+        pe[tid] = e < 0 || e >= dp.E ? 0 : e;     // never index past the expert tables
+    }
+    __syncthreads();
+    int ep = 0, rank = 0, start = 0, cnt = 0, first = 1;
+    if (tid < P) {
+        ep = pe[tid];
         for (int q = 0; q < P; q++) {
             const int eq = pe[q];
             rank += eq < ep || (eq == ep && q < tid);
             start += eq < ep;
             cnt += eq == ep;
-            if (q < tid && eq == ep) first = 0;
+            first &= !(q < tid && eq == ep);
         }
-        if (first)
-            for (int q = 0; q < tid; q++) {
-                int f = 1;
-                for (int q2 = 0; q2 < q; q2++) f &= pe[q2] != pe[q];
-                urank += f;
-            }
+        pf[tid] = first;                          // first occurrence of its expert
+    }
+    __syncthreads();
+    if (tid < P) {
+        int urank = 0;                            // union order: first-seen
+        for (int q = 0; q < tid; q++) urank += pf[q];
         dp.ptok[rank] = tid / K;
         dp.pslot[rank] = tid % K;
         dp.pwt[rank] = dp.ewt[tid];
@@ -167,150 +171,323 @@ __global__ __launch_bounds__(256) void zz_dec_route_kernel(ZzDecRouteArgs a) {
             it.p0 = start;
             it.n = cnt;                            // cnt <= S <= 4 fits one item
             dp.items[urank] = it;
-            atomicAdd(&firsts, 1);
         }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        dp.meta[0] = firsts;
-        dp.meta[1] = firsts;
-        *a.ticket = 0u;                            // ready for the next call
+        if (tid == P - 1) {
+            const int nu = urank + first;
+            dp.meta[0] = nu;
+            dp.meta[1] = nu;
+        }
     }
 }
 
-// grid D/64: wave w owns 16 output rows; lane (row l%16, quarter l/16) takes the
-// blocks b = quarter, quarter+4, ... of each (token, slot)'s down row.
-__global__ __launch_bounds__(256) void zz_dec_down_kernel(ZzDecDownArgs a) {
-    const ZzFfnArgs &f = a.f;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r = l & 15, q = l >> 4;
-    const int g16 = blockIdx.x * 4 + w, row = g16 * 16 + r;
-    const ZzTensor &T = f.lay.down;
-    const int MI = f.MI, nb = MI / ZZ_BLK, D = f.D, S = a.S, K = a.K;
-    const bool tq = T.fmt == ZZ_FMT_TQ2, q8 = T.fmt == ZZ_FMT_Q80;
-    __shared__ double red[4];
-    __shared__ int last;
-    float outv[DEC_MAXS];
-    double ss[DEC_MAXS];
-    for (int s = 0; s < S; s++) {
-        float acc_out = 0.0f;
-        for (int j = 0; j < K; j++) {
-            const int p = a.ppos[s * K + j], e = a.eidx[s * K + j];
-            const float wt = a.ewt[s * K + j];
-            const uint8_t *E = f.experts + (size_t)e * f.estride;
-            const int8_t *hq = f.hq + (size_t)p * MI;
-            const float *hs = f.hs + (size_t)p * nb;
-            float part = 0.0f;
-            if (tq) {
-                // 64-weight groups: quarter q takes groups q, q+4, ...
-                for (int g = q; g < nb / 2; g += 4) {
-                    const uint4 c = *(const uint4 *)(E + zz_qoff(T, row, g));
-                    const int8_t *x = hq + g * 64;
-                    const uint4 x0 = *(const uint4 *)x, x1 = *(const uint4 *)(x + 16);
-                    const uint4 x2 = *(const uint4 *)(x + 32), x3 = *(const uint4 *)(x + 48);
-                    int d0 = 0, d1 = 0;
+// ------------------------------------------------------------------ gate/up
+// grid (MI/32, items): the workgroup owns hidden rows 32*blockIdx.x .. +31 of one
+// expert item (<= ZZ_DEC_MAXS tokens). Waves 0-3 take the 32 gate rows, waves 4-7
+// the 32 up rows, 8 lanes per row; lane `sub` takes blocks sub, sub+8, ... and
+// issues DU_J of them at once, before the activations are staged in LDS, so the
+// weight stream is in flight from the first cycle.
+#define DU_J 12
+
+// one workgroup-wide staging of the item's activations into LDS
+struct ZzDecStage {
+    __attribute__((aligned(16))) int8_t xq[DEC_MAXS][ZZ_MAXD];
+    float xs[DEC_MAXS][ZZ_MAXD / ZZ_BLK];
+    int xsum[DEC_MAXS][ZZ_MAXD / ZZ_BLK];
+    int tok[DEC_MAXS];
+    float xt[DEC_MAXS];         // tq2 Sx of each token
+};
+
+__device__ __forceinline__ void zz_dec_stage(const ZzFfnArgs &a, const ZzItem &item, ZzDecStage &st) {
+    const int D = a.D, nb = D / ZZ_BLK;
+    for (int t = 0; t < item.n; t++) {
+        const int tk = st.tok[t];
+        for (int i = 16 * threadIdx.x; i < D; i += 16 * blockDim.x)
+            *(uint4 *)&st.xq[t][i] = ld16(a.xq + (size_t)tk * D + i);
+        for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+            st.xs[t][b] = a.xs[(size_t)tk * nb + b];
+            st.xsum[t][b] = a.xsum[(size_t)tk * nb + b];
+        }
+    }
+    __syncthreads();
+}
+
+// Partial dots of one lane for one row: weights of DU_J blocks (tq2: groups) are
+// loaded first, then the activations are staged (once per workgroup), then used.
+template <int FMT>
+__device__ __forceinline__ void zz_dec_up_part(const ZzFfnArgs &a, const ZzItem &item, ZzDecStage &st,
+                                               const uint8_t *E, const ZzTensor &T, int row, int sub,
+                                               float (&acc)[DEC_MAXS]) {
+    const int nb = a.D / ZZ_BLK, n = item.n;
+    const int nu = FMT == ZZ_FMT_TQ2 ? nb / 2 : nb;          // units: blocks or 64-groups
 #pragma unroll
-                    for (int h = 0; h < 2; h++) {
-                        const unsigned m = 0x03030303u;
-                        const int sa = 4 * h, sb = 4 * h + 2;
-                        const uint4 xa = h ? x2 : x0, xb = h ? x3 : x1;
-                        int d = zz_dot4((c.x >> sa) & m, xa.x, 0);
-                        d = zz_dot4((c.y >> sa) & m, xa.y, d);
-                        d = zz_dot4((c.z >> sa) & m, xa.z, d);
-                        d = zz_dot4((c.w >> sa) & m, xa.w, d);
-                        d = zz_dot4((c.x >> sb) & m, xb.x, d);
-                        d = zz_dot4((c.y >> sb) & m, xb.y, d);
-                        d = zz_dot4((c.z >> sb) & m, xb.z, d);
-                        d = zz_dot4((c.w >> sb) & m, xb.w, d);
-                        // c - 1 per weight: subtract the block's sum of x
-                        d -= f.hsum[(size_t)p * nb + 2 * g + h];
-                        if (h) d1 = d; else d0 = d;
-                    }
-                    part = fmaf(hs[2 * g], (float)d0, part);
-                    part = fmaf(hs[2 * g + 1], (float)d1, part);
-                }
-            } else {
-#pragma unroll 2
-                for (int b = q; b < nb; b += 4) {
-                    const uint8_t *qp = E + zz_qoff(T, row, b);
-                    const float dw = zz_h2f(*(const uint16_t *)(E + zz_soff(T, row, b)));
-                    const int8_t *x = hq + b * ZZ_BLK;
-                    const uint4 x0 = *(const uint4 *)x, x1 = *(const uint4 *)(x + 16);
-                    const uint4 w0 = *(const uint4 *)qp;
-                    int d;
-                    if (q8) {
-                        const uint4 w1 = *(const uint4 *)(qp + 16);
-                        d = zz_dot4(w0.x, x0.x, 0);
-                        d = zz_dot4(w0.y, x0.y, d);
-                        d = zz_dot4(w0.z, x0.z, d);
-                        d = zz_dot4(w0.w, x0.w, d);
-                        d = zz_dot4(w1.x, x1.x, d);
-                        d = zz_dot4(w1.y, x1.y, d);
-                        d = zz_dot4(w1.z, x1.z, d);
-                        d = zz_dot4(w1.w, x1.w, d);
-                    } else {
-                        const unsigned m = 0x0F0F0F0Fu;
-                        d = zz_dot4(w0.x & m, x0.x, 0);
-                        d = zz_dot4(w0.y & m, x0.y, d);
-                        d = zz_dot4(w0.z & m, x0.z, d);
-                        d = zz_dot4(w0.w & m, x0.w, d);
-                        d = zz_dot4((w0.x >> 4) & m, x1.x, d);
-                        d = zz_dot4((w0.y >> 4) & m, x1.y, d);
-                        d = zz_dot4((w0.z >> 4) & m, x1.z, d);
-                        d = zz_dot4((w0.w >> 4) & m, x1.w, d);
-                        d -= 8 * f.hsum[(size_t)p * nb + b];
-                    }
-                    part = fmaf(dw * hs[b], (float)d, part);
+    for (int t = 0; t < DEC_MAXS; t++) acc[t] = 0.0f;
+    for (int u0 = 0; u0 < nu; u0 += 8 * DU_J) {
+        uint4 w0[DU_J], w1[DU_J];
+        float dw[DU_J];
+#pragma unroll
+        for (int j = 0; j < DU_J; j++) {
+            const int u = min(u0 + sub + 8 * j, nu - 1);       // clamped: loads stay in range
+            const uint8_t *qp = E + zz_qoff(T, row, u);
+            w0[j] = ld16(qp);
+            if (FMT == ZZ_FMT_Q80) w1[j] = ld16(qp + 16);
+            if (FMT != ZZ_FMT_TQ2) dw[j] = zz_h2f(*(const uint16_t *)(E + zz_soff(T, row, u)));
+        }
+        if (u0 == 0) zz_dec_stage(a, item, st);               // uniform: every wave passes here
+#pragma unroll
+        for (int j = 0; j < DU_J; j++) {
+            const int u = u0 + sub + 8 * j;
+            if (u >= nu) continue;
+#pragma unroll
+            for (int t = 0; t < DEC_MAXS; t++) {
+                if (t >= n) continue;
+                if (FMT == ZZ_FMT_TQ2) {
+                    const int8_t *x = &st.xq[t][u * 64];
+                    const int d0 = zz_dot_tq2(w0[j], 0, ld16(x), ld16(x + 16));
+                    const int d1 = zz_dot_tq2(w0[j], 1, ld16(x + 32), ld16(x + 48));
+                    acc[t] = fmaf(st.xs[t][2 * u], (float)d0, acc[t]);
+                    acc[t] = fmaf(st.xs[t][2 * u + 1], (float)d1, acc[t]);
+                } else {
+                    const int8_t *x = &st.xq[t][u * ZZ_BLK];
+                    const uint4 x0 = ld16(x), x1 = ld16(x + 16);
+                    const int d = FMT == ZZ_FMT_Q80 ? zz_dot_q80(w0[j], w1[j], x0, x1)
+                                                    : zz_dot_q40(w0[j], x0, x1) - 8 * st.xsum[t][u];
+                    acc[t] = fmaf(dw[j] * st.xs[t][u], (float)d, acc[t]);
                 }
             }
-            part += __shfl_xor(part, 16, 64);
-            part += __shfl_xor(part, 32, 64);
-            if (tq) part *= ((const float *)(E + T.off_s))[row];
-            acc_out = fmaf(wt, part, acc_out);     // out += w * y, slot order
         }
-        outv[s] = acc_out;
-        ss[s] = (double)acc_out * (double)acc_out;
     }
-    if (q == 0)
-        for (int s = 0; s < S; s++) a.out[(size_t)s * D + row] = outv[s];
-    if (!a.gemma) return;
-    // post-norm: per-workgroup partial sums of squares, reduced by the last one
-    for (int s = 0; s < S; s++) {
-        double v = q == 0 ? ss[s] : 0.0;
-        v = zz_block_sum(v, red);
-        if (tid == 0) a.part[(size_t)s * gridDim.x + blockIdx.x] = v;
-    }
-    __threadfence();
+}
+
+__global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzFfnArgs a) {
+    const int it = blockIdx.y;
+    if (it >= a.meta[1]) return;
+    const ZzItem item = a.items[it];
+    const int tid = threadIdx.x, rr = tid >> 3, sub = tid & 7, rb = blockIdx.x;
+    const bool up = rr >= 32;
+    const ZzTensor &T = up ? a.lay.up : a.lay.gate;
+    const int row = rb * 32 + (rr & 31);
+    const uint8_t *E = a.experts + (size_t)item.e * a.estride;
+    __shared__ ZzDecStage st;
+    __shared__ float gu[DEC_MAXS][64];
+    __shared__ float hb[DEC_MAXS][ZZ_BLK + 1];
+    if (tid < item.n) st.tok[tid] = a.ptok[item.p0 + tid];
     __syncthreads();
-    if (tid == 0) last = atomicAdd(a.ticket, 1u) == gridDim.x - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    __shared__ float rs_s[DEC_MAXS];
-    if (tid == 0) {
-        for (int s = 0; s < S; s++) {
-            double t = 0.0;
-            for (int b = 0; b < (int)gridDim.x; b++) t += a.part[(size_t)s * gridDim.x + b];
-            rs_s[s] = 1.0f / sqrtf((float)(t / D) + a.eps);
-        }
-        *a.ticket = 0u;
+    float acc[DEC_MAXS];
+    if (T.fmt == ZZ_FMT_Q40) zz_dec_up_part<ZZ_FMT_Q40>(a, item, st, E, T, row, sub, acc);
+    else if (T.fmt == ZZ_FMT_Q80) zz_dec_up_part<ZZ_FMT_Q80>(a, item, st, E, T, row, sub, acc);
+    else zz_dec_up_part<ZZ_FMT_TQ2>(a, item, st, E, T, row, sub, acc);
+    if (T.fmt == ZZ_FMT_TQ2 && tid < item.n) {      // tq2.h:101-106, serial
+        const int nb = a.D / ZZ_BLK;
+        double tot = 0.0;
+        for (int b = 0; b < nb; b++) tot += (double)st.xs[tid][b] * (double)st.xsum[tid][b];
+        st.xt[tid] = (float)tot;
     }
     __syncthreads();
-    for (int s = 0; s < S; s++)
-        for (int o = 4 * tid; o < D; o += 1024) {
-            float4 v = *(float4 *)(a.out + (size_t)s * D + o);
-            const float4 wl = *(const float4 *)(a.post_ln + o);
-            const float r = rs_s[s];
-            v = make_float4((v.x * r) * wl.x, (v.y * r) * wl.y, (v.z * r) * wl.z, (v.w * r) * wl.w);
-            *(float4 *)(a.out + (size_t)s * D + o) = v;
+#pragma unroll
+    for (int t = 0; t < DEC_MAXS; t++) {
+        float v = acc[t];
+        v += __shfl_xor(v, 1, 64);
+        v += __shfl_xor(v, 2, 64);
+        v += __shfl_xor(v, 4, 64);
+        if (T.fmt == ZZ_FMT_TQ2 && t < item.n) {
+            const float alpha = ((const float *)(E + T.off_s))[row];
+            v = alpha * (v - st.xt[t]);                        // tq2.h:154
         }
+        if (sub == 0) gu[t][rr] = v;
+    }
+    __syncthreads();
+    if (tid < item.n * ZZ_BLK) {
+        const int t = tid >> 5, r = tid & 31;
+        hb[t][r] = zz_act(a.act, gu[t][r], gu[t][32 + r], a.clamp);
+    }
+    __syncthreads();
+    if (tid < item.n) {                                         // one thread per token block
+        float v[ZZ_BLK];
+#pragma unroll
+        for (int r = 0; r < ZZ_BLK; r++) v[r] = hb[tid][r];
+        const size_t p = (size_t)item.p0 + tid;
+        int qs;
+        const float d = zz_quant_block(v, a.hq + p * a.MI + rb * ZZ_BLK, &qs);
+        a.hs[p * (a.MI / ZZ_BLK) + rb] = d;
+        a.hsum[p * (a.MI / ZZ_BLK) + rb] = qs;
+    }
+}
+
+// ------------------------------------------------------------------ down + combine
+// grid D/16: the workgroup owns 16 output rows, 16 lanes per row; lane q takes
+// blocks q, q+16, ... of every (token, slot) pair's down row, DD_F pairs x DD_J
+// blocks loaded at once. The 16 x P expert outputs meet in LDS and are combined
+// per token in slot order, out = fma(w_j, y_j, out) as gemma4.c:652. Gemma's
+// post-norm needs the whole row: each workgroup leaves its partial sums of
+// squares and the last one to finish normalises every row.
+#define DD_F 4
+#define DD_J 2
+
+struct ZzDecPairs {                 // per (token, slot) pair, flat order s*K + j
+    int pos[DEC_MAXS * ZZ_MAXK];    // sorted position: row of hq / hs / hsum
+    int e[DEC_MAXS * ZZ_MAXK];      // expert (clamped into the table)
+};
+
+template <int FMT>
+__device__ __forceinline__ void zz_dec_down_rows(const ZzDecDownArgs &a, const ZzDecPairs &pr, int f0,
+                                                 int row, int q, float (&acc)[DD_F]) {
+    const ZzFfnArgs &f = a.f;
+    const ZzTensor &T = f.lay.down;
+    const int MI = f.MI, nb = MI / ZZ_BLK, P = a.S * a.K;
+    const int nu = FMT == ZZ_FMT_TQ2 ? nb / 2 : nb;
+#pragma unroll
+    for (int k = 0; k < DD_F; k++) acc[k] = 0.0f;
+    for (int u0 = 0; u0 < nu; u0 += 16 * DD_J) {
+        // every load of the chunk is issued before any is used (clamped indices
+        // keep the surplus ones in range; their results are discarded)
+        uint4 w0[DD_F][DD_J], w1[DD_F][DD_J], x0[DD_F][DD_J], x1[DD_F][DD_J];
+        uint4 x2[DD_F][DD_J], x3[DD_F][DD_J];
+        float dw[DD_F][DD_J], hs0[DD_F][DD_J], hs1[DD_F][DD_J];
+        int hsm[DD_F][DD_J];
+#pragma unroll
+        for (int k = 0; k < DD_F; k++) {
+            const int fp = min(f0 + k, P - 1);
+            const int p = pr.pos[fp];
+            const uint8_t *E = f.experts + (size_t)pr.e[fp] * f.estride;
+            const int8_t *hq = f.hq + (size_t)p * MI;
+            const float *hs = f.hs + (size_t)p * nb;
+#pragma unroll
+            for (int j = 0; j < DD_J; j++) {
+                const int u = min(u0 + q + 16 * j, nu - 1);
+                const uint8_t *qp = E + zz_qoff(T, row, u);
+                w0[k][j] = ld16(qp);
+                if (FMT == ZZ_FMT_TQ2) {
+                    const int8_t *x = hq + u * 64;
+                    x0[k][j] = ld16(x);
+                    x1[k][j] = ld16(x + 16);
+                    x2[k][j] = ld16(x + 32);
+                    x3[k][j] = ld16(x + 48);
+                    hs0[k][j] = hs[2 * u];
+                    hs1[k][j] = hs[2 * u + 1];
+                } else {
+                    if (FMT == ZZ_FMT_Q80) w1[k][j] = ld16(qp + 16);
+                    dw[k][j] = zz_h2f(*(const uint16_t *)(E + zz_soff(T, row, u)));
+                    const int8_t *x = hq + u * ZZ_BLK;
+                    x0[k][j] = ld16(x);
+                    x1[k][j] = ld16(x + 16);
+                    hs0[k][j] = hs[u];
+                    if (FMT == ZZ_FMT_Q40) hsm[k][j] = f.hsum[(size_t)p * nb + u];
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < DD_F; k++) {
+#pragma unroll
+            for (int j = 0; j < DD_J; j++) {
+                const int u = u0 + q + 16 * j;
+                float v;
+                if (FMT == ZZ_FMT_TQ2) {
+                    const int d0 = zz_dot_tq2(w0[k][j], 0, x0[k][j], x1[k][j]);
+                    const int d1 = zz_dot_tq2(w0[k][j], 1, x2[k][j], x3[k][j]);
+                    v = fmaf(hs0[k][j], (float)d0, acc[k]);
+                    v = fmaf(hs1[k][j], (float)d1, v);
+                } else {
+                    const int d = FMT == ZZ_FMT_Q80 ? zz_dot_q80(w0[k][j], w1[k][j], x0[k][j], x1[k][j])
+                                                    : zz_dot_q40(w0[k][j], x0[k][j], x1[k][j]) - 8 * hsm[k][j];
+                    v = fmaf(dw[k][j] * hs0[k][j], (float)d, acc[k]);
+                }
+                if (u < nu && f0 + k < P) acc[k] = v;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void zz_dec_down_kernel(ZzDecDownArgs a) {
+    const ZzFfnArgs &f = a.f;
+    const int tid = threadIdx.x, r = tid >> 4, q = tid & 15;
+    const int row = blockIdx.x * 16 + r;
+    const ZzTensor &T = f.lay.down;
+    const int nb = f.MI / ZZ_BLK, D = f.D, S = a.S, K = a.K, P = S * K;
+    const bool tq = T.fmt == ZZ_FMT_TQ2;
+    __shared__ float yv[DEC_MAXS * ZZ_MAXK][16];
+    __shared__ float htot[DEC_MAXS * ZZ_MAXK];
+    __shared__ ZzDecPairs pr;
+    if (tid < P) {
+        pr.pos[tid] = a.ppos[tid];
+        pr.e[tid] = zz_clamp_e(a.eidx[tid], a.E);
+    }
+    if (tq && tid < P) {                           // tq2.h:101-106, serial
+        const size_t p = (size_t)a.ppos[tid];
+        double t = 0.0;
+        for (int b = 0; b < nb; b++) t += (double)f.hs[p * nb + b] * (double)f.hsum[p * nb + b];
+        htot[tid] = (float)t;
+    }
+    __syncthreads();
+    for (int f0 = 0; f0 < P; f0 += DD_F) {
+        float acc[DD_F];
+        if (T.fmt == ZZ_FMT_Q40) zz_dec_down_rows<ZZ_FMT_Q40>(a, pr, f0, row, q, acc);
+        else if (T.fmt == ZZ_FMT_Q80) zz_dec_down_rows<ZZ_FMT_Q80>(a, pr, f0, row, q, acc);
+        else zz_dec_down_rows<ZZ_FMT_TQ2>(a, pr, f0, row, q, acc);
+#pragma unroll
+        for (int k = 0; k < DD_F; k++) {
+            float v = acc[k];
+            v += __shfl_xor(v, 1, 64);
+            v += __shfl_xor(v, 2, 64);
+            v += __shfl_xor(v, 4, 64);
+            v += __shfl_xor(v, 8, 64);
+            if (q == 0 && f0 + k < P) yv[f0 + k][r] = v;
+        }
+    }
+    __syncthreads();
+    if (tid < S * 16) {
+        const int s = tid >> 4, rr = tid & 15, o = blockIdx.x * 16 + rr;
+        float v = 0.0f;
+        for (int j = 0; j < K; j++) {
+            const int fp = s * K + j;
+            float y = yv[fp][rr];
+            if (tq) {
+                const float alpha = ((const float *)(f.experts + (size_t)pr.e[fp] * f.estride + T.off_s))[o];
+                y = alpha * (y - htot[fp]);        // tq2.h:154
+            }
+            v = fmaf(a.ewt[fp], y, v);
+        }
+        a.out[(size_t)s * D + o] = v;
+    }
+}
+
+// gemma post-norm of the decode rows: out = rmsnorm(out, post_ffn_ln2)
+// (gemma4.c:807-808), one workgroup per token, sum of squares in double
+__global__ __launch_bounds__(256) void zz_dec_norm_kernel(float *out, const float *post_ln, int D, float eps) {
+    __shared__ double red[4];
+    float *o = out + (size_t)blockIdx.x * D;
+    double ss = 0.0;
+    for (int i = 4 * threadIdx.x; i < D; i += 1024) {
+        const float4 v = *(const float4 *)(o + i);
+        ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+    }
+    ss = zz_block_sum(ss, red);
+    const float r = 1.0f / sqrtf((float)(ss / D) + eps);
+    for (int i = 4 * threadIdx.x; i < D; i += 1024) {
+        float4 v = *(const float4 *)(o + i);
+        const float4 w = *(const float4 *)(post_ln + i);
+        v = make_float4((v.x * r) * w.x, (v.y * r) * w.y, (v.z * r) * w.z, (v.w * r) * w.w);
+        *(float4 *)(o + i) = v;
+    }
 }
 
 int zz_launch_dec_route(const ZzDecRouteArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(zz_dec_route_kernel, dim3((a.lg.E + 3) / 4), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(zz_dec_logits_kernel, dim3(a.lg.E), dim3(256), 0, st, a);
+    if (hipGetLastError() != hipSuccess) return 0;
+    hipLaunchKernelGGL(zz_dec_gate_kernel, dim3(1), dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess;
+}
+
+int zz_launch_dec_up(const ZzFfnArgs &a, int max_items, hipStream_t st) {
+    hipLaunchKernelGGL(zz_dec_up_kernel, dim3(a.MI / 32, max_items), dim3(512), 0, st, a);
     return hipGetLastError() == hipSuccess;
 }
 
 int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(zz_dec_down_kernel, dim3(a.f.D / 64), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(zz_dec_down_kernel, dim3(a.f.D / 16), dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess;
+}
+
+int zz_launch_dec_norm(float *out, const float *post_ln, int D, float eps, int S, hipStream_t st) {
+    hipLaunchKernelGGL(zz_dec_norm_kernel, dim3(S), dim3(256), 0, st, out, post_ln, D, eps);
     return hipGetLastError() == hipSuccess;
 }

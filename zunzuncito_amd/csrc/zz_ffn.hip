@@ -9,52 +9,9 @@
 // output matches the reference within the fp32 tolerance, the integers exactly.
 #include "zz_common.h"
 #include "zz_kernels.h"
+#include "zz_dot_dev.h"
 
 #define ZZ_TCH 8   // pairs (token, expert) per FFN work item
-
-// ------------------------------------------------------------------ block dots
-__device__ __forceinline__ int zz_dot_q40(uint4 w, uint4 x0, uint4 x1) {
-    const unsigned m = 0x0F0F0F0Fu;
-    int s = zz_dot4(w.x & m, x0.x, 0);
-    s = zz_dot4(w.y & m, x0.y, s);
-    s = zz_dot4(w.z & m, x0.z, s);
-    s = zz_dot4(w.w & m, x0.w, s);
-    s = zz_dot4((w.x >> 4) & m, x1.x, s);
-    s = zz_dot4((w.y >> 4) & m, x1.y, s);
-    s = zz_dot4((w.z >> 4) & m, x1.z, s);
-    s = zz_dot4((w.w >> 4) & m, x1.w, s);
-    return s;                      // sum q*x with q in 0..15
-}
-
-__device__ __forceinline__ int zz_dot_q80(uint4 w0, uint4 w1, uint4 x0, uint4 x1) {
-    int s = zz_dot4(w0.x, x0.x, 0);
-    s = zz_dot4(w0.y, x0.y, s);
-    s = zz_dot4(w0.z, x0.z, s);
-    s = zz_dot4(w0.w, x0.w, s);
-    s = zz_dot4(w1.x, x1.x, s);
-    s = zz_dot4(w1.y, x1.y, s);
-    s = zz_dot4(w1.z, x1.z, s);
-    s = zz_dot4(w1.w, x1.w, s);
-    return s;
-}
-
-// half h of a tq2 group: weights 32h..32h+31 are bit planes 2h (weights 32h+k) and
-// 2h+1 (weights 32h+16+k) of the 16 code bytes (tq2.h:46-51)
-__device__ __forceinline__ int zz_dot_tq2(uint4 c, int h, uint4 xa, uint4 xb) {
-    const unsigned m = 0x03030303u;
-    const int sa = 4 * h, sb = 4 * h + 2;
-    int s = zz_dot4((c.x >> sa) & m, xa.x, 0);
-    s = zz_dot4((c.y >> sa) & m, xa.y, s);
-    s = zz_dot4((c.z >> sa) & m, xa.z, s);
-    s = zz_dot4((c.w >> sa) & m, xa.w, s);
-    s = zz_dot4((c.x >> sb) & m, xb.x, s);
-    s = zz_dot4((c.y >> sb) & m, xb.y, s);
-    s = zz_dot4((c.z >> sb) & m, xb.z, s);
-    s = zz_dot4((c.w >> sb) & m, xb.w, s);
-    return s;                      // sum c*x with c in {0,1,2}
-}
-
-__device__ __forceinline__ uint4 ld16(const void *p) { return *(const uint4 *)p; }
 
 // Partial row dot of one lane: blocks b = sub, sub+4, ... of row `row` of tensor T
 // against the int8 activations of up to ZZ_TCH tokens. Returns per-token partial

@@ -86,29 +86,26 @@ struct ZzCombineArgs {
     float *out;                 // [S, D]
 };
 
-// Fused decode router: logits on every workgroup, then top-k and the small-batch
-// dispatch in the last workgroup to finish (device-scope ticket).
+#define ZZ_DEC_MAXS 4   // largest batch of the fused decode path
+
+// Decode router (two kernels): logits per expert workgroup, then top-k gating and
+// the small-batch dispatch in one workgroup.
 struct ZzDecRouteArgs {
     ZzPrepArgs prep;            // quantisation of the expert input
     ZzLogitArgs lg;             // logits (cen/bnd) of all tokens
     ZzTopkArgs tk;              // top-k of all tokens
     ZzDispatchArgs dp;          // dispatch lists and work items
     int S;
-    unsigned *ticket;           // zero between calls; reset by the last workgroup
 };
 
-// Fused decode down projection + gate-weighted combine (+ gemma post-norm).
+// Fused decode down projection + gate-weighted combine.
 struct ZzDecDownArgs {
     ZzFfnArgs f;
-    int S, K, gemma;
-    float eps;
+    int S, K, E;
     const int *eidx;            // [S, K]
     const float *ewt;           // [S, K]
     const int *ppos;            // [S*K] -> sorted pair
-    const float *post_ln;       // [D]
     float *out;                 // [S, D]
-    double *part;               // [S, gridDim.x] partial sums of squares
-    unsigned *ticket;
 };
 
 struct ZzRepackArgs {
@@ -125,7 +122,9 @@ int zz_launch_dispatch(const ZzDispatchArgs &a, hipStream_t st);
 int zz_launch_ffn_up(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_ffn_down(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_dec_route(const ZzDecRouteArgs &a, hipStream_t st);
+int zz_launch_dec_up(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st);
+int zz_launch_dec_norm(float *out, const float *post_ln, int D, float eps, int S, hipStream_t st);
 // int8-MFMA grouped GEMM versions for work items of up to 64 tokens
 int zz_launch_up_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_down_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st);

@@ -9,9 +9,10 @@
 // roundings cheaply. Instead each value is computed in parallel together with a
 // rigorous bound on its distance from the reference's serial result; a decision
 // (a rounding to float, the top-k set and order) is taken on the GPU only when
-// the bound proves it equals the reference's. Otherwise the few contested values
-// are recomputed: first with a tighter bound from exact prefix sums, and as a last
-// resort by replaying the reference's serial chain in the reference's order.
+// the bound proves it equals the reference's. Gemma logits carry a tight bound
+// from their exact-order prefix sums; the rare values still contested are
+// recomputed by replaying the reference's serial chain in the reference's order.
+// Batches of 16+ tokens compute the gemma chains exactly instead (tiled kernel).
 #include "zz_common.h"
 #include "zz_kernels.h"
 #include "zz_route_dev.h"
@@ -98,9 +99,17 @@ __global__ __launch_bounds__(256) void zz_prep_kernel(ZzPrepArgs a) {
 }
 
 __global__ __launch_bounds__(256) void zz_logits_kernel(ZzLogitArgs a) {
+    __shared__ __attribute__((aligned(16))) float buf[4 * ZZ_TBUF];
     const int s = blockIdx.y, e = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (e >= a.E) return;
-    zz_logit_wave(a, s, e);
+    if (a.gating == ZZ_GATE_SOFTMAX_PES) {
+        const size_t o = (size_t)s * a.E + e;
+        zz_tight_wave<1, false>(a.router + (size_t)e * a.D, a.xn + (size_t)s * a.D, nullptr, nullptr,
+                                1.0f, a.D, a.bias, e, buf + (threadIdx.x >> 6) * ZZ_TBUF, a.cen + o,
+                                a.bnd + o, a.E, nullptr);
+    } else {
+        zz_logit_wave_f64(a, s, e);
+    }
 }
 
 // -------------------------------------------------------------------------------
