@@ -12,6 +12,7 @@
 #include "zz_common.h"
 #include "zz_kernels.h"
 #include "zz_route_dev.h"
+#include "zz_topk_wave.h"
 #include "zz_dot_dev.h"
 
 #define DEC_MAXS ZZ_DEC_MAXS
@@ -26,6 +27,8 @@ __device__ __forceinline__ int zz_clamp_e(int e, int E) { return e < 0 || e >= E
 // is replayed; the logit gets the tight bound of zz_tight_block_scan. lfm/maple:
 // wave s computes token s's logit. Then the workgroup quantises its share of the
 // expert input (blocks e, e + E, ...).
+// RB >= ceil(D/256): loads per thread and token, all issued before any is used.
+template <int RB>
 __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
     const ZzPrepArgs &pp = a.prep;
     const ZzLogitArgs &lg = a.lg;
@@ -37,29 +40,26 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
     __shared__ float cert;
     const float rs = 1.0f / sqrtf((float)D);
     if (gem) {
-        const int R = (D + 255) >> 8;                         // <= 32
+        const int R = (D + 255) >> 8;                         // <= RB
         const float *w = lg.router + (size_t)e * D;
-        float wr[32], sr[32];
+        float wr[RB], sr[RB];
 #pragma unroll
-        for (int j = 0; j < 32; j++) {
-            if (j < R) {
-                const int i = min(tid + 256 * j, D - 1);      // clamped: loads stay in range
-                wr[j] = w[i];
-                sr[j] = pp.router_scale[i] * rs;
-            }
+        for (int j = 0; j < RB; j++) {                        // clamped: loads stay in range
+            const int i = min(tid + 256 * j, D - 1);
+            wr[j] = w[i];
+            sr[j] = pp.router_scale[i];
         }
+#pragma unroll
+        for (int j = 0; j < RB; j++) sr[j] = sr[j] * rs;
         for (int s = 0; s < S; s++) {
             const float *x = pp.in + (size_t)s * D;
-            float xr[32];
+            float xr[RB];
+#pragma unroll
+            for (int j = 0; j < RB; j++) xr[j] = x[min(tid + 256 * j, D - 1)];
             double sq = 0.0;
 #pragma unroll
-            for (int j = 0; j < 32; j++) {
-                if (j < R) {
-                    const int i = tid + 256 * j;
-                    xr[j] = x[min(i, D - 1)];
-                    if (i < D) sq += (double)xr[j] * (double)xr[j];
-                }
-            }
+            for (int j = 0; j < RB; j++)
+                if (j < R && tid + 256 * j < D) sq += (double)xr[j] * (double)xr[j];
             // every square is exact in double; each term meets at most R - 1 + 6 + 3
             // roundings here and D - 1 in the reference's serial sum
             sq = zz_block_sum(sq, red);
@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
             const float r = 1.0f / sqrtf(cert + pp.eps);
             if (tid == 0) rr[s] = r;
 #pragma unroll
-            for (int j = 0; j < 32; j++) {
+            for (int j = 0; j < RB; j++) {
                 const int i = tid + 256 * j;
                 if (j < R && i < D) {
                     const float xv = (xr[j] * r) * sr[j];     // xn as zz_prep_kernel forms it
@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
                 }
             }
             __syncthreads();
-            zz_tight_block_scan(buf, D, lg.bias, e, red, lg.cen + (size_t)s * lg.E + e,
+            zz_tight_block_scan<RB>(buf, D, lg.bias, e, red, lg.cen + (size_t)s * lg.E + e,
                                 lg.bnd + (size_t)s * lg.E + e);
         }
     } else if ((tid >> 6) < S) {
@@ -123,15 +123,13 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
     }
 }
 
-// Decode router, part 2 (one workgroup): certified top-k gating of every token,
-// then the dispatch of the S*K pairs.
+// Decode router, part 2 (one workgroup, one wave per token): certified top-k
+// gating (zz_topk_wave.h), then the dispatch of the S*K pairs.
 __global__ __launch_bounds__(256) void zz_dec_gate_kernel(ZzDecRouteArgs a) {
-    const int S = a.S, tid = threadIdx.x;
-    __shared__ ZzTopkShared sh;
-    for (int s = 0; s < S; s++) {
-        zz_topk_token(a.tk, s, sh);
-        __syncthreads();
-    }
+    extern __shared__ __attribute__((aligned(16))) char tk_lds[];
+    const int S = a.S, tid = threadIdx.x, w = tid >> 6;
+    zz_topk_wave_any(a.tk, w, tk_lds + w * zz_topk_wave_bytes(a.tk.E));
+    __syncthreads();
     // dispatch of P = S*K <= 64 pairs: stable ranking by (expert, pair index)
     const ZzDispatchArgs &dp = a.dp;
     const int K = dp.K, P = S * K;
@@ -314,14 +312,15 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzFfnArgs a) {
 }
 
 // ------------------------------------------------------------------ down + combine
-// grid D/16: the workgroup owns 16 output rows, 16 lanes per row; lane q takes
-// blocks q, q+16, ... of every (token, slot) pair's down row, DD_F pairs x DD_J
-// blocks loaded at once. The 16 x P expert outputs meet in LDS and are combined
-// per token in slot order, out = fma(w_j, y_j, out) as gemma4.c:652. Gemma's
-// post-norm needs the whole row: each workgroup leaves its partial sums of
-// squares and the last one to finish normalises every row.
-#define DD_F 4
-#define DD_J 2
+// grid D/8: the workgroup owns 8 output rows, 32 lanes per row. A row's work is
+// P * nu units (pair, block) -- nu blocks of 32 (q4_0 / q8_0) or 64-groups (tq2)
+// per (token, slot) pair; lane q takes units q, q+32, ..., DD_U at a time with
+// every load issued before any is used. Unit results meet in LDS and each
+// (row, pair) sum runs in block order; the 8 x P expert outputs are then combined
+// per token in slot order, out = fma(w_j, y_j, out) as gemma4.c:652.
+#define DD_RW 8
+#define DD_U 12
+#define DD_UB 1024                    // unit results per row held at once
 
 struct ZzDecPairs {                 // per (token, slot) pair, flat order s*K + j
     int pos[DEC_MAXS * ZZ_MAXK];    // sorted position: row of hq / hs / hsum
@@ -329,118 +328,94 @@ struct ZzDecPairs {                 // per (token, slot) pair, flat order s*K + 
 };
 
 template <int FMT>
-__device__ __forceinline__ void zz_dec_down_rows(const ZzDecDownArgs &a, const ZzDecPairs &pr, int f0,
-                                                 int row, int q, float (&acc)[DD_F]) {
-    const ZzFfnArgs &f = a.f;
-    const ZzTensor &T = f.lay.down;
-    const int MI = f.MI, nb = MI / ZZ_BLK, P = a.S * a.K;
-    const int nu = FMT == ZZ_FMT_TQ2 ? nb / 2 : nb;
-#pragma unroll
-    for (int k = 0; k < DD_F; k++) acc[k] = 0.0f;
-    for (int u0 = 0; u0 < nu; u0 += 16 * DD_J) {
-        // every load of the chunk is issued before any is used (clamped indices
-        // keep the surplus ones in range; their results are discarded)
-        uint4 w0[DD_F][DD_J], w1[DD_F][DD_J], x0[DD_F][DD_J], x1[DD_F][DD_J];
-        uint4 x2[DD_F][DD_J], x3[DD_F][DD_J];
-        float dw[DD_F][DD_J], hs0[DD_F][DD_J], hs1[DD_F][DD_J];
-        int hsm[DD_F][DD_J];
-#pragma unroll
-        for (int k = 0; k < DD_F; k++) {
-            const int fp = min(f0 + k, P - 1);
-            const int p = pr.pos[fp];
-            const uint8_t *E = f.experts + (size_t)pr.e[fp] * f.estride;
-            const int8_t *hq = f.hq + (size_t)p * MI;
-            const float *hs = f.hs + (size_t)p * nb;
-#pragma unroll
-            for (int j = 0; j < DD_J; j++) {
-                const int u = min(u0 + q + 16 * j, nu - 1);
-                const uint8_t *qp = E + zz_qoff(T, row, u);
-                w0[k][j] = ld16(qp);
-                if (FMT == ZZ_FMT_TQ2) {
-                    const int8_t *x = hq + u * 64;
-                    x0[k][j] = ld16(x);
-                    x1[k][j] = ld16(x + 16);
-                    x2[k][j] = ld16(x + 32);
-                    x3[k][j] = ld16(x + 48);
-                    hs0[k][j] = hs[2 * u];
-                    hs1[k][j] = hs[2 * u + 1];
-                } else {
-                    if (FMT == ZZ_FMT_Q80) w1[k][j] = ld16(qp + 16);
-                    dw[k][j] = zz_h2f(*(const uint16_t *)(E + zz_soff(T, row, u)));
-                    const int8_t *x = hq + u * ZZ_BLK;
-                    x0[k][j] = ld16(x);
-                    x1[k][j] = ld16(x + 16);
-                    hs0[k][j] = hs[u];
-                    if (FMT == ZZ_FMT_Q40) hsm[k][j] = f.hsum[(size_t)p * nb + u];
-                }
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < DD_F; k++) {
-#pragma unroll
-            for (int j = 0; j < DD_J; j++) {
-                const int u = u0 + q + 16 * j;
-                float v;
-                if (FMT == ZZ_FMT_TQ2) {
-                    const int d0 = zz_dot_tq2(w0[k][j], 0, x0[k][j], x1[k][j]);
-                    const int d1 = zz_dot_tq2(w0[k][j], 1, x2[k][j], x3[k][j]);
-                    v = fmaf(hs0[k][j], (float)d0, acc[k]);
-                    v = fmaf(hs1[k][j], (float)d1, v);
-                } else {
-                    const int d = FMT == ZZ_FMT_Q80 ? zz_dot_q80(w0[k][j], w1[k][j], x0[k][j], x1[k][j])
-                                                    : zz_dot_q40(w0[k][j], x0[k][j], x1[k][j]) - 8 * hsm[k][j];
-                    v = fmaf(dw[k][j] * hs0[k][j], (float)d, acc[k]);
-                }
-                if (u < nu && f0 + k < P) acc[k] = v;
-            }
-        }
-    }
-}
-
 __global__ __launch_bounds__(256) void zz_dec_down_kernel(ZzDecDownArgs a) {
     const ZzFfnArgs &f = a.f;
-    const int tid = threadIdx.x, r = tid >> 4, q = tid & 15;
-    const int row = blockIdx.x * 16 + r;
+    const int tid = threadIdx.x, r = tid >> 5, q = tid & 31;
+    const int row = blockIdx.x * DD_RW + r;
     const ZzTensor &T = f.lay.down;
-    const int nb = f.MI / ZZ_BLK, D = f.D, S = a.S, K = a.K, P = S * K;
-    const bool tq = T.fmt == ZZ_FMT_TQ2;
-    __shared__ float yv[DEC_MAXS * ZZ_MAXK][16];
-    __shared__ float htot[DEC_MAXS * ZZ_MAXK];
+    const int MI = f.MI, nb = MI / ZZ_BLK, D = f.D, S = a.S, K = a.K, P = S * K;
+    const int nu = FMT == ZZ_FMT_TQ2 ? nb / 2 : nb;
+    const int PG = min(P, DD_UB / nu);                          // pairs per group, >= 1
     __shared__ ZzDecPairs pr;
+    __shared__ float ub[DD_RW][DD_UB];
+    __shared__ float yv[DEC_MAXS * ZZ_MAXK][DD_RW];
+    __shared__ float htot[DEC_MAXS * ZZ_MAXK];
     if (tid < P) {
         pr.pos[tid] = a.ppos[tid];
         pr.e[tid] = zz_clamp_e(a.eidx[tid], a.E);
     }
-    if (tq && tid < P) {                           // tq2.h:101-106, serial
+    if (FMT == ZZ_FMT_TQ2 && tid < P) {            // tq2.h:101-106, serial
         const size_t p = (size_t)a.ppos[tid];
         double t = 0.0;
         for (int b = 0; b < nb; b++) t += (double)f.hs[p * nb + b] * (double)f.hsum[p * nb + b];
         htot[tid] = (float)t;
     }
     __syncthreads();
-    for (int f0 = 0; f0 < P; f0 += DD_F) {
-        float acc[DD_F];
-        if (T.fmt == ZZ_FMT_Q40) zz_dec_down_rows<ZZ_FMT_Q40>(a, pr, f0, row, q, acc);
-        else if (T.fmt == ZZ_FMT_Q80) zz_dec_down_rows<ZZ_FMT_Q80>(a, pr, f0, row, q, acc);
-        else zz_dec_down_rows<ZZ_FMT_TQ2>(a, pr, f0, row, q, acc);
+    for (int pg0 = 0; pg0 < P; pg0 += PG) {
+        const int np = min(PG, P - pg0), U = np * nu;
+        for (int u0 = 0; u0 < U; u0 += 32 * DD_U) {
+            uint4 w0[DD_U], w1[DD_U], x0[DD_U], x1[DD_U], x2[DD_U], x3[DD_U];
+            float dw[DD_U], s0[DD_U], s1[DD_U];
+            int hm[DD_U];
 #pragma unroll
-        for (int k = 0; k < DD_F; k++) {
-            float v = acc[k];
-            v += __shfl_xor(v, 1, 64);
-            v += __shfl_xor(v, 2, 64);
-            v += __shfl_xor(v, 4, 64);
-            v += __shfl_xor(v, 8, 64);
-            if (q == 0 && f0 + k < P) yv[f0 + k][r] = v;
+            for (int j = 0; j < DD_U; j++) {                     // clamped: loads stay in range
+                const int u = min(u0 + q + 32 * j, U - 1);
+                const int pp = pg0 + u / nu, b = u % nu;
+                const int p = pr.pos[pp];
+                const uint8_t *E = f.experts + (size_t)pr.e[pp] * f.estride;
+                const uint8_t *qp = E + zz_qoff(T, row, b);
+                w0[j] = ld16(qp);
+                if (FMT == ZZ_FMT_TQ2) {
+                    const int8_t *x = f.hq + (size_t)p * MI + b * 64;
+                    x0[j] = ld16(x);
+                    x1[j] = ld16(x + 16);
+                    x2[j] = ld16(x + 32);
+                    x3[j] = ld16(x + 48);
+                    s0[j] = f.hs[(size_t)p * nb + 2 * b];
+                    s1[j] = f.hs[(size_t)p * nb + 2 * b + 1];
+                } else {
+                    if (FMT == ZZ_FMT_Q80) w1[j] = ld16(qp + 16);
+                    dw[j] = zz_h2f(*(const uint16_t *)(E + zz_soff(T, row, b)));
+                    const int8_t *x = f.hq + (size_t)p * MI + b * ZZ_BLK;
+                    x0[j] = ld16(x);
+                    x1[j] = ld16(x + 16);
+                    s0[j] = f.hs[(size_t)p * nb + b];
+                    if (FMT == ZZ_FMT_Q40) hm[j] = f.hsum[(size_t)p * nb + b];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < DD_U; j++) {
+                const int u = u0 + q + 32 * j;
+                float c;
+                if (FMT == ZZ_FMT_TQ2) {
+                    const int d0 = zz_dot_tq2(w0[j], 0, x0[j], x1[j]);
+                    const int d1 = zz_dot_tq2(w0[j], 1, x2[j], x3[j]);
+                    c = fmaf(s1[j], (float)d1, s0[j] * (float)d0);
+                } else {
+                    const int d = FMT == ZZ_FMT_Q80 ? zz_dot_q80(w0[j], w1[j], x0[j], x1[j])
+                                                    : zz_dot_q40(w0[j], x0[j], x1[j]) - 8 * hm[j];
+                    c = (dw[j] * s0[j]) * (float)d;
+                }
+                if (u < U) ub[r][u] = c;
+            }
         }
+        __syncthreads();
+        for (int t = tid; t < DD_RW * np; t += 256) {             // (row, pair) sums, block order
+            const int rr = t / np, pl = t % np;
+            const float *c = &ub[rr][pl * nu];
+            float y = 0.0f;
+            for (int b = 0; b < nu; b++) y += c[b];
+            yv[pg0 + pl][rr] = y;
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    if (tid < S * 16) {
-        const int s = tid >> 4, rr = tid & 15, o = blockIdx.x * 16 + rr;
+    if (tid < S * DD_RW) {
+        const int s = tid / DD_RW, rr = tid % DD_RW, o = blockIdx.x * DD_RW + rr;
         float v = 0.0f;
         for (int j = 0; j < K; j++) {
             const int fp = s * K + j;
             float y = yv[fp][rr];
-            if (tq) {
+            if (FMT == ZZ_FMT_TQ2) {
                 const float alpha = ((const float *)(f.experts + (size_t)pr.e[fp] * f.estride + T.off_s))[o];
                 y = alpha * (y - htot[fp]);        // tq2.h:154
             }
@@ -471,9 +446,15 @@ __global__ __launch_bounds__(256) void zz_dec_norm_kernel(float *out, const floa
 }
 
 int zz_launch_dec_route(const ZzDecRouteArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(zz_dec_logits_kernel, dim3(a.lg.E), dim3(256), 0, st, a);
+    const int R = (a.prep.D + 255) / 256;
+    if (R <= 4) hipLaunchKernelGGL(zz_dec_logits_kernel<4>, dim3(a.lg.E), dim3(256), 0, st, a);
+    else if (R <= 8) hipLaunchKernelGGL(zz_dec_logits_kernel<8>, dim3(a.lg.E), dim3(256), 0, st, a);
+    else if (R <= 12) hipLaunchKernelGGL(zz_dec_logits_kernel<12>, dim3(a.lg.E), dim3(256), 0, st, a);
+    else if (R <= 16) hipLaunchKernelGGL(zz_dec_logits_kernel<16>, dim3(a.lg.E), dim3(256), 0, st, a);
+    else if (R <= 24) hipLaunchKernelGGL(zz_dec_logits_kernel<24>, dim3(a.lg.E), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(zz_dec_logits_kernel<32>, dim3(a.lg.E), dim3(256), 0, st, a);
     if (hipGetLastError() != hipSuccess) return 0;
-    hipLaunchKernelGGL(zz_dec_gate_kernel, dim3(1), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(zz_dec_gate_kernel, dim3(1), dim3(64 * a.S), a.S * zz_topk_wave_bytes(a.tk.E), st, a);
     return hipGetLastError() == hipSuccess;
 }
 
@@ -483,7 +464,13 @@ int zz_launch_dec_up(const ZzFfnArgs &a, int max_items, hipStream_t st) {
 }
 
 int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(zz_dec_down_kernel, dim3(a.f.D / 16), dim3(256), 0, st, a);
+    const dim3 grid(a.f.D / DD_RW);
+    switch (a.f.lay.down.fmt) {
+    case ZZ_FMT_Q40: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q40>, grid, dim3(256), 0, st, a); break;
+    case ZZ_FMT_Q80: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q80>, grid, dim3(256), 0, st, a); break;
+    case ZZ_FMT_TQ2: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_TQ2>, grid, dim3(256), 0, st, a); break;
+    default: return 0;
+    }
     return hipGetLastError() == hipSuccess;
 }
 

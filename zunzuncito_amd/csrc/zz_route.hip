@@ -16,6 +16,7 @@
 #include "zz_common.h"
 #include "zz_kernels.h"
 #include "zz_route_dev.h"
+#include "zz_topk_wave.h"
 #include <float.h>
 
 // Prep: one workgroup per token. Gemma: the mean square is certified to round to
@@ -191,9 +192,12 @@ __global__ __launch_bounds__(256) void zz_logits_exact_kernel(ZzLogitArgs a) {
     }
 }
 
-__global__ __launch_bounds__(256) void zz_topk_kernel(ZzTopkArgs a) {
-    __shared__ ZzTopkShared sh;
-    zz_topk_token(a, blockIdx.x, sh);
+// Top-k gating, one wave per token (zz_topk_wave.h), four tokens per workgroup.
+__global__ __launch_bounds__(256) void zz_topk_kernel(ZzTopkArgs a, int S) {
+    extern __shared__ __attribute__((aligned(16))) char tk_lds[];
+    const int w = threadIdx.x >> 6, s = blockIdx.x * 4 + w;
+    if (s >= S) return;
+    zz_topk_wave_any(a, s, tk_lds + w * zz_topk_wave_bytes(a.E));
 }
 
 // -------------------------------------------------------------------------------
@@ -315,7 +319,7 @@ int zz_launch_logits(const ZzLogitArgs &a, int S, hipStream_t st) {
 }
 
 int zz_launch_topk(const ZzTopkArgs &a, int S, hipStream_t st) {
-    hipLaunchKernelGGL(zz_topk_kernel, dim3(S), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(zz_topk_kernel, dim3((S + 3) / 4), dim3(256), 4 * zz_topk_wave_bytes(a.E), st, a, S);
     return hipGetLastError() == hipSuccess;
 }
 

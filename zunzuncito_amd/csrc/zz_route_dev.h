@@ -135,20 +135,23 @@ __device__ void zz_tight_wave(const float *w, const float *src, const float *rsc
 // batches), from the D rounded products t_i staged in LDS at buf[zz_pad32(i)] (one
 // pad word per 32 against bank conflicts): each thread owns a contiguous run of
 // R = ceil(D/256) elements of the order, a block scan joins the runs. red: 12
-// doubles of LDS. Thread 0 writes *cen / *bnd. Ends with a barrier (buf and red
-// may be reused).
+// doubles of LDS; RB >= R is the compile-time run capacity. Thread 0 writes
+// *cen / *bnd. Ends with a barrier (buf and red may be reused).
 __device__ __forceinline__ int zz_pad32(int i) { return i + (i >> 5); }
 
+template <int RB>
 __device__ void zz_tight_block_scan(const float *buf, int D, const float *bias, int e, double *red,
                                     double *cen, double *bnd) {
     const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6;
-    const int R = (D + 255) >> 8;                             // <= 32 for D <= 8192
+    const int R = (D + 255) >> 8;                             // R <= RB
     const int i0 = tid * R;
-    float p[32];
+    float p[RB];
     double loc = 0.0, T = 0.0;
 #pragma unroll
-    for (int k = 0; k < 32; k++) {
-        p[k] = k < R && i0 + k < D ? buf[zz_pad32(i0 + k)] : 0.0f;
+    for (int k = 0; k < RB; k++) p[k] = buf[zz_pad32(min(i0 + k, D - 1))];   // all reads issued first
+#pragma unroll
+    for (int k = 0; k < RB; k++) {
+        if (!(k < R && i0 + k < D)) p[k] = 0.0f;
         loc += (double)p[k];
         T += fabs((double)p[k]);
     }
@@ -163,7 +166,7 @@ __device__ void zz_tight_block_scan(const float *buf, int D, const float *bias, 
     double run = inc - loc, sabs = 0.0;
     for (int q = 0; q < wv; q++) run += red[q];
 #pragma unroll
-    for (int k = 0; k < 32; k++) {
+    for (int k = 0; k < RB; k++) {
         run += (double)p[k];
         if (k < R && i0 + k >= 1 && i0 + k < D) sabs += fabs(run);
     }
@@ -223,238 +226,3 @@ __device__ void zz_logit_wave_f64(const ZzLogitArgs &a, int s, int e) {
         a.bnd[o] = 0.0;
     }
 }
-
-// -------------------------------------------------------------------------------
-// Top-k with interval certification. Each expert carries [lo, hi] containing the
-// reference's selection score. Candidates are experts whose hi reaches the k-th
-// largest lo; a candidate is contested when its interval meets another
-// candidate's. No contested candidate => the reference's top-k set and order are
-// fixed by the centres. Contested gemma experts are refined (exact prefix-sum
-// bound), then replayed serially; contested lfm scores (glibc expf in the
-// reference, lfm25.c:648) are flagged for the caller.
-struct ZzTopkShared {
-    __attribute__((aligned(16))) double lo[ZZ_MAXE + 8], hi[ZZ_MAXE + 8];
-    int clist[ZZ_MAXE];                  // candidates (any order)
-    int ncand;
-    float sg[ZZ_MAXE];
-    int list[ZZ_MAXE];                   // contested candidates (any order)
-    int nlist;
-    int any;
-    int width;                           // some interval has non-zero width
-    double lk;
-    int idx[ZZ_MAXK];
-    float topv[ZZ_MAXK];
-    float wj[ZZ_MAXK], pj[ZZ_MAXK], wsum;   // gate weights before normalisation
-    double red[4];
-    __attribute__((aligned(16))) float buf[4 * ZZ_TBUF];   // per-wave transposes; chain replay
-};
-
-// Candidates are the experts whose hi reaches lk, the k-th largest lo (ties by
-// index); a candidate is contested when its interval meets another candidate's.
-// The all-pairs pass for lk reads the lo table 8 entries at a time as broadcast
-// LDS loads; the candidate passes run over the (short) candidate list.
-__device__ void zz_mark_contested(ZzTopkShared &sh, int E, int K) {
-    if (threadIdx.x == 0) {
-        sh.lk = -INFINITY;
-        sh.ncand = 0;
-        sh.nlist = 0;
-        sh.any = 0;
-    }
-    __syncthreads();
-    // T adjacent threads share expert e, each ranking it against a slice of lo
-    const int T = E <= 32 ? 8 : (E <= 64 ? 4 : (E <= 128 ? 2 : 1));
-    const int per = (E + T - 1) / T;
-    for (int base = 0; base < E * T; base += 256) {
-        const int v = base + threadIdx.x, e = v / T, h = v % T;
-        const bool act = e < E;
-        const double le = act ? sh.lo[e] : 0.0;
-        int rank = 0;
-        const int f1 = act ? min(E, (h + 1) * per) : 0;
-        for (int f0 = h * per; f0 < f1; f0 += 8) {
-            double lf[8];                        // lo has 8 spare entries past ZZ_MAXE
-#pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                const double2 w = *(const double2 *)&sh.lo[(f0 & ~1) + j];
-                lf[j] = w.x;
-                lf[j + 1] = w.y;
-            }
-            const int fb = f0 & ~1;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int f = fb + j;
-                rank += (f >= f0) & (f < f1) & ((lf[j] > le) | ((lf[j] == le) & (f < e)));
-            }
-        }
-        // T is a power of two and the T threads of e are adjacent lanes of one wave
-        for (int o = 1; o < T; o <<= 1) rank += __shfl_xor(rank, o, 64);
-        if (act && h == 0 && rank == K - 1) sh.lk = le;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < E; e += 256)
-        if (sh.hi[e] >= sh.lk) sh.clist[atomicAdd(&sh.ncand, 1)] = e;
-    __syncthreads();
-    const int nc = sh.ncand;
-    for (int i = threadIdx.x; i < nc; i += 256) {
-        const int e = sh.clist[i];
-        const double le = sh.lo[e], he = sh.hi[e];
-        int c = 0;
-        for (int j = 0; j < nc; j++) {
-            const int f = sh.clist[j];
-            c |= (f != e) & (sh.lo[f] <= he) & (le <= sh.hi[f]);
-        }
-        if (c) {
-            sh.any = 1;
-            sh.list[atomicAdd(&sh.nlist, 1)] = e;
-        }
-    }
-    __syncthreads();
-}
-
-// Top-k for token s by a whole 256-thread workgroup.
-__device__ void zz_topk_token(const ZzTopkArgs &a, int s, ZzTopkShared &sh) {
-    const int E = a.E, K = a.K;
-    const double *cen = a.cen + (size_t)s * E, *bnd = a.bnd + (size_t)s * E;
-    int contested = 0;
-    if (threadIdx.x == 0) sh.width = a.gating == ZZ_GATE_SIGMOID_BIAS;
-    __syncthreads();
-    if (threadIdx.x < K) {          // valid ids even if NaN scores leave ranks unfilled
-        sh.idx[threadIdx.x] = threadIdx.x;
-        sh.topv[threadIdx.x] = 0.0f;
-    }
-
-    if (a.gating == ZZ_GATE_SIGMOID_BIAS) {
-        // s = 1/(1+expf(-v)) with exp evaluated in double and rounded once; glibc's
-        // expf is within 1 ulp of that, so each s is within 2 ulps of the
-        // reference's and sel = s + bias within 2 ulp(s) + ulp(sel).
-        for (int e = threadIdx.x; e < E; e += 256) {
-            float v = (float)cen[e];
-            float ex = (float)exp(-(double)v);
-            float sg = 1.0f / (1.0f + ex);
-            float sel = a.bias ? sg + a.bias[e] : sg;
-            double sl = 2.0 * (double)ulp_of(sg) + (double)ulp_of(sel);
-            sh.sg[e] = sg;
-            sh.lo[e] = (double)sel - sl;
-            sh.hi[e] = (double)sel + sl;
-        }
-    } else {
-        for (int e = threadIdx.x; e < E; e += 256) {
-            sh.lo[e] = cen[e] - bnd[e];
-            sh.hi[e] = cen[e] + bnd[e];
-            if (bnd[e] > 0.0) sh.width = 1;
-        }
-    }
-    __syncthreads();
-    zz_mark_contested(sh, E, K);
-    // exact logits (zero-width intervals) can only "overlap" by being equal, which
-    // the index tie-break below resolves as the reference does
-    if (threadIdx.x == 0 && !sh.width) sh.any = 0;
-    __syncthreads();
-
-    if (sh.any && a.gating == ZZ_GATE_SOFTMAX_PES) {
-        // every gemma logit already carries its tight bound (zz_tight_wave); what
-        // is still contested is settled by replaying the reference's chain
-        const float *xn = a.xn + (size_t)s * a.D;
-        {
-            // replay the reference's in-order fp32 chain (gemma4.c:600-601). The
-            // wave forms the rounded products in LDS, one lane adds them in order.
-            const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-            if (a.D <= 2 * ZZ_TBUF && wv < 2) {
-                for (int k = wv; k < sh.nlist; k += 2) {
-                    const int e = sh.list[k];
-                    const float *w = a.router + (size_t)e * a.D;
-                    float *pr = sh.buf + wv * 2 * ZZ_TBUF;
-                    for (int i = l; i < a.D; i += 64) pr[i] = w[i] * xn[i];
-                    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-                    __builtin_amdgcn_wave_barrier();
-                    if (l == 0) {
-                        float v = 0.0f;
-                        for (int i = 0; i < a.D; i += 4) {
-                            const float4 p = *(const float4 *)(pr + i);
-                            v = v + p.x;
-                            v = v + p.y;
-                            v = v + p.z;
-                            v = v + p.w;
-                        }
-                        if (a.bias) v = v + a.bias[e];
-                        sh.lo[e] = sh.hi[e] = (double)v;
-                    }
-                    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-                    __builtin_amdgcn_wave_barrier();
-                }
-            } else if (a.D > 2 * ZZ_TBUF) {
-                for (int k = threadIdx.x; k < sh.nlist; k += 256) {
-                    const int e = sh.list[k];
-                    const float *w = a.router + (size_t)e * a.D;
-                    float v = 0.0f;
-                    for (int i = 0; i < a.D; i++) v = v + w[i] * xn[i];
-                    if (a.bias) v = v + a.bias[e];
-                    sh.lo[e] = sh.hi[e] = (double)v;
-                }
-            }
-            if (threadIdx.x == 0) atomicAdd(a.diag + 2, 1u);
-            __syncthreads();
-            zz_mark_contested(sh, E, K);       // recomputes the candidate set
-            // exact values may tie: ordering below breaks ties by index, as the
-            // reference's strict '>' insertion does
-        }
-    } else if (sh.any && a.gating == ZZ_GATE_SIGMOID_BIAS) {
-        contested = 1;
-    }
-
-    // rank candidates by (centre desc, index asc); centres of disjoint intervals
-    // order exactly as the reference's values do
-    const int nc = sh.ncand;
-    for (int i = threadIdx.x; i < nc; i += 256) {
-        const int e = sh.clist[i];
-        const double me = 0.5 * (sh.lo[e] + sh.hi[e]);
-        int rank = 0;
-        for (int j = 0; j < nc; j++) {
-            const int f = sh.clist[j];
-            const double mf = 0.5 * (sh.lo[f] + sh.hi[f]);
-            rank += (f != e) & ((mf > me) | ((mf == me) & (f < e)));
-        }
-        if (rank < K) {
-            sh.idx[rank] = e;
-            sh.topv[rank] = (float)me;
-        }
-    }
-    __syncthreads();
-    // gate weights: each slot's w_j in parallel, their sum serially in slot order
-    // as the reference adds them, then each slot's normalisation
-    const int j = threadIdx.x;
-    if (j < K) {
-        const int e = sh.idx[j];
-        sh.wj[j] = a.gating == ZZ_GATE_SIGMOID_BIAS ? sh.sg[e] : expf(sh.topv[j] - sh.topv[0]);
-        sh.pj[j] = a.gating == ZZ_GATE_SOFTMAX_PES ? a.pes[e] : 1.0f;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float sum = 0.0f;
-        for (int i = 0; i < K; i++) sum += sh.wj[i];
-        sh.wsum = sum;
-        if (a.gating == ZZ_GATE_SIGMOID_BIAS) {
-            if (a.contested) a.contested[s] = contested;
-            if (contested) atomicAdd(a.diag + 3, 1u);
-        }
-    }
-    __syncthreads();
-    if (j < K) {
-        const float sum = sh.wsum, v = sh.wj[j];
-        float out;
-        if (a.gating == ZZ_GATE_SOFTMAX_PES) {                     // gemma4.c:609-612
-            out = (v / sum) * sh.pj[j];
-        } else if (a.gating == ZZ_GATE_SIGMOID_BIAS) {             // lfm25.c:661-667
-            float t = v;
-            if (a.norm_topk) t /= (sum + 1e-6f);
-            out = t * a.routed_scaling;
-        } else {                                                   // maple.c:596-600
-            float t = v;
-            if (a.norm_topk) t /= (sum + 1e-20f);
-            out = t;
-        }
-        a.eidx[(size_t)s * K + j] = sh.idx[j];
-        a.ewt[(size_t)s * K + j] = out;
-        if (a.topv) a.topv[(size_t)s * K + j] = sh.topv[j];
-    }
-}
-

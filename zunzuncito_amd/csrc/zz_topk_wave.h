@@ -1,0 +1,273 @@
+// zz_topk_wave.h -- certified top-k gating of one token by one wave.
+//
+// Each expert's selection score is known as an interval [lo, hi] that contains
+// the reference's value (zz_route_dev.h). The top k by the reference's order
+// (value descending, index ascending: the strict '>' insertion of
+// gemma4.c:604-607, lfm25.c:650-659, maple.c:588-594) are fixed without any
+// block-wide pass over all experts:
+//   1. keys (lo rounded down to float, index) in registers, EPL experts per lane;
+//      the k-th largest of the 64 lane maxima is <= the k-th largest key;
+//   2. the few keys at or above it are compacted to LDS and ranked exactly: lk,
+//      a float lower bound of the k-th largest lo (rounding down is monotone);
+//   3. candidates are the experts with hi >= lk -- a superset of the top k;
+//   4. a candidate whose interval meets another candidate's is contested; gemma
+//      replays contested logits with the reference's serial fp32 chain
+//      (gemma4.c:600-601), lfm flags the token (expf, lfm25.c:648);
+//   5. candidates are ranked by centre (disjoint intervals order as their
+//      values do; replayed ones are exact), and the gate weights are formed.
+#pragma once
+#include "zz_route_dev.h"
+
+struct ZzTopkWaveHdr {
+    unsigned long long lmax[64];
+    unsigned long long lk;
+    int idx[ZZ_MAXK];
+    float topv[ZZ_MAXK];
+};
+// LDS of one wave: the header, then u64 ck[E], double clo[E], chi[E], int ci[E]
+__host__ __device__ inline size_t zz_topk_wave_bytes(int E) {
+    return (sizeof(ZzTopkWaveHdr) + (size_t)E * (8 + 8 + 8 + 4) + 15) & ~(size_t)15;
+}
+
+__device__ __forceinline__ unsigned zz_ord32(float f) {          // order-preserving bits
+    const unsigned u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float zz_unord32(unsigned u) {
+    return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+__device__ __forceinline__ float zz_round_down(double v) {
+    float f = (float)v;
+    if ((double)f > v) f = nextafterf(f, -INFINITY);
+    return f;
+}
+__device__ __forceinline__ unsigned long long zz_lane_lt_mask() {
+    const int l = threadIdx.x & 63;
+    return l ? (~0ull >> (64 - l)) : 0ull;
+}
+
+// lfm sigmoid score of a logit: 1/(1+expf(-v)) with the exponential evaluated in
+// double and rounded once; glibc's expf is within 1 ulp of that
+__device__ __forceinline__ float zz_sigmoid_score(double logit) {
+    const float v = (float)logit;
+    const float ex = (float)exp(-(double)v);
+    return 1.0f / (1.0f + ex);
+}
+
+// The reference's gemma logit of expert e for router input xn: in-order fp32 sum
+// of the rounded products, then + bias. Every lane computes the same chain.
+__device__ float zz_gemma_chain(const float *w, const float *xn, int D, const float *bias, int e) {
+    const int l = threadIdx.x & 63;
+    float v = 0.0f;
+    for (int i0 = 0; i0 < D; i0 += 64) {                     // D % 64 == 0
+        const float p = w[i0 + l] * xn[i0 + l];
+        const int pi = __float_as_int(p);
+#pragma unroll
+        for (int k = 0; k < 64; k++) v = v + __int_as_float(__builtin_amdgcn_readlane(pi, k));
+    }
+    if (bias) v = v + bias[e];
+    return v;
+}
+
+template <int EPL>
+__device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds) {
+    ZzTopkWaveHdr &h = *(ZzTopkWaveHdr *)lds;
+    const int E = a.E, K = a.K, l = threadIdx.x & 63;
+    unsigned long long *ck = (unsigned long long *)(lds + sizeof(ZzTopkWaveHdr));
+    double *clo = (double *)(ck + E), *chi = clo + E;
+    int *ci = (int *)(chi + E);
+    const double *cen = a.cen + (size_t)s * E, *bnd = a.bnd + (size_t)s * E;
+    const bool sig = a.gating == ZZ_GATE_SIGMOID_BIAS;
+    const unsigned long long ltm = zz_lane_lt_mask();
+
+    // intervals and keys; every load is issued before any is used
+    double cv[EPL], bv[EPL];
+    float bi[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const int e = min(l + 64 * j, E - 1);
+        cv[j] = cen[e];
+        bv[j] = sig ? 0.0 : bnd[e];
+        bi[j] = sig && a.bias ? a.bias[e] : 0.0f;
+    }
+    double lo[EPL], hi[EPL];
+    unsigned long long key[EPL];
+    int width = sig;
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const int e = l + 64 * j;
+        if (sig) {
+            // sel = s + bias within 2 ulp(s) + ulp(sel) of the reference's
+            const float sg = zz_sigmoid_score(cv[j]);
+            const float sel = a.bias ? sg + bi[j] : sg;
+            const double sl = 2.0 * (double)ulp_of(sg) + (double)ulp_of(sel);
+            lo[j] = (double)sel - sl;
+            hi[j] = (double)sel + sl;
+        } else {
+            lo[j] = cv[j] - bv[j];
+            hi[j] = cv[j] + bv[j];
+            width |= bv[j] > 0.0;
+        }
+        if (!(lo[j] == lo[j])) lo[j] = -INFINITY;            // NaN scores never win
+        if (!(hi[j] == hi[j])) hi[j] = -INFINITY;
+        key[j] = e < E ? ((unsigned long long)zz_ord32(zz_round_down(lo[j])) << 32) |
+                             (0xffffffffu - (unsigned)e)
+                       : 0ull;
+        if (e >= E) lo[j] = hi[j] = -INFINITY;
+    }
+    width = __ballot(width) != 0ull;
+
+    // 1. the k-th largest lane maximum (keys are distinct; empty lanes hold 0)
+    unsigned long long mk = 0ull;
+#pragma unroll
+    for (int j = 0; j < EPL; j++) mk = key[j] > mk ? key[j] : mk;
+    h.lmax[l] = mk;
+    if (l < K) {
+        h.idx[l] = l;                                         // valid ids whatever happens
+        h.topv[l] = 0.0f;
+    }
+    zz_wave_sync_lds();
+    int r = 0;
+#pragma unroll 16
+    for (int q = 0; q < 64; q++) r += h.lmax[q] > mk;
+    if (r == K - 1) h.lk = mk;
+    zz_wave_sync_lds();
+    const unsigned long long thr = h.lk;
+
+    // 2. exact k-th largest key among the keys >= thr
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const bool p = key[j] >= thr && key[j] != 0ull;
+        const unsigned long long m = __ballot(p);
+        if (p) ck[c + __popcll(m & ltm)] = key[j];
+        c += __popcll(m);
+    }
+    zz_wave_sync_lds();
+    for (int i = l; i < c; i += 64) {
+        const unsigned long long k = ck[i];
+        int rk = 0;
+        for (int q = 0; q < c; q++) rk += ck[q] > k;
+        if (rk == K - 1) h.lk = k;
+    }
+    zz_wave_sync_lds();
+    const double lk = (double)zz_unord32((unsigned)(h.lk >> 32));
+
+    // 3. candidates: hi >= lk
+    int nc = 0;
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const bool p = l + 64 * j < E && hi[j] >= lk;
+        const unsigned long long m = __ballot(p);
+        if (p) {
+            const int pos = nc + __popcll(m & ltm);
+            ci[pos] = l + 64 * j;
+            clo[pos] = lo[j];
+            chi[pos] = hi[j];
+        }
+        nc += __popcll(m);
+    }
+    zz_wave_sync_lds();
+
+    // 4. contested candidates (exact logits can only tie, which the index order
+    // below resolves as the reference does)
+    int any = 0;
+    if (width) {
+        for (int i = l; i < nc; i += 64) {
+            const double li = clo[i], hi_ = chi[i];
+            int cf = 0;
+            for (int q = 0; q < nc; q++) cf |= (q != i) & (clo[q] <= hi_) & (li <= chi[q]);
+            if (cf) ci[i] = -1 - ci[i];
+            any |= cf;
+        }
+        any = __ballot(any) != 0ull;
+        zz_wave_sync_lds();
+    }
+    int contested = 0;
+    if (any) {
+        if (a.gating == ZZ_GATE_SOFTMAX_PES) {
+            const float *xn = a.xn + (size_t)s * a.D;
+            for (int i = 0; i < nc; i++) {                     // wave-uniform
+                const int ce = ci[i];
+                if (ce >= 0) continue;
+                const int e = -1 - ce;
+                const float v = zz_gemma_chain(a.router + (size_t)e * a.D, xn, a.D, a.bias, e);
+                zz_wave_sync_lds();
+                if (l == 0) {
+                    clo[i] = chi[i] = (double)v;
+                    ci[i] = e;
+                }
+                zz_wave_sync_lds();
+            }
+            if (l == 0) atomicAdd(a.diag + 2, 1u);
+        } else {
+            for (int i = l; i < nc; i += 64)
+                if (ci[i] < 0) ci[i] = -1 - ci[i];
+            contested = sig;
+            zz_wave_sync_lds();
+        }
+    }
+
+    // 5. rank candidates by (centre desc, index asc)
+    for (int i = l; i < nc; i += 64) {
+        const int e = ci[i];
+        const double me = 0.5 * (clo[i] + chi[i]);
+        int rk = 0;
+        for (int q = 0; q < nc; q++) {
+            const int f = ci[q];
+            const double mf = 0.5 * (clo[q] + chi[q]);
+            rk += (f != e) & ((mf > me) | ((mf == me) & (f < e)));
+        }
+        if (rk < K) {
+            h.idx[rk] = e;
+            h.topv[rk] = (float)me;
+        }
+    }
+    zz_wave_sync_lds();
+
+    // gate weights: per slot in parallel, their sum serially in slot order as the
+    // reference adds them, then each slot's normalisation
+    float wj = 0.0f, pj = 1.0f;
+    int ej = 0;
+    if (l < K) {
+        ej = h.idx[l];
+        wj = sig ? zz_sigmoid_score(cen[ej]) : expf(h.topv[l] - h.topv[0]);
+        if (a.gating == ZZ_GATE_SOFTMAX_PES) pj = a.pes[ej];
+    }
+    float sum = 0.0f;
+    for (int j = 0; j < K; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wj), j));
+    if (l < K) {
+        float out;
+        if (a.gating == ZZ_GATE_SOFTMAX_PES) {                     // gemma4.c:609-612
+            out = (wj / sum) * pj;
+        } else if (sig) {                                          // lfm25.c:661-667
+            float t = wj;
+            if (a.norm_topk) t /= (sum + 1e-6f);
+            out = t * a.routed_scaling;
+        } else {                                                   // maple.c:596-600
+            float t = wj;
+            if (a.norm_topk) t /= (sum + 1e-20f);
+            out = t;
+        }
+        a.eidx[(size_t)s * K + l] = ej;
+        a.ewt[(size_t)s * K + l] = out;
+        if (a.topv) a.topv[(size_t)s * K + l] = h.topv[l];
+    }
+    if (l == 0 && sig) {
+        if (a.contested) a.contested[s] = contested;
+        if (contested) atomicAdd(a.diag + 3, 1u);
+    }
+}
+
+// experts per lane of zz_topk_wave for E experts
+__host__ __device__ inline int zz_topk_epl(int E) { return E <= 64 ? 1 : (E <= 128 ? 2 : (E <= 256 ? 4 : 8)); }
+
+// zz_topk_wave with the lane count chosen at run time
+__device__ __forceinline__ void zz_topk_wave_any(const ZzTopkArgs &a, int s, char *lds) {
+    switch (zz_topk_epl(a.E)) {
+    case 1: zz_topk_wave<1>(a, s, lds); break;
+    case 2: zz_topk_wave<2>(a, s, lds); break;
+    case 4: zz_topk_wave<4>(a, s, lds); break;
+    default: zz_topk_wave<8>(a, s, lds); break;
+    }
+}
