@@ -39,6 +39,19 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (scaled by a known-size copy), or None when absent."""
+    p = os.path.join(HERE, "profiles", "ffn_mfma_gemma_s512_traffic.md")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == kernel:
+            return float(f[2])
+    return None
+
+
 def build_layers(zz, torch, n_layers, seed):
     """n_layers Gemma layers. Experts: N(0, 0.02) weights drawn on the device and
     quantised by zz_quantize (bit-exact q40_quant_row); router/norms on the host."""
@@ -201,6 +214,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="only run one plain device-to-device copy of this many MiB (the "
+                         "known-size kernel that scales FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -210,6 +226,15 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.calib_copy_mb:
+        n = args.calib_copy_mb << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty(n, dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {n} bytes device to device")
+        return
     import zunzuncito_amd as zz
     name = zz.init()
     log("device:", name)
@@ -270,7 +295,7 @@ def main():
                    "tokens_per_step": S, "layers": len(layers), "mean_union_experts": r["nu"]},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None, "algorithmic_bytes": r["bytes"][dom],
+                     "traffic": measured_traffic(dom), "algorithmic_bytes": r["bytes"][dom],
                      "kernel_us": dom_us},
         "layer_roofline": {"bound": "hbm", "algorithmic_bytes": r["bytes"]["layer"],
                            "achieved": r["bytes"]["layer"] / step_s / 1e9,

@@ -237,8 +237,8 @@ __device__ __forceinline__ void zz_mfma_kloop_n(const ZzACursor<FMT> &A, int nb,
 }
 
 template <int FMT>
-__device__ __forceinline__ void zz_up_body(const ZzFfnArgs &a, const ZzItem &item) {
-    const int rb = blockIdx.x, tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+__device__ __forceinline__ void zz_up_body(const ZzFfnArgs &a, const ZzItem &item, int rb) {
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
     const ZzTensor &T = w < 2 ? a.lay.gate : a.lay.up;
     const int g16 = rb * 2 + (w & 1);
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
@@ -288,10 +288,10 @@ __device__ __forceinline__ void zz_up_body(const ZzFfnArgs &a, const ZzItem &ite
 }
 
 template <int FMT>
-__device__ __forceinline__ void zz_down_body(const ZzFfnArgs &a, const ZzItem &item) {
+__device__ __forceinline__ void zz_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt) {
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
     const ZzTensor &T = a.lay.down;
-    const int g16 = blockIdx.x * 4 + w;
+    const int g16 = rt * 4 + w;
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
     const int MI = a.MI, nb = MI / ZZ_BLK, n = item.n;
     __shared__ ZzStage st[2];
@@ -316,24 +316,41 @@ __device__ __forceinline__ void zz_down_body(const ZzFfnArgs &a, const ZzItem &i
     }
 }
 
+// XCD-aware work order. Workgroup g of a launch runs on XCD g % 8 (round-robin
+// dispatch), and each XCD has its own L2. All row tiles of one work item read the
+// same activations, so they are given workgroup ids of one residue mod 8: the item
+// stays in one L2 and its row tiles run back to back. Item i goes to XCD i % 8 as
+// that XCD's (i / 8)-th item; ids past the last item exit.
+#define ZZ_XCDS 8
+__device__ __forceinline__ void zz_xcd_tile(int ntiles, int *item, int *tile) {
+    const int g = blockIdx.x, x = g % ZZ_XCDS, k = g / ZZ_XCDS;
+    *item = (k / ntiles) * ZZ_XCDS + x;
+    *tile = k % ntiles;
+}
+__host__ __device__ inline unsigned zz_xcd_grid(int max_items, int ntiles) {
+    return (unsigned)((max_items + ZZ_XCDS - 1) / ZZ_XCDS * ZZ_XCDS * ntiles);
+}
+
 // gate and up share one format in these instantiations (the host checks)
 template <int FMT>
 __global__ __launch_bounds__(256) void zz_up_mfma_kernel(ZzFfnArgs a) {
-    const int it = blockIdx.y;
+    int it, rb;
+    zz_xcd_tile(a.MI / 32, &it, &rb);
     if (it >= a.meta[1]) return;
-    zz_up_body<FMT>(a, a.items[it]);
+    zz_up_body<FMT>(a, a.items[it], rb);
 }
 
 template <int FMT>
 __global__ __launch_bounds__(256) void zz_down_mfma_kernel(ZzFfnArgs a) {
-    const int it = blockIdx.y;
+    int it, rt;
+    zz_xcd_tile(a.D / 64, &it, &rt);
     if (it >= a.meta[1]) return;
-    zz_down_body<FMT>(a, a.items[it]);
+    zz_down_body<FMT>(a, a.items[it], rt);
 }
 
 int zz_launch_up_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st) {
     if (a.lay.gate.fmt != a.lay.up.fmt) return 0;
-    dim3 g(a.MI / 32, max_items);
+    dim3 g(zz_xcd_grid(max_items, a.MI / 32));
     switch (a.lay.gate.fmt) {
     case ZZ_FMT_Q40: hipLaunchKernelGGL(zz_up_mfma_kernel<ZZ_FMT_Q40>, g, dim3(256), 0, st, a); break;
     case ZZ_FMT_Q80: hipLaunchKernelGGL(zz_up_mfma_kernel<ZZ_FMT_Q80>, g, dim3(256), 0, st, a); break;
@@ -343,7 +360,7 @@ int zz_launch_up_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st) {
 }
 
 int zz_launch_down_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st) {
-    dim3 g(a.D / 64, max_items);
+    dim3 g(zz_xcd_grid(max_items, a.D / 64));
     switch (a.lay.down.fmt) {
     case ZZ_FMT_Q40: hipLaunchKernelGGL(zz_down_mfma_kernel<ZZ_FMT_Q40>, g, dim3(256), 0, st, a); break;
     case ZZ_FMT_Q80: hipLaunchKernelGGL(zz_down_mfma_kernel<ZZ_FMT_Q80>, g, dim3(256), 0, st, a); break;
