@@ -29,8 +29,6 @@ void zz_set_error(const char *fmt, ...) {
     } while (0)
 
 static int g_ready = 0;
-// batches of at least this many tokens take the matrix-core FFN (ZZ_MFMA_MIN_S)
-static int g_mfma_min_s = 16;
 // batches of at most this many tokens take the three-launch decode path
 // (ZZ_DECODE_MAX_S, 0 turns it off; never above ZZ_DEC_MAXS)
 static int g_dec_max_s = ZZ_DEC_MAXS;
@@ -60,8 +58,6 @@ extern "C" int gpu_init(void) {
     ZZ_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     ZZ_CHECK(hipMalloc(&g_diag, 16 * sizeof(unsigned)));
     ZZ_CHECK(hipMemset(g_diag, 0, 16 * sizeof(unsigned)));
-    const char *ms = getenv("ZZ_MFMA_MIN_S");
-    if (ms && atoi(ms) > 0) g_mfma_min_s = atoi(ms);
     const char *dm = getenv("ZZ_DECODE_MAX_S");
     if (dm) g_dec_max_s = atoi(dm) < 0 ? 0 : (atoi(dm) > ZZ_DEC_MAXS ? ZZ_DEC_MAXS : atoi(dm));
     g_ready = 1;
@@ -459,11 +455,10 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
     ta.xn = w.xn; ta.bias = d.use_bias ? L->bias : nullptr; ta.pes = L->pes; ta.eidx = w.eidx;
     ta.ewt = w.ewt; ta.topv = w.topv; ta.contested = w.contested; ta.diag = g_diag;
 
-    // many tokens per expert: 64-token items on the matrix cores; smaller
-    // batches: 8-token items on the dot4 GEMV
-    const bool mfma = S >= g_mfma_min_s && d.fmt_gate == d.fmt_up;
+    // decode-sized batches take the GEMV path; larger ones the matrix cores, on
+    // work items of up to ZZ_MMA_TOKENS tokens of one expert
     const bool dec = S <= g_dec_max_s;
-    const int tch = mfma ? 64 : 8;
+    const int tch = dec ? ZZ_DEC_MAXS : ZZ_MMA_TOKENS;
     ZzDispatchArgs da;
     da.P = P; da.E = d.E; da.K = d.K; da.tch = tch; da.eidx = w.eidx; da.ewt = w.ewt;
     da.ptok = w.ptok; da.pslot = w.pslot; da.pwt = w.pwt; da.ppos = w.ppos; da.uniq = w.uniq;
@@ -496,13 +491,8 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
             ZZ_FAIL("decode post-norm launch failed");
         return 1;
     }
-    if (mfma) {
-        if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_up_mfma(fa, max_items, st))) ZZ_FAIL("ffn_up launch failed");
-        if (!(ProfScope(ZZ_K_FFN_DOWN, st), zz_launch_down_mfma(fa, max_items, st))) ZZ_FAIL("ffn_down launch failed");
-    } else {
-        if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_ffn_up(fa, max_items, st))) ZZ_FAIL("ffn_up launch failed");
-        if (!(ProfScope(ZZ_K_FFN_DOWN, st), zz_launch_ffn_down(fa, max_items, st))) ZZ_FAIL("ffn_down launch failed");
-    }
+    if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_up_mfma(fa, max_items, st))) ZZ_FAIL("ffn_up launch failed");
+    if (!(ProfScope(ZZ_K_FFN_DOWN, st), zz_launch_down_mfma(fa, max_items, st))) ZZ_FAIL("ffn_down launch failed");
 
     ZzCombineArgs ca;
     ca.D = d.D; ca.K = d.K; ca.gemma = gemma; ca.eps = d.eps; ca.y = w.y; ca.ppos = w.ppos;

@@ -58,15 +58,43 @@ struct ZzTensor {
 __host__ __device__ __forceinline__ int zz_nblk(const ZzTensor &T) {
     return T.fmt == ZZ_FMT_TQ2 ? T.I / 64 : T.I / ZZ_BLK;
 }
+
+// q4_0 / q8_0 payload, matrix-core lane order. Rows are grouped by 16 (g = row/16)
+// and the 32-weight blocks of a row by 4 (chunk = b/4; the last chunk of a row holds
+// 2 when I/32 % 4 == 2). Lane l = 16*qq + r of a chunk holds, for row 16g + r, the
+// weights k = 8qq..8qq+7 of every block of the chunk, ZZ_LB bytes per block:
+//   q8_0: those 8 int8 in order;
+//   q4_0: 4 bytes, byte m = nibble(8qq+m) | nibble(8qq+m+4) << 4.
+// A lane's bytes for the blocks of one chunk are contiguous (one 16/32-byte load),
+// and a chunk is 64 lanes x its blocks x ZZ_LB bytes. This is the A operand layout of
+// v_mfma_i32_16x16x32_i8 (lane l: row l%16, k = 8*(l/16)..+7). The fp16 block
+// scales of a chunk are ordered [row][block]: one row's scales of a chunk are
+// contiguous, and so are 4 consecutive rows'. The plane sizes equal the reference
+// tensor's payload and scale bytes.
+__host__ __device__ __forceinline__ int zz_lb(const ZzTensor &T) { return T.fmt == ZZ_FMT_Q80 ? 8 : 4; }
+// blocks in the chunk holding block b (4, or 2 for a short last chunk)
+__host__ __device__ __forceinline__ int zz_cbs(const ZzTensor &T, int b) {
+    const int left = T.I / ZZ_BLK - (b & ~3);
+    return left < 4 ? left : 4;
+}
+// byte offset of lane `lane`'s ZZ_LB bytes of block b in row group g
+__host__ __device__ __forceinline__ int64_t zz_qlane(const ZzTensor &T, int g, int b, int lane) {
+    const int nb = T.I / ZZ_BLK, lb = zz_lb(T);
+    return T.off_q + ((int64_t)g * nb + (b & ~3)) * 64 * lb + (int64_t)lane * zz_cbs(T, b) * lb + (b & 3) * lb;
+}
+// byte offset of the fp16 scale of row 16g + r, block b
+__host__ __device__ __forceinline__ int64_t zz_sidx(const ZzTensor &T, int g, int b, int r) {
+    const int nb = T.I / ZZ_BLK;
+    return T.off_s + ((int64_t)g * nb + (b & ~3)) * 32 + (r * zz_cbs(T, b) + (b & 3)) * 2;
+}
+// tq2 codes: 16-row groups, each a run of the 16 rows' 16-byte 64-weight groups in
+// the reference byte order (byte k: weights k, k+16, k+32, k+48 at bits 0, 2, 4, 6)
+__host__ __device__ __forceinline__ int64_t zz_tq2off(const ZzTensor &T, int row, int gp) {
+    return T.off_q + (((int64_t)(row >> 4) * (T.I / 64) + gp) * 16 + (row & 15)) * 16;
+}
+// payload bytes per row and 32-weight block (q4_0 16, q8_0 32)
 __host__ __device__ __forceinline__ int zz_pbytes(const ZzTensor &T) {
     return T.fmt == ZZ_FMT_Q80 ? 32 : 16;
-}
-// byte offset of row `row`, block `b` payload; of its fp16 scale (q4_0/q8_0)
-__host__ __device__ __forceinline__ int64_t zz_qoff(const ZzTensor &T, int row, int b) {
-    return T.off_q + (((int64_t)(row >> 4) * zz_nblk(T) + b) * 16 + (row & 15)) * zz_pbytes(T);
-}
-__host__ __device__ __forceinline__ int64_t zz_soff(const ZzTensor &T, int row, int b) {
-    return T.off_s + (((int64_t)(row >> 4) * zz_nblk(T) + b) * 16 + (row & 15)) * 2;
 }
 
 struct ZzLayout {        // byte layout of one repacked expert, all 256-aligned

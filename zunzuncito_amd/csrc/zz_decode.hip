@@ -179,14 +179,15 @@ __global__ __launch_bounds__(256) void zz_dec_gate_kernel(ZzDecRouteArgs a) {
 }
 
 // ------------------------------------------------------------------ gate/up
-// grid (MI/32, items): the workgroup owns hidden rows 32*blockIdx.x .. +31 of one
-// expert item (<= ZZ_DEC_MAXS tokens). Waves 0-3 take the 32 gate rows, waves 4-7
-// the 32 up rows, 8 lanes per row; lane `sub` takes blocks sub, sub+8, ... and
-// issues DU_J of them at once, before the activations are staged in LDS, so the
-// weight stream is in flight from the first cycle.
-#define DU_J 12
+// grid (MI/32, items), 512 threads. The workgroup owns hidden rows 32*rb..+31 of one
+// expert item (<= ZZ_DEC_MAXS tokens): row groups 2rb, 2rb+1 of gate and of up.
+// Wave w = 4*h + q takes row group q (0, 1 gate; 2, 3 up) and half h of the K range.
+// Lane l = 16*qq + r is the slot table's lane: row r of the group, weights
+// 8qq..8qq+7 of every block, so one chunk of 4 blocks is one contiguous 16-byte
+// (q4_0) or 32-byte (q8_0) load; tq2 lanes take whole 64-groups of row r. A lane
+// issues all its weight loads before the activations are staged in LDS.
+#define DU_C 12          // chunks (tq2: groups) per lane issued together
 
-// one workgroup-wide staging of the item's activations into LDS
 struct ZzDecStage {
     __attribute__((aligned(16))) int8_t xq[DEC_MAXS][ZZ_MAXD];
     float xs[DEC_MAXS][ZZ_MAXD / ZZ_BLK];
@@ -209,47 +210,104 @@ __device__ __forceinline__ void zz_dec_stage(const ZzFfnArgs &a, const ZzItem &i
     __syncthreads();
 }
 
-// Partial dots of one lane for one row: weights of DU_J blocks (tq2: groups) are
-// loaded first, then the activations are staged (once per workgroup), then used.
+// One lane-order chunk of a q4_0 / q8_0 row group: the lane's weight bytes (q4_0 in
+// .a, q8_0 in .a and .b) and its row's fp16 scales, for the chunk's 4 or 2 blocks.
+struct ZzChunk {
+    uint4 a, b;
+    uint2 s;
+};
+
+template <int FMT>
+__device__ __forceinline__ ZzChunk zz_load_chunk(const uint8_t *E, const ZzTensor &T, int g, int c, int l) {
+    ZzChunk k;
+    const int b0 = 4 * c, r = l & 15;
+    const uint8_t *q = E + zz_qlane(T, g, b0, l);
+    const uint8_t *sp = E + zz_sidx(T, g, b0, r);
+    if (zz_cbs(T, b0) == 4) {
+        k.a = ld16(q);
+        k.b = FMT == ZZ_FMT_Q80 ? ld16(q + 16) : make_uint4(0, 0, 0, 0);
+        k.s = *(const uint2 *)sp;
+    } else {                                               // short last chunk: 2 blocks
+        if (FMT == ZZ_FMT_Q80) k.a = ld16(q);
+        else { const uint2 v = *(const uint2 *)q; k.a = make_uint4(v.x, v.y, 0, 0); }
+        k.b = make_uint4(0, 0, 0, 0);
+        k.s = make_uint2(*(const unsigned *)sp, 0);
+    }
+    return k;
+}
+
+// signed int8 weights k = 8qq..8qq+7 of block j of a chunk, and its scale
+template <int FMT>
+__device__ __forceinline__ uint2 zz_chunk_w(const ZzChunk &k, int j) {
+    if (FMT == ZZ_FMT_Q80) {
+        const uint4 v = j < 2 ? k.a : k.b;
+        return (j & 1) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y);
+    }
+    const unsigned w = j == 0 ? k.a.x : (j == 1 ? k.a.y : (j == 2 ? k.a.z : k.a.w));
+    return zz_q4_unpack(w);
+}
+__device__ __forceinline__ float zz_chunk_dw(const ZzChunk &k, int j) {
+    const unsigned v = j < 2 ? k.s.x : k.s.y;
+    return zz_h2f((uint16_t)((j & 1) ? v >> 16 : v & 0xffff));
+}
+
 template <int FMT>
 __device__ __forceinline__ void zz_dec_up_part(const ZzFfnArgs &a, const ZzItem &item, ZzDecStage &st,
-                                               const uint8_t *E, const ZzTensor &T, int row, int sub,
+                                               const uint8_t *E, const ZzTensor &T, int g, int h, int l,
                                                float (&acc)[DEC_MAXS]) {
-    const int nb = a.D / ZZ_BLK, n = item.n;
-    const int nu = FMT == ZZ_FMT_TQ2 ? nb / 2 : nb;          // units: blocks or 64-groups
+    const int nb = a.D / ZZ_BLK, n = item.n, r = l & 15, qq = l >> 4;
 #pragma unroll
     for (int t = 0; t < DEC_MAXS; t++) acc[t] = 0.0f;
-    for (int u0 = 0; u0 < nu; u0 += 8 * DU_J) {
-        uint4 w0[DU_J], w1[DU_J];
-        float dw[DU_J];
+    if (FMT == ZZ_FMT_TQ2) {
+        const int ng = nb / 2;                                  // lane's groups qq + 4h + 8i
+        // wave-uniform trip count (the staging barrier is inside), at least once
+        for (int i0 = 0; 4 * h + 8 * i0 < ng || i0 == 0; i0 += DU_C) {
+            uint4 c[DU_C];
 #pragma unroll
-        for (int j = 0; j < DU_J; j++) {
-            const int u = min(u0 + sub + 8 * j, nu - 1);       // clamped: loads stay in range
-            const uint8_t *qp = E + zz_qoff(T, row, u);
-            w0[j] = ld16(qp);
-            if (FMT == ZZ_FMT_Q80) w1[j] = ld16(qp + 16);
-            if (FMT != ZZ_FMT_TQ2) dw[j] = zz_h2f(*(const uint16_t *)(E + zz_soff(T, row, u)));
+            for (int i = 0; i < DU_C; i++)                     // clamped: loads stay in range
+                c[i] = ld16(E + zz_tq2off(T, 16 * g + r, min(qq + 4 * h + 8 * (i0 + i), ng - 1)));
+            if (i0 == 0) zz_dec_stage(a, item, st);           // every wave passes here once
+#pragma unroll
+            for (int i = 0; i < DU_C; i++) {
+                const int gp = qq + 4 * h + 8 * (i0 + i);
+                if (gp >= ng) continue;
+#pragma unroll
+                for (int t = 0; t < DEC_MAXS; t++) {
+                    if (t >= n) continue;
+                    const int8_t *x = &st.xq[t][gp * 64];
+                    const int d0 = zz_dot_tq2(c[i], 0, ld16(x), ld16(x + 16));
+                    const int d1 = zz_dot_tq2(c[i], 1, ld16(x + 32), ld16(x + 48));
+                    acc[t] = fmaf(st.xs[t][2 * gp], (float)d0, acc[t]);
+                    acc[t] = fmaf(st.xs[t][2 * gp + 1], (float)d1, acc[t]);
+                }
+            }
         }
-        if (u0 == 0) zz_dec_stage(a, item, st);               // uniform: every wave passes here
+        return;
+    }
+    const int nch = (nb + 3) / 4;                               // lane's chunks h + 2i
+    for (int i0 = 0; h + 2 * i0 < nch || i0 == 0; i0 += DU_C) {   // at least once: barrier
+        ZzChunk k[DU_C];
 #pragma unroll
-        for (int j = 0; j < DU_J; j++) {
-            const int u = u0 + sub + 8 * j;
-            if (u >= nu) continue;
+        for (int i = 0; i < DU_C; i++) k[i] = zz_load_chunk<FMT>(E, T, g, min(h + 2 * (i0 + i), nch - 1), l);
+        if (i0 == 0) zz_dec_stage(a, item, st);
 #pragma unroll
-            for (int t = 0; t < DEC_MAXS; t++) {
-                if (t >= n) continue;
-                if (FMT == ZZ_FMT_TQ2) {
-                    const int8_t *x = &st.xq[t][u * 64];
-                    const int d0 = zz_dot_tq2(w0[j], 0, ld16(x), ld16(x + 16));
-                    const int d1 = zz_dot_tq2(w0[j], 1, ld16(x + 32), ld16(x + 48));
-                    acc[t] = fmaf(st.xs[t][2 * u], (float)d0, acc[t]);
-                    acc[t] = fmaf(st.xs[t][2 * u + 1], (float)d1, acc[t]);
-                } else {
-                    const int8_t *x = &st.xq[t][u * ZZ_BLK];
-                    const uint4 x0 = ld16(x), x1 = ld16(x + 16);
-                    const int d = FMT == ZZ_FMT_Q80 ? zz_dot_q80(w0[j], w1[j], x0, x1)
-                                                    : zz_dot_q40(w0[j], x0, x1) - 8 * st.xsum[t][u];
-                    acc[t] = fmaf(dw[j] * st.xs[t][u], (float)d, acc[t]);
+        for (int i = 0; i < DU_C; i++) {
+            const int c = h + 2 * (i0 + i);
+            if (c >= nch) continue;
+            const int cbs = zz_cbs(T, 4 * c);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (j >= cbs) continue;
+                const int b = 4 * c + j;
+                const uint2 w = zz_chunk_w<FMT>(k[i], j);
+                const float dw = zz_chunk_dw(k[i], j);
+#pragma unroll
+                for (int t = 0; t < DEC_MAXS; t++) {
+                    if (t >= n) continue;
+                    const uint2 xv = *(const uint2 *)&st.xq[t][b * ZZ_BLK + 8 * qq];
+                    int d = zz_dot4(w.x, xv.x, 0);
+                    d = zz_dot4(w.y, xv.y, d);
+                    acc[t] = fmaf(dw * st.xs[t][b], (float)d, acc[t]);
                 }
             }
         }
@@ -260,20 +318,27 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzFfnArgs a) {
     const int it = blockIdx.y;
     if (it >= a.meta[1]) return;
     const ZzItem item = a.items[it];
-    const int tid = threadIdx.x, rr = tid >> 3, sub = tid & 7, rb = blockIdx.x;
-    const bool up = rr >= 32;
-    const ZzTensor &T = up ? a.lay.up : a.lay.gate;
-    const int row = rb * 32 + (rr & 31);
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = w >> 2, q = w & 3, rb = blockIdx.x;
+    const ZzTensor &T = q < 2 ? a.lay.gate : a.lay.up;
+    const int g = 2 * rb + (q & 1);
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
     __shared__ ZzDecStage st;
+    __shared__ float part[2][DEC_MAXS][64];
     __shared__ float gu[DEC_MAXS][64];
     __shared__ float hb[DEC_MAXS][ZZ_BLK + 1];
     if (tid < item.n) st.tok[tid] = a.ptok[item.p0 + tid];
     __syncthreads();
     float acc[DEC_MAXS];
-    if (T.fmt == ZZ_FMT_Q40) zz_dec_up_part<ZZ_FMT_Q40>(a, item, st, E, T, row, sub, acc);
-    else if (T.fmt == ZZ_FMT_Q80) zz_dec_up_part<ZZ_FMT_Q80>(a, item, st, E, T, row, sub, acc);
-    else zz_dec_up_part<ZZ_FMT_TQ2>(a, item, st, E, T, row, sub, acc);
+    if (T.fmt == ZZ_FMT_Q40) zz_dec_up_part<ZZ_FMT_Q40>(a, item, st, E, T, g, h, l, acc);
+    else if (T.fmt == ZZ_FMT_Q80) zz_dec_up_part<ZZ_FMT_Q80>(a, item, st, E, T, g, h, l, acc);
+    else zz_dec_up_part<ZZ_FMT_TQ2>(a, item, st, E, T, g, h, l, acc);
+#pragma unroll
+    for (int t = 0; t < DEC_MAXS; t++) {                       // sum over the 4 k-quarters
+        float v = acc[t];
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        if (l < 16) part[h][t][16 * q + l] = v;
+    }
     if (T.fmt == ZZ_FMT_TQ2 && tid < item.n) {      // tq2.h:101-106, serial
         const int nb = a.D / ZZ_BLK;
         double tot = 0.0;
@@ -281,17 +346,15 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzFfnArgs a) {
         st.xt[tid] = (float)tot;
     }
     __syncthreads();
-#pragma unroll
-    for (int t = 0; t < DEC_MAXS; t++) {
-        float v = acc[t];
-        v += __shfl_xor(v, 1, 64);
-        v += __shfl_xor(v, 2, 64);
-        v += __shfl_xor(v, 4, 64);
-        if (T.fmt == ZZ_FMT_TQ2 && t < item.n) {
-            const float alpha = ((const float *)(E + T.off_s))[row];
+    if (tid < item.n * 64) {                                    // token t, gate/up row rr
+        const int t = tid >> 6, rr = tid & 63;
+        float v = part[0][t][rr] + part[1][t][rr];
+        if (T.fmt == ZZ_FMT_TQ2) {
+            const ZzTensor &Tr = rr < 32 ? a.lay.gate : a.lay.up;
+            const float alpha = ((const float *)(E + Tr.off_s))[rb * 32 + (rr & 31)];
             v = alpha * (v - st.xt[t]);                        // tq2.h:154
         }
-        if (sub == 0) gu[t][rr] = v;
+        gu[t][rr] = v;
     }
     __syncthreads();
     if (tid < item.n * ZZ_BLK) {
@@ -312,15 +375,15 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzFfnArgs a) {
 }
 
 // ------------------------------------------------------------------ down + combine
-// grid D/8: the workgroup owns 8 output rows, 32 lanes per row. A row's work is
-// P * nu units (pair, block) -- nu blocks of 32 (q4_0 / q8_0) or 64-groups (tq2)
-// per (token, slot) pair; lane q takes units q, q+32, ..., DD_U at a time with
-// every load issued before any is used. Unit results meet in LDS and each
-// (row, pair) sum runs in block order; the 8 x P expert outputs are then combined
-// per token in slot order, out = fma(w_j, y_j, out) as gemma4.c:652.
-#define DD_RW 8
-#define DD_U 12
-#define DD_UB 1024                    // unit results per row held at once
+// grid D/16: the workgroup owns the 16 output rows of row group g of down. Wave w
+// takes the (token, slot) pairs w, w+4, ... and walks their units (pair, chunk) in
+// order, DD_C units' loads at a time; lane l = 16*qq + r as in the gate/up kernel.
+// A pair's partial dots are summed over the 4 k-quarters when its last unit is
+// done. The pairs' int8 hidden rows are staged in LDS when they fit. The 16 x P
+// expert outputs are then combined per token in slot order, out = fma(w_j, y_j, out)
+// as gemma4.c:652.
+#define DD_C 12
+#define DD_HB 24576                   // LDS bytes for staged hidden rows and scales
 
 struct ZzDecPairs {                 // per (token, slot) pair, flat order s*K + j
     int pos[DEC_MAXS * ZZ_MAXK];    // sorted position: row of hq / hs / hsum
@@ -330,87 +393,104 @@ struct ZzDecPairs {                 // per (token, slot) pair, flat order s*K + 
 template <int FMT>
 __global__ __launch_bounds__(256) void zz_dec_down_kernel(ZzDecDownArgs a) {
     const ZzFfnArgs &f = a.f;
-    const int tid = threadIdx.x, r = tid >> 5, q = tid & 31;
-    const int row = blockIdx.x * DD_RW + r;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r = l & 15, qq = l >> 4;
+    const int g = blockIdx.x;
     const ZzTensor &T = f.lay.down;
     const int MI = f.MI, nb = MI / ZZ_BLK, D = f.D, S = a.S, K = a.K, P = S * K;
-    const int nu = FMT == ZZ_FMT_TQ2 ? nb / 2 : nb;
-    const int PG = min(P, DD_UB / nu);                          // pairs per group, >= 1
+    const int nch = FMT == ZZ_FMT_TQ2 ? (nb / 2 + 3) / 4 : (nb + 3) / 4;   // units per pair
+    const int npw = (P - w + 3) / 4;                            // this wave's pairs
+    const int U = npw * nch;
     __shared__ ZzDecPairs pr;
-    __shared__ float ub[DD_RW][DD_UB];
-    __shared__ float yv[DEC_MAXS * ZZ_MAXK][DD_RW];
+    __shared__ float yv[DEC_MAXS * ZZ_MAXK][16];
     __shared__ float htot[DEC_MAXS * ZZ_MAXK];
+    __shared__ __attribute__((aligned(16))) char hbuf[DD_HB];
+    const bool staged = (size_t)P * (MI + 4 * nb) <= DD_HB;
+    int8_t *sh_q = (int8_t *)hbuf;
+    float *sh_s = (float *)(hbuf + (size_t)P * MI);
     if (tid < P) {
         pr.pos[tid] = a.ppos[tid];
         pr.e[tid] = zz_clamp_e(a.eidx[tid], a.E);
     }
+    __syncthreads();
     if (FMT == ZZ_FMT_TQ2 && tid < P) {            // tq2.h:101-106, serial
-        const size_t p = (size_t)a.ppos[tid];
+        const size_t p = (size_t)pr.pos[tid];
         double t = 0.0;
         for (int b = 0; b < nb; b++) t += (double)f.hs[p * nb + b] * (double)f.hsum[p * nb + b];
         htot[tid] = (float)t;
     }
-    __syncthreads();
-    for (int pg0 = 0; pg0 < P; pg0 += PG) {
-        const int np = min(PG, P - pg0), U = np * nu;
-        for (int u0 = 0; u0 < U; u0 += 32 * DD_U) {
-            uint4 w0[DD_U], w1[DD_U], x0[DD_U], x1[DD_U], x2[DD_U], x3[DD_U];
-            float dw[DD_U], s0[DD_U], s1[DD_U];
-            int hm[DD_U];
+    float acc = 0.0f;
+    int cur = -1;
+    for (int u0 = 0; u0 < U || u0 == 0; u0 += DD_C) {
+        ZzChunk k[DD_C];
+        uint4 c[DD_C];
 #pragma unroll
-            for (int j = 0; j < DD_U; j++) {                     // clamped: loads stay in range
-                const int u = min(u0 + q + 32 * j, U - 1);
-                const int pp = pg0 + u / nu, b = u % nu;
-                const int p = pr.pos[pp];
-                const uint8_t *E = f.experts + (size_t)pr.e[pp] * f.estride;
-                const uint8_t *qp = E + zz_qoff(T, row, b);
-                w0[j] = ld16(qp);
-                if (FMT == ZZ_FMT_TQ2) {
-                    const int8_t *x = f.hq + (size_t)p * MI + b * 64;
-                    x0[j] = ld16(x);
-                    x1[j] = ld16(x + 16);
-                    x2[j] = ld16(x + 32);
-                    x3[j] = ld16(x + 48);
-                    s0[j] = f.hs[(size_t)p * nb + 2 * b];
-                    s1[j] = f.hs[(size_t)p * nb + 2 * b + 1];
-                } else {
-                    if (FMT == ZZ_FMT_Q80) w1[j] = ld16(qp + 16);
-                    dw[j] = zz_h2f(*(const uint16_t *)(E + zz_soff(T, row, b)));
-                    const int8_t *x = f.hq + (size_t)p * MI + b * ZZ_BLK;
-                    x0[j] = ld16(x);
-                    x1[j] = ld16(x + 16);
-                    s0[j] = f.hs[(size_t)p * nb + b];
-                    if (FMT == ZZ_FMT_Q40) hm[j] = f.hsum[(size_t)p * nb + b];
+        for (int i = 0; i < DD_C; i++) {                        // clamped: loads stay in range
+            const int u = min(u0 + i, max(U - 1, 0));
+            const int fp = w + 4 * (u / nch), ch = u % nch;
+            const uint8_t *E = f.experts + (size_t)pr.e[min(fp, P - 1)] * f.estride;
+            if (FMT == ZZ_FMT_TQ2) c[i] = ld16(E + zz_tq2off(T, 16 * g + r, min(qq + 4 * ch, nb / 2 - 1)));
+            else k[i] = zz_load_chunk<FMT>(E, T, g, ch, l);
+        }
+        if (u0 == 0) {                                          // stage the hidden rows once
+            if (staged) {
+                for (int fp = 0; fp < P; fp++) {
+                    const size_t p = (size_t)pr.pos[fp];
+                    for (int i = 16 * tid; i < MI; i += 16 * 256)
+                        *(uint4 *)(sh_q + (size_t)fp * MI + i) = ld16(f.hq + p * MI + i);
+                    for (int b = tid; b < nb; b += 256) sh_s[fp * nb + b] = f.hs[p * nb + b];
                 }
             }
+            __syncthreads();
+        }
 #pragma unroll
-            for (int j = 0; j < DD_U; j++) {
-                const int u = u0 + q + 32 * j;
-                float c;
-                if (FMT == ZZ_FMT_TQ2) {
-                    const int d0 = zz_dot_tq2(w0[j], 0, x0[j], x1[j]);
-                    const int d1 = zz_dot_tq2(w0[j], 1, x2[j], x3[j]);
-                    c = fmaf(s1[j], (float)d1, s0[j] * (float)d0);
-                } else {
-                    const int d = FMT == ZZ_FMT_Q80 ? zz_dot_q80(w0[j], w1[j], x0[j], x1[j])
-                                                    : zz_dot_q40(w0[j], x0[j], x1[j]) - 8 * hm[j];
-                    c = (dw[j] * s0[j]) * (float)d;
+        for (int i = 0; i < DD_C; i++) {
+            const int u = u0 + i;
+            if (u >= U) continue;
+            const int fp = w + 4 * (u / nch), ch = u % nch;
+            if (fp != cur) {                                    // wave-uniform
+                if (cur >= 0) {
+                    acc += __shfl_xor(acc, 16, 64);
+                    acc += __shfl_xor(acc, 32, 64);
+                    if (qq == 0) yv[cur][r] = acc;
                 }
-                if (u < U) ub[r][u] = c;
+                cur = fp;
+                acc = 0.0f;
+            }
+            const size_t p = (size_t)pr.pos[fp];
+            const int8_t *hx = staged ? sh_q + (size_t)fp * MI : f.hq + p * MI;
+            const float *hsx = staged ? sh_s + fp * nb : f.hs + p * nb;
+            if (FMT == ZZ_FMT_TQ2) {
+                const int gp = qq + 4 * ch;
+                if (gp < nb / 2) {
+                    const int8_t *x = hx + gp * 64;
+                    const int d0 = zz_dot_tq2(c[i], 0, ld16(x), ld16(x + 16));
+                    const int d1 = zz_dot_tq2(c[i], 1, ld16(x + 32), ld16(x + 48));
+                    acc = fmaf(hsx[2 * gp], (float)d0, acc);
+                    acc = fmaf(hsx[2 * gp + 1], (float)d1, acc);
+                }
+            } else {
+                const int cbs = zz_cbs(T, 4 * ch);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    if (j >= cbs) continue;
+                    const int b = 4 * ch + j;
+                    const uint2 wv = zz_chunk_w<FMT>(k[i], j);
+                    const uint2 xv = *(const uint2 *)(hx + b * ZZ_BLK + 8 * qq);
+                    int d = zz_dot4(wv.x, xv.x, 0);
+                    d = zz_dot4(wv.y, xv.y, d);
+                    acc = fmaf(zz_chunk_dw(k[i], j) * hsx[b], (float)d, acc);
+                }
             }
         }
-        __syncthreads();
-        for (int t = tid; t < DD_RW * np; t += 256) {             // (row, pair) sums, block order
-            const int rr = t / np, pl = t % np;
-            const float *c = &ub[rr][pl * nu];
-            float y = 0.0f;
-            for (int b = 0; b < nu; b++) y += c[b];
-            yv[pg0 + pl][rr] = y;
-        }
-        __syncthreads();
     }
-    if (tid < S * DD_RW) {
-        const int s = tid / DD_RW, rr = tid % DD_RW, o = blockIdx.x * DD_RW + rr;
+    if (cur >= 0) {
+        acc += __shfl_xor(acc, 16, 64);
+        acc += __shfl_xor(acc, 32, 64);
+        if (qq == 0) yv[cur][r] = acc;
+    }
+    __syncthreads();
+    if (tid < S * 16) {
+        const int s = tid >> 4, rr = tid & 15, o = g * 16 + rr;
         float v = 0.0f;
         for (int j = 0; j < K; j++) {
             const int fp = s * K + j;
@@ -464,7 +544,7 @@ int zz_launch_dec_up(const ZzFfnArgs &a, int max_items, hipStream_t st) {
 }
 
 int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st) {
-    const dim3 grid(a.f.D / DD_RW);
+    const dim3 grid(a.f.D / 16);
     switch (a.f.lay.down.fmt) {
     case ZZ_FMT_Q40: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q40>, grid, dim3(256), 0, st, a); break;
     case ZZ_FMT_Q80: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q80>, grid, dim3(256), 0, st, a); break;

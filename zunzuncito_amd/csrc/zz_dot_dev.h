@@ -45,3 +45,13 @@ __device__ __forceinline__ int zz_dot_tq2(uint4 c, int h, uint4 xa, uint4 xb) {
 }
 
 __device__ __forceinline__ uint4 ld16(const void *p) { return *(const uint4 *)p; }
+
+// bytewise q - 8 of four nibbles held one per byte (0..15 -> -8..7 as int8); the
+// add cannot carry between bytes
+__device__ __forceinline__ unsigned zz_nib_s8(unsigned x) { return (x + 0x78787878u) ^ 0x80808080u; }
+
+// one lane-order q4_0 word (weights k = 8qq..8qq+7 of one block) as 8 signed int8
+// weights q - 8: .x holds k 0..3, .y k 4..7 of the quarter
+__device__ __forceinline__ uint2 zz_q4_unpack(unsigned w) {
+    return make_uint2(zz_nib_s8(w & 0x0F0F0F0Fu), zz_nib_s8((w >> 4) & 0x0F0F0F0Fu));
+}

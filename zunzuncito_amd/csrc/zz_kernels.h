@@ -119,13 +119,12 @@ int zz_launch_prep(const ZzPrepArgs &a, int S, hipStream_t st);
 int zz_launch_logits(const ZzLogitArgs &a, int S, hipStream_t st);
 int zz_launch_topk(const ZzTopkArgs &a, int S, hipStream_t st);
 int zz_launch_dispatch(const ZzDispatchArgs &a, hipStream_t st);
-int zz_launch_ffn_up(const ZzFfnArgs &a, int max_items, hipStream_t st);
-int zz_launch_ffn_down(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_dec_route(const ZzDecRouteArgs &a, hipStream_t st);
 int zz_launch_dec_up(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st);
 int zz_launch_dec_norm(float *out, const float *post_ln, int D, float eps, int S, hipStream_t st);
-// int8-MFMA grouped GEMM versions for work items of up to 64 tokens
+// int8-MFMA grouped GEMM for work items of up to ZZ_MMA_TOKENS tokens
+#define ZZ_MMA_TOKENS 128
 int zz_launch_up_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_down_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_combine(const ZzCombineArgs &a, int S, hipStream_t st);

@@ -1,0 +1,395 @@
+// zz_mma.hip -- grouped expert FFN for batches (S >= 5) on the int8 matrix cores of
+// gfx950 (v_mfma_i32_16x16x32_i8).
+//
+// One MFMA step covers exactly one 32-weight block (K = 32), so its int32 results are
+// the reference's per-block integer dots (q40.h:27 <q_w - 8, q_x>, q8_0's <q_w, q_x>,
+// tq2's <c - 1, x>). Each is scaled by d_w[row,b] * d_x[token,b] into an fp32
+// accumulator, as the reference's per-block FMA does (q40.h:186).
+//
+// Work unit: (item, tile). An item is one expert with up to 128 of its tokens (the
+// dispatch work list); a tile is 64 weight rows: 4 waves x one 16-row group each.
+// Every wave multiplies its rows by all of the item's tokens (up to 8 MFMA tiles of
+// 16 tokens), so each weight fragment is loaded and unpacked once per item.
+//   up:   hidden rows 32*rb..+31: waves 0, 1 the gate groups, waves 2, 3 the up
+//         groups; then h = act(g, u) and its per-token q8_0 quantisation
+//         (gemma4.c:642-645, lfm25.c:712-723, maple.c:665-684) in registers;
+//   down: rows 64*rt..+63 of down; the unweighted y[pair][row] for the combine.
+// The K loop walks the slot table's chunks of 4 blocks. Weights go straight to
+// registers, two chunks ahead: the slot table holds each lane's bytes for a chunk
+// contiguously (zz_common.h). Activations are staged through LDS, one chunk ahead.
+#include "zz_common.h"
+#include "zz_kernels.h"
+#include "zz_dot_dev.h"
+
+typedef int zz_v4i __attribute__((ext_vector_type(4)));
+
+#define MM_TN ZZ_MMA_TOKENS            // tokens per work item: 8 tiles of 16
+// LDS row stride of a staged token: one 4-block chunk (128 bytes) + 8, so the 16
+// tokens a quarter-wave reads fall on distinct banks
+#define MM_XS (4 * ZZ_BLK + 8)
+
+struct MmStage {
+    __attribute__((aligned(16))) int8_t x[MM_TN][MM_XS];
+    float s[4][MM_TN];               // block scales d_x, [block][token]
+};
+
+// One wave's weight operand for one chunk (4 blocks, or 2 in a short last chunk).
+//   q4_0: q = the lane's 4 words (k 8qq..8qq+7 of each block, zz_common.h)
+//   q8_0: q, q2 = the lane's 32 bytes
+//   tq2:  q.xy, q.zw = 8 bytes of row r's 64-groups 2c, 2c+1 (bit planes)
+// s0, s1: fp16 scales of rows 4qq..4qq+3, [row][block] (q4_0, q8_0).
+struct MmA {
+    uint4 q, q2, s0, s1;
+};
+
+template <int FMT>
+__device__ __forceinline__ MmA mm_load_a(const uint8_t *E, const ZzTensor &T, int g, int c, int l) {
+    const int b0 = 4 * c, r = l & 15, qq = l >> 4;
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    MmA A = {z, z, z, z};
+    if (FMT == ZZ_FMT_TQ2) {
+        const int ng = T.I / 64, row = 16 * g + r;
+        const uint2 v0 = *(const uint2 *)(E + zz_tq2off(T, row, 2 * c) + (qq & 1) * 8);
+        const uint2 v1 = *(const uint2 *)(E + zz_tq2off(T, row, min(2 * c + 1, ng - 1)) + (qq & 1) * 8);
+        A.q = make_uint4(v0.x, v0.y, v1.x, v1.y);
+        return A;
+    }
+    const uint8_t *q = E + zz_qlane(T, g, b0, l);
+    const uint8_t *s = E + zz_sidx(T, g, b0, 4 * qq);        // 16-byte aligned
+    if (zz_cbs(T, b0) == 4) {
+        A.q = ld16(q);
+        if (FMT == ZZ_FMT_Q80) A.q2 = ld16(q + 16);
+        A.s0 = ld16(s);
+        A.s1 = ld16(s + 16);
+    } else {                                  // short last chunk: 2 blocks
+        if (FMT == ZZ_FMT_Q80) A.q = ld16(q);
+        else { const uint2 v = *(const uint2 *)q; A.q = make_uint4(v.x, v.y, 0, 0); }
+        A.s0 = ld16(s);
+    }
+    return A;
+}
+
+// A fragment of block j (8 signed int8, k = 8qq..8qq+7 of the lane's row)
+template <int FMT>
+__device__ __forceinline__ long mm_frag(const MmA &A, int j, int l) {
+    if (FMT == ZZ_FMT_Q80) {
+        const uint4 v = j < 2 ? A.q : A.q2;
+        const uint2 w = (j & 1) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y);
+        return (long)((unsigned long)w.x | ((unsigned long)w.y << 32));
+    }
+    if (FMT == ZZ_FMT_Q40) {
+        const unsigned w = j == 0 ? A.q.x : (j == 1 ? A.q.y : (j == 2 ? A.q.z : A.q.w));
+        const uint2 u = zz_q4_unpack(w);
+        return (long)((unsigned long)u.x | ((unsigned long)u.y << 32));
+    }
+    // tq2: block j is half j&1 of group j/2; k 0..15 of a half are bit plane
+    // 2*(j&1), k 16..31 plane 2*(j&1)+1, byte k%16 (tq2.h:46-51)
+    const uint2 v = j < 2 ? make_uint2(A.q.x, A.q.y) : make_uint2(A.q.z, A.q.w);
+    const unsigned sh = 2 * (2 * (j & 1) + ((l >> 4) >> 1));
+    unsigned x = (v.x >> sh) & 0x03030303u, y = (v.y >> sh) & 0x03030303u;
+    x = (x + 0x7F7F7F7Fu) ^ 0x80808080u;          // bytewise c - 1
+    y = (y + 0x7F7F7F7Fu) ^ 0x80808080u;
+    return (long)((unsigned long)x | ((unsigned long)y << 32));
+}
+
+// d_w of rows 4qq+i, block j of the chunk (cbs blocks): halfword i*cbs + j of s0|s1.
+// i and j are compile-time after unrolling; only the full/short chunk choice is not.
+__device__ __forceinline__ unsigned mm_half(const MmA &A, int h) {
+    const int w = h >> 1;
+    const unsigned u = w == 0 ? A.s0.x : w == 1 ? A.s0.y : w == 2 ? A.s0.z : w == 3 ? A.s0.w
+                     : w == 4 ? A.s1.x : w == 5 ? A.s1.y : w == 6 ? A.s1.z : A.s1.w;
+    return (h & 1) ? u >> 16 : u & 0xffff;
+}
+__device__ __forceinline__ float mm_dw(const MmA &A, bool full, int j, int i) {
+    const unsigned h4 = mm_half(A, 4 * i + j), h2 = mm_half(A, 2 * i + j);
+    return zz_h2f((uint16_t)(full ? h4 : h2));
+}
+
+// Activations of one chunk: a thread moves 4 16-byte pieces (token, segment) and
+// two block scales (token, block) per chunk, always the same slots.
+struct MmX {
+    uint4 v[4];
+    float s[2];
+};
+
+struct MmSrc {
+    const int8_t *row[4];            // activation row of each piece's token, or null
+    const float *srow[2];            // scale row of each scale slot's token, or null
+    int seg[4], kb[2];
+};
+
+__device__ __forceinline__ void mm_load_x(const MmSrc &src, int c, int cbs, MmX &x) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (src.row[k] && src.seg[k] < 2 * cbs) v = ld16(src.row[k] + c * 4 * ZZ_BLK + 16 * src.seg[k]);
+        x.v[k] = v;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) x.s[k] = src.srow[k] && src.kb[k] < cbs ? src.srow[k][4 * c + src.kb[k]] : 0.0f;
+}
+
+__device__ __forceinline__ void mm_store_x(const MmX &x, MmStage &st) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = tid + 256 * k, t = i >> 3, seg = i & 7;
+        uint2 *d = (uint2 *)&st.x[t][16 * seg];
+        d[0] = make_uint2(x.v[k].x, x.v[k].y);
+        d[1] = make_uint2(x.v[k].z, x.v[k].w);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int i = tid + 256 * k;
+        st.s[i >> 7][i & 127] = x.s[k];
+    }
+}
+
+// acc[tt][i] = sum over blocks of d_w * d_x * int32 for row 4qq+i of row group g
+// and token 16tt + l%16, NT tiles. Weights two chunks ahead in registers, activations
+// one chunk ahead through the two LDS stages.
+template <int FMT, int NT>
+__device__ __forceinline__ void mm_kloop(const uint8_t *E, const ZzTensor &T, int g, const MmSrc &src,
+                                         MmStage (&st)[2], float (&acc)[NT][4]) {
+    const int l = threadIdx.x & 63, nb = T.I / ZZ_BLK, nch = (nb + 3) / 4;
+    const zz_v4i zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[t][i] = 0.0f;
+    MmA a0 = mm_load_a<FMT>(E, T, g, 0, l);
+    MmA a1 = mm_load_a<FMT>(E, T, g, min(1, nch - 1), l);
+    MmA a2 = a1;
+    MmX xr;
+    mm_load_x(src, 0, min(4, nb), xr);
+    mm_store_x(xr, st[0]);
+    for (int c = 0; c < nch; c++) {
+        if (c + 2 < nch) a2 = mm_load_a<FMT>(E, T, g, c + 2, l);
+        if (c + 1 < nch) mm_load_x(src, c + 1, min(4, nb - 4 * (c + 1)), xr);
+        __syncthreads();                         // stage c%2 complete; stage (c+1)%2 free
+        const MmStage &S = st[c & 1];
+        const int cbs = min(4, nb - 4 * c);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (j >= cbs) continue;
+            const long fa = mm_frag<FMT>(a0, j, l);
+            float dw[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) dw[i] = FMT == ZZ_FMT_TQ2 ? 1.0f : mm_dw(a0, cbs == 4, j, i);
+            long B[NT];
+            float sx[NT];
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                B[t] = *(const long *)&S.x[16 * t + (l & 15)][j * ZZ_BLK + 8 * (l >> 4)];
+                sx[t] = S.s[j][16 * t + (l & 15)];
+            }
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const zz_v4i r = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa, B[t], zero, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[t][i] = fmaf(dw[i] * sx[t], (float)r[i], acc[t][i]);
+            }
+        }
+        if (c + 1 < nch) mm_store_x(xr, st[(c + 1) & 1]);
+        a0 = a1;
+        a1 = a2;
+    }
+}
+
+// ------------------------------------------------------------------ up
+union MmUpShared {
+    MmStage st[2];
+    struct {
+        float u[32][MM_TN + 1];              // up values, [hidden row][token]
+        float amax[2][MM_TN];
+        int qsum[2][MM_TN];
+    } e;
+};
+
+template <int NT>
+__device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &item, int rb, MmUpShared &sm,
+                                           int *tok) {
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, qq = l >> 4;
+    const ZzTensor &T = w < 2 ? a.lay.gate : a.lay.up;
+    const int g = 2 * rb + (w & 1), n = item.n, D = a.D, nb = D / ZZ_BLK;
+    const uint8_t *E = a.experts + (size_t)item.e * a.estride;
+    if (tid < MM_TN) tok[tid] = tid < n ? a.ptok[item.p0 + tid] : 0;
+    __syncthreads();
+    MmSrc src;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = tid + 256 * k, t = i >> 3;
+        src.row[k] = t < n ? a.xq + (size_t)tok[t] * D : nullptr;
+        src.seg[k] = i & 7;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int i = tid + 256 * k, t = i & 127;
+        src.srow[k] = t < n ? a.xs + (size_t)tok[t] * nb : nullptr;
+        src.kb[k] = i >> 7;
+    }
+    // gate and up may differ in format (q4_0 / q8_0); each wave runs its tensor's loop
+    // (the same number of chunks and barriers either way)
+    float acc[NT][4];
+    if (T.fmt == ZZ_FMT_Q40) mm_kloop<ZZ_FMT_Q40, NT>(E, T, g, src, sm.st, acc);
+    else if (T.fmt == ZZ_FMT_Q80) mm_kloop<ZZ_FMT_Q80, NT>(E, T, g, src, sm.st, acc);
+    else mm_kloop<ZZ_FMT_TQ2, NT>(E, T, g, src, sm.st, acc);
+    if (T.fmt == ZZ_FMT_TQ2) {                   // tq2.h:154, alpha of the row
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float al = ((const float *)(E + T.off_s))[16 * g + 4 * qq + i];
+#pragma unroll
+            for (int t = 0; t < NT; t++) acc[t][i] *= al;
+        }
+    }
+    __syncthreads();                             // the stages are done with
+    if (w >= 2) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) sm.e.u[16 * (w & 1) + 4 * qq + i][16 * t + (l & 15)] = acc[t][i];
+    }
+    __syncthreads();
+    // waves 0, 1: h = act(g, u) for hidden rows 16w + 4qq + i, then the q8_0
+    // quantisation of each token's 32-row block (q40.h:124-138)
+    float amx[NT];
+    if (w < 2) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            float m = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float h = zz_act(a.act, acc[t][i], sm.e.u[16 * w + 4 * qq + i][16 * t + (l & 15)], a.clamp);
+                acc[t][i] = h;
+                m = fmaxf(m, fabsf(h));
+            }
+            m = fmaxf(m, __shfl_xor(m, 16, 64));
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            amx[t] = m;
+            if (qq == 0) sm.e.amax[w][16 * t + l] = m;
+        }
+    }
+    __syncthreads();
+    if (w < 2) {
+        const int nbM = a.MI / ZZ_BLK;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const int tk = 16 * t + (l & 15);
+            const float amax = fmaxf(amx[t], sm.e.amax[w ^ 1][tk]);
+            const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+            unsigned pk = 0;
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float f = rintf(acc[t][i] * id);
+                f = fminf(fmaxf(f, -127.0f), 127.0f);
+                const int qi = (int)f;
+                s += qi;
+                pk |= (unsigned)(qi & 0xff) << (8 * i);
+            }
+            s += __shfl_xor(s, 16, 64);
+            s += __shfl_xor(s, 32, 64);
+            if (qq == 0) sm.e.qsum[w][tk] = s;
+            if (tk < n) {
+                const size_t p = (size_t)item.p0 + tk;
+                *(unsigned *)(a.hq + p * a.MI + rb * ZZ_BLK + 16 * w + 4 * qq) = pk;
+                if (w == 0 && qq == 0) a.hs[p * nbM + rb] = d;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < n) a.hsum[((size_t)item.p0 + tid) * (a.MI / ZZ_BLK) + rb] = sm.e.qsum[0][tid] + sm.e.qsum[1][tid];
+}
+
+// ------------------------------------------------------------------ down
+template <int FMT, int NT>
+__device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, MmStage (&st)[2]) {
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, qq = l >> 4;
+    const ZzTensor &T = a.lay.down;
+    const int g = 4 * rt + w, n = item.n, MI = a.MI, nb = MI / ZZ_BLK;
+    const uint8_t *E = a.experts + (size_t)item.e * a.estride;
+    MmSrc src;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = tid + 256 * k, t = i >> 3;
+        src.row[k] = t < n ? a.hq + ((size_t)item.p0 + t) * MI : nullptr;
+        src.seg[k] = i & 7;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int i = tid + 256 * k, t = i & 127;
+        src.srow[k] = t < n ? a.hs + ((size_t)item.p0 + t) * nb : nullptr;
+        src.kb[k] = i >> 7;
+    }
+    float acc[NT][4];
+    mm_kloop<FMT, NT>(E, T, g, src, st, acc);
+    const int row0 = 16 * g + 4 * qq;
+    float al[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if (FMT == ZZ_FMT_TQ2)
+        for (int i = 0; i < 4; i++) al[i] = ((const float *)(E + T.off_s))[row0 + i];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int tk = 16 * t + (l & 15);
+        if (tk < n)
+            *(float4 *)(a.y + ((size_t)item.p0 + tk) * a.D + row0) =
+                make_float4(acc[t][0] * al[0], acc[t][1] * al[1], acc[t][2] * al[2], acc[t][3] * al[3]);
+    }
+}
+
+// XCD-aware work order. Workgroup g of a launch runs on XCD g % 8 (round-robin
+// dispatch), and each XCD has its own L2. All tiles of one item read the same
+// activations, so they get workgroup ids of one residue mod 8: item i runs on XCD
+// i % 8 as that XCD's (i / 8)-th item, its tiles back to back. Ids past the last
+// item exit.
+#define ZZ_XCDS 8
+__device__ __forceinline__ void zz_xcd_tile(int ntiles, int *item, int *tile) {
+    const int g = blockIdx.x, x = g % ZZ_XCDS, k = g / ZZ_XCDS;
+    *item = (k / ntiles) * ZZ_XCDS + x;
+    *tile = k % ntiles;
+}
+static unsigned zz_xcd_grid(int max_items, int ntiles) {
+    return (unsigned)((max_items + ZZ_XCDS - 1) / ZZ_XCDS * ZZ_XCDS * ntiles);
+}
+
+__global__ __launch_bounds__(256) void zz_up_mma_kernel(ZzFfnArgs a) {
+    int it, rb;
+    zz_xcd_tile(a.MI / 32, &it, &rb);
+    if (it >= a.meta[1]) return;
+    const ZzItem item = a.items[it];
+    __shared__ MmUpShared sm;
+    __shared__ int tok[MM_TN];
+    const int nt = (item.n + 15) / 16;
+    if (nt <= 1) mm_up_body<1>(a, item, rb, sm, tok);
+    else if (nt <= 2) mm_up_body<2>(a, item, rb, sm, tok);
+    else if (nt <= 4) mm_up_body<4>(a, item, rb, sm, tok);
+    else mm_up_body<8>(a, item, rb, sm, tok);
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void zz_down_mma_kernel(ZzFfnArgs a) {
+    int it, rt;
+    zz_xcd_tile(a.D / 64, &it, &rt);
+    if (it >= a.meta[1]) return;
+    const ZzItem item = a.items[it];
+    __shared__ MmStage st[2];
+    const int nt = (item.n + 15) / 16;
+    if (nt <= 1) mm_down_body<FMT, 1>(a, item, rt, st);
+    else if (nt <= 2) mm_down_body<FMT, 2>(a, item, rt, st);
+    else if (nt <= 4) mm_down_body<FMT, 4>(a, item, rt, st);
+    else mm_down_body<FMT, 8>(a, item, rt, st);
+}
+
+int zz_launch_up_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st) {
+    hipLaunchKernelGGL(zz_up_mma_kernel, dim3(zz_xcd_grid(max_items, a.MI / 32)), dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess;
+}
+
+int zz_launch_down_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st) {
+    dim3 g(zz_xcd_grid(max_items, a.D / 64));
+    switch (a.lay.down.fmt) {
+    case ZZ_FMT_Q40: hipLaunchKernelGGL(zz_down_mma_kernel<ZZ_FMT_Q40>, g, dim3(256), 0, st, a); break;
+    case ZZ_FMT_Q80: hipLaunchKernelGGL(zz_down_mma_kernel<ZZ_FMT_Q80>, g, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL(zz_down_mma_kernel<ZZ_FMT_TQ2>, g, dim3(256), 0, st, a); break;
+    }
+    return hipGetLastError() == hipSuccess;
+}
