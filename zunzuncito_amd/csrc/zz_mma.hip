@@ -20,6 +20,7 @@
 #include "zz_common.h"
 #include "zz_kernels.h"
 #include "zz_dot_dev.h"
+#include <type_traits>
 
 typedef int zz_v4i __attribute__((ext_vector_type(4)));
 
@@ -54,18 +55,18 @@ __device__ __forceinline__ MmA mm_load_a(const uint8_t *E, const ZzTensor &T, in
         A.q = make_uint4(v0.x, v0.y, v1.x, v1.y);
         return A;
     }
+    // Branch-free: the same loads on every path (only addresses are selected), so
+    // the compiler's load counters stay exact across the pipelined loops. A short
+    // last chunk (2 blocks) has 8 (q4_0) or 16 (q8_0) bytes per lane and 4 scale
+    // words per lane group; the extra bytes read stay inside the slot (the q plane
+    // is followed by the scale plane) and belong to blocks the loop skips.
+    const bool full = zz_cbs(T, b0) == 4;
     const uint8_t *q = E + zz_qlane(T, g, b0, l);
     const uint8_t *s = E + zz_sidx(T, g, b0, 4 * qq);        // 16-byte aligned
-    if (zz_cbs(T, b0) == 4) {
-        A.q = ld16(q);
-        if (FMT == ZZ_FMT_Q80) A.q2 = ld16(q + 16);
-        A.s0 = ld16(s);
-        A.s1 = ld16(s + 16);
-    } else {                                  // short last chunk: 2 blocks
-        if (FMT == ZZ_FMT_Q80) A.q = ld16(q);
-        else { const uint2 v = *(const uint2 *)q; A.q = make_uint4(v.x, v.y, 0, 0); }
-        A.s0 = ld16(s);
-    }
+    A.q = ld16(q);
+    if (FMT == ZZ_FMT_Q80) A.q2 = ld16(q + (full ? 16 : 0));
+    A.s0 = ld16(s);
+    A.s1 = ld16(s + (full ? 16 : 0));
     return A;
 }
 
@@ -78,6 +79,7 @@ __device__ __forceinline__ long mm_frag(const MmA &A, int j, int l) {
         return (long)((unsigned long)w.x | ((unsigned long)w.y << 32));
     }
     if (FMT == ZZ_FMT_Q40) {
+        // byte m of the word = nibble(8qq + m) | nibble(8qq + m + 4) << 4
         const unsigned w = j == 0 ? A.q.x : (j == 1 ? A.q.y : (j == 2 ? A.q.z : A.q.w));
         const uint2 u = zz_q4_unpack(w);
         return (long)((unsigned long)u.x | ((unsigned long)u.y << 32));
@@ -92,47 +94,79 @@ __device__ __forceinline__ long mm_frag(const MmA &A, int j, int l) {
     return (long)((unsigned long)x | ((unsigned long)y << 32));
 }
 
-// d_w of rows 4qq+i, block j of the chunk (cbs blocks): halfword i*cbs + j of s0|s1.
-// i and j are compile-time after unrolling; only the full/short chunk choice is not.
-__device__ __forceinline__ unsigned mm_half(const MmA &A, int h) {
-    const int w = h >> 1;
+// d_w of row 4qq+i, block j of the chunk, as fp16: halfword i*cbs + j of s0|s1
+// (i, j and the chunk size compile-time, so this is a register and a half select).
+template <bool FULL>
+__device__ __forceinline__ _Float16 mm_dwh(const MmA &A, int j, int i) {
+    const int h = FULL ? 4 * i + j : 2 * i + j, w = h >> 1;
     const unsigned u = w == 0 ? A.s0.x : w == 1 ? A.s0.y : w == 2 ? A.s0.z : w == 3 ? A.s0.w
                      : w == 4 ? A.s1.x : w == 5 ? A.s1.y : w == 6 ? A.s1.z : A.s1.w;
-    return (h & 1) ? u >> 16 : u & 0xffff;
+    return __builtin_bit_cast(_Float16, (unsigned short)((h & 1) ? u >> 16 : u & 0xffff));
 }
-__device__ __forceinline__ float mm_dw(const MmA &A, bool full, int j, int i) {
-    const unsigned h4 = mm_half(A, 4 * i + j), h2 = mm_half(A, 2 * i + j);
-    return zz_h2f((uint16_t)(full ? h4 : h2));
+
+// One chunk: acc[t][i] += d_w * d_x * <w, x> for row 4qq+i of the wave's row group
+// and token 16t + l%16, over the chunk's 4 (FULL) or 2 blocks. X(t, j) is the 8-byte
+// B operand of token tile t, block j; SX(t, j) that token's d_x.
+// Per product: d_w * d_x in one mixed-precision FMA from the fp16 d_w, the int32
+// conversion, the accumulating FMA.
+template <int FMT, int NT, bool FULL, typename XF, typename SF>
+__device__ __forceinline__ void mm_chunk(const MmA &A, int l, float (&acc)[NT][4], XF X, SF SX) {
+    const zz_v4i zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < (FULL ? 4 : 2); j++) {
+        const long fa = mm_frag<FMT>(A, j, l);
+        long B[NT];
+        float sx[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            B[t] = X(t, j);
+            sx[t] = SX(t, j);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const zz_v4i r = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa, B[t], zero, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float s = FMT == ZZ_FMT_TQ2 ? sx[t] : fmaf((float)mm_dwh<FULL>(A, j, i), sx[t], 0.0f);
+                acc[t][i] = fmaf(s, (float)r[i], acc[t][i]);
+            }
+        }
+        // one block at a time: the next block's LDS reads hoisted over this one
+        // would hold NT more operand registers
+        __builtin_amdgcn_sched_barrier(0);
+    }
 }
 
 // Activations of one chunk: a thread moves 4 16-byte pieces (token, segment) and
-// two block scales (token, block) per chunk, always the same slots.
+// two (token, block) scales per chunk, always the same slots.
 struct MmX {
     uint4 v[4];
     float s[2];
 };
 
 struct MmSrc {
-    const int8_t *row[4];            // activation row of each piece's token, or null
-    const float *srow[2];            // scale row of each scale slot's token, or null
+    const int8_t *row[4];            // activation row of each piece's token
+    const float *srow[2];            // d_x row of each scale slot's token
     int seg[4], kb[2];
 };
 
+// No masks: padding tokens of an item read a real token's row (so their columns hold
+// finite values that the epilogues never store), and the segments and scales of a
+// short chunk's missing blocks are clamped into the row and never read back.
+// KP pieces per thread cover tokens 0 .. 32KP-1 (16 NT <= 32 KP).
+template <int KP>
 __device__ __forceinline__ void mm_load_x(const MmSrc &src, int c, int cbs, MmX &x) {
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (src.row[k] && src.seg[k] < 2 * cbs) v = ld16(src.row[k] + c * 4 * ZZ_BLK + 16 * src.seg[k]);
-        x.v[k] = v;
-    }
+    for (int k = 0; k < KP; k++) x.v[k] = ld16(src.row[k] + c * 4 * ZZ_BLK + 16 * min(src.seg[k], 2 * cbs - 1));
 #pragma unroll
-    for (int k = 0; k < 2; k++) x.s[k] = src.srow[k] && src.kb[k] < cbs ? src.srow[k][4 * c + src.kb[k]] : 0.0f;
+    for (int k = 0; k < 2; k++) x.s[k] = src.srow[k][4 * c + min(src.kb[k], cbs - 1)];
 }
 
+template <int KP>
 __device__ __forceinline__ void mm_store_x(const MmX &x, MmStage &st) {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < KP; k++) {
         const int i = tid + 256 * k, t = i >> 3, seg = i & 7;
         uint2 *d = (uint2 *)&st.x[t][16 * seg];
         d[0] = make_uint2(x.v[k].x, x.v[k].y);
@@ -145,56 +179,65 @@ __device__ __forceinline__ void mm_store_x(const MmX &x, MmStage &st) {
     }
 }
 
-// acc[tt][i] = sum over blocks of d_w * d_x * int32 for row 4qq+i of row group g
-// and token 16tt + l%16, NT tiles. Weights two chunks ahead in registers, activations
-// one chunk ahead through the two LDS stages.
-template <int FMT, int NT>
+// Weight chunks live in a ring of RING register sets with static indices (the loop
+// body is unrolled RING times, so no register copies): chunk c + RING - 1 is
+// requested at step c, RING - 1 steps before its use. The main loop runs whole
+// rings of full chunks with every load unconditional (clamped past the end); the
+// remaining chunks (fewer than RING + 1, the short one last) run in a tail.
+//
+// Large items: activations one chunk ahead through the two LDS stages, one
+// workgroup barrier per chunk.
+template <int FMT, int NT, int RING>
 __device__ __forceinline__ void mm_kloop(const uint8_t *E, const ZzTensor &T, int g, const MmSrc &src,
                                          MmStage (&st)[2], float (&acc)[NT][4]) {
-    const int l = threadIdx.x & 63, nb = T.I / ZZ_BLK, nch = (nb + 3) / 4;
-    const zz_v4i zero = {0, 0, 0, 0};
+    const int l = threadIdx.x & 63, nb = T.I / ZZ_BLK, nch = (nb + 3) / 4, nfull = nb / 4;
 #pragma unroll
     for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[t][i] = 0.0f;
-    MmA a0 = mm_load_a<FMT>(E, T, g, 0, l);
-    MmA a1 = mm_load_a<FMT>(E, T, g, min(1, nch - 1), l);
-    MmA a2 = a1;
+    constexpr int KP = (NT + 1) / 2;
+    MmA r[RING];
+#pragma unroll
+    for (int i = 0; i < RING - 1; i++) r[i] = mm_load_a<FMT>(E, T, g, min(i, nch - 1), l);
     MmX xr;
-    mm_load_x(src, 0, min(4, nb), xr);
-    mm_store_x(xr, st[0]);
-    for (int c = 0; c < nch; c++) {
-        if (c + 2 < nch) a2 = mm_load_a<FMT>(E, T, g, c + 2, l);
-        if (c + 1 < nch) mm_load_x(src, c + 1, min(4, nb - 4 * (c + 1)), xr);
+    mm_load_x<KP>(src, 0, min(4, nb), xr);
+    mm_store_x<KP>(xr, st[0]);
+    // x of chunk c + 1 is requested before the weight prefetch: the wait for it at
+    // the end of the step (loads complete in order) then leaves the prefetch in flight
+    auto load_x = [&](int c) {
+        const int c1 = min(c + 1, nch - 1);
+        mm_load_x<KP>(src, c1, min(4, nb - 4 * c1), xr);
+    };
+    auto step = [&](int c, const MmA &A, auto full) {
         __syncthreads();                         // stage c%2 complete; stage (c+1)%2 free
         const MmStage &S = st[c & 1];
-        const int cbs = min(4, nb - 4 * c);
+        mm_chunk<FMT, NT, decltype(full)::value>(
+            A, l, acc, [&](int t, int j) { return *(const long *)&S.x[16 * t + (l & 15)][j * ZZ_BLK + 8 * (l >> 4)]; },
+            [&](int t, int j) { return S.s[j][16 * t + (l & 15)]; });
+        mm_store_x<KP>(xr, st[(c + 1) & 1]);     // the last step refills the free stage: harmless
+    };
+    int c0 = 0;
+    for (; c0 + RING <= nfull; c0 += RING) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            if (j >= cbs) continue;
-            const long fa = mm_frag<FMT>(a0, j, l);
-            float dw[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) dw[i] = FMT == ZZ_FMT_TQ2 ? 1.0f : mm_dw(a0, cbs == 4, j, i);
-            long B[NT];
-            float sx[NT];
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                B[t] = *(const long *)&S.x[16 * t + (l & 15)][j * ZZ_BLK + 8 * (l >> 4)];
-                sx[t] = S.s[j][16 * t + (l & 15)];
-            }
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const zz_v4i r = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa, B[t], zero, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[t][i] = fmaf(dw[i] * sx[t], (float)r[i], acc[t][i]);
-            }
+        for (int u = 0; u < RING; u++) {
+            load_x(c0 + u);
+            r[(u + RING - 1) % RING] = mm_load_a<FMT>(E, T, g, min(c0 + u + RING - 1, nch - 1), l);
+            step(c0 + u, r[u], std::true_type());
         }
-        if (c + 1 < nch) mm_store_x(xr, st[(c + 1) & 1]);
-        a0 = a1;
-        a1 = a2;
+    }
+#pragma unroll
+    for (int u = 0; u < RING; u++) {
+        const int c = c0 + u;
+        if (c < nch) {
+            load_x(c);
+            if (u == RING - 1) r[u] = mm_load_a<FMT>(E, T, g, c, l);
+            if (c < nfull) step(c, r[u], std::true_type());
+            else step(c, r[u], std::false_type());
+        }
     }
 }
+
+#define MM_RING(NT) ((NT) <= 4 ? 4 : 2)
 
 // ------------------------------------------------------------------ up
 union MmUpShared {
@@ -213,27 +256,32 @@ __device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &ite
     const ZzTensor &T = w < 2 ? a.lay.gate : a.lay.up;
     const int g = 2 * rb + (w & 1), n = item.n, D = a.D, nb = D / ZZ_BLK;
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
-    if (tid < MM_TN) tok[tid] = tid < n ? a.ptok[item.p0 + tid] : 0;
+    if (tid < MM_TN) tok[tid] = a.ptok[item.p0 + min(tid, n - 1)];
     __syncthreads();
     MmSrc src;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const int i = tid + 256 * k, t = i >> 3;
-        src.row[k] = t < n ? a.xq + (size_t)tok[t] * D : nullptr;
+        src.row[k] = a.xq + (size_t)tok[t] * D;          // tok[t >= n]: token n - 1
         src.seg[k] = i & 7;
     }
 #pragma unroll
     for (int k = 0; k < 2; k++) {
         const int i = tid + 256 * k, t = i & 127;
-        src.srow[k] = t < n ? a.xs + (size_t)tok[t] * nb : nullptr;
+        src.srow[k] = a.xs + (size_t)tok[t] * nb;
         src.kb[k] = i >> 7;
     }
+
     // gate and up may differ in format (q4_0 / q8_0); each wave runs its tensor's loop
     // (the same number of chunks and barriers either way)
     float acc[NT][4];
-    if (T.fmt == ZZ_FMT_Q40) mm_kloop<ZZ_FMT_Q40, NT>(E, T, g, src, sm.st, acc);
-    else if (T.fmt == ZZ_FMT_Q80) mm_kloop<ZZ_FMT_Q80, NT>(E, T, g, src, sm.st, acc);
-    else mm_kloop<ZZ_FMT_TQ2, NT>(E, T, g, src, sm.st, acc);
+    if (T.fmt == ZZ_FMT_Q40) {
+        mm_kloop<ZZ_FMT_Q40, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
+    } else if (T.fmt == ZZ_FMT_Q80) {
+        mm_kloop<ZZ_FMT_Q80, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
+    } else {
+        mm_kloop<ZZ_FMT_TQ2, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
+    }
     if (T.fmt == ZZ_FMT_TQ2) {                   // tq2.h:154, alpha of the row
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -302,8 +350,12 @@ __device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &ite
 }
 
 // ------------------------------------------------------------------ down
+struct MmDownShared {
+    MmStage st[2];
+};
+
 template <int FMT, int NT>
-__device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, MmStage (&st)[2]) {
+__device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, MmDownShared &sm) {
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, qq = l >> 4;
     const ZzTensor &T = a.lay.down;
     const int g = 4 * rt + w, n = item.n, MI = a.MI, nb = MI / ZZ_BLK;
@@ -312,17 +364,18 @@ __device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &i
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const int i = tid + 256 * k, t = i >> 3;
-        src.row[k] = t < n ? a.hq + ((size_t)item.p0 + t) * MI : nullptr;
+        src.row[k] = a.hq + ((size_t)item.p0 + min(t, n - 1)) * MI;
         src.seg[k] = i & 7;
     }
 #pragma unroll
     for (int k = 0; k < 2; k++) {
         const int i = tid + 256 * k, t = i & 127;
-        src.srow[k] = t < n ? a.hs + ((size_t)item.p0 + t) * nb : nullptr;
+        src.srow[k] = a.hs + ((size_t)item.p0 + min(t, n - 1)) * nb;
         src.kb[k] = i >> 7;
     }
+
     float acc[NT][4];
-    mm_kloop<FMT, NT>(E, T, g, src, st, acc);
+    mm_kloop<FMT, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
     const int row0 = 16 * g + 4 * qq;
     float al[4] = {1.0f, 1.0f, 1.0f, 1.0f};
     if (FMT == ZZ_FMT_TQ2)
@@ -371,12 +424,12 @@ __global__ __launch_bounds__(256) void zz_down_mma_kernel(ZzFfnArgs a) {
     zz_xcd_tile(a.D / 64, &it, &rt);
     if (it >= a.meta[1]) return;
     const ZzItem item = a.items[it];
-    __shared__ MmStage st[2];
+    __shared__ MmDownShared sm;
     const int nt = (item.n + 15) / 16;
-    if (nt <= 1) mm_down_body<FMT, 1>(a, item, rt, st);
-    else if (nt <= 2) mm_down_body<FMT, 2>(a, item, rt, st);
-    else if (nt <= 4) mm_down_body<FMT, 4>(a, item, rt, st);
-    else mm_down_body<FMT, 8>(a, item, rt, st);
+    if (nt <= 1) mm_down_body<FMT, 1>(a, item, rt, sm);
+    else if (nt <= 2) mm_down_body<FMT, 2>(a, item, rt, sm);
+    else if (nt <= 4) mm_down_body<FMT, 4>(a, item, rt, sm);
+    else mm_down_body<FMT, 8>(a, item, rt, sm);
 }
 
 int zz_launch_up_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st) {
