@@ -222,61 +222,75 @@ __device__ __forceinline__ int zz_block_excl_scan(int v, int *tmp) {
     return incl - v;
 }
 
+#define DP_PT 16                      // pairs per thread: S*K <= 8192 = 512 * DP_PT
 __global__ __launch_bounds__(512) void zz_dispatch_kernel(ZzDispatchArgs a) {
     extern __shared__ unsigned dsm[];
     __shared__ int cnt[ZZ_MAXE], start[ZZ_MAXE], first[ZZ_MAXE], order[ZZ_MAXE], tmp[512];
-    __shared__ int nu_s;
     const int P = a.P, E = a.E, K = a.K, S = P / K, W = (S + 31) / 32, t = threadIdx.x;
     unsigned *mask = dsm, *wpre = dsm + E * W;
     for (int i = t; i < E * W; i += 512) mask[i] = 0u;
-    for (int e = t; e < E; e += 512) first[e] = 0x7fffffff;
-    __syncthreads();
-    for (int p = t; p < P; p += 512) {
-        int e = a.eidx[p];
-        e = e < 0 || e >= E ? 0 : e;            // never index past the expert tables
-        const int s = p / K;
-        atomicOr(&mask[e * W + (s >> 5)], 1u << (s & 31));
-        atomicMin(&first[e], p);
+    // every pair's expert and weight in registers first: one round of loads
+    int ev[DP_PT];
+    float wv[DP_PT];
+#pragma unroll
+    for (int k = 0; k < DP_PT; k++) {
+        const int p = min(t + 512 * k, P - 1);
+        const int e = a.eidx[p];
+        ev[k] = e < 0 || e >= E ? 0 : e;            // never index past the expert tables
+        wv[k] = a.ewt[p];
     }
     __syncthreads();
+#pragma unroll
+    for (int k = 0; k < DP_PT; k++) {
+        const int p = t + 512 * k, s = p / K;
+        if (p < P) atomicOr(&mask[ev[k] * W + (s >> 5)], 1u << (s & 31));
+    }
+    __syncthreads();
+    // per expert: word prefix counts, the count, and the first pair that routes to
+    // it (its lowest token, that token's slot holding e)
     for (int e = t; e < E; e += 512) {
-        int run = 0;
+        int run = 0, s0 = -1;
         for (int w = 0; w < W; w++) {
+            const unsigned m = mask[e * W + w];
             wpre[e * W + w] = run;
-            run += __popc(mask[e * W + w]);
+            if (s0 < 0 && m) s0 = 32 * w + __ffs(m) - 1;
+            run += __popc(m);
         }
         cnt[e] = run;
+        int f = 0x7fffffff;
+        if (s0 >= 0)
+            for (int j = K - 1; j >= 0; j--) {
+                const int ej = a.eidx[s0 * K + j];
+                if ((ej < 0 || ej >= E ? 0 : ej) == e) f = s0 * K + j;
+            }
+        first[e] = f;
     }
     __syncthreads();
     const int st = zz_block_excl_scan(t < E ? cnt[t] : 0, tmp);
     if (t < E) start[t] = st;
     __syncthreads();
-    for (int p = t; p < P; p += 512) {
-        int e = a.eidx[p];
-        e = e < 0 || e >= E ? 0 : e;
-        const int s = p / K, w = s >> 5, bit = s & 31;
-        const int pos = start[e] + wpre[e * W + w] + __popc(mask[e * W + w] & ((1u << bit) - 1u));
-        a.ptok[pos] = s;
-        a.pslot[pos] = p - s * K;
-        a.pwt[pos] = a.ewt[p];
-        a.ppos[p] = pos;
+#pragma unroll
+    for (int k = 0; k < DP_PT; k++) {
+        const int p = t + 512 * k;
+        if (p < P) {
+            const int e = ev[k], s = p / K, w = s >> 5, bit = s & 31;
+            const int pos = start[e] + wpre[e * W + w] + __popc(mask[e * W + w] & ((1u << bit) - 1u));
+            a.ptok[pos] = s;
+            a.pslot[pos] = p - s * K;
+            a.pwt[pos] = wv[k];
+            a.ppos[p] = pos;
+        }
     }
     // union order: rank the present experts by first-seen pair index
-    for (int e = t; e < E; e += 512) {
-        if (!cnt[e]) continue;
-        const int fe = first[e];
+    const bool present = t < E && cnt[t] != 0;
+    if (present) {
+        const int fe = first[t];
         int r = 0;
 #pragma unroll 8
         for (int f = 0; f < E; f++) r += cnt[f] != 0 && first[f] < fe;
-        order[r] = e;
+        order[r] = t;
     }
-    if (t == 0) {
-        int nu = 0;
-        for (int e = 0; e < E; e++) nu += cnt[e] != 0;
-        nu_s = nu;
-    }
-    __syncthreads();
-    const int nu = nu_s;
+    const int nu = __syncthreads_count(present);
     const int ce = t < nu ? cnt[order[t]] : 0;
     const int nit = (ce + a.tch - 1) / a.tch;
     const int i0 = zz_block_excl_scan(nit, tmp);
