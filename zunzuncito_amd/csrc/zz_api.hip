@@ -166,6 +166,7 @@ struct Workspace {
     float *hs = nullptr;
     int *hsum = nullptr;
     float *y = nullptr;
+    float *hf = nullptr;
     void *block = nullptr;      // one allocation holds everything above
 };
 
@@ -351,7 +352,7 @@ static int ensure_ws(Layer *L, int S) {
     size_t o_uniq = take(4 * (size_t)d.E), o_uoff = take(4 * (size_t)d.E), o_ucnt = take(4 * (size_t)d.E);
     size_t o_meta = take(64), o_items = take(sizeof(ZzItem) * nitems);
     size_t o_hq = take(P * d.MI), o_hs = take(4 * P * nbM), o_hsum = take(4 * P * nbM);
-    size_t o_y = take(4 * P * d.D);
+    size_t o_y = take(4 * P * d.D), o_hf = take(4 * P * d.MI);
     void *blk = nullptr;
     ZZ_CHECK(hipStreamSynchronize(g_stream));
     ZZ_CHECK(hipMalloc(&blk, off));
@@ -367,7 +368,7 @@ static int ensure_ws(Layer *L, int S) {
     w.ppos = (int *)(b + o_ppos); w.pwt = (float *)(b + o_pwt); w.uniq = (int *)(b + o_uniq);
     w.uoff = (int *)(b + o_uoff); w.ucnt = (int *)(b + o_ucnt); w.meta = (int *)(b + o_meta);
     w.items = (ZzItem *)(b + o_items); w.hq = (int8_t *)(b + o_hq); w.hs = (float *)(b + o_hs);
-    w.hsum = (int *)(b + o_hsum); w.y = (float *)(b + o_y);
+    w.hsum = (int *)(b + o_hsum); w.y = (float *)(b + o_y); w.hf = (float *)(b + o_hf);
     ZZ_CHECK(hipStreamSynchronize(g_stream));
     return 1;
 }
@@ -457,7 +458,7 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
 
     // decode-sized batches take the GEMV path; larger ones the matrix cores, on
     // work items of up to ZZ_MMA_TOKENS tokens of one expert
-    const bool dec = S <= g_dec_max_s;
+    const bool dec = S <= g_dec_max_s && zz_dec_fits(S, d.K, d.MI);
     const int tch = dec ? ZZ_DEC_MAXS : ZZ_MMA_TOKENS;
     ZzDispatchArgs da;
     da.P = P; da.E = d.E; da.K = d.K; da.tch = tch; da.eidx = w.eidx; da.ewt = w.ewt;
@@ -479,7 +480,7 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
     fa.D = d.D; fa.MI = d.MI; fa.K = d.K; fa.act = d.act; fa.clamp = d.clamp;
     fa.experts = L->slots; fa.estride = L->lay.bytes; fa.lay = L->lay; fa.items = w.items;
     fa.meta = w.meta; fa.ptok = w.ptok; fa.xq = w.xq; fa.xs = w.xs; fa.xsum = w.xsum; fa.xt = w.xt;
-    fa.hq = w.hq; fa.hs = w.hs; fa.hsum = w.hsum; fa.y = w.y;
+    fa.hq = w.hq; fa.hs = w.hs; fa.hsum = w.hsum; fa.y = w.y; fa.hf = w.hf;
     const int max_items = (P < d.E ? P : d.E) + (P + tch - 1) / tch;
     if (dec) {
         ZzDecDownArgs dd;

@@ -179,13 +179,14 @@ __global__ __launch_bounds__(256) void zz_dec_gate_kernel(ZzDecRouteArgs a) {
 }
 
 // ------------------------------------------------------------------ gate/up
-// grid (MI/32, items), 512 threads. The workgroup owns hidden rows 32*rb..+31 of one
-// expert item (<= ZZ_DEC_MAXS tokens): row groups 2rb, 2rb+1 of gate and of up.
-// Wave w = 4*h + q takes row group q (0, 1 gate; 2, 3 up) and half h of the K range.
-// Lane l = 16*qq + r is the slot table's lane: row r of the group, weights
-// 8qq..8qq+7 of every block, so one chunk of 4 blocks is one contiguous 16-byte
-// (q4_0) or 32-byte (q8_0) load; tq2 lanes take whole 64-groups of row r. A lane
-// issues all its weight loads before the activations are staged in LDS.
+// grid (MI/16, items), 256 threads. The workgroup owns hidden rows 16j..16j+15 of
+// one expert item (<= ZZ_DEC_MAXS tokens); wave w takes row group j of gate (w even)
+// or up (w odd) over half w/2 of the K range. Lane l = 16*qq + r is the slot
+// table's lane: row r of the group, weights 8qq..8qq+7 of every block, so one chunk
+// of 4 blocks is one contiguous 16-byte (q4_0) or 32-byte (q8_0) load; tq2 lanes take
+// whole 64-groups of row r. A lane issues all its weight loads before the
+// activations are staged in LDS. The output is h = act(g, u) in fp32; its q8_0
+// quantisation happens where it is consumed (the down kernel).
 #define DU_C 12          // chunks (tq2: groups) per lane issued together
 
 struct ZzDecStage {
@@ -314,30 +315,27 @@ __device__ __forceinline__ void zz_dec_up_part(const ZzFfnArgs &a, const ZzItem 
     }
 }
 
-__global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzFfnArgs a) {
+__global__ __launch_bounds__(256) void zz_dec_up_kernel(ZzFfnArgs a) {
     const int it = blockIdx.y;
     if (it >= a.meta[1]) return;
     const ZzItem item = a.items[it];
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = w >> 2, q = w & 3, rb = blockIdx.x;
-    const ZzTensor &T = q < 2 ? a.lay.gate : a.lay.up;
-    const int g = 2 * rb + (q & 1);
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = w >> 1, q = w & 1, j = blockIdx.x;
+    const ZzTensor &T = q ? a.lay.up : a.lay.gate;
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
     __shared__ ZzDecStage st;
-    __shared__ float part[2][DEC_MAXS][64];
-    __shared__ float gu[DEC_MAXS][64];
-    __shared__ float hb[DEC_MAXS][ZZ_BLK + 1];
+    __shared__ float part[2][2][DEC_MAXS][16];      // [half][gate/up][token][row]
     if (tid < item.n) st.tok[tid] = a.ptok[item.p0 + tid];
     __syncthreads();
     float acc[DEC_MAXS];
-    if (T.fmt == ZZ_FMT_Q40) zz_dec_up_part<ZZ_FMT_Q40>(a, item, st, E, T, g, h, l, acc);
-    else if (T.fmt == ZZ_FMT_Q80) zz_dec_up_part<ZZ_FMT_Q80>(a, item, st, E, T, g, h, l, acc);
-    else zz_dec_up_part<ZZ_FMT_TQ2>(a, item, st, E, T, g, h, l, acc);
+    if (T.fmt == ZZ_FMT_Q40) zz_dec_up_part<ZZ_FMT_Q40>(a, item, st, E, T, j, h, l, acc);
+    else if (T.fmt == ZZ_FMT_Q80) zz_dec_up_part<ZZ_FMT_Q80>(a, item, st, E, T, j, h, l, acc);
+    else zz_dec_up_part<ZZ_FMT_TQ2>(a, item, st, E, T, j, h, l, acc);
 #pragma unroll
     for (int t = 0; t < DEC_MAXS; t++) {                       // sum over the 4 k-quarters
         float v = acc[t];
         v += __shfl_xor(v, 16, 64);
         v += __shfl_xor(v, 32, 64);
-        if (l < 16) part[h][t][16 * q + l] = v;
+        if (l < 16) part[h][q][t][l] = v;
     }
     if (T.fmt == ZZ_FMT_TQ2 && tid < item.n) {      // tq2.h:101-106, serial
         const int nb = a.D / ZZ_BLK;
@@ -346,78 +344,60 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzFfnArgs a) {
         st.xt[tid] = (float)tot;
     }
     __syncthreads();
-    if (tid < item.n * 64) {                                    // token t, gate/up row rr
-        const int t = tid >> 6, rr = tid & 63;
-        float v = part[0][t][rr] + part[1][t][rr];
-        if (T.fmt == ZZ_FMT_TQ2) {
-            const ZzTensor &Tr = rr < 32 ? a.lay.gate : a.lay.up;
-            const float alpha = ((const float *)(E + Tr.off_s))[rb * 32 + (rr & 31)];
-            v = alpha * (v - st.xt[t]);                        // tq2.h:154
+    if (tid < item.n * 16) {                                    // token t, hidden row 16j + r
+        const int t = tid >> 4, r = tid & 15;
+        float g = part[0][0][t][r] + part[1][0][t][r];
+        float u = part[0][1][t][r] + part[1][1][t][r];
+        if (T.fmt == ZZ_FMT_TQ2) {                              // tq2.h:154
+            g = ((const float *)(E + a.lay.gate.off_s))[16 * j + r] * (g - st.xt[t]);
+            u = ((const float *)(E + a.lay.up.off_s))[16 * j + r] * (u - st.xt[t]);
         }
-        gu[t][rr] = v;
-    }
-    __syncthreads();
-    if (tid < item.n * ZZ_BLK) {
-        const int t = tid >> 5, r = tid & 31;
-        hb[t][r] = zz_act(a.act, gu[t][r], gu[t][32 + r], a.clamp);
-    }
-    __syncthreads();
-    if (tid < item.n) {                                         // one thread per token block
-        float v[ZZ_BLK];
-#pragma unroll
-        for (int r = 0; r < ZZ_BLK; r++) v[r] = hb[tid][r];
-        const size_t p = (size_t)item.p0 + tid;
-        int qs;
-        const float d = zz_quant_block(v, a.hq + p * a.MI + rb * ZZ_BLK, &qs);
-        a.hs[p * (a.MI / ZZ_BLK) + rb] = d;
-        a.hsum[p * (a.MI / ZZ_BLK) + rb] = qs;
+        a.hf[((size_t)item.p0 + t) * a.MI + 16 * j + r] = zz_act(a.act, g, u, a.clamp);
     }
 }
 
 // ------------------------------------------------------------------ down + combine
-// grid D/16: the workgroup owns the 16 output rows of row group g of down. Wave w
-// takes the (token, slot) pairs w, w+4, ... and walks their units (pair, chunk) in
-// order, DD_C units' loads at a time; lane l = 16*qq + r as in the gate/up kernel.
-// A pair's partial dots are summed over the 4 k-quarters when its last unit is
-// done. The pairs' int8 hidden rows are staged in LDS when they fit. The 16 x P
-// expert outputs are then combined per token in slot order, out = fma(w_j, y_j, out)
-// as gemma4.c:652.
+// grid D/16, 512 threads: the workgroup owns the 16 output rows of row group g of
+// down. First every (token, slot) pair's hidden h is quantised to q8_0 into LDS
+// (gemma4.c:646, the same rounding as zz_quant_block; workgroup 0 also writes the
+// codes out). Wave w takes the pairs w, w+8, ... and walks their units (pair,
+// chunk) in order, DD_C units' loads at a time; lane l = 16*qq + r as in the
+// gate/up kernel. A pair's partial dots are summed over the 4 k-quarters when its
+// last unit is done. The 16 x P expert outputs are then combined per token in slot
+// order, out = fma(w_j, y_j, out) as gemma4.c:652.
 #define DD_C 12
-#define DD_HB 24576                   // LDS bytes for staged hidden rows and scales
+#define DD_W 8                        // waves
 
 struct ZzDecPairs {                 // per (token, slot) pair, flat order s*K + j
-    int pos[DEC_MAXS * ZZ_MAXK];    // sorted position: row of hq / hs / hsum
+    int pos[DEC_MAXS * ZZ_MAXK];    // sorted position: row of hf / hq / hs / hsum
     int e[DEC_MAXS * ZZ_MAXK];      // expert (clamped into the table)
 };
 
+// LDS bytes of the staged hidden rows of P pairs: int8 codes, block scales and sums
+static inline size_t zz_dec_down_lds(int P, int MI) { return (size_t)P * MI + 8 * (size_t)P * (MI / ZZ_BLK); }
+
 template <int FMT>
-__global__ __launch_bounds__(256) void zz_dec_down_kernel(ZzDecDownArgs a) {
+__global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     const ZzFfnArgs &f = a.f;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r = l & 15, qq = l >> 4;
     const int g = blockIdx.x;
     const ZzTensor &T = f.lay.down;
     const int MI = f.MI, nb = MI / ZZ_BLK, D = f.D, S = a.S, K = a.K, P = S * K;
     const int nch = FMT == ZZ_FMT_TQ2 ? (nb / 2 + 3) / 4 : (nb + 3) / 4;   // units per pair
-    const int npw = (P - w + 3) / 4;                            // this wave's pairs
+    const int npw = (P - w + DD_W - 1) / DD_W;                  // this wave's pairs
     const int U = npw * nch;
     __shared__ ZzDecPairs pr;
     __shared__ float yv[DEC_MAXS * ZZ_MAXK][16];
     __shared__ float htot[DEC_MAXS * ZZ_MAXK];
-    __shared__ __attribute__((aligned(16))) char hbuf[DD_HB];
-    const bool staged = (size_t)P * (MI + 4 * nb) <= DD_HB;
-    int8_t *sh_q = (int8_t *)hbuf;
-    float *sh_s = (float *)(hbuf + (size_t)P * MI);
+    extern __shared__ __attribute__((aligned(16))) char dd_lds[];
+    int8_t *sh_q = (int8_t *)dd_lds;                            // [P][MI] by flat pair
+    float *sh_s = (float *)(dd_lds + (size_t)P * MI);           // [P][nb]
+    int *sh_c = (int *)(sh_s + P * nb);                         // [P][nb]
     if (tid < P) {
         pr.pos[tid] = a.ppos[tid];
         pr.e[tid] = zz_clamp_e(a.eidx[tid], a.E);
     }
     __syncthreads();
-    if (FMT == ZZ_FMT_TQ2 && tid < P) {            // tq2.h:101-106, serial
-        const size_t p = (size_t)pr.pos[tid];
-        double t = 0.0;
-        for (int b = 0; b < nb; b++) t += (double)f.hs[p * nb + b] * (double)f.hsum[p * nb + b];
-        htot[tid] = (float)t;
-    }
     float acc = 0.0f;
     int cur = -1;
     for (int u0 = 0; u0 < U || u0 == 0; u0 += DD_C) {
@@ -426,27 +406,49 @@ __global__ __launch_bounds__(256) void zz_dec_down_kernel(ZzDecDownArgs a) {
 #pragma unroll
         for (int i = 0; i < DD_C; i++) {                        // clamped: loads stay in range
             const int u = min(u0 + i, max(U - 1, 0));
-            const int fp = w + 4 * (u / nch), ch = u % nch;
+            const int fp = w + DD_W * (u / nch), ch = u % nch;
             const uint8_t *E = f.experts + (size_t)pr.e[min(fp, P - 1)] * f.estride;
             if (FMT == ZZ_FMT_TQ2) c[i] = ld16(E + zz_tq2off(T, 16 * g + r, min(qq + 4 * ch, nb / 2 - 1)));
             else k[i] = zz_load_chunk<FMT>(E, T, g, ch, l);
         }
-        if (u0 == 0) {                                          // stage the hidden rows once
-            if (staged) {
-                for (int fp = 0; fp < P; fp++) {
-                    const size_t p = (size_t)pr.pos[fp];
-                    for (int i = 16 * tid; i < MI; i += 16 * 256)
-                        *(uint4 *)(sh_q + (size_t)fp * MI + i) = ld16(f.hq + p * MI + i);
-                    for (int b = tid; b < nb; b += 256) sh_s[fp * nb + b] = f.hs[p * nb + b];
+        if (u0 == 0) {                                          // quantise the hidden rows once
+            for (int i = tid; i < P * nb; i += 512) {
+                const int fp = i / nb, b = i % nb;
+                const size_t p = (size_t)pr.pos[fp];
+                float v[ZZ_BLK];
+#pragma unroll
+                for (int m = 0; m < ZZ_BLK; m += 4) {
+                    const float4 t4 = *(const float4 *)(f.hf + p * MI + b * ZZ_BLK + m);
+                    v[m] = t4.x; v[m + 1] = t4.y; v[m + 2] = t4.z; v[m + 3] = t4.w;
+                }
+                int qs;
+                int8_t *dq = sh_q + (size_t)fp * MI + b * ZZ_BLK;
+                const float d = zz_quant_block(v, dq, &qs);
+                sh_s[fp * nb + b] = d;
+                sh_c[fp * nb + b] = qs;
+                if (g == 0) {                                   // the codes, for the record
+                    const uint4 *s4 = (const uint4 *)dq;
+                    uint4 *d4 = (uint4 *)(f.hq + p * MI + b * ZZ_BLK);
+                    d4[0] = s4[0];
+                    d4[1] = s4[1];
+                    f.hs[p * nb + b] = d;
+                    f.hsum[p * nb + b] = qs;
                 }
             }
             __syncthreads();
+            if (FMT == ZZ_FMT_TQ2) {
+                if (tid < P) {                                  // tq2.h:101-106, serial
+                    double t = 0.0;
+                    for (int b = 0; b < nb; b++) t += (double)sh_s[tid * nb + b] * (double)sh_c[tid * nb + b];
+                    htot[tid] = (float)t;
+                }
+            }
         }
 #pragma unroll
         for (int i = 0; i < DD_C; i++) {
             const int u = u0 + i;
             if (u >= U) continue;
-            const int fp = w + 4 * (u / nch), ch = u % nch;
+            const int fp = w + DD_W * (u / nch), ch = u % nch;
             if (fp != cur) {                                    // wave-uniform
                 if (cur >= 0) {
                     acc += __shfl_xor(acc, 16, 64);
@@ -456,15 +458,14 @@ __global__ __launch_bounds__(256) void zz_dec_down_kernel(ZzDecDownArgs a) {
                 cur = fp;
                 acc = 0.0f;
             }
-            const size_t p = (size_t)pr.pos[fp];
-            const int8_t *hx = staged ? sh_q + (size_t)fp * MI : f.hq + p * MI;
-            const float *hsx = staged ? sh_s + fp * nb : f.hs + p * nb;
+            const int8_t *hx = sh_q + (size_t)fp * MI;
+            const float *hsx = sh_s + fp * nb;
             if (FMT == ZZ_FMT_TQ2) {
                 const int gp = qq + 4 * ch;
                 if (gp < nb / 2) {
                     const int8_t *x = hx + gp * 64;
-                    const int d0 = zz_dot_tq2(c[i], 0, ld16(x), ld16(x + 16));
-                    const int d1 = zz_dot_tq2(c[i], 1, ld16(x + 32), ld16(x + 48));
+                    const int d0 = zz_dot_tq2(c[i], 0, *(const uint4 *)x, *(const uint4 *)(x + 16));
+                    const int d1 = zz_dot_tq2(c[i], 1, *(const uint4 *)(x + 32), *(const uint4 *)(x + 48));
                     acc = fmaf(hsx[2 * gp], (float)d0, acc);
                     acc = fmaf(hsx[2 * gp + 1], (float)d1, acc);
                 }
@@ -539,16 +540,20 @@ int zz_launch_dec_route(const ZzDecRouteArgs &a, hipStream_t st) {
 }
 
 int zz_launch_dec_up(const ZzFfnArgs &a, int max_items, hipStream_t st) {
-    hipLaunchKernelGGL(zz_dec_up_kernel, dim3(a.MI / 32, max_items), dim3(512), 0, st, a);
+    hipLaunchKernelGGL(zz_dec_up_kernel, dim3(a.MI / 16, max_items), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess;
 }
 
+int zz_dec_fits(int S, int K, int MI) { return zz_dec_down_lds(S * K, MI) <= ZZ_DEC_LDS; }
+
 int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st) {
     const dim3 grid(a.f.D / 16);
+    const size_t lds = zz_dec_down_lds(a.S * a.K, a.f.MI);
+    if (lds > ZZ_DEC_LDS) return 0;
     switch (a.f.lay.down.fmt) {
-    case ZZ_FMT_Q40: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q40>, grid, dim3(256), 0, st, a); break;
-    case ZZ_FMT_Q80: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q80>, grid, dim3(256), 0, st, a); break;
-    case ZZ_FMT_TQ2: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_TQ2>, grid, dim3(256), 0, st, a); break;
+    case ZZ_FMT_Q40: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q40>, grid, dim3(512), lds, st, a); break;
+    case ZZ_FMT_Q80: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q80>, grid, dim3(512), lds, st, a); break;
+    case ZZ_FMT_TQ2: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_TQ2>, grid, dim3(512), lds, st, a); break;
     default: return 0;
     }
     return hipGetLastError() == hipSuccess;

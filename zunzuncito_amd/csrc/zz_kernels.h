@@ -74,6 +74,7 @@ struct ZzFfnArgs {
     float *hs;                  // [P, MI/32]
     int *hsum;                  // [P, MI/32]
     float *y;                   // [P, D] expert outputs before weighting
+    float *hf;                  // [P, MI] fp32 hidden of the decode path
 };
 
 struct ZzCombineArgs {
@@ -87,6 +88,7 @@ struct ZzCombineArgs {
 };
 
 #define ZZ_DEC_MAXS 4   // largest batch of the fused decode path
+#define ZZ_DEC_LDS 49152  // LDS for the decode down kernel's quantised hidden rows
 
 // Decode router (two kernels): logits per expert workgroup, then top-k gating and
 // the small-batch dispatch in one workgroup.
@@ -122,6 +124,7 @@ int zz_launch_dispatch(const ZzDispatchArgs &a, hipStream_t st);
 int zz_launch_dec_route(const ZzDecRouteArgs &a, hipStream_t st);
 int zz_launch_dec_up(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st);
+int zz_dec_fits(int S, int K, int MI);   // the decode path's LDS holds S*K hidden rows
 int zz_launch_dec_norm(float *out, const float *post_ln, int D, float eps, int S, hipStream_t st);
 // int8-MFMA grouped GEMM for work items of up to ZZ_MMA_TOKENS tokens
 #define ZZ_MMA_TOKENS 128
