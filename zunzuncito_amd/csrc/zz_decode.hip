@@ -197,16 +197,42 @@ struct ZzDecStage {
     float xt[DEC_MAXS];         // tq2 Sx of each token
 };
 
-__device__ __forceinline__ void zz_dec_stage(const ZzFfnArgs &a, const ZzItem &item, ZzDecStage &st) {
-    const int D = a.D, nb = D / ZZ_BLK;
-    for (int t = 0; t < item.n; t++) {
-        const int tk = st.tok[t];
-        for (int i = 16 * threadIdx.x; i < D; i += 16 * blockDim.x)
-            *(uint4 *)&st.xq[t][i] = ld16(a.xq + (size_t)tk * D + i);
-        for (int b = threadIdx.x; b < nb; b += blockDim.x) {
-            st.xs[t][b] = a.xs[(size_t)tk * nb + b];
-            st.xsum[t][b] = a.xsum[(size_t)tk * nb + b];
-        }
+// The item's activations into LDS in two steps: zz_dec_stage_issue requests every
+// segment of every token (the token ids are uniform loads) before the weight loads
+// are issued, so that waiting for them in zz_dec_stage_commit leaves the weights in
+// flight (loads complete in order); the commit writes LDS and syncs.
+#define DEC_SEG (ZZ_MAXD / 16 / 256)          // activation segments per thread and token
+struct ZzDecStageRegs {
+    uint4 xv[DEC_MAXS][DEC_SEG];
+    float sv[DEC_MAXS];
+    int cv[DEC_MAXS];
+};
+
+__device__ __forceinline__ void zz_dec_stage_issue(const ZzFfnArgs &a, const ZzItem &item, ZzDecStageRegs &r) {
+    const int D = a.D, nb = D / ZZ_BLK, nseg = D / 16, tid = threadIdx.x, n = item.n;
+    int tk[DEC_MAXS];
+#pragma unroll
+    for (int t = 0; t < DEC_MAXS; t++) tk[t] = a.ptok[item.p0 + min(t, n - 1)];
+#pragma unroll
+    for (int t = 0; t < DEC_MAXS; t++) {
+#pragma unroll
+        for (int k = 0; k < DEC_SEG; k++)
+            r.xv[t][k] = ld16(a.xq + (size_t)tk[t] * D + 16 * min(tid + 256 * k, nseg - 1));
+        r.sv[t] = a.xs[(size_t)tk[t] * nb + min(tid, nb - 1)];
+        r.cv[t] = a.xsum[(size_t)tk[t] * nb + min(tid, nb - 1)];
+    }
+}
+
+__device__ __forceinline__ void zz_dec_stage_commit(const ZzFfnArgs &a, const ZzDecStageRegs &r, ZzDecStage &st) {
+    const int nb = a.D / ZZ_BLK, nseg = a.D / 16, tid = threadIdx.x;
+    // unconditional writes (clamped slots hold copies of the same value, rows past
+    // the item's tokens are never read): the loads cannot sink past the weights
+#pragma unroll
+    for (int t = 0; t < DEC_MAXS; t++) {
+#pragma unroll
+        for (int k = 0; k < DEC_SEG; k++) *(uint4 *)&st.xq[t][16 * min(tid + 256 * k, nseg - 1)] = r.xv[t][k];
+        st.xs[t][min(tid, nb - 1)] = r.sv[t];
+        st.xsum[t][min(tid, nb - 1)] = r.cv[t];
     }
     __syncthreads();
 }
@@ -218,22 +244,20 @@ struct ZzChunk {
     uint2 s;
 };
 
+// Branch-free (only addresses are selected), so the load counters stay exact. A
+// short last chunk (2 blocks) has 8 (q4_0) or 16 (q8_0) bytes per lane and 2 scales
+// per row: the extra bytes read stay inside the slot (the q plane is followed by
+// the scale plane, which is preceded by the q plane) and are not used.
 template <int FMT>
 __device__ __forceinline__ ZzChunk zz_load_chunk(const uint8_t *E, const ZzTensor &T, int g, int c, int l) {
     ZzChunk k;
     const int b0 = 4 * c, r = l & 15;
+    const bool full = zz_cbs(T, b0) == 4;
     const uint8_t *q = E + zz_qlane(T, g, b0, l);
     const uint8_t *sp = E + zz_sidx(T, g, b0, r);
-    if (zz_cbs(T, b0) == 4) {
-        k.a = ld16(q);
-        k.b = FMT == ZZ_FMT_Q80 ? ld16(q + 16) : make_uint4(0, 0, 0, 0);
-        k.s = *(const uint2 *)sp;
-    } else {                                               // short last chunk: 2 blocks
-        if (FMT == ZZ_FMT_Q80) k.a = ld16(q);
-        else { const uint2 v = *(const uint2 *)q; k.a = make_uint4(v.x, v.y, 0, 0); }
-        k.b = make_uint4(0, 0, 0, 0);
-        k.s = make_uint2(*(const unsigned *)sp, 0);
-    }
+    k.a = ld16(q);
+    k.b = FMT == ZZ_FMT_Q80 ? ld16(q + (full ? 16 : 0)) : make_uint4(0, 0, 0, 0);
+    k.s = *(const uint2 *)(sp - (full ? 0 : 4));   // short: the 2 scales in .y
     return k;
 }
 
@@ -247,9 +271,67 @@ __device__ __forceinline__ uint2 zz_chunk_w(const ZzChunk &k, int j) {
     const unsigned w = j == 0 ? k.a.x : (j == 1 ? k.a.y : (j == 2 ? k.a.z : k.a.w));
     return zz_q4_unpack(w);
 }
-__device__ __forceinline__ float zz_chunk_dw(const ZzChunk &k, int j) {
-    const unsigned v = j < 2 ? k.s.x : k.s.y;
+__device__ __forceinline__ float zz_chunk_dw(const ZzChunk &k, int j, bool full) {
+    const unsigned v = j < 2 && full ? k.s.x : k.s.y;
     return zz_h2f((uint16_t)((j & 1) ? v >> 16 : v & 0xffff));
+}
+
+// The dots of one batch of a wave's chunks (h + 2i) for NT tokens. The activation
+// operands of a chunk (4 blocks' 8 bytes and d_x, per token) are read from LDS one
+// chunk ahead, so LDS latency overlaps the dots; no branch inside a chunk.
+template <int FMT, int NT>
+__device__ __forceinline__ void zz_dec_up_comp(const ZzChunk (&k)[DU_C], const ZzDecStage &st, int nb, int h,
+                                               int i0, int qq, float (&acc)[DEC_MAXS]) {
+    const int nch = (nb + 3) / 4, nfull = nb / 4;
+    auto ldx = [&](int c, uint2 (&xv)[NT][4], float4 (&xs)[NT]) {
+        c = min(c, nch - 1);               // a short chunk's extra slots stay inside the rows
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) xv[t][j] = *(const uint2 *)&st.xq[t][(4 * c + j) * ZZ_BLK + 8 * qq];
+            xs[t] = *(const float4 *)&st.xs[t][4 * c];
+        }
+    };
+    auto chunk = [&](const ZzChunk &kk, const uint2 (&xv)[NT][4], const float4 (&xs)[NT], int c) {
+        if (c >= nch) return;
+        const bool full = c < nfull;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (j >= 2 && !full) break;
+            const uint2 w = zz_chunk_w<FMT>(kk, j);
+            const float dw = zz_chunk_dw(kk, j, full);
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                int d = zz_dot4(w.x, xv[t][j].x, 0);
+                d = zz_dot4(w.y, xv[t][j].y, d);
+                const float sx = j == 0 ? xs[t].x : j == 1 ? xs[t].y : j == 2 ? xs[t].z : xs[t].w;
+                acc[t] = fmaf(dw * sx, (float)d, acc[t]);
+            }
+        }
+    };
+    uint2 xa[NT][4], xb[NT][4];
+    float4 sa[NT], sb[NT];
+    if (NT > 2) {                          // registers: no read-ahead for 3-4 tokens
+#pragma unroll
+        for (int i = 0; i < DU_C; i++) {
+            const int c = h + 2 * (i0 + i);
+            ldx(c, xa, sa);
+            chunk(k[i], xa, sa, c);
+        }
+        return;
+    }
+    ldx(h + 2 * i0, xa, sa);
+#pragma unroll
+    for (int i = 0; i < DU_C; i++) {
+        const int c = h + 2 * (i0 + i);
+        if (i % 2 == 0) {
+            if (i + 1 < DU_C) ldx(c + 2, xb, sb);
+            chunk(k[i], xa, sa, c);
+        } else {
+            if (i + 1 < DU_C) ldx(c + 2, xa, sa);
+            chunk(k[i], xb, sb, c);
+        }
+    }
 }
 
 template <int FMT>
@@ -259,15 +341,20 @@ __device__ __forceinline__ void zz_dec_up_part(const ZzFfnArgs &a, const ZzItem 
     const int nb = a.D / ZZ_BLK, n = item.n, r = l & 15, qq = l >> 4;
 #pragma unroll
     for (int t = 0; t < DEC_MAXS; t++) acc[t] = 0.0f;
+    ZzDecStageRegs sr;
+    zz_dec_stage_issue(a, item, sr);
+    // the first batch of loads, the staging commit (waits only for the activations,
+    // requested first), then batches past the first (K > 2 * DU_C chunks) in a loop
+    // without a barrier
     if (FMT == ZZ_FMT_TQ2) {
         const int ng = nb / 2;                                  // lane's groups qq + 4h + 8i
-        // wave-uniform trip count (the staging barrier is inside), at least once
-        for (int i0 = 0; 4 * h + 8 * i0 < ng || i0 == 0; i0 += DU_C) {
-            uint4 c[DU_C];
+        uint4 c[DU_C];
+        auto load = [&](int i0) {
 #pragma unroll
             for (int i = 0; i < DU_C; i++)                     // clamped: loads stay in range
                 c[i] = ld16(E + zz_tq2off(T, 16 * g + r, min(qq + 4 * h + 8 * (i0 + i), ng - 1)));
-            if (i0 == 0) zz_dec_stage(a, item, st);           // every wave passes here once
+        };
+        auto comp = [&](int i0) {
 #pragma unroll
             for (int i = 0; i < DU_C; i++) {
                 const int gp = qq + 4 * h + 8 * (i0 + i);
@@ -282,36 +369,36 @@ __device__ __forceinline__ void zz_dec_up_part(const ZzFfnArgs &a, const ZzItem 
                     acc[t] = fmaf(st.xs[t][2 * gp + 1], (float)d1, acc[t]);
                 }
             }
+        };
+        __builtin_amdgcn_sched_barrier(0);                      // activation loads issue first
+        load(0);
+        zz_dec_stage_commit(a, sr, st);
+        comp(0);
+        for (int i0 = DU_C; 4 * h + 8 * i0 < ng; i0 += DU_C) {
+            load(i0);
+            comp(i0);
         }
         return;
     }
     const int nch = (nb + 3) / 4;                               // lane's chunks h + 2i
-    for (int i0 = 0; h + 2 * i0 < nch || i0 == 0; i0 += DU_C) {   // at least once: barrier
-        ZzChunk k[DU_C];
+    ZzChunk k[DU_C];
+    auto load = [&](int i0) {
 #pragma unroll
         for (int i = 0; i < DU_C; i++) k[i] = zz_load_chunk<FMT>(E, T, g, min(h + 2 * (i0 + i), nch - 1), l);
-        if (i0 == 0) zz_dec_stage(a, item, st);
-#pragma unroll
-        for (int i = 0; i < DU_C; i++) {
-            const int c = h + 2 * (i0 + i);
-            if (c >= nch) continue;
-            const int cbs = zz_cbs(T, 4 * c);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                if (j >= cbs) continue;
-                const int b = 4 * c + j;
-                const uint2 w = zz_chunk_w<FMT>(k[i], j);
-                const float dw = zz_chunk_dw(k[i], j);
-#pragma unroll
-                for (int t = 0; t < DEC_MAXS; t++) {
-                    if (t >= n) continue;
-                    const uint2 xv = *(const uint2 *)&st.xq[t][b * ZZ_BLK + 8 * qq];
-                    int d = zz_dot4(w.x, xv.x, 0);
-                    d = zz_dot4(w.y, xv.y, d);
-                    acc[t] = fmaf(dw * st.xs[t][b], (float)d, acc[t]);
-                }
-            }
-        }
+    };
+    auto comp = [&](int i0) {                                   // n is uniform
+        if (n == 1) zz_dec_up_comp<FMT, 1>(k, st, nb, h, i0, qq, acc);
+        else if (n == 2) zz_dec_up_comp<FMT, 2>(k, st, nb, h, i0, qq, acc);
+        else if (n == 3) zz_dec_up_comp<FMT, 3>(k, st, nb, h, i0, qq, acc);
+        else zz_dec_up_comp<FMT, 4>(k, st, nb, h, i0, qq, acc);
+    };
+    __builtin_amdgcn_sched_barrier(0);                          // activation loads issue first
+    load(0);
+    zz_dec_stage_commit(a, sr, st);
+    comp(0);
+    for (int i0 = DU_C; h + 2 * i0 < nch; i0 += DU_C) {
+        load(i0);
+        comp(i0);
     }
 }
 
@@ -324,8 +411,6 @@ __global__ __launch_bounds__(256) void zz_dec_up_kernel(ZzFfnArgs a) {
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
     __shared__ ZzDecStage st;
     __shared__ float part[2][2][DEC_MAXS][16];      // [half][gate/up][token][row]
-    if (tid < item.n) st.tok[tid] = a.ptok[item.p0 + tid];
-    __syncthreads();
     float acc[DEC_MAXS];
     if (T.fmt == ZZ_FMT_Q40) zz_dec_up_part<ZZ_FMT_Q40>(a, item, st, E, T, j, h, l, acc);
     else if (T.fmt == ZZ_FMT_Q80) zz_dec_up_part<ZZ_FMT_Q80>(a, item, st, E, T, j, h, l, acc);
@@ -367,6 +452,7 @@ __global__ __launch_bounds__(256) void zz_dec_up_kernel(ZzFfnArgs a) {
 // order, out = fma(w_j, y_j, out) as gemma4.c:652.
 #define DD_C 12
 #define DD_W 8                        // waves
+#define DD_QB 4                       // hidden float4 per thread requested ahead
 
 struct ZzDecPairs {                 // per (token, slot) pair, flat order s*K + j
     int pos[DEC_MAXS * ZZ_MAXK];    // sorted position: row of hf / hq / hs / hsum
@@ -398,11 +484,56 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
         pr.e[tid] = zz_clamp_e(a.eidx[tid], a.E);
     }
     __syncthreads();
-    float acc = 0.0f;
-    int cur = -1;
-    for (int u0 = 0; u0 < U || u0 == 0; u0 += DD_C) {
-        ZzChunk k[DD_C];
-        uint4 c[DD_C];
+    // the pairs' fp32 hidden, requested before the weights: 8 lanes per 32-block, a
+    // float4 each, the first DD_QB per thread (the wait for them then leaves the
+    // weight loads in flight; loads complete in order)
+    const int nquad = P * nb * 8;
+    auto hload = [&](int qd) {
+        qd = min(qd, nquad - 1);
+        const int blk = qd >> 3, fp = blk / nb;
+        return *(const float4 *)(f.hf + (size_t)pr.pos[fp] * MI + (blk - fp * nb) * ZZ_BLK + 4 * (qd & 7));
+    };
+    float4 hv[DD_QB];
+#pragma unroll
+    for (int k = 0; k < DD_QB; k++) hv[k] = hload(tid + 512 * k);
+    // q8_0 of a 32-block as zz_quant_block forms it: amax over the block's 8 lanes,
+    // d = amax / 127, codes rint(v / d) clamped, their sum. Called by whole waves.
+    auto quant = [&](int qd, float4 v) {
+        const int blk = qd >> 3, sub = qd & 7, fp = blk / nb, b = blk - fp * nb;
+        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        m = fmaxf(m, __shfl_xor(m, 1, 64));
+        m = fmaxf(m, __shfl_xor(m, 2, 64));
+        m = fmaxf(m, __shfl_xor(m, 4, 64));
+        const float d = m / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+        const int q0 = (int)fminf(fmaxf(rintf(v.x * id), -127.0f), 127.0f);
+        const int q1 = (int)fminf(fmaxf(rintf(v.y * id), -127.0f), 127.0f);
+        const int q2 = (int)fminf(fmaxf(rintf(v.z * id), -127.0f), 127.0f);
+        const int q3 = (int)fminf(fmaxf(rintf(v.w * id), -127.0f), 127.0f);
+        int qs = q0 + q1 + q2 + q3;
+        qs += __shfl_xor(qs, 1, 64);
+        qs += __shfl_xor(qs, 2, 64);
+        qs += __shfl_xor(qs, 4, 64);
+        const unsigned pk = (unsigned)(q0 & 0xff) | (unsigned)(q1 & 0xff) << 8 |
+                            (unsigned)(q2 & 0xff) << 16 | (unsigned)(q3 & 0xff) << 24;
+        if (qd < nquad) {
+            *(unsigned *)(sh_q + (size_t)fp * MI + b * ZZ_BLK + 4 * sub) = pk;
+            if (sub == 0) {
+                sh_s[fp * nb + b] = d;
+                sh_c[fp * nb + b] = qs;
+            }
+            if (g == 0) {                                       // the codes, for the record
+                const size_t p = (size_t)pr.pos[fp];
+                *(unsigned *)(f.hq + p * MI + b * ZZ_BLK + 4 * sub) = pk;
+                if (sub == 0) {
+                    f.hs[p * nb + b] = d;
+                    f.hsum[p * nb + b] = qs;
+                }
+            }
+        }
+    };
+    ZzChunk k[DD_C];
+    uint4 c[DD_C];
+    auto load_units = [&](int u0) {
 #pragma unroll
         for (int i = 0; i < DD_C; i++) {                        // clamped: loads stay in range
             const int u = min(u0 + i, max(U - 1, 0));
@@ -411,39 +542,10 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
             if (FMT == ZZ_FMT_TQ2) c[i] = ld16(E + zz_tq2off(T, 16 * g + r, min(qq + 4 * ch, nb / 2 - 1)));
             else k[i] = zz_load_chunk<FMT>(E, T, g, ch, l);
         }
-        if (u0 == 0) {                                          // quantise the hidden rows once
-            for (int i = tid; i < P * nb; i += 512) {
-                const int fp = i / nb, b = i % nb;
-                const size_t p = (size_t)pr.pos[fp];
-                float v[ZZ_BLK];
-#pragma unroll
-                for (int m = 0; m < ZZ_BLK; m += 4) {
-                    const float4 t4 = *(const float4 *)(f.hf + p * MI + b * ZZ_BLK + m);
-                    v[m] = t4.x; v[m + 1] = t4.y; v[m + 2] = t4.z; v[m + 3] = t4.w;
-                }
-                int qs;
-                int8_t *dq = sh_q + (size_t)fp * MI + b * ZZ_BLK;
-                const float d = zz_quant_block(v, dq, &qs);
-                sh_s[fp * nb + b] = d;
-                sh_c[fp * nb + b] = qs;
-                if (g == 0) {                                   // the codes, for the record
-                    const uint4 *s4 = (const uint4 *)dq;
-                    uint4 *d4 = (uint4 *)(f.hq + p * MI + b * ZZ_BLK);
-                    d4[0] = s4[0];
-                    d4[1] = s4[1];
-                    f.hs[p * nb + b] = d;
-                    f.hsum[p * nb + b] = qs;
-                }
-            }
-            __syncthreads();
-            if (FMT == ZZ_FMT_TQ2) {
-                if (tid < P) {                                  // tq2.h:101-106, serial
-                    double t = 0.0;
-                    for (int b = 0; b < nb; b++) t += (double)sh_s[tid * nb + b] * (double)sh_c[tid * nb + b];
-                    htot[tid] = (float)t;
-                }
-            }
-        }
+    };
+    float acc = 0.0f;
+    int cur = -1;
+    auto comp_units = [&](int u0) {
 #pragma unroll
         for (int i = 0; i < DD_C; i++) {
             const int u = u0 + i;
@@ -479,10 +581,27 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
                     const uint2 xv = *(const uint2 *)(hx + b * ZZ_BLK + 8 * qq);
                     int d = zz_dot4(wv.x, xv.x, 0);
                     d = zz_dot4(wv.y, xv.y, d);
-                    acc = fmaf(zz_chunk_dw(k[i], j) * hsx[b], (float)d, acc);
+                    acc = fmaf(zz_chunk_dw(k[i], j, cbs == 4) * hsx[b], (float)d, acc);
                 }
             }
         }
+    };
+    __builtin_amdgcn_sched_barrier(0);                          // hidden loads issue first
+    load_units(0);
+#pragma unroll
+    for (int kq = 0; kq < DD_QB; kq++)
+        if (512 * kq < nquad) quant(tid + 512 * kq, hv[kq]);     // uniform condition
+    for (int q0 = 512 * DD_QB; q0 < nquad; q0 += 512) quant(q0 + tid, hload(q0 + tid));
+    __syncthreads();
+    if (FMT == ZZ_FMT_TQ2 && tid < P) {                         // tq2.h:101-106, serial
+        double t = 0.0;
+        for (int b = 0; b < nb; b++) t += (double)sh_s[tid * nb + b] * (double)sh_c[tid * nb + b];
+        htot[tid] = (float)t;
+    }
+    comp_units(0);
+    for (int u0 = DD_C; u0 < U; u0 += DD_C) {
+        load_units(u0);
+        comp_units(u0);
     }
     if (cur >= 0) {
         acc += __shfl_xor(acc, 16, 64);
@@ -549,7 +668,7 @@ int zz_dec_fits(int S, int K, int MI) { return zz_dec_down_lds(S * K, MI) <= ZZ_
 int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st) {
     const dim3 grid(a.f.D / 16);
     const size_t lds = zz_dec_down_lds(a.S * a.K, a.f.MI);
-    if (lds > ZZ_DEC_LDS) return 0;
+    if (!zz_dec_fits(a.S, a.K, a.f.MI)) return 0;
     switch (a.f.lay.down.fmt) {
     case ZZ_FMT_Q40: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q40>, grid, dim3(512), lds, st, a); break;
     case ZZ_FMT_Q80: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q80>, grid, dim3(512), lds, st, a); break;
