@@ -135,7 +135,7 @@ int zz_moe_stats(unsigned *counters4);
 #define ZZ_K_FFN_UP 4
 #define ZZ_K_FFN_DOWN 5
 #define ZZ_K_COMBINE 6
-#define ZZ_K_DEC_ROUTE 7      /* decode batches: input quantisation + router + dispatch */
+#define ZZ_K_DEC_ROUTE 7      /* decode batches: input quantisation + router logits */
 #define ZZ_K_DEC_DOWN 8       /* decode batches: down projection + combine (+ post-norm) */
 #define ZZ_K_COUNT 9
 int zz_moe_profile(int on);

@@ -434,6 +434,10 @@ extern "C" int zz_moe_profile_read(double *ms, int *launches, int n) {
 }
 
 // One chunk of S <= chunk_tokens tokens: in/out device pointers.
+// decode-sized batches whose hidden rows fit the decode kernels' LDS take the GEMV
+// path; larger ones the matrix cores
+static bool takes_decode(const zz_moe_desc &d, int S) { return S <= g_dec_max_s && zz_dec_fits(S, d.K, d.MI); }
+
 static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream_t st) {
     const zz_moe_desc &d = L->d;
     Workspace &w = L->ws;
@@ -458,7 +462,7 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
 
     // decode-sized batches take the GEMV path; larger ones the matrix cores, on
     // work items of up to ZZ_MMA_TOKENS tokens of one expert
-    const bool dec = S <= g_dec_max_s && zz_dec_fits(S, d.K, d.MI);
+    const bool dec = takes_decode(d, S);
     const int tch = dec ? ZZ_DEC_MAXS : ZZ_MMA_TOKENS;
     ZzDispatchArgs da;
     da.P = P; da.E = d.E; da.K = d.K; da.tch = tch; da.eidx = w.eidx; da.ewt = w.ewt;
@@ -468,7 +472,7 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
     if (dec) {
         ZzDecRouteArgs ra;
         ra.prep = pa; ra.lg = la; ra.tk = ta; ra.dp = da; ra.S = S;
-        if (!(ProfScope(ZZ_K_DEC_ROUTE, st), zz_launch_dec_route(ra, st))) ZZ_FAIL("decode route launch failed");
+        if (!(ProfScope(ZZ_K_DEC_ROUTE, st), zz_launch_dec_logits(ra, st))) ZZ_FAIL("decode router launch failed");
     } else {
         if (!(ProfScope(ZZ_K_PREP, st), zz_launch_prep(pa, S, st))) ZZ_FAIL("prep launch failed");
         if (!(ProfScope(ZZ_K_LOGITS, st), zz_launch_logits(la, S, st))) ZZ_FAIL("logits launch failed");
@@ -486,7 +490,9 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
         ZzDecDownArgs dd;
         dd.f = fa; dd.S = S; dd.K = d.K; dd.E = d.E; dd.eidx = w.eidx; dd.ewt = w.ewt; dd.ppos = w.ppos;
         dd.out = d_out;
-        if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_dec_up(fa, max_items, st))) ZZ_FAIL("ffn_up launch failed");
+        ZzDecUpArgs ua;
+        ua.f = fa; ua.tk = ta;
+        if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_dec_up(ua, S, st))) ZZ_FAIL("ffn_up launch failed");
         if (!(ProfScope(ZZ_K_DEC_DOWN, st), zz_launch_dec_down(dd, st))) ZZ_FAIL("decode down launch failed");
         if (gemma && !(ProfScope(ZZ_K_COMBINE, st), zz_launch_dec_norm(d_out, L->post_ln, d.D, d.eps, S, st)))
             ZZ_FAIL("decode post-norm launch failed");
@@ -593,6 +599,17 @@ extern "C" int zz_moe_debug(int id, zz_moe_dump *dp) {
     const zz_moe_desc &d = L->d;
     Workspace &w = L->ws;
     const int S = L->last_S, P = S * d.K;
+    const bool dec = takes_decode(d, S);
+    ZZ_CHECK(hipDeviceSynchronize());              // the forward may have run on any stream
+    if (dec) {
+        // the decode path routes inside its gate/up kernel and keeps the hidden by
+        // flat pair: the dispatch lists are built here, from its routing outputs
+        ZzDispatchArgs da;
+        da.P = P; da.E = d.E; da.K = d.K; da.tch = ZZ_DEC_MAXS; da.eidx = w.eidx; da.ewt = w.ewt;
+        da.ptok = w.ptok; da.pslot = w.pslot; da.pwt = w.pwt; da.ppos = w.ppos; da.uniq = w.uniq;
+        da.uoff = w.uoff; da.ucnt = w.ucnt; da.items = w.items; da.meta = w.meta;
+        if (!zz_launch_dispatch(da, g_stream)) ZZ_FAIL("zz_moe_debug: dispatch launch failed");
+    }
     ZZ_CHECK(hipStreamSynchronize(g_stream));
     if (dp->xq) ZZ_CHECK(hipMemcpy(dp->xq, w.xq, (size_t)S * d.D, hipMemcpyDeviceToHost));
     if (dp->xs) ZZ_CHECK(hipMemcpy(dp->xs, w.xs, sizeof(float) * S * (d.D / ZZ_BLK), hipMemcpyDeviceToHost));
@@ -624,7 +641,7 @@ extern "C" int zz_moe_debug(int id, zz_moe_dump *dp) {
         ZZ_CHECK(hipMemcpy(hq.data(), w.hq, hq.size(), hipMemcpyDeviceToHost));
         ZZ_CHECK(hipMemcpy(hs.data(), w.hs, sizeof(float) * hs.size(), hipMemcpyDeviceToHost));
         for (int f = 0; f < P; f++) {              // (token, slot) order
-            int p = ppos[f];
+            int p = dec ? f : ppos[f];
             if (dp->hq) memcpy(dp->hq + (size_t)f * d.MI, hq.data() + (size_t)p * d.MI, d.MI);
             if (dp->hs) memcpy(dp->hs + (size_t)f * nbM, hs.data() + (size_t)p * nbM, sizeof(float) * nbM);
         }

@@ -6,7 +6,7 @@
 //      dispatch lists (gemma4.c:750-790 for a handful of rows);
 //   3. zz_dec_up_kernel: gate/up GEMV with the activation and the int8
 //      re-quantisation of the hidden, per expert work item;
-//   4. zz_dec_down_kernel: down GEMV for all (token, slot) pairs of a row tile
+//   3. zz_dec_down_kernel: down GEMV for all (token, slot) pairs of a row tile
 //      and the gate-weighted combine (gemma4.c:652); gemma's post-norm
 //      (gemma4.c:807-808) follows as a one-workgroup-per-token kernel.
 #include "zz_common.h"
@@ -123,117 +123,53 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
     }
 }
 
-// Decode router, part 2 (one workgroup, one wave per token): certified top-k
-// gating (zz_topk_wave.h), then the dispatch of the S*K pairs.
-__global__ __launch_bounds__(256) void zz_dec_gate_kernel(ZzDecRouteArgs a) {
-    extern __shared__ __attribute__((aligned(16))) char tk_lds[];
-    const int S = a.S, tid = threadIdx.x, w = tid >> 6;
-    zz_topk_wave_any(a.tk, w, tk_lds + w * zz_topk_wave_bytes(a.tk.E));
-    __syncthreads();
-    // dispatch of P = S*K <= 64 pairs: stable ranking by (expert, pair index)
-    const ZzDispatchArgs &dp = a.dp;
-    const int K = dp.K, P = S * K;
-    __shared__ int pe[DEC_MAXS * ZZ_MAXK], pf[DEC_MAXS * ZZ_MAXK];
-    if (tid < P) {
-        const int e = dp.eidx[tid];
-        pe[tid] = e < 0 || e >= dp.E ? 0 : e;     // never index past the expert tables
-    }
-    __syncthreads();
-    int ep = 0, rank = 0, start = 0, cnt = 0, first = 1;
-    if (tid < P) {
-        ep = pe[tid];
-        for (int q = 0; q < P; q++) {
-            const int eq = pe[q];
-            rank += eq < ep || (eq == ep && q < tid);
-            start += eq < ep;
-            cnt += eq == ep;
-            first &= !(q < tid && eq == ep);
-        }
-        pf[tid] = first;                          // first occurrence of its expert
-    }
-    __syncthreads();
-    if (tid < P) {
-        int urank = 0;                            // union order: first-seen
-        for (int q = 0; q < tid; q++) urank += pf[q];
-        dp.ptok[rank] = tid / K;
-        dp.pslot[rank] = tid % K;
-        dp.pwt[rank] = dp.ewt[tid];
-        dp.ppos[tid] = rank;
-        if (first) {
-            dp.uniq[urank] = ep;
-            dp.uoff[urank] = start;
-            dp.ucnt[urank] = cnt;
-            ZzItem it;
-            it.e = ep;
-            it.u = urank;
-            it.p0 = start;
-            it.n = cnt;                            // cnt <= S <= 4 fits one item
-            dp.items[urank] = it;
-        }
-        if (tid == P - 1) {
-            const int nu = urank + first;
-            dp.meta[0] = nu;
-            dp.meta[1] = nu;
-        }
-    }
-}
-
 // ------------------------------------------------------------------ gate/up
-// grid (MI/16, items), 256 threads. The workgroup owns hidden rows 16j..16j+15 of
-// one expert item (<= ZZ_DEC_MAXS tokens); wave w takes row group j of gate (w even)
-// or up (w odd) over half w/2 of the K range. Lane l = 16*qq + r is the slot
-// table's lane: row r of the group, weights 8qq..8qq+7 of every block, so one chunk
-// of 4 blocks is one contiguous 16-byte (q4_0) or 32-byte (q8_0) load; tq2 lanes take
-// whole 64-groups of row r. A lane issues all its weight loads before the
-// activations are staged in LDS. The output is h = act(g, u) in fp32; its q8_0
-// quantisation happens where it is consumed (the down kernel).
+// grid (MI/16, S*K), 256 threads. Workgroup (j, p) owns hidden rows 16j..16j+15 of
+// (token, slot) pair p = s*K + slot. Wave 0 first runs the certified top-k of token
+// s (zz_topk_wave.h): every workgroup of the token repeats it, so no separate gating
+// launch or dispatch list stands between the router and the expert weights; the
+// token's first workgroup writes the routing outputs. Then wave w takes row group j
+// of gate (w even) or up (w odd) of the pair's expert over half w/2 of the K range.
+// Lane l = 16*qq + r is the slot table's lane: row r of the group, weights
+// 8qq..8qq+7 of every block, so one chunk of 4 blocks is one contiguous 16-byte
+// (q4_0) or 32-byte (q8_0) load; tq2 lanes take whole 64-groups of row r. The
+// token's activations are requested first, the weights as soon as the expert is
+// known. The output is h = act(g, u) in fp32 by flat pair; its q8_0 quantisation
+// happens where it is consumed (the down kernel).
 #define DU_C 12          // chunks (tq2: groups) per lane issued together
+#define DEC_SEG (ZZ_MAXD / 16 / 256)          // activation segments per thread
 
 struct ZzDecStage {
-    __attribute__((aligned(16))) int8_t xq[DEC_MAXS][ZZ_MAXD];
-    float xs[DEC_MAXS][ZZ_MAXD / ZZ_BLK];
-    int xsum[DEC_MAXS][ZZ_MAXD / ZZ_BLK];
-    int tok[DEC_MAXS];
-    float xt[DEC_MAXS];         // tq2 Sx of each token
+    __attribute__((aligned(16))) int8_t xq[ZZ_MAXD];
+    float xs[ZZ_MAXD / ZZ_BLK];
+    int xsum[ZZ_MAXD / ZZ_BLK];
+    float xt;                   // tq2 Sx of the token
 };
 
-// The item's activations into LDS in two steps: zz_dec_stage_issue requests every
-// segment of every token (the token ids are uniform loads) before the weight loads
-// are issued, so that waiting for them in zz_dec_stage_commit leaves the weights in
-// flight (loads complete in order); the commit writes LDS and syncs.
-#define DEC_SEG (ZZ_MAXD / 16 / 256)          // activation segments per thread and token
+// The token's activations into LDS in two steps: the issue requests every segment
+// before the weight loads, so that waiting for them in the commit leaves the
+// weights in flight (loads complete in order); the commit writes LDS (unconditional
+// clamped slots, copies of one value: the loads cannot sink past the weights).
 struct ZzDecStageRegs {
-    uint4 xv[DEC_MAXS][DEC_SEG];
-    float sv[DEC_MAXS];
-    int cv[DEC_MAXS];
+    uint4 xv[DEC_SEG];
+    float sv;
+    int cv;
 };
 
-__device__ __forceinline__ void zz_dec_stage_issue(const ZzFfnArgs &a, const ZzItem &item, ZzDecStageRegs &r) {
-    const int D = a.D, nb = D / ZZ_BLK, nseg = D / 16, tid = threadIdx.x, n = item.n;
-    int tk[DEC_MAXS];
+__device__ __forceinline__ void zz_dec_stage_issue(const ZzFfnArgs &a, int tk, ZzDecStageRegs &r) {
+    const int D = a.D, nb = D / ZZ_BLK, nseg = D / 16, tid = threadIdx.x;
 #pragma unroll
-    for (int t = 0; t < DEC_MAXS; t++) tk[t] = a.ptok[item.p0 + min(t, n - 1)];
-#pragma unroll
-    for (int t = 0; t < DEC_MAXS; t++) {
-#pragma unroll
-        for (int k = 0; k < DEC_SEG; k++)
-            r.xv[t][k] = ld16(a.xq + (size_t)tk[t] * D + 16 * min(tid + 256 * k, nseg - 1));
-        r.sv[t] = a.xs[(size_t)tk[t] * nb + min(tid, nb - 1)];
-        r.cv[t] = a.xsum[(size_t)tk[t] * nb + min(tid, nb - 1)];
-    }
+    for (int k = 0; k < DEC_SEG; k++) r.xv[k] = ld16(a.xq + (size_t)tk * D + 16 * min(tid + 256 * k, nseg - 1));
+    r.sv = a.xs[(size_t)tk * nb + min(tid, nb - 1)];
+    r.cv = a.xsum[(size_t)tk * nb + min(tid, nb - 1)];
 }
 
 __device__ __forceinline__ void zz_dec_stage_commit(const ZzFfnArgs &a, const ZzDecStageRegs &r, ZzDecStage &st) {
     const int nb = a.D / ZZ_BLK, nseg = a.D / 16, tid = threadIdx.x;
-    // unconditional writes (clamped slots hold copies of the same value, rows past
-    // the item's tokens are never read): the loads cannot sink past the weights
 #pragma unroll
-    for (int t = 0; t < DEC_MAXS; t++) {
-#pragma unroll
-        for (int k = 0; k < DEC_SEG; k++) *(uint4 *)&st.xq[t][16 * min(tid + 256 * k, nseg - 1)] = r.xv[t][k];
-        st.xs[t][min(tid, nb - 1)] = r.sv[t];
-        st.xsum[t][min(tid, nb - 1)] = r.cv[t];
-    }
+    for (int k = 0; k < DEC_SEG; k++) *(uint4 *)&st.xq[16 * min(tid + 256 * k, nseg - 1)] = r.xv[k];
+    st.xs[min(tid, nb - 1)] = r.sv;
+    st.xsum[min(tid, nb - 1)] = r.cv;
     __syncthreads();
 }
 
@@ -276,50 +212,34 @@ __device__ __forceinline__ float zz_chunk_dw(const ZzChunk &k, int j, bool full)
     return zz_h2f((uint16_t)((j & 1) ? v >> 16 : v & 0xffff));
 }
 
-// The dots of one batch of a wave's chunks (h + 2i) for NT tokens. The activation
-// operands of a chunk (4 blocks' 8 bytes and d_x, per token) are read from LDS one
-// chunk ahead, so LDS latency overlaps the dots; no branch inside a chunk.
-template <int FMT, int NT>
-__device__ __forceinline__ void zz_dec_up_comp(const ZzChunk (&k)[DU_C], const ZzDecStage &st, int nb, int h,
-                                               int i0, int qq, float (&acc)[DEC_MAXS]) {
+// The dots of one batch of a wave's chunks (h + 2i). The activation operands of a
+// chunk (4 blocks' 8 bytes and d_x) are read from LDS one chunk ahead, so LDS
+// latency overlaps the dots; no branch inside a chunk.
+template <int FMT>
+__device__ __forceinline__ float zz_dec_up_comp(const ZzChunk (&k)[DU_C], const ZzDecStage &st, int nb, int h,
+                                                int i0, int qq, float acc) {
     const int nch = (nb + 3) / 4, nfull = nb / 4;
-    auto ldx = [&](int c, uint2 (&xv)[NT][4], float4 (&xs)[NT]) {
-        c = min(c, nch - 1);               // a short chunk's extra slots stay inside the rows
+    auto ldx = [&](int c, uint2 (&xv)[4], float4 &xs) {
+        c = min(c, nch - 1);               // a short chunk's extra slots stay inside the row
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) xv[t][j] = *(const uint2 *)&st.xq[t][(4 * c + j) * ZZ_BLK + 8 * qq];
-            xs[t] = *(const float4 *)&st.xs[t][4 * c];
-        }
+        for (int j = 0; j < 4; j++) xv[j] = *(const uint2 *)&st.xq[(4 * c + j) * ZZ_BLK + 8 * qq];
+        xs = *(const float4 *)&st.xs[4 * c];
     };
-    auto chunk = [&](const ZzChunk &kk, const uint2 (&xv)[NT][4], const float4 (&xs)[NT], int c) {
+    auto chunk = [&](const ZzChunk &kk, const uint2 (&xv)[4], const float4 &xs, int c) {
         if (c >= nch) return;
         const bool full = c < nfull;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             if (j >= 2 && !full) break;
             const uint2 w = zz_chunk_w<FMT>(kk, j);
-            const float dw = zz_chunk_dw(kk, j, full);
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                int d = zz_dot4(w.x, xv[t][j].x, 0);
-                d = zz_dot4(w.y, xv[t][j].y, d);
-                const float sx = j == 0 ? xs[t].x : j == 1 ? xs[t].y : j == 2 ? xs[t].z : xs[t].w;
-                acc[t] = fmaf(dw * sx, (float)d, acc[t]);
-            }
+            int d = zz_dot4(w.x, xv[j].x, 0);
+            d = zz_dot4(w.y, xv[j].y, d);
+            const float sx = j == 0 ? xs.x : j == 1 ? xs.y : j == 2 ? xs.z : xs.w;
+            acc = fmaf(zz_chunk_dw(kk, j, full) * sx, (float)d, acc);
         }
     };
-    uint2 xa[NT][4], xb[NT][4];
-    float4 sa[NT], sb[NT];
-    if (NT > 2) {                          // registers: no read-ahead for 3-4 tokens
-#pragma unroll
-        for (int i = 0; i < DU_C; i++) {
-            const int c = h + 2 * (i0 + i);
-            ldx(c, xa, sa);
-            chunk(k[i], xa, sa, c);
-        }
-        return;
-    }
+    uint2 xa[4], xb[4];
+    float4 sa, sb;
     ldx(h + 2 * i0, xa, sa);
 #pragma unroll
     for (int i = 0; i < DU_C; i++) {
@@ -332,17 +252,15 @@ __device__ __forceinline__ void zz_dec_up_comp(const ZzChunk (&k)[DU_C], const Z
             chunk(k[i], xb, sb, c);
         }
     }
+    return acc;
 }
 
+// the wave's partial dot of row r of group g over its half h of the K range
 template <int FMT>
-__device__ __forceinline__ void zz_dec_up_part(const ZzFfnArgs &a, const ZzItem &item, ZzDecStage &st,
-                                               const uint8_t *E, const ZzTensor &T, int g, int h, int l,
-                                               float (&acc)[DEC_MAXS]) {
-    const int nb = a.D / ZZ_BLK, n = item.n, r = l & 15, qq = l >> 4;
-#pragma unroll
-    for (int t = 0; t < DEC_MAXS; t++) acc[t] = 0.0f;
-    ZzDecStageRegs sr;
-    zz_dec_stage_issue(a, item, sr);
+__device__ __forceinline__ float zz_dec_up_part(const ZzFfnArgs &a, const ZzDecStageRegs &sr, ZzDecStage &st,
+                                                const uint8_t *E, const ZzTensor &T, int g, int h, int l) {
+    const int nb = a.D / ZZ_BLK, r = l & 15, qq = l >> 4;
+    float acc = 0.0f;
     // the first batch of loads, the staging commit (waits only for the activations,
     // requested first), then batches past the first (K > 2 * DU_C chunks) in a loop
     // without a barrier
@@ -359,18 +277,13 @@ __device__ __forceinline__ void zz_dec_up_part(const ZzFfnArgs &a, const ZzItem 
             for (int i = 0; i < DU_C; i++) {
                 const int gp = qq + 4 * h + 8 * (i0 + i);
                 if (gp >= ng) continue;
-#pragma unroll
-                for (int t = 0; t < DEC_MAXS; t++) {
-                    if (t >= n) continue;
-                    const int8_t *x = &st.xq[t][gp * 64];
-                    const int d0 = zz_dot_tq2(c[i], 0, ld16(x), ld16(x + 16));
-                    const int d1 = zz_dot_tq2(c[i], 1, ld16(x + 32), ld16(x + 48));
-                    acc[t] = fmaf(st.xs[t][2 * gp], (float)d0, acc[t]);
-                    acc[t] = fmaf(st.xs[t][2 * gp + 1], (float)d1, acc[t]);
-                }
+                const int8_t *x = &st.xq[gp * 64];
+                const int d0 = zz_dot_tq2(c[i], 0, ld16(x), ld16(x + 16));
+                const int d1 = zz_dot_tq2(c[i], 1, ld16(x + 32), ld16(x + 48));
+                acc = fmaf(st.xs[2 * gp], (float)d0, acc);
+                acc = fmaf(st.xs[2 * gp + 1], (float)d1, acc);
             }
         };
-        __builtin_amdgcn_sched_barrier(0);                      // activation loads issue first
         load(0);
         zz_dec_stage_commit(a, sr, st);
         comp(0);
@@ -378,7 +291,7 @@ __device__ __forceinline__ void zz_dec_up_part(const ZzFfnArgs &a, const ZzItem 
             load(i0);
             comp(i0);
         }
-        return;
+        return acc;
     }
     const int nch = (nb + 3) / 4;                               // lane's chunks h + 2i
     ZzChunk k[DU_C];
@@ -386,58 +299,52 @@ __device__ __forceinline__ void zz_dec_up_part(const ZzFfnArgs &a, const ZzItem 
 #pragma unroll
         for (int i = 0; i < DU_C; i++) k[i] = zz_load_chunk<FMT>(E, T, g, min(h + 2 * (i0 + i), nch - 1), l);
     };
-    auto comp = [&](int i0) {                                   // n is uniform
-        if (n == 1) zz_dec_up_comp<FMT, 1>(k, st, nb, h, i0, qq, acc);
-        else if (n == 2) zz_dec_up_comp<FMT, 2>(k, st, nb, h, i0, qq, acc);
-        else if (n == 3) zz_dec_up_comp<FMT, 3>(k, st, nb, h, i0, qq, acc);
-        else zz_dec_up_comp<FMT, 4>(k, st, nb, h, i0, qq, acc);
-    };
-    __builtin_amdgcn_sched_barrier(0);                          // activation loads issue first
     load(0);
     zz_dec_stage_commit(a, sr, st);
-    comp(0);
+    acc = zz_dec_up_comp<FMT>(k, st, nb, h, 0, qq, acc);
     for (int i0 = DU_C; h + 2 * i0 < nch; i0 += DU_C) {
         load(i0);
-        comp(i0);
+        acc = zz_dec_up_comp<FMT>(k, st, nb, h, i0, qq, acc);
     }
+    return acc;
 }
 
-__global__ __launch_bounds__(256) void zz_dec_up_kernel(ZzFfnArgs a) {
-    const int it = blockIdx.y;
-    if (it >= a.meta[1]) return;
-    const ZzItem item = a.items[it];
+__global__ __launch_bounds__(256) void zz_dec_up_kernel(ZzDecUpArgs a) {
+    const ZzFfnArgs &f = a.f;
+    const int K = a.tk.K, p = blockIdx.y, s = p / K, js = p - s * K;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = w >> 1, q = w & 1, j = blockIdx.x;
-    const ZzTensor &T = q ? a.lay.up : a.lay.gate;
-    const uint8_t *E = a.experts + (size_t)item.e * a.estride;
+    extern __shared__ __attribute__((aligned(16))) char tk_lds[];
     __shared__ ZzDecStage st;
-    __shared__ float part[2][2][DEC_MAXS][16];      // [half][gate/up][token][row]
-    float acc[DEC_MAXS];
-    if (T.fmt == ZZ_FMT_Q40) zz_dec_up_part<ZZ_FMT_Q40>(a, item, st, E, T, j, h, l, acc);
-    else if (T.fmt == ZZ_FMT_Q80) zz_dec_up_part<ZZ_FMT_Q80>(a, item, st, E, T, j, h, l, acc);
-    else zz_dec_up_part<ZZ_FMT_TQ2>(a, item, st, E, T, j, h, l, acc);
-#pragma unroll
-    for (int t = 0; t < DEC_MAXS; t++) {                       // sum over the 4 k-quarters
-        float v = acc[t];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        if (l < 16) part[h][q][t][l] = v;
-    }
-    if (T.fmt == ZZ_FMT_TQ2 && tid < item.n) {      // tq2.h:101-106, serial
-        const int nb = a.D / ZZ_BLK;
+    __shared__ float part[2][2][16];                // [half][gate/up][row]
+    ZzDecStageRegs sr;
+    zz_dec_stage_issue(f, s, sr);
+    if (w == 0) zz_topk_wave_any(a.tk, s, tk_lds, j == 0 && js == 0);
+    __syncthreads();
+    const int e = zz_clamp_e(((const ZzTopkWaveHdr *)tk_lds)->idx[js], a.tk.E);
+    const ZzTensor &T = q ? f.lay.up : f.lay.gate;
+    const uint8_t *E = f.experts + (size_t)e * f.estride;
+    float acc;
+    if (T.fmt == ZZ_FMT_Q40) acc = zz_dec_up_part<ZZ_FMT_Q40>(f, sr, st, E, T, j, h, l);
+    else if (T.fmt == ZZ_FMT_Q80) acc = zz_dec_up_part<ZZ_FMT_Q80>(f, sr, st, E, T, j, h, l);
+    else acc = zz_dec_up_part<ZZ_FMT_TQ2>(f, sr, st, E, T, j, h, l);
+    acc += __shfl_xor(acc, 16, 64);                             // sum over the 4 k-quarters
+    acc += __shfl_xor(acc, 32, 64);
+    if (l < 16) part[h][q][l] = acc;
+    if (T.fmt == ZZ_FMT_TQ2 && tid == 0) {          // tq2.h:101-106, serial
+        const int nb = f.D / ZZ_BLK;
         double tot = 0.0;
-        for (int b = 0; b < nb; b++) tot += (double)st.xs[tid][b] * (double)st.xsum[tid][b];
-        st.xt[tid] = (float)tot;
+        for (int b = 0; b < nb; b++) tot += (double)st.xs[b] * (double)st.xsum[b];
+        st.xt = (float)tot;
     }
     __syncthreads();
-    if (tid < item.n * 16) {                                    // token t, hidden row 16j + r
-        const int t = tid >> 4, r = tid & 15;
-        float g = part[0][0][t][r] + part[1][0][t][r];
-        float u = part[0][1][t][r] + part[1][1][t][r];
+    if (tid < 16) {                                             // hidden row 16j + tid
+        float g = part[0][0][tid] + part[1][0][tid];
+        float u = part[0][1][tid] + part[1][1][tid];
         if (T.fmt == ZZ_FMT_TQ2) {                              // tq2.h:154
-            g = ((const float *)(E + a.lay.gate.off_s))[16 * j + r] * (g - st.xt[t]);
-            u = ((const float *)(E + a.lay.up.off_s))[16 * j + r] * (u - st.xt[t]);
+            g = ((const float *)(E + f.lay.gate.off_s))[16 * j + tid] * (g - st.xt);
+            u = ((const float *)(E + f.lay.up.off_s))[16 * j + tid] * (u - st.xt);
         }
-        a.hf[((size_t)item.p0 + t) * a.MI + 16 * j + r] = zz_act(a.act, g, u, a.clamp);
+        f.hf[(size_t)p * f.MI + 16 * j + tid] = zz_act(f.act, g, u, f.clamp);
     }
 }
 
@@ -480,7 +387,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     float *sh_s = (float *)(dd_lds + (size_t)P * MI);           // [P][nb]
     int *sh_c = (int *)(sh_s + P * nb);                         // [P][nb]
     if (tid < P) {
-        pr.pos[tid] = a.ppos[tid];
+        pr.pos[tid] = tid;                        // the up kernel writes the hidden by flat pair
         pr.e[tid] = zz_clamp_e(a.eidx[tid], a.E);
     }
     __syncthreads();
@@ -645,7 +552,7 @@ __global__ __launch_bounds__(256) void zz_dec_norm_kernel(float *out, const floa
     }
 }
 
-int zz_launch_dec_route(const ZzDecRouteArgs &a, hipStream_t st) {
+int zz_launch_dec_logits(const ZzDecRouteArgs &a, hipStream_t st) {
     const int R = (a.prep.D + 255) / 256;
     if (R <= 4) hipLaunchKernelGGL(zz_dec_logits_kernel<4>, dim3(a.lg.E), dim3(256), 0, st, a);
     else if (R <= 8) hipLaunchKernelGGL(zz_dec_logits_kernel<8>, dim3(a.lg.E), dim3(256), 0, st, a);
@@ -653,13 +560,11 @@ int zz_launch_dec_route(const ZzDecRouteArgs &a, hipStream_t st) {
     else if (R <= 16) hipLaunchKernelGGL(zz_dec_logits_kernel<16>, dim3(a.lg.E), dim3(256), 0, st, a);
     else if (R <= 24) hipLaunchKernelGGL(zz_dec_logits_kernel<24>, dim3(a.lg.E), dim3(256), 0, st, a);
     else hipLaunchKernelGGL(zz_dec_logits_kernel<32>, dim3(a.lg.E), dim3(256), 0, st, a);
-    if (hipGetLastError() != hipSuccess) return 0;
-    hipLaunchKernelGGL(zz_dec_gate_kernel, dim3(1), dim3(64 * a.S), a.S * zz_topk_wave_bytes(a.tk.E), st, a);
     return hipGetLastError() == hipSuccess;
 }
 
-int zz_launch_dec_up(const ZzFfnArgs &a, int max_items, hipStream_t st) {
-    hipLaunchKernelGGL(zz_dec_up_kernel, dim3(a.MI / 16, max_items), dim3(256), 0, st, a);
+int zz_launch_dec_up(const ZzDecUpArgs &a, int S, hipStream_t st) {
+    hipLaunchKernelGGL(zz_dec_up_kernel, dim3(a.f.MI / 16, S * a.tk.K), dim3(256), zz_topk_wave_bytes(a.tk.E), st, a);
     return hipGetLastError() == hipSuccess;
 }
 

@@ -100,6 +100,12 @@ struct ZzDecRouteArgs {
     int S;
 };
 
+// Decode gate/up: the routing of each token and the expert GEMVs of its pairs.
+struct ZzDecUpArgs {
+    ZzFfnArgs f;
+    ZzTopkArgs tk;
+};
+
 // Fused decode down projection + gate-weighted combine.
 struct ZzDecDownArgs {
     ZzFfnArgs f;
@@ -121,8 +127,8 @@ int zz_launch_prep(const ZzPrepArgs &a, int S, hipStream_t st);
 int zz_launch_logits(const ZzLogitArgs &a, int S, hipStream_t st);
 int zz_launch_topk(const ZzTopkArgs &a, int S, hipStream_t st);
 int zz_launch_dispatch(const ZzDispatchArgs &a, hipStream_t st);
-int zz_launch_dec_route(const ZzDecRouteArgs &a, hipStream_t st);
-int zz_launch_dec_up(const ZzFfnArgs &a, int max_items, hipStream_t st);
+int zz_launch_dec_logits(const ZzDecRouteArgs &a, hipStream_t st);
+int zz_launch_dec_up(const ZzDecUpArgs &a, int S, hipStream_t st);
 int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st);
 int zz_dec_fits(int S, int K, int MI);   // the decode path's LDS holds S*K hidden rows
 int zz_launch_dec_norm(float *out, const float *post_ln, int D, float eps, int S, hipStream_t st);

@@ -21,8 +21,9 @@
 struct ZzTopkWaveHdr {
     unsigned long long lmax[64];
     unsigned long long lk;
-    int idx[ZZ_MAXK];
+    int idx[ZZ_MAXK];           // the result: expert of each slot
     float topv[ZZ_MAXK];
+    float wt[ZZ_MAXK];          // the result: gate weight of each slot
 };
 // LDS of one wave: the header, then u64 ck[E], double clo[E], chi[E], int ci[E]
 __host__ __device__ inline size_t zz_topk_wave_bytes(int E) {
@@ -69,8 +70,10 @@ __device__ float zz_gemma_chain(const float *w, const float *xn, int D, const fl
     return v;
 }
 
+// write: store the routing outputs (eidx, ewt, topv, contested, counters); the
+// result is in the header's idx / wt either way
 template <int EPL>
-__device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds) {
+__device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) {
     ZzTopkWaveHdr &h = *(ZzTopkWaveHdr *)lds;
     const int E = a.E, K = a.K, l = threadIdx.x & 63;
     unsigned long long *ck = (unsigned long long *)(lds + sizeof(ZzTopkWaveHdr));
@@ -199,7 +202,7 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds) {
                 }
                 zz_wave_sync_lds();
             }
-            if (l == 0) atomicAdd(a.diag + 2, 1u);
+            if (l == 0 && write) atomicAdd(a.diag + 2, 1u);
         } else {
             for (int i = l; i < nc; i += 64)
                 if (ci[i] < 0) ci[i] = -1 - ci[i];
@@ -249,11 +252,15 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds) {
             if (a.norm_topk) t /= (sum + 1e-20f);
             out = t;
         }
-        a.eidx[(size_t)s * K + l] = ej;
-        a.ewt[(size_t)s * K + l] = out;
-        if (a.topv) a.topv[(size_t)s * K + l] = h.topv[l];
+        h.wt[l] = out;
+        if (write) {
+            a.eidx[(size_t)s * K + l] = ej;
+            a.ewt[(size_t)s * K + l] = out;
+            if (a.topv) a.topv[(size_t)s * K + l] = h.topv[l];
+        }
     }
-    if (l == 0 && sig) {
+    zz_wave_sync_lds();
+    if (l == 0 && sig && write) {
         if (a.contested) a.contested[s] = contested;
         if (contested) atomicAdd(a.diag + 3, 1u);
     }
@@ -263,11 +270,11 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds) {
 __host__ __device__ inline int zz_topk_epl(int E) { return E <= 64 ? 1 : (E <= 128 ? 2 : (E <= 256 ? 4 : 8)); }
 
 // zz_topk_wave with the lane count chosen at run time
-__device__ __forceinline__ void zz_topk_wave_any(const ZzTopkArgs &a, int s, char *lds) {
+__device__ __forceinline__ void zz_topk_wave_any(const ZzTopkArgs &a, int s, char *lds, bool write = true) {
     switch (zz_topk_epl(a.E)) {
-    case 1: zz_topk_wave<1>(a, s, lds); break;
-    case 2: zz_topk_wave<2>(a, s, lds); break;
-    case 4: zz_topk_wave<4>(a, s, lds); break;
-    default: zz_topk_wave<8>(a, s, lds); break;
+    case 1: zz_topk_wave<1>(a, s, lds, write); break;
+    case 2: zz_topk_wave<2>(a, s, lds, write); break;
+    case 4: zz_topk_wave<4>(a, s, lds, write); break;
+    default: zz_topk_wave<8>(a, s, lds, write); break;
     }
 }
