@@ -167,6 +167,7 @@ struct Workspace {
     int *hsum = nullptr;
     float *y = nullptr;
     float *hf = nullptr;
+    double *ss = nullptr;       // decode post-norm per-tile sums of squares
     void *block = nullptr;      // one allocation holds everything above
 };
 
@@ -352,7 +353,7 @@ static int ensure_ws(Layer *L, int S) {
     size_t o_uniq = take(4 * (size_t)d.E), o_uoff = take(4 * (size_t)d.E), o_ucnt = take(4 * (size_t)d.E);
     size_t o_meta = take(64), o_items = take(sizeof(ZzItem) * nitems);
     size_t o_hq = take(P * d.MI), o_hs = take(4 * P * nbM), o_hsum = take(4 * P * nbM);
-    size_t o_y = take(4 * P * d.D), o_hf = take(4 * P * d.MI);
+    size_t o_y = take(4 * P * d.D), o_hf = take(4 * P * d.MI), o_ss = take(8 * S * (size_t)(d.D / 16));
     void *blk = nullptr;
     ZZ_CHECK(hipStreamSynchronize(g_stream));
     ZZ_CHECK(hipMalloc(&blk, off));
@@ -369,6 +370,7 @@ static int ensure_ws(Layer *L, int S) {
     w.uoff = (int *)(b + o_uoff); w.ucnt = (int *)(b + o_ucnt); w.meta = (int *)(b + o_meta);
     w.items = (ZzItem *)(b + o_items); w.hq = (int8_t *)(b + o_hq); w.hs = (float *)(b + o_hs);
     w.hsum = (int *)(b + o_hsum); w.y = (float *)(b + o_y); w.hf = (float *)(b + o_hf);
+    w.ss = (double *)(b + o_ss);
     ZZ_CHECK(hipStreamSynchronize(g_stream));
     return 1;
 }
@@ -489,12 +491,12 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
     if (dec) {
         ZzDecDownArgs dd;
         dd.f = fa; dd.S = S; dd.K = d.K; dd.E = d.E; dd.eidx = w.eidx; dd.ewt = w.ewt; dd.ppos = w.ppos;
-        dd.out = d_out;
+        dd.out = d_out; dd.ss = gemma ? w.ss : nullptr;
         ZzDecUpArgs ua;
         ua.f = fa; ua.tk = ta;
         if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_dec_up(ua, S, st))) ZZ_FAIL("ffn_up launch failed");
         if (!(ProfScope(ZZ_K_DEC_DOWN, st), zz_launch_dec_down(dd, st))) ZZ_FAIL("decode down launch failed");
-        if (gemma && !(ProfScope(ZZ_K_COMBINE, st), zz_launch_dec_norm(d_out, L->post_ln, d.D, d.eps, S, st)))
+        if (gemma && !(ProfScope(ZZ_K_COMBINE, st), zz_launch_dec_norm(d_out, L->post_ln, w.ss, d.D, d.eps, S, st)))
             ZZ_FAIL("decode post-norm launch failed");
         return 1;
     }

@@ -170,6 +170,30 @@ __device__ __forceinline__ float zz_quant_block(const float (&v)[ZZ_BLK], int8_t
     return d;
 }
 
+// zz_quant_block of a 32-block held by 8 consecutive lanes of a wave, 4 values each
+// (lane 8i + m holds values 4m..4m+3): the same amax, scale and rounding. Returns the
+// lane's 4 codes packed; d and the block's code sum go to every lane of the 8.
+// Every lane of the wave must call it.
+__device__ __forceinline__ unsigned zz_quant8(float4 v, float *d_out, int *sum_out) {
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    const float d = m / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+    const int q0 = (int)fminf(fmaxf(rintf(v.x * id), -127.0f), 127.0f);
+    const int q1 = (int)fminf(fmaxf(rintf(v.y * id), -127.0f), 127.0f);
+    const int q2 = (int)fminf(fmaxf(rintf(v.z * id), -127.0f), 127.0f);
+    const int q3 = (int)fminf(fmaxf(rintf(v.w * id), -127.0f), 127.0f);
+    int qs = q0 + q1 + q2 + q3;
+    qs += __shfl_xor(qs, 1, 64);
+    qs += __shfl_xor(qs, 2, 64);
+    qs += __shfl_xor(qs, 4, 64);
+    *d_out = d;
+    *sum_out = qs;
+    return (unsigned)(q0 & 0xff) | (unsigned)(q1 & 0xff) << 8 | (unsigned)(q2 & 0xff) << 16 |
+           (unsigned)(q3 & 0xff) << 24;
+}
+
 __device__ __forceinline__ float zz_gelu_tanh(float x) {
     float inner = fmaf((0.044715f * x) * x, x, x);
     return (0.5f * x) * (1.0f + tanhf(0.7978845608028654f * inner));

@@ -96,30 +96,26 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
     } else if ((tid >> 6) < S) {
         zz_logit_wave_f64(lg, tid >> 6, e);
     }
-    // the expert input quantisation, block g on workgroup g % gridDim.x
+    // the expert input quantisation: block g on workgroup g % E, lanes 8(g / E)..+7
     __syncthreads();
-    for (int g = e + gridDim.x * tid; g < S * nb; g += gridDim.x * 256) {
-        const int s = g / nb, b = g % nb;
-        const float *x = pp.in + (size_t)s * D + b * ZZ_BLK;
-        float v[ZZ_BLK];
-#pragma unroll
-        for (int j = 0; j < ZZ_BLK; j += 4) {
-            const float4 t = *(const float4 *)(x + j);
-            v[j] = t.x; v[j + 1] = t.y; v[j + 2] = t.z; v[j + 3] = t.w;
-        }
+    for (int g0 = e + gridDim.x * (tid >> 3); g0 - (tid >> 3) * (int)gridDim.x < S * nb; g0 += gridDim.x * 32) {
+        const int g = min(g0, S * nb - 1), s = g / nb, b = g % nb, m = tid & 7;   // whole waves iterate
+        float4 v = *(const float4 *)(pp.in + (size_t)s * D + b * ZZ_BLK + 4 * m);
         if (gem) {
             const float r = rr[s];
-#pragma unroll
-            for (int j = 0; j < ZZ_BLK; j += 4) {
-                const float4 w = *(const float4 *)(pp.pre_ln + b * ZZ_BLK + j);
-                v[j] = (v[j] * r) * w.x; v[j + 1] = (v[j + 1] * r) * w.y;
-                v[j + 2] = (v[j + 2] * r) * w.z; v[j + 3] = (v[j + 3] * r) * w.w;
+            const float4 w = *(const float4 *)(pp.pre_ln + b * ZZ_BLK + 4 * m);
+            v = make_float4((v.x * r) * w.x, (v.y * r) * w.y, (v.z * r) * w.z, (v.w * r) * w.w);
+        }
+        float d;
+        int qs;
+        const unsigned pk = zz_quant8(v, &d, &qs);
+        if (g0 < S * nb) {
+            *(unsigned *)(pp.xq + (size_t)s * D + b * ZZ_BLK + 4 * m) = pk;
+            if (m == 0) {
+                pp.xs[(size_t)s * nb + b] = d;
+                pp.xsum[(size_t)s * nb + b] = qs;
             }
         }
-        int qs;
-        const float d = zz_quant_block(v, pp.xq + (size_t)s * D + b * ZZ_BLK, &qs);
-        pp.xs[(size_t)s * nb + b] = d;
-        pp.xsum[(size_t)s * nb + b] = qs;
     }
 }
 
@@ -403,25 +399,12 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     float4 hv[DD_QB];
 #pragma unroll
     for (int k = 0; k < DD_QB; k++) hv[k] = hload(tid + 512 * k);
-    // q8_0 of a 32-block as zz_quant_block forms it: amax over the block's 8 lanes,
-    // d = amax / 127, codes rint(v / d) clamped, their sum. Called by whole waves.
+    // q8_0 of a 32-block as zz_quant_block forms it, on the block's 8 lanes
     auto quant = [&](int qd, float4 v) {
         const int blk = qd >> 3, sub = qd & 7, fp = blk / nb, b = blk - fp * nb;
-        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        m = fmaxf(m, __shfl_xor(m, 1, 64));
-        m = fmaxf(m, __shfl_xor(m, 2, 64));
-        m = fmaxf(m, __shfl_xor(m, 4, 64));
-        const float d = m / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
-        const int q0 = (int)fminf(fmaxf(rintf(v.x * id), -127.0f), 127.0f);
-        const int q1 = (int)fminf(fmaxf(rintf(v.y * id), -127.0f), 127.0f);
-        const int q2 = (int)fminf(fmaxf(rintf(v.z * id), -127.0f), 127.0f);
-        const int q3 = (int)fminf(fmaxf(rintf(v.w * id), -127.0f), 127.0f);
-        int qs = q0 + q1 + q2 + q3;
-        qs += __shfl_xor(qs, 1, 64);
-        qs += __shfl_xor(qs, 2, 64);
-        qs += __shfl_xor(qs, 4, 64);
-        const unsigned pk = (unsigned)(q0 & 0xff) | (unsigned)(q1 & 0xff) << 8 |
-                            (unsigned)(q2 & 0xff) << 16 | (unsigned)(q3 & 0xff) << 24;
+        float d;
+        int qs;
+        const unsigned pk = zz_quant8(v, &d, &qs);
         if (qd < nquad) {
             *(unsigned *)(sh_q + (size_t)fp * MI + b * ZZ_BLK + 4 * sub) = pk;
             if (sub == 0) {
@@ -529,27 +512,34 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
             v = fmaf(a.ewt[fp], y, v);
         }
         a.out[(size_t)s * D + o] = v;
+        if (a.ss) {                               // this tile's sum of squares, for the post-norm
+            double q = (double)v * (double)v;
+#pragma unroll
+            for (int m = 1; m < 16; m <<= 1) q += __shfl_xor(q, m, 64);
+            if (rr == 0) a.ss[(size_t)s * gridDim.x + g] = q;
+        }
     }
 }
 
 // gemma post-norm of the decode rows: out = rmsnorm(out, post_ffn_ln2)
-// (gemma4.c:807-808), one workgroup per token, sum of squares in double
-__global__ __launch_bounds__(256) void zz_dec_norm_kernel(float *out, const float *post_ln, int D, float eps) {
-    __shared__ double red[4];
-    float *o = out + (size_t)blockIdx.x * D;
-    double ss = 0.0;
-    for (int i = 4 * threadIdx.x; i < D; i += 1024) {
-        const float4 v = *(const float4 *)(o + i);
-        ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+// (gemma4.c:807-808). grid (D/256, S): every workgroup sums the token's G per-tile
+// sums of squares (double, fixed order: lane-strided, then a fixed butterfly) while
+// its 256 outputs and weights are in flight, then scales them.
+__global__ __launch_bounds__(256) void zz_dec_norm_kernel(float *out, const float *post_ln, const double *ss, int G,
+                                                          int D, float eps) {
+    __shared__ float rn;
+    const int tid = threadIdx.x, s = blockIdx.y, i = min(256 * blockIdx.x + tid, D - 1);
+    float *o = out + (size_t)s * D;
+    const float v = o[i], w = post_ln[i];
+    if (tid < 64) {
+        double q = 0.0;
+        for (int k = tid; k < G; k += 64) q += ss[(size_t)s * G + k];
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+        if (tid == 0) rn = 1.0f / sqrtf((float)(q / D) + eps);
     }
-    ss = zz_block_sum(ss, red);
-    const float r = 1.0f / sqrtf((float)(ss / D) + eps);
-    for (int i = 4 * threadIdx.x; i < D; i += 1024) {
-        float4 v = *(const float4 *)(o + i);
-        const float4 w = *(const float4 *)(post_ln + i);
-        v = make_float4((v.x * r) * w.x, (v.y * r) * w.y, (v.z * r) * w.z, (v.w * r) * w.w);
-        *(float4 *)(o + i) = v;
-    }
+    __syncthreads();
+    if (256 * blockIdx.x + tid < D) o[i] = (v * rn) * w;
 }
 
 int zz_launch_dec_logits(const ZzDecRouteArgs &a, hipStream_t st) {
@@ -583,7 +573,7 @@ int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st) {
     return hipGetLastError() == hipSuccess;
 }
 
-int zz_launch_dec_norm(float *out, const float *post_ln, int D, float eps, int S, hipStream_t st) {
-    hipLaunchKernelGGL(zz_dec_norm_kernel, dim3(S), dim3(256), 0, st, out, post_ln, D, eps);
+int zz_launch_dec_norm(float *out, const float *post_ln, const double *ss, int D, float eps, int S, hipStream_t st) {
+    hipLaunchKernelGGL(zz_dec_norm_kernel, dim3((D + 255) / 256, S), dim3(256), 0, st, out, post_ln, ss, D / 16, D, eps);
     return hipGetLastError() == hipSuccess;
 }
