@@ -134,24 +134,33 @@ __global__ __launch_bounds__(256) void zz_logits_exact_kernel(ZzLogitArgs a) {
     const float *X = gem ? a.xn : a.x;
     __shared__ float xs_t[2][LG_T][LG_K + 4];
     __shared__ float ws_t[2][LG_E][LG_K + 4];
-    // staging: each thread moves one float4 of each tile per chunk
-    const int lr = tid / (LG_K / 4), lc = (tid % (LG_K / 4)) * 4;   // row 0..15, col 0..60
-    const bool xrow_ok = s0 + lr < a.S, wrow_ok = e0 + lr < a.E;
-    const float *xsrc = X + (size_t)(s0 + lr) * D + lc;
-    const float *wsrc = a.router + (size_t)(e0 + lr) * D + lc;
-    float4 xv = xrow_ok ? *(const float4 *)xsrc : make_float4(0, 0, 0, 0);
-    float4 wv = wrow_ok ? *(const float4 *)wsrc : make_float4(0, 0, 0, 0);
-    *(float4 *)&xs_t[0][lr][lc] = xv;
-    *(float4 *)&ws_t[0][lr][lc] = wv;
+    // staging: each thread moves LG_V float4 of each tile per chunk (rows clamped
+    // into range: a row past the end holds copies, its chains are not stored)
+    constexpr int LG_V = LG_T * LG_K / 4 / 256;
+    const int lr = tid / (LG_K / 4 / LG_V), lc = (tid % (LG_K / 4 / LG_V)) * 4 * LG_V;
+    const float *xsrc = X + (size_t)min(s0 + lr, a.S - 1) * D + lc;
+    const float *wsrc = a.router + (size_t)min(e0 + lr, a.E - 1) * D + lc;
+    float4 xv[LG_V], wv[LG_V];
+#pragma unroll
+    for (int v = 0; v < LG_V; v++) {
+        xv[v] = *(const float4 *)(xsrc + 4 * v);
+        wv[v] = *(const float4 *)(wsrc + 4 * v);
+    }
+#pragma unroll
+    for (int v = 0; v < LG_V; v++) {
+        *(float4 *)&xs_t[0][lr][lc + 4 * v] = xv[v];
+        *(float4 *)&ws_t[0][lr][lc + 4 * v] = wv[v];
+    }
     __syncthreads();
     float vf = 0.0f;
     double vd = 0.0;
     int buf = 0;
     for (int k0 = 0; k0 < D; k0 += LG_K) {
-        const int k1 = k0 + LG_K;
-        if (k1 < D) {
-            xv = xrow_ok ? *(const float4 *)(xsrc + k1) : make_float4(0, 0, 0, 0);
-            wv = wrow_ok ? *(const float4 *)(wsrc + k1) : make_float4(0, 0, 0, 0);
+        const int k1 = min(k0 + LG_K, D - LG_K);    // the last chunk reloads itself
+#pragma unroll
+        for (int v = 0; v < LG_V; v++) {
+            xv[v] = *(const float4 *)(xsrc + k1 + 4 * v);
+            wv[v] = *(const float4 *)(wsrc + k1 + 4 * v);
         }
         const float *xr = xs_t[buf][tt], *wr = ws_t[buf][te];
         if (gem) {
@@ -173,9 +182,10 @@ __global__ __launch_bounds__(256) void zz_logits_exact_kernel(ZzLogitArgs a) {
                 vd = vd + (double)w4.w * (double)x4.w;
             }
         }
-        if (k1 < D) {
-            *(float4 *)&xs_t[buf ^ 1][lr][lc] = xv;
-            *(float4 *)&ws_t[buf ^ 1][lr][lc] = wv;
+#pragma unroll
+        for (int v = 0; v < LG_V; v++) {
+            *(float4 *)&xs_t[buf ^ 1][lr][lc + 4 * v] = xv[v];
+            *(float4 *)&ws_t[buf ^ 1][lr][lc + 4 * v] = wv[v];
         }
         __syncthreads();
         buf ^= 1;
