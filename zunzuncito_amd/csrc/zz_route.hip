@@ -217,28 +217,40 @@ __global__ __launch_bounds__(256) void zz_topk_kernel(ZzTopkArgs a, int S) {
 // exactly rows[] of gemma4.c:779-786, ascending tokens. The smallest pair index
 // of each expert orders the union as first-seen (gemma4.c:756-761). Also emits
 // the FFN work list: per expert in union order, chunks of at most `tch` pairs.
+// exclusive prefix sum over the 512 threads of a workgroup: a shuffle scan per wave,
+// then the wave totals (two barriers)
 __device__ __forceinline__ int zz_block_excl_scan(int v, int *tmp) {
-    const int t = threadIdx.x;
-    tmp[t] = v;
-    __syncthreads();
-    for (int off = 1; off < 512; off <<= 1) {
-        const int add = t >= off ? tmp[t - off] : 0;
-        __syncthreads();
-        tmp[t] += add;
-        __syncthreads();
+    const int t = threadIdx.x, l = t & 63, w = t >> 6;
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int n = __shfl_up(x, off, 64);
+        if (l >= off) x += n;
     }
-    const int incl = tmp[t];
+    if (l == 63) tmp[w] = x;
     __syncthreads();
-    return incl - v;
+    int base = 0;
+    for (int q = 0; q < w; q++) base += tmp[q];
+    __syncthreads();                           // tmp is free again for the next scan
+    return base + x - v;
 }
 
 #define DP_PT 16                      // pairs per thread: S*K <= 8192 = 512 * DP_PT
+// One workgroup: the per-expert token bitmasks give each expert's count, its pairs'
+// positions (a stable counting sort by expert, gemma4.c:779-786) and its first pair;
+// the union order is the order of first pairs (gemma4.c:756-761), read off a bitmap
+// over the pairs by prefix popcounts.
+// LDS: mask and word prefixes [E][W] (W = S/32 words), pair experts [P], first-pair
+// bitmap [P/32].
 __global__ __launch_bounds__(512) void zz_dispatch_kernel(ZzDispatchArgs a) {
     extern __shared__ unsigned dsm[];
-    __shared__ int cnt[ZZ_MAXE], start[ZZ_MAXE], first[ZZ_MAXE], order[ZZ_MAXE], tmp[512];
-    const int P = a.P, E = a.E, K = a.K, S = P / K, W = (S + 31) / 32, t = threadIdx.x;
-    unsigned *mask = dsm, *wpre = dsm + E * W;
+    __shared__ int cnt[ZZ_MAXE], start[ZZ_MAXE], first[ZZ_MAXE], order[ZZ_MAXE], tmp[16];
+    __shared__ int fbase[DP_PT * 512 / 32];      // first pairs before each bitmap word
+    const int P = a.P, E = a.E, K = a.K, S = P / K, W = (S + 31) / 32, PW = (P + 31) / 32, t = threadIdx.x;
+    unsigned *mask = dsm, *wpre = dsm + E * W, *fb = wpre + E * W;
+    int *pe = (int *)(fb + PW);
     for (int i = t; i < E * W; i += 512) mask[i] = 0u;
+    for (int i = t; i < PW; i += 512) fb[i] = 0u;
     // every pair's expert and weight in registers first: one round of loads
     int ev[DP_PT];
     float wv[DP_PT];
@@ -249,6 +261,9 @@ __global__ __launch_bounds__(512) void zz_dispatch_kernel(ZzDispatchArgs a) {
         ev[k] = e < 0 || e >= E ? 0 : e;            // never index past the expert tables
         wv[k] = a.ewt[p];
     }
+#pragma unroll
+    for (int k = 0; k < DP_PT; k++)
+        if (t + 512 * k < P) pe[t + 512 * k] = ev[k];
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < DP_PT; k++) {
@@ -268,16 +283,19 @@ __global__ __launch_bounds__(512) void zz_dispatch_kernel(ZzDispatchArgs a) {
         }
         cnt[e] = run;
         int f = 0x7fffffff;
-        if (s0 >= 0)
-            for (int j = K - 1; j >= 0; j--) {
-                const int ej = a.eidx[s0 * K + j];
-                if ((ej < 0 || ej >= E ? 0 : ej) == e) f = s0 * K + j;
-            }
+        if (s0 >= 0) {
+            for (int j = K - 1; j >= 0; j--)
+                if (pe[s0 * K + j] == e) f = s0 * K + j;
+            atomicOr(&fb[f >> 5], 1u << (f & 31));
+        }
         first[e] = f;
     }
-    __syncthreads();
-    const int st = zz_block_excl_scan(t < E ? cnt[t] : 0, tmp);
+    const int st = zz_block_excl_scan(t < E ? cnt[t] : 0, tmp);   // its barrier orders the above
     if (t < E) start[t] = st;
+    // union rank of each present expert: first pairs below its own
+    const int fw = t < PW ? __popc(fb[t]) : 0;
+    const int fpre = zz_block_excl_scan(fw, tmp);
+    if (t < PW) fbase[t] = fpre;
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < DP_PT; k++) {
@@ -291,14 +309,10 @@ __global__ __launch_bounds__(512) void zz_dispatch_kernel(ZzDispatchArgs a) {
             a.ppos[p] = pos;
         }
     }
-    // union order: rank the present experts by first-seen pair index
     const bool present = t < E && cnt[t] != 0;
     if (present) {
-        const int fe = first[t];
-        int r = 0;
-#pragma unroll 8
-        for (int f = 0; f < E; f++) r += cnt[f] != 0 && first[f] < fe;
-        order[r] = t;
+        const int f = first[t];
+        order[fbase[f >> 5] + __popc(fb[f >> 5] & ((1u << (f & 31)) - 1u))] = t;
     }
     const int nu = __syncthreads_count(present);
     const int ce = t < nu ? cnt[order[t]] : 0;
@@ -348,7 +362,8 @@ int zz_launch_topk(const ZzTopkArgs &a, int S, hipStream_t st) {
 }
 
 int zz_launch_dispatch(const ZzDispatchArgs &a, hipStream_t st) {
-    const int W = (a.P / a.K + 31) / 32;
-    hipLaunchKernelGGL(zz_dispatch_kernel, dim3(1), dim3(512), sizeof(unsigned) * 2 * a.E * W, st, a);
+    const int W = (a.P / a.K + 31) / 32, PW = (a.P + 31) / 32;
+    const size_t lds = sizeof(unsigned) * (2 * (size_t)a.E * W + PW) + sizeof(int) * (size_t)a.P;
+    hipLaunchKernelGGL(zz_dispatch_kernel, dim3(1), dim3(512), lds, st, a);
     return hipGetLastError() == hipSuccess;
 }
