@@ -240,15 +240,16 @@ __device__ __forceinline__ int zz_block_excl_scan(int v, int *tmp) {
 // positions (a stable counting sort by expert, gemma4.c:779-786) and its first pair;
 // the union order is the order of first pairs (gemma4.c:756-761), read off a bitmap
 // over the pairs by prefix popcounts.
-// LDS: mask and word prefixes [E][W] (W = S/32 words), pair experts [P], first-pair
-// bitmap [P/32].
+// LDS: mask and word prefixes [E][W] (W = S/32 words), first-pair bitmap [P/32],
+// pair experts [P] (then the inverse permutation) and weights by position [P].
 __global__ __launch_bounds__(512) void zz_dispatch_kernel(ZzDispatchArgs a) {
     extern __shared__ unsigned dsm[];
     __shared__ int cnt[ZZ_MAXE], start[ZZ_MAXE], first[ZZ_MAXE], order[ZZ_MAXE], tmp[16];
     __shared__ int fbase[DP_PT * 512 / 32];      // first pairs before each bitmap word
     const int P = a.P, E = a.E, K = a.K, S = P / K, W = (S + 31) / 32, PW = (P + 31) / 32, t = threadIdx.x;
     unsigned *mask = dsm, *wpre = dsm + E * W, *fb = wpre + E * W;
-    int *pe = (int *)(fb + PW);
+    int *pe = (int *)(fb + PW);                  // pair -> expert, later position -> pair
+    float *pwl = (float *)(pe + P);              // position -> weight
     for (int i = t; i < E * W; i += 512) mask[i] = 0u;
     for (int i = t; i < PW; i += 512) fb[i] = 0u;
     // every pair's expert and weight in registers first: one round of loads
@@ -297,16 +298,28 @@ __global__ __launch_bounds__(512) void zz_dispatch_kernel(ZzDispatchArgs a) {
     const int fpre = zz_block_excl_scan(fw, tmp);
     if (t < PW) fbase[t] = fpre;
     __syncthreads();
+    // positions; the sorted lists are then written in position order (coalesced)
+    // through the inverse permutation, which reuses the pair-expert array
 #pragma unroll
     for (int k = 0; k < DP_PT; k++) {
         const int p = t + 512 * k;
         if (p < P) {
             const int e = ev[k], s = p / K, w = s >> 5, bit = s & 31;
             const int pos = start[e] + wpre[e * W + w] + __popc(mask[e * W + w] & ((1u << bit) - 1u));
-            a.ptok[pos] = s;
-            a.pslot[pos] = p - s * K;
-            a.pwt[pos] = wv[k];
             a.ppos[p] = pos;
+            pe[pos] = p;
+            pwl[pos] = wv[k];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < DP_PT; k++) {
+        const int i = t + 512 * k;
+        if (i < P) {
+            const int p = pe[i], s = p / K;
+            a.ptok[i] = s;
+            a.pslot[i] = p - s * K;
+            a.pwt[i] = pwl[i];
         }
     }
     const bool present = t < E && cnt[t] != 0;
@@ -363,7 +376,7 @@ int zz_launch_topk(const ZzTopkArgs &a, int S, hipStream_t st) {
 
 int zz_launch_dispatch(const ZzDispatchArgs &a, hipStream_t st) {
     const int W = (a.P / a.K + 31) / 32, PW = (a.P + 31) / 32;
-    const size_t lds = sizeof(unsigned) * (2 * (size_t)a.E * W + PW) + sizeof(int) * (size_t)a.P;
+    const size_t lds = sizeof(unsigned) * (2 * (size_t)a.E * W + PW) + 8 * (size_t)a.P;
     hipLaunchKernelGGL(zz_dispatch_kernel, dim3(1), dim3(512), lds, st, a);
     return hipGetLastError() == hipSuccess;
 }
