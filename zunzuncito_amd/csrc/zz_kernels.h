@@ -134,7 +134,7 @@ int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st);
 int zz_dec_fits(int S, int K, int MI);   // the decode path's LDS holds S*K hidden rows
 int zz_launch_dec_norm(float *out, const float *post_ln, const double *ss, int D, float eps, int S, hipStream_t st);
 // int8-MFMA grouped GEMM for work items of up to ZZ_MMA_TOKENS tokens
-#define ZZ_MMA_TOKENS 128
+#define ZZ_MMA_TOKENS 64
 int zz_launch_up_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_down_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_combine(const ZzCombineArgs &a, int S, hipStream_t st);

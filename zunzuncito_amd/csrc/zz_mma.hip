@@ -6,7 +6,7 @@
 // tq2's <c - 1, x>). Each is scaled by d_w[row,b] * d_x[token,b] into an fp32
 // accumulator, as the reference's per-block FMA does (q40.h:186).
 //
-// Work unit: (item, tile). An item is one expert with up to 128 of its tokens (the
+// Work unit: (item, tile). An item is one expert with up to 64 of its tokens (the
 // dispatch work list); a tile is 64 weight rows: 4 waves x one 16-row group each.
 // Every wave multiplies its rows by all of the item's tokens (up to 8 MFMA tiles of
 // 16 tokens), so each weight fragment is loaded and unpacked once per item.
@@ -24,7 +24,9 @@
 
 typedef int zz_v4i __attribute__((ext_vector_type(4)));
 
-#define MM_TN ZZ_MMA_TOKENS            // tokens per work item: 8 tiles of 16
+#define MM_TN ZZ_MMA_TOKENS            // tokens per work item: 4 tiles of 16
+#define MM_XP (8 * MM_TN / 256)        // 16-byte activation pieces per thread and chunk
+#define MM_SP (4 * MM_TN / 256)        // activation scales per thread and chunk
 // LDS row stride of a staged token: one 4-block chunk (128 bytes) + 8, so the 16
 // tokens a quarter-wave reads fall on distinct banks
 #define MM_XS (4 * ZZ_BLK + 8)
@@ -140,14 +142,14 @@ __device__ __forceinline__ void mm_chunk(const MmA &A, int l, float (&acc)[NT][4
 // Activations of one chunk: a thread moves 4 16-byte pieces (token, segment) and
 // two (token, block) scales per chunk, always the same slots.
 struct MmX {
-    uint4 v[4];
-    float s[2];
+    uint4 v[MM_XP];
+    float s[MM_SP];
 };
 
 struct MmSrc {
-    const int8_t *row[4];            // activation row of each piece's token
-    const float *srow[2];            // d_x row of each scale slot's token
-    int seg[4], kb[2];
+    const int8_t *row[MM_XP];        // activation row of each piece's token
+    const float *srow[MM_SP];        // d_x row of each scale slot's token
+    int seg[MM_XP], kb[MM_SP];
 };
 
 // No masks: padding tokens of an item read a real token's row (so their columns hold
@@ -159,7 +161,7 @@ __device__ __forceinline__ void mm_load_x(const MmSrc &src, int c, int cbs, MmX 
 #pragma unroll
     for (int k = 0; k < KP; k++) x.v[k] = ld16(src.row[k] + c * 4 * ZZ_BLK + 16 * min(src.seg[k], 2 * cbs - 1));
 #pragma unroll
-    for (int k = 0; k < 2; k++) x.s[k] = src.srow[k][4 * c + min(src.kb[k], cbs - 1)];
+    for (int k = 0; k < MM_SP; k++) x.s[k] = src.srow[k][4 * c + min(src.kb[k], cbs - 1)];
 }
 
 template <int KP>
@@ -173,9 +175,9 @@ __device__ __forceinline__ void mm_store_x(const MmX &x, MmStage &st) {
         d[1] = make_uint2(x.v[k].z, x.v[k].w);
     }
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
+    for (int k = 0; k < MM_SP; k++) {
         const int i = tid + 256 * k;
-        st.s[i >> 7][i & 127] = x.s[k];
+        st.s[i / MM_TN][i % MM_TN] = x.s[k];
     }
 }
 
@@ -195,7 +197,7 @@ __device__ __forceinline__ void mm_kloop(const uint8_t *E, const ZzTensor &T, in
     for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[t][i] = 0.0f;
-    constexpr int KP = (NT + 1) / 2;
+    constexpr int KP = (NT + 1) / 2 < MM_XP ? (NT + 1) / 2 : MM_XP;
     MmA r[RING];
 #pragma unroll
     for (int i = 0; i < RING - 1; i++) r[i] = mm_load_a<FMT>(E, T, g, min(i, nch - 1), l);
@@ -237,7 +239,7 @@ __device__ __forceinline__ void mm_kloop(const uint8_t *E, const ZzTensor &T, in
     }
 }
 
-#define MM_RING(NT) ((NT) <= 4 ? 4 : 2)
+#define MM_RING(NT) ((NT) <= 2 ? 4 : 3)
 
 // ------------------------------------------------------------------ up
 union MmUpShared {
@@ -249,7 +251,8 @@ union MmUpShared {
     } e;
 };
 
-template <int NT>
+// GF, UF: the gate and up formats (gate and up are both tq2 or neither)
+template <int GF, int UF, int NT>
 __device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &item, int rb, MmUpShared &sm,
                                            int *tok) {
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, qq = l >> 4;
@@ -260,29 +263,24 @@ __device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &ite
     __syncthreads();
     MmSrc src;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < MM_XP; k++) {
         const int i = tid + 256 * k, t = i >> 3;
         src.row[k] = a.xq + (size_t)tok[t] * D;          // tok[t >= n]: token n - 1
         src.seg[k] = i & 7;
     }
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
-        const int i = tid + 256 * k, t = i & 127;
+    for (int k = 0; k < MM_SP; k++) {
+        const int i = tid + 256 * k, t = i % MM_TN;
         src.srow[k] = a.xs + (size_t)tok[t] * nb;
-        src.kb[k] = i >> 7;
+        src.kb[k] = i / MM_TN;
     }
 
     // gate and up may differ in format (q4_0 / q8_0); each wave runs its tensor's loop
     // (the same number of chunks and barriers either way)
     float acc[NT][4];
-    if (T.fmt == ZZ_FMT_Q40) {
-        mm_kloop<ZZ_FMT_Q40, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
-    } else if (T.fmt == ZZ_FMT_Q80) {
-        mm_kloop<ZZ_FMT_Q80, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
-    } else {
-        mm_kloop<ZZ_FMT_TQ2, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
-    }
-    if (T.fmt == ZZ_FMT_TQ2) {                   // tq2.h:154, alpha of the row
+    if (GF == UF || w < 2) mm_kloop<GF, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
+    else mm_kloop<UF, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
+    if (GF == ZZ_FMT_TQ2) {                      // tq2.h:154, alpha of the row
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const float al = ((const float *)(E + T.off_s))[16 * g + 4 * qq + i];
@@ -362,16 +360,16 @@ __device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &i
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
     MmSrc src;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < MM_XP; k++) {
         const int i = tid + 256 * k, t = i >> 3;
         src.row[k] = a.hq + ((size_t)item.p0 + min(t, n - 1)) * MI;
         src.seg[k] = i & 7;
     }
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
-        const int i = tid + 256 * k, t = i & 127;
+    for (int k = 0; k < MM_SP; k++) {
+        const int i = tid + 256 * k, t = i % MM_TN;
         src.srow[k] = a.hs + ((size_t)item.p0 + min(t, n - 1)) * nb;
-        src.kb[k] = i >> 7;
+        src.kb[k] = i / MM_TN;
     }
 
     float acc[NT][4];
@@ -404,6 +402,7 @@ static unsigned zz_xcd_grid(int max_items, int ntiles) {
     return (unsigned)((max_items + ZZ_XCDS - 1) / ZZ_XCDS * ZZ_XCDS * ntiles);
 }
 
+template <int GF, int UF>
 __global__ __launch_bounds__(256) void zz_up_mma_kernel(ZzFfnArgs a) {
     int it, rb;
     zz_xcd_tile(a.MI / 32, &it, &rb);
@@ -412,10 +411,9 @@ __global__ __launch_bounds__(256) void zz_up_mma_kernel(ZzFfnArgs a) {
     __shared__ MmUpShared sm;
     __shared__ int tok[MM_TN];
     const int nt = (item.n + 15) / 16;
-    if (nt <= 1) mm_up_body<1>(a, item, rb, sm, tok);
-    else if (nt <= 2) mm_up_body<2>(a, item, rb, sm, tok);
-    else if (nt <= 4) mm_up_body<4>(a, item, rb, sm, tok);
-    else mm_up_body<8>(a, item, rb, sm, tok);
+    if (nt <= 1) mm_up_body<GF, UF, 1>(a, item, rb, sm, tok);
+    else if (nt <= 2) mm_up_body<GF, UF, 2>(a, item, rb, sm, tok);
+    else mm_up_body<GF, UF, 4>(a, item, rb, sm, tok);
 }
 
 template <int FMT>
@@ -428,12 +426,17 @@ __global__ __launch_bounds__(256) void zz_down_mma_kernel(ZzFfnArgs a) {
     const int nt = (item.n + 15) / 16;
     if (nt <= 1) mm_down_body<FMT, 1>(a, item, rt, sm);
     else if (nt <= 2) mm_down_body<FMT, 2>(a, item, rt, sm);
-    else if (nt <= 4) mm_down_body<FMT, 4>(a, item, rt, sm);
-    else mm_down_body<FMT, 8>(a, item, rt, sm);
+    else mm_down_body<FMT, 4>(a, item, rt, sm);
 }
 
 int zz_launch_up_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st) {
-    hipLaunchKernelGGL(zz_up_mma_kernel, dim3(zz_xcd_grid(max_items, a.MI / 32)), dim3(256), 0, st, a);
+    const dim3 g(zz_xcd_grid(max_items, a.MI / 32));
+    const int gf = a.lay.gate.fmt, uf = a.lay.up.fmt;
+    if (gf == ZZ_FMT_TQ2) hipLaunchKernelGGL((zz_up_mma_kernel<ZZ_FMT_TQ2, ZZ_FMT_TQ2>), g, dim3(256), 0, st, a);
+    else if (gf == ZZ_FMT_Q40 && uf == ZZ_FMT_Q40) hipLaunchKernelGGL((zz_up_mma_kernel<ZZ_FMT_Q40, ZZ_FMT_Q40>), g, dim3(256), 0, st, a);
+    else if (gf == ZZ_FMT_Q80 && uf == ZZ_FMT_Q80) hipLaunchKernelGGL((zz_up_mma_kernel<ZZ_FMT_Q80, ZZ_FMT_Q80>), g, dim3(256), 0, st, a);
+    else if (gf == ZZ_FMT_Q40) hipLaunchKernelGGL((zz_up_mma_kernel<ZZ_FMT_Q40, ZZ_FMT_Q80>), g, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((zz_up_mma_kernel<ZZ_FMT_Q80, ZZ_FMT_Q40>), g, dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess;
 }
 
