@@ -166,7 +166,6 @@ struct Workspace {
     float *hs = nullptr;
     int *hsum = nullptr;
     float *y = nullptr;
-    float *hf = nullptr;
     double *ss = nullptr;       // decode post-norm per-tile sums of squares
     void *block = nullptr;      // one allocation holds everything above
 };
@@ -353,7 +352,7 @@ static int ensure_ws(Layer *L, int S) {
     size_t o_uniq = take(4 * (size_t)d.E), o_uoff = take(4 * (size_t)d.E), o_ucnt = take(4 * (size_t)d.E);
     size_t o_meta = take(64), o_items = take(sizeof(ZzItem) * nitems);
     size_t o_hq = take(P * d.MI), o_hs = take(4 * P * nbM), o_hsum = take(4 * P * nbM);
-    size_t o_y = take(4 * P * d.D), o_hf = take(4 * P * d.MI), o_ss = take(8 * S * (size_t)(d.D / 16));
+    size_t o_y = take(4 * P * d.D), o_ss = take(8 * S * (size_t)(d.D / 16));
     void *blk = nullptr;
     ZZ_CHECK(hipStreamSynchronize(g_stream));
     ZZ_CHECK(hipMalloc(&blk, off));
@@ -369,7 +368,7 @@ static int ensure_ws(Layer *L, int S) {
     w.ppos = (int *)(b + o_ppos); w.pwt = (float *)(b + o_pwt); w.uniq = (int *)(b + o_uniq);
     w.uoff = (int *)(b + o_uoff); w.ucnt = (int *)(b + o_ucnt); w.meta = (int *)(b + o_meta);
     w.items = (ZzItem *)(b + o_items); w.hq = (int8_t *)(b + o_hq); w.hs = (float *)(b + o_hs);
-    w.hsum = (int *)(b + o_hsum); w.y = (float *)(b + o_y); w.hf = (float *)(b + o_hf);
+    w.hsum = (int *)(b + o_hsum); w.y = (float *)(b + o_y);
     w.ss = (double *)(b + o_ss);
     ZZ_CHECK(hipStreamSynchronize(g_stream));
     return 1;
@@ -486,7 +485,7 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
     fa.D = d.D; fa.MI = d.MI; fa.K = d.K; fa.act = d.act; fa.clamp = d.clamp;
     fa.experts = L->slots; fa.estride = L->lay.bytes; fa.lay = L->lay; fa.items = w.items;
     fa.meta = w.meta; fa.ptok = w.ptok; fa.xq = w.xq; fa.xs = w.xs; fa.xsum = w.xsum; fa.xt = w.xt;
-    fa.hq = w.hq; fa.hs = w.hs; fa.hsum = w.hsum; fa.y = w.y; fa.hf = w.hf;
+    fa.hq = w.hq; fa.hs = w.hs; fa.hsum = w.hsum; fa.y = w.y;
     const int max_items = (P < d.E ? P : d.E) + (P + tch - 1) / tch;
     if (dec) {
         ZzDecDownArgs dd;

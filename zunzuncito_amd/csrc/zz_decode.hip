@@ -120,18 +120,18 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
 }
 
 // ------------------------------------------------------------------ gate/up
-// grid (MI/16, S*K), 256 threads. Workgroup (j, p) owns hidden rows 16j..16j+15 of
+// grid (MI/32, S*K), 512 threads. Workgroup (j, p) owns hidden rows 32j..32j+31 of
 // (token, slot) pair p = s*K + slot. Wave 0 first runs the certified top-k of token
 // s (zz_topk_wave.h): every workgroup of the token repeats it, so no separate gating
 // launch or dispatch list stands between the router and the expert weights; the
-// token's first workgroup writes the routing outputs. Then wave w takes row group j
-// of gate (w even) or up (w odd) of the pair's expert over half w/2 of the K range.
+// token's first workgroup writes the routing outputs. Then wave w takes row group
+// 2j + (w & 1) of gate (w & 3 < 2) or up of the pair's expert over half w/4 of the
+// K range.
 // Lane l = 16*qq + r is the slot table's lane: row r of the group, weights
 // 8qq..8qq+7 of every block, so one chunk of 4 blocks is one contiguous 16-byte
 // (q4_0) or 32-byte (q8_0) load; tq2 lanes take whole 64-groups of row r. The
 // token's activations are requested first, the weights as soon as the expert is
-// known. The output is h = act(g, u) in fp32 by flat pair; its q8_0 quantisation
-// happens where it is consumed (the down kernel).
+// known. The output is h = act(g, u) quantised to q8_0 (hq, hs, hsum by flat pair).
 #define DU_C 12          // chunks (tq2: groups) per lane issued together
 #define DEC_SEG (ZZ_MAXD / 16 / 256)          // activation segments per thread
 
@@ -305,24 +305,26 @@ __device__ __forceinline__ float zz_dec_up_part(const ZzFfnArgs &a, const ZzDecS
     return acc;
 }
 
-__global__ __launch_bounds__(256) void zz_dec_up_kernel(ZzDecUpArgs a) {
+__global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
     const ZzFfnArgs &f = a.f;
     const int K = a.tk.K, p = blockIdx.y, s = p / K, js = p - s * K;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = w >> 1, q = w & 1, j = blockIdx.x;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = w >> 2, q = w & 3, j = blockIdx.x;
     extern __shared__ __attribute__((aligned(16))) char tk_lds[];
     __shared__ ZzDecStage st;
-    __shared__ float part[2][2][16];                // [half][gate/up][row]
+    __shared__ float part[2][4][16];                // [half][gate g0, g1, up g0, g1][row]
+    __shared__ float hb[ZZ_BLK];
     ZzDecStageRegs sr;
     zz_dec_stage_issue(f, s, sr);
     if (w == 0) zz_topk_wave_any(a.tk, s, tk_lds, j == 0 && js == 0);
     __syncthreads();
     const int e = zz_clamp_e(((const ZzTopkWaveHdr *)tk_lds)->idx[js], a.tk.E);
-    const ZzTensor &T = q ? f.lay.up : f.lay.gate;
+    const ZzTensor &T = q >= 2 ? f.lay.up : f.lay.gate;
+    const int g = 2 * j + (q & 1);
     const uint8_t *E = f.experts + (size_t)e * f.estride;
     float acc;
-    if (T.fmt == ZZ_FMT_Q40) acc = zz_dec_up_part<ZZ_FMT_Q40>(f, sr, st, E, T, j, h, l);
-    else if (T.fmt == ZZ_FMT_Q80) acc = zz_dec_up_part<ZZ_FMT_Q80>(f, sr, st, E, T, j, h, l);
-    else acc = zz_dec_up_part<ZZ_FMT_TQ2>(f, sr, st, E, T, j, h, l);
+    if (T.fmt == ZZ_FMT_Q40) acc = zz_dec_up_part<ZZ_FMT_Q40>(f, sr, st, E, T, g, h, l);
+    else if (T.fmt == ZZ_FMT_Q80) acc = zz_dec_up_part<ZZ_FMT_Q80>(f, sr, st, E, T, g, h, l);
+    else acc = zz_dec_up_part<ZZ_FMT_TQ2>(f, sr, st, E, T, g, h, l);
     acc += __shfl_xor(acc, 16, 64);                             // sum over the 4 k-quarters
     acc += __shfl_xor(acc, 32, 64);
     if (l < 16) part[h][q][l] = acc;
@@ -333,32 +335,46 @@ __global__ __launch_bounds__(256) void zz_dec_up_kernel(ZzDecUpArgs a) {
         st.xt = (float)tot;
     }
     __syncthreads();
-    if (tid < 16) {                                             // hidden row 16j + tid
-        float g = part[0][0][tid] + part[1][0][tid];
-        float u = part[0][1][tid] + part[1][1][tid];
+    if (tid < ZZ_BLK) {                                         // hidden row 32j + tid
+        const int gg = tid >> 4, r = tid & 15;
+        float gv = part[0][gg][r] + part[1][gg][r];
+        float uv = part[0][2 + gg][r] + part[1][2 + gg][r];
         if (T.fmt == ZZ_FMT_TQ2) {                              // tq2.h:154
-            g = ((const float *)(E + f.lay.gate.off_s))[16 * j + tid] * (g - st.xt);
-            u = ((const float *)(E + f.lay.up.off_s))[16 * j + tid] * (u - st.xt);
+            gv = ((const float *)(E + f.lay.gate.off_s))[32 * j + tid] * (gv - st.xt);
+            uv = ((const float *)(E + f.lay.up.off_s))[32 * j + tid] * (uv - st.xt);
         }
-        f.hf[(size_t)p * f.MI + 16 * j + tid] = zz_act(f.act, g, u, f.clamp);
+        hb[tid] = zz_act(f.act, gv, uv, f.clamp);
+    }
+    __syncthreads();
+    if (w == 0) {                                               // q8_0 of the block (gemma4.c:646)
+        const int m = l & 7;
+        const float4 v = *(const float4 *)&hb[4 * m];
+        float d;
+        int qs;
+        const unsigned pk = zz_quant8(v, &d, &qs);
+        const int nbM = f.MI / ZZ_BLK;
+        if (l < 8) *(unsigned *)(f.hq + (size_t)p * f.MI + 32 * j + 4 * m) = pk;
+        if (l == 0) {
+            f.hs[(size_t)p * nbM + j] = d;
+            f.hsum[(size_t)p * nbM + j] = qs;
+        }
     }
 }
 
 // ------------------------------------------------------------------ down + combine
 // grid D/16, 512 threads: the workgroup owns the 16 output rows of row group g of
-// down. First every (token, slot) pair's hidden h is quantised to q8_0 into LDS
-// (gemma4.c:646, the same rounding as zz_quant_block; workgroup 0 also writes the
-// codes out). Wave w takes the pairs w, w+8, ... and walks their units (pair,
+// down. First every (token, slot) pair's q8_0 hidden is staged in LDS. Wave w
+// takes the pairs w, w+8, ... and walks their units (pair,
 // chunk) in order, DD_C units' loads at a time; lane l = 16*qq + r as in the
 // gate/up kernel. A pair's partial dots are summed over the 4 k-quarters when its
 // last unit is done. The 16 x P expert outputs are then combined per token in slot
 // order, out = fma(w_j, y_j, out) as gemma4.c:652.
 #define DD_C 12
 #define DD_W 8                        // waves
-#define DD_QB 4                       // hidden float4 per thread requested ahead
+#define DD_QB 4                       // hidden 16-byte segments per thread requested ahead
+#define DD_SB 2                       // hidden block scales per thread requested ahead
 
 struct ZzDecPairs {                 // per (token, slot) pair, flat order s*K + j
-    int pos[DEC_MAXS * ZZ_MAXK];    // sorted position: row of hf / hq / hs / hsum
     int e[DEC_MAXS * ZZ_MAXK];      // expert (clamped into the table)
 };
 
@@ -383,44 +399,25 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     float *sh_s = (float *)(dd_lds + (size_t)P * MI);           // [P][nb]
     int *sh_c = (int *)(sh_s + P * nb);                         // [P][nb]
     if (tid < P) {
-        pr.pos[tid] = tid;                        // the up kernel writes the hidden by flat pair
         pr.e[tid] = zz_clamp_e(a.eidx[tid], a.E);
     }
     __syncthreads();
-    // the pairs' fp32 hidden, requested before the weights: 8 lanes per 32-block, a
-    // float4 each, the first DD_QB per thread (the wait for them then leaves the
-    // weight loads in flight; loads complete in order)
-    const int nquad = P * nb * 8;
-    auto hload = [&](int qd) {
-        qd = min(qd, nquad - 1);
-        const int blk = qd >> 3, fp = blk / nb;
-        return *(const float4 *)(f.hf + (size_t)pr.pos[fp] * MI + (blk - fp * nb) * ZZ_BLK + 4 * (qd & 7));
-    };
-    float4 hv[DD_QB];
+    // the pairs' q8_0 hidden (codes, scales, sums by flat pair), requested before the
+    // weights (the wait for them then leaves the weight loads in flight; loads
+    // complete in order); the LDS writes are unconditional, clamped slots holding
+    // copies, so the loads cannot sink past the weights
+    const int nseg = P * MI / 16, nsc = P * nb;
+    uint4 hv[DD_QB];
+    float sv[DD_SB];
+    int cv[DD_SB];
 #pragma unroll
-    for (int k = 0; k < DD_QB; k++) hv[k] = hload(tid + 512 * k);
-    // q8_0 of a 32-block as zz_quant_block forms it, on the block's 8 lanes
-    auto quant = [&](int qd, float4 v) {
-        const int blk = qd >> 3, sub = qd & 7, fp = blk / nb, b = blk - fp * nb;
-        float d;
-        int qs;
-        const unsigned pk = zz_quant8(v, &d, &qs);
-        if (qd < nquad) {
-            *(unsigned *)(sh_q + (size_t)fp * MI + b * ZZ_BLK + 4 * sub) = pk;
-            if (sub == 0) {
-                sh_s[fp * nb + b] = d;
-                sh_c[fp * nb + b] = qs;
-            }
-            if (g == 0) {                                       // the codes, for the record
-                const size_t p = (size_t)pr.pos[fp];
-                *(unsigned *)(f.hq + p * MI + b * ZZ_BLK + 4 * sub) = pk;
-                if (sub == 0) {
-                    f.hs[p * nb + b] = d;
-                    f.hsum[p * nb + b] = qs;
-                }
-            }
-        }
-    };
+    for (int k = 0; k < DD_QB; k++) hv[k] = ld16(f.hq + 16 * (size_t)min(tid + 512 * k, nseg - 1));
+#pragma unroll
+    for (int k = 0; k < DD_SB; k++) {
+        const int i = min(tid + 512 * k, nsc - 1);
+        sv[k] = f.hs[i];
+        cv[k] = f.hsum[i];
+    }
     ZzChunk k[DD_C];
     uint4 c[DD_C];
     auto load_units = [&](int u0) {
@@ -479,9 +476,18 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     __builtin_amdgcn_sched_barrier(0);                          // hidden loads issue first
     load_units(0);
 #pragma unroll
-    for (int kq = 0; kq < DD_QB; kq++)
-        if (512 * kq < nquad) quant(tid + 512 * kq, hv[kq]);     // uniform condition
-    for (int q0 = 512 * DD_QB; q0 < nquad; q0 += 512) quant(q0 + tid, hload(q0 + tid));
+    for (int k = 0; k < DD_QB; k++) *(uint4 *)(sh_q + 16 * (size_t)min(tid + 512 * k, nseg - 1)) = hv[k];
+#pragma unroll
+    for (int k = 0; k < DD_SB; k++) {
+        const int i = min(tid + 512 * k, nsc - 1);
+        sh_s[i] = sv[k];
+        sh_c[i] = cv[k];
+    }
+    for (int i = tid + 512 * DD_QB; i < nseg; i += 512) *(uint4 *)(sh_q + 16 * (size_t)i) = ld16(f.hq + 16 * (size_t)i);
+    for (int i = tid + 512 * DD_SB; i < nsc; i += 512) {
+        sh_s[i] = f.hs[i];
+        sh_c[i] = f.hsum[i];
+    }
     __syncthreads();
     if (FMT == ZZ_FMT_TQ2 && tid < P) {                         // tq2.h:101-106, serial
         double t = 0.0;
@@ -554,7 +560,7 @@ int zz_launch_dec_logits(const ZzDecRouteArgs &a, hipStream_t st) {
 }
 
 int zz_launch_dec_up(const ZzDecUpArgs &a, int S, hipStream_t st) {
-    hipLaunchKernelGGL(zz_dec_up_kernel, dim3(a.f.MI / 16, S * a.tk.K), dim3(256), zz_topk_wave_bytes(a.tk.E), st, a);
+    hipLaunchKernelGGL(zz_dec_up_kernel, dim3(a.f.MI / 32, S * a.tk.K), dim3(512), zz_topk_wave_bytes(a.tk.E), st, a);
     return hipGetLastError() == hipSuccess;
 }
 

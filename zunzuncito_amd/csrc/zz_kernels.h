@@ -74,7 +74,6 @@ struct ZzFfnArgs {
     float *hs;                  // [P, MI/32]
     int *hsum;                  // [P, MI/32]
     float *y;                   // [P, D] expert outputs before weighting
-    float *hf;                  // [P, MI] fp32 hidden of the decode path
 };
 
 struct ZzCombineArgs {
