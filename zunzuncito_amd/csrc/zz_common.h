@@ -89,6 +89,33 @@ __host__ __device__ __forceinline__ int64_t zz_sidx(const ZzTensor &T, int g, in
 }
 // tq2 codes: 16-row groups, each a run of the 16 rows' 16-byte 64-weight groups in
 // the reference byte order (byte k: weights k, k+16, k+32, k+48 at bits 0, 2, 4, 6)
+// A lane's walk over the chunks of one 16-row group of a q4_0 / q8_0 tensor, with
+// the offsets of zz_qlane / zz_sidx strength-reduced: a full chunk is chunk 0 plus c
+// strides, the short last chunk (if any) has its own offset. rr is the row of the
+// scale pointer within the group. Offsets are from the expert's base.
+struct ZzWalk {
+    int64_t qb, qs, sb, ss;
+    int nfull, qstep;
+};
+__device__ __forceinline__ ZzWalk zz_walk(const ZzTensor &T, int g, int lane, int rr) {
+    ZzWalk w;
+    const int nb = T.I / ZZ_BLK, lb = zz_lb(T);
+    w.nfull = nb / 4;
+    w.qstep = 256 * lb;
+    w.qb = zz_qlane(T, g, 0, lane);
+    w.sb = zz_sidx(T, g, 0, rr);
+    const int bl = 4 * (w.nfull < (nb + 3) / 4 ? w.nfull : 0);     // the short chunk's first block
+    w.qs = zz_qlane(T, g, bl, lane);
+    w.ss = zz_sidx(T, g, bl, rr);
+    return w;
+}
+__device__ __forceinline__ const uint8_t *zz_walk_q(const uint8_t *E, const ZzWalk &w, int c) {
+    return E + (c < w.nfull ? w.qb + (int64_t)c * w.qstep : w.qs);
+}
+__device__ __forceinline__ const uint8_t *zz_walk_s(const uint8_t *E, const ZzWalk &w, int c) {
+    return E + (c < w.nfull ? w.sb + (int64_t)c * 128 : w.ss);
+}
+
 __host__ __device__ __forceinline__ int64_t zz_tq2off(const ZzTensor &T, int row, int gp) {
     return T.off_q + (((int64_t)(row >> 4) * (T.I / 64) + gp) * 16 + (row & 15)) * 16;
 }

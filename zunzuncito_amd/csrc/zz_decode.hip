@@ -181,12 +181,11 @@ struct ZzChunk {
 // per row: the extra bytes read stay inside the slot (the q plane is followed by
 // the scale plane, which is preceded by the q plane) and are not used.
 template <int FMT>
-__device__ __forceinline__ ZzChunk zz_load_chunk(const uint8_t *E, const ZzTensor &T, int g, int c, int l) {
+__device__ __forceinline__ ZzChunk zz_load_chunk(const uint8_t *E, const ZzWalk &W, int c) {
     ZzChunk k;
-    const int b0 = 4 * c, r = l & 15;
-    const bool full = zz_cbs(T, b0) == 4;
-    const uint8_t *q = E + zz_qlane(T, g, b0, l);
-    const uint8_t *sp = E + zz_sidx(T, g, b0, r);
+    const bool full = c < W.nfull;
+    const uint8_t *q = zz_walk_q(E, W, c);
+    const uint8_t *sp = zz_walk_s(E, W, c);
     k.a = ld16(q);
     k.b = FMT == ZZ_FMT_Q80 ? ld16(q + (full ? 16 : 0)) : make_uint4(0, 0, 0, 0);
     k.s = *(const uint2 *)(sp - (full ? 0 : 4));   // short: the 2 scales in .y
@@ -290,10 +289,11 @@ __device__ __forceinline__ float zz_dec_up_part(const ZzFfnArgs &a, const ZzDecS
         return acc;
     }
     const int nch = (nb + 3) / 4;                               // lane's chunks h + 2i
+    const ZzWalk W = zz_walk(T, g, l, r);
     ZzChunk k[DU_C];
     auto load = [&](int i0) {
 #pragma unroll
-        for (int i = 0; i < DU_C; i++) k[i] = zz_load_chunk<FMT>(E, T, g, min(h + 2 * (i0 + i), nch - 1), l);
+        for (int i = 0; i < DU_C; i++) k[i] = zz_load_chunk<FMT>(E, W, min(h + 2 * (i0 + i), nch - 1));
     };
     load(0);
     zz_dec_stage_commit(a, sr, st);
@@ -420,6 +420,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     }
     ZzChunk k[DD_C];
     uint4 c[DD_C];
+    const ZzWalk W = zz_walk(T, g, l, r);
     auto load_units = [&](int u0) {
 #pragma unroll
         for (int i = 0; i < DD_C; i++) {                        // clamped: loads stay in range
@@ -427,7 +428,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
             const int fp = w + DD_W * (u / nch), ch = u % nch;
             const uint8_t *E = f.experts + (size_t)pr.e[min(fp, P - 1)] * f.estride;
             if (FMT == ZZ_FMT_TQ2) c[i] = ld16(E + zz_tq2off(T, 16 * g + r, min(qq + 4 * ch, nb / 2 - 1)));
-            else k[i] = zz_load_chunk<FMT>(E, T, g, ch, l);
+            else k[i] = zz_load_chunk<FMT>(E, W, ch);
         }
     };
     float acc = 0.0f;

@@ -46,8 +46,9 @@ struct MmA {
 };
 
 template <int FMT>
-__device__ __forceinline__ MmA mm_load_a(const uint8_t *E, const ZzTensor &T, int g, int c, int l) {
-    const int b0 = 4 * c, r = l & 15, qq = l >> 4;
+__device__ __forceinline__ MmA mm_load_a(const uint8_t *E, const ZzTensor &T, const ZzWalk &W, int g, int c,
+                                         int l) {
+    const int r = l & 15, qq = l >> 4;
     const uint4 z = make_uint4(0, 0, 0, 0);
     MmA A = {z, z, z, z};
     if (FMT == ZZ_FMT_TQ2) {
@@ -62,9 +63,9 @@ __device__ __forceinline__ MmA mm_load_a(const uint8_t *E, const ZzTensor &T, in
     // last chunk (2 blocks) has 8 (q4_0) or 16 (q8_0) bytes per lane and 4 scale
     // words per lane group; the extra bytes read stay inside the slot (the q plane
     // is followed by the scale plane) and belong to blocks the loop skips.
-    const bool full = zz_cbs(T, b0) == 4;
-    const uint8_t *q = E + zz_qlane(T, g, b0, l);
-    const uint8_t *s = E + zz_sidx(T, g, b0, 4 * qq);        // 16-byte aligned
+    const bool full = c < W.nfull;
+    const uint8_t *q = zz_walk_q(E, W, c);
+    const uint8_t *s = zz_walk_s(E, W, c);                    // 16-byte aligned
     A.q = ld16(q);
     if (FMT == ZZ_FMT_Q80) A.q2 = ld16(q + (full ? 16 : 0));
     A.s0 = ld16(s);
@@ -198,9 +199,10 @@ __device__ __forceinline__ void mm_kloop(const uint8_t *E, const ZzTensor &T, in
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[t][i] = 0.0f;
     constexpr int KP = (NT + 1) / 2 < MM_XP ? (NT + 1) / 2 : MM_XP;
+    const ZzWalk W = zz_walk(T, g, l, 4 * (l >> 4));
     MmA r[RING];
 #pragma unroll
-    for (int i = 0; i < RING - 1; i++) r[i] = mm_load_a<FMT>(E, T, g, min(i, nch - 1), l);
+    for (int i = 0; i < RING - 1; i++) r[i] = mm_load_a<FMT>(E, T, W, g, min(i, nch - 1), l);
     MmX xr;
     mm_load_x<KP>(src, 0, min(4, nb), xr);
     mm_store_x<KP>(xr, st[0]);
@@ -223,7 +225,7 @@ __device__ __forceinline__ void mm_kloop(const uint8_t *E, const ZzTensor &T, in
 #pragma unroll
         for (int u = 0; u < RING; u++) {
             load_x(c0 + u);
-            r[(u + RING - 1) % RING] = mm_load_a<FMT>(E, T, g, min(c0 + u + RING - 1, nch - 1), l);
+            r[(u + RING - 1) % RING] = mm_load_a<FMT>(E, T, W, g, min(c0 + u + RING - 1, nch - 1), l);
             step(c0 + u, r[u], std::true_type());
         }
     }
@@ -232,7 +234,7 @@ __device__ __forceinline__ void mm_kloop(const uint8_t *E, const ZzTensor &T, in
         const int c = c0 + u;
         if (c < nch) {
             load_x(c);
-            if (u == RING - 1) r[u] = mm_load_a<FMT>(E, T, g, c, l);
+            if (u == RING - 1) r[u] = mm_load_a<FMT>(E, T, W, g, c, l);
             if (c < nfull) step(c, r[u], std::true_type());
             else step(c, r[u], std::false_type());
         }
