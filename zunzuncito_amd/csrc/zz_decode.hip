@@ -200,7 +200,7 @@ __device__ __forceinline__ uint2 zz_chunk_w(const ZzChunk &k, int j) {
         return (j & 1) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y);
     }
     const unsigned w = j == 0 ? k.a.x : (j == 1 ? k.a.y : (j == 2 ? k.a.z : k.a.w));
-    return zz_q4_unpack(w);
+    return zz_q4_unpack16(w);                       // 16 * (q - 8): sums scaled by 1/16
 }
 __device__ __forceinline__ float zz_chunk_dw(const ZzChunk &k, int j, bool full) {
     const unsigned v = j < 2 && full ? k.s.x : k.s.y;
@@ -302,7 +302,7 @@ __device__ __forceinline__ float zz_dec_up_part(const ZzFfnArgs &a, const ZzDecS
         load(i0);
         acc = zz_dec_up_comp<FMT>(k, st, nb, h, i0, qq, acc);
     }
-    return acc;
+    return FMT == ZZ_FMT_Q40 ? acc * 0.0625f : acc;            // the 16*(q - 8) weights
 }
 
 __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
@@ -443,7 +443,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
                 if (cur >= 0) {
                     acc += __shfl_xor(acc, 16, 64);
                     acc += __shfl_xor(acc, 32, 64);
-                    if (qq == 0) yv[cur][r] = acc;
+                    if (qq == 0) yv[cur][r] = FMT == ZZ_FMT_Q40 ? acc * 0.0625f : acc;
                 }
                 cur = fp;
                 acc = 0.0f;
@@ -503,7 +503,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     if (cur >= 0) {
         acc += __shfl_xor(acc, 16, 64);
         acc += __shfl_xor(acc, 32, 64);
-        if (qq == 0) yv[cur][r] = acc;
+        if (qq == 0) yv[cur][r] = FMT == ZZ_FMT_Q40 ? acc * 0.0625f : acc;   // 16*(q - 8) weights
     }
     __syncthreads();
     if (tid < S * 16) {

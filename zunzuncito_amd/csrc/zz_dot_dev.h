@@ -46,12 +46,12 @@ __device__ __forceinline__ int zz_dot_tq2(uint4 c, int h, uint4 xa, uint4 xb) {
 
 __device__ __forceinline__ uint4 ld16(const void *p) { return *(const uint4 *)p; }
 
-// bytewise q - 8 of four nibbles held one per byte (0..15 -> -8..7 as int8); the
-// add cannot carry between bytes
-__device__ __forceinline__ unsigned zz_nib_s8(unsigned x) { return (x + 0x78787878u) ^ 0x80808080u; }
-
-// one lane-order q4_0 word (weights k = 8qq..8qq+7 of one block) as 8 signed int8
-// weights q - 8: .x holds k 0..3, .y k 4..7 of the quarter
-__device__ __forceinline__ uint2 zz_q4_unpack(unsigned w) {
-    return make_uint2(zz_nib_s8(w & 0x0F0F0F0Fu), zz_nib_s8((w >> 4) & 0x0F0F0F0Fu));
+// One lane-order q4_0 word of the slot table (weights k = 8qq..8qq+7 of one block).
+// The slot table stores each nibble as q ^ 8, the 4-bit two's complement of q - 8,
+// so moving a nibble to the high half of its byte gives the int8 16*(q - 8) with one
+// shift and mask: .x holds k 0..3, .y k 4..7 of the quarter, both scaled by 16. Dots
+// of these are exactly 16 times the reference's integer dots; the kernels scale
+// their fp32 sums by 1/16 (exact) at the end.
+__device__ __forceinline__ uint2 zz_q4_unpack16(unsigned w) {
+    return make_uint2((w << 4) & 0xF0F0F0F0u, w & 0xF0F0F0F0u);
 }

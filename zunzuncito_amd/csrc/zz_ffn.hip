@@ -44,7 +44,7 @@ __global__ void zz_repack_kernel(ZzRepackArgs a) {
                     const int k0 = 8 * qq + m, k1 = k0 + 4;
                     const int n0 = k0 < 16 ? qs[k0] & 15 : qs[k0 - 16] >> 4;
                     const int n1 = k1 < 16 ? qs[k1] & 15 : qs[k1 - 16] >> 4;
-                    q[m] = (uint8_t)(n0 | (n1 << 4));
+                    q[m] = (uint8_t)((n0 ^ 8) | ((n1 ^ 8) << 4));   // q - 8 as 4-bit two's complement
                 }
             }
         }
@@ -124,10 +124,11 @@ __global__ void zz_blockdots_kernel(const uint8_t *E, ZzTensor T, int row0, int 
             const uint2 xv = *(const uint2 *)(x + 8 * qq);
             uint2 w;
             if (T.fmt == ZZ_FMT_Q80) w = *(const uint2 *)q;
-            else w = zz_q4_unpack(*(const unsigned *)q);
+            else w = zz_q4_unpack16(*(const unsigned *)q);
             d = zz_dot4(w.x, xv.x, d);
             d = zz_dot4(w.y, xv.y, d);
         }
+        if (T.fmt == ZZ_FMT_Q40) d >>= 4;          // the 16*(q - 8) weights: exact
     }
     out[i] = d;
 }

@@ -84,7 +84,7 @@ __device__ __forceinline__ long mm_frag(const MmA &A, int j, int l) {
     if (FMT == ZZ_FMT_Q40) {
         // byte m of the word = nibble(8qq + m) | nibble(8qq + m + 4) << 4
         const unsigned w = j == 0 ? A.q.x : (j == 1 ? A.q.y : (j == 2 ? A.q.z : A.q.w));
-        const uint2 u = zz_q4_unpack(w);
+        const uint2 u = zz_q4_unpack16(w);             // 16 * (q - 8)
         return (long)((unsigned long)u.x | ((unsigned long)u.y << 32));
     }
     // tq2: block j is half j&1 of group j/2; k 0..15 of a half are bit plane
@@ -282,6 +282,11 @@ __device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &ite
     float acc[NT][4];
     if (GF == UF || w < 2) mm_kloop<GF, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
     else mm_kloop<UF, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
+    if ((w < 2 ? GF : UF) == ZZ_FMT_Q40)         // the 16*(q - 8) weights
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[t][i] *= 0.0625f;
     if (GF == ZZ_FMT_TQ2) {                      // tq2.h:154, alpha of the row
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -376,6 +381,11 @@ __device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &i
 
     float acc[NT][4];
     mm_kloop<FMT, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
+    if (FMT == ZZ_FMT_Q40)                       // the 16*(q - 8) weights
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[t][i] *= 0.0625f;
     const int row0 = 16 * g + 4 * qq;
     float al[4] = {1.0f, 1.0f, 1.0f, 1.0f};
     if (FMT == ZZ_FMT_TQ2)
