@@ -100,10 +100,10 @@ __device__ __forceinline__ long mm_frag(const MmA &A, int j, int l) {
 // d_w of row 4qq+i, block j of the chunk, as fp16: halfword i*cbs + j of s0|s1
 // (i, j and the chunk size compile-time, so this is a register and a half select).
 template <bool FULL>
-__device__ __forceinline__ _Float16 mm_dwh(const MmA &A, int j, int i) {
+__device__ __forceinline__ _Float16 mm_dwh(const uint4 &s0, const uint4 &s1, int j, int i) {
     const int h = FULL ? 4 * i + j : 2 * i + j, w = h >> 1;
-    const unsigned u = w == 0 ? A.s0.x : w == 1 ? A.s0.y : w == 2 ? A.s0.z : w == 3 ? A.s0.w
-                     : w == 4 ? A.s1.x : w == 5 ? A.s1.y : w == 6 ? A.s1.z : A.s1.w;
+    const unsigned u = w == 0 ? s0.x : w == 1 ? s0.y : w == 2 ? s0.z : w == 3 ? s0.w
+                     : w == 4 ? s1.x : w == 5 ? s1.y : w == 6 ? s1.z : s1.w;
     return __builtin_bit_cast(_Float16, (unsigned short)((h & 1) ? u >> 16 : u & 0xffff));
 }
 
@@ -130,7 +130,7 @@ __device__ __forceinline__ void mm_chunk(const MmA &A, int l, float (&acc)[NT][4
             const zz_v4i r = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa, B[t], zero, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float s = FMT == ZZ_FMT_TQ2 ? sx[t] : fmaf((float)mm_dwh<FULL>(A, j, i), sx[t], 0.0f);
+                const float s = FMT == ZZ_FMT_TQ2 ? sx[t] : fmaf((float)mm_dwh<FULL>(A.s0, A.s1, j, i), sx[t], 0.0f);
                 acc[t][i] = fmaf(s, (float)r[i], acc[t][i]);
             }
         }
@@ -243,9 +243,148 @@ __device__ __forceinline__ void mm_kloop(const uint8_t *E, const ZzTensor &T, in
 
 #define MM_RING(NT) ((NT) <= 2 ? 4 : 3)
 
+// ------------------------------------------------------------------ tiny items
+// Items of <= 4 tokens (the long tail of experts under skewed routing) would fill a
+// 16-token tile with padding. They run on v_mfma_i32_4x4x4_16b_i8 instead: its 16
+// blocks are 16 row quads of the workgroup's 64 weight rows, its 4 columns the 4
+// tokens. Lane l owns weight row l (the row's four lane-order pieces of a chunk) and,
+// after the 8 steps of a 32-weight block, the block's int32 dots of rows 4(l/4)..+3
+// with token l%4 (layout checked on the device: A lane 4b+i = row i of block b,
+// B lane 4b+j = column j, D lane 4b+j, VGPR v = row v). The 4 waves split the K range
+// by chunks (c = w, w+4, ...) and their partial sums meet in LDS. Per 32-weight block
+// a lane spends 12 unpack and 12 epilogue operations for 64 rows x 4 tokens, where
+// the 16x16x32 path spends 4 x 15 for 64 rows x 16 padded tokens.
+#define MM4_K 4096                       // largest K whose 4 token rows are staged whole
+struct Mm4Stage {
+    __attribute__((aligned(16))) int8_t x[4][MM4_K];
+    float s[4][MM4_K / ZZ_BLK];
+};
+struct Mm4Red {
+    float part[4][64][4];                // [wave][lane][row of the quad]
+    float res[64][5];                    // [row][token]
+};
+
+// The item's (up to) 4 token rows and block scales, whole. row(t) / srow(t) for
+// t < 4 (callers clamp t to the item's last token).
+template <typename RF, typename SF>
+__device__ __forceinline__ void mm4_stage(Mm4Stage &st, RF row, SF srow, int K) {
+    const int tid = threadIdx.x, nseg = K / 16, nb = K / ZZ_BLK;
+    for (int i = tid; i < 4 * nseg; i += 256) {
+        const int t = i / nseg, sg = i - t * nseg;
+        *(uint4 *)&st.x[t][16 * sg] = ld16(row(t) + 16 * sg);
+    }
+    for (int i = tid; i < 4 * nb; i += 256) {
+        const int t = i / nb, b = i - t * nb;
+        st.s[t][b] = srow(t)[b];
+    }
+    __syncthreads();
+}
+
+// A lane's chunk: its row's four pieces (q4_0 16 bytes each, q8_0 32) and the fp16
+// scales of its row quad, rows 4((l>>2)&3)..+3 of its group.
+struct Mm4A {
+    uint4 q[4], q2[4], s0, s1;
+};
+
+template <int FMT>
+__device__ __forceinline__ Mm4A mm4_load(const uint8_t *E, const ZzWalk &W, int c) {
+    Mm4A A;
+    const bool full = c < W.nfull;
+    const uint8_t *q = zz_walk_q(E, W, c), *s = zz_walk_s(E, W, c);
+    // piece qq of row r is lane 16qq + r of the chunk: 16 lanes of 4 (full) or 2
+    // blocks' bytes further
+    const int ps = 16 * (full ? 4 : 2) * (FMT == ZZ_FMT_Q80 ? 8 : 4);
+#pragma unroll
+    for (int qq = 0; qq < 4; qq++) {
+        A.q[qq] = ld16(q + qq * ps);
+        A.q2[qq] = FMT == ZZ_FMT_Q80 ? ld16(q + qq * ps + (full ? 16 : 0)) : make_uint4(0, 0, 0, 0);
+    }
+    A.s0 = ld16(s);
+    A.s1 = ld16(s + (full ? 16 : 0));
+    return A;
+}
+
+// the int8 operand of step m (k = 4m..4m+3) of block j: piece m/2, low (m even) or
+// high half of its 8 weights
+template <int FMT>
+__device__ __forceinline__ int mm4_frag(const Mm4A &A, int j, int m) {
+    const int qq = m >> 1;
+    if (FMT == ZZ_FMT_Q80) {
+        const uint4 v = j < 2 ? A.q[qq] : A.q2[qq];
+        const unsigned w0 = (j & 1) ? v.z : v.x, w1 = (j & 1) ? v.w : v.y;
+        return (int)((m & 1) ? w1 : w0);
+    }
+    const uint4 v = A.q[qq];
+    const unsigned w = j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
+    const uint2 u = zz_q4_unpack16(w);                 // 16 * (q - 8)
+    return (int)((m & 1) ? u.y : u.x);
+}
+
+// acc[v]: row 4(l/4)+v of the 64, token l%4, over this wave's chunks c = w, w+4, ...
+template <int FMT, bool FULLC>
+__device__ __forceinline__ void mm4_chunk(const Mm4A &A, const Mm4Stage &st, int c, int l, float (&acc)[4]) {
+    const int t = l & 3;
+#pragma unroll
+    for (int j = 0; j < (FULLC ? 4 : 2); j++) {
+        const int b = 4 * c + j;
+        const uint4 xa = *(const uint4 *)&st.x[t][b * ZZ_BLK], xb = *(const uint4 *)&st.x[t][b * ZZ_BLK + 16];
+        const unsigned xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        zz_v4i d = {0, 0, 0, 0};
+#pragma unroll
+        for (int m = 0; m < 8; m++) d = __builtin_amdgcn_mfma_i32_4x4x4i8(mm4_frag<FMT>(A, j, m), (int)xw[m], d, 0, 0, 0);
+        const float sx = st.s[t][b];
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            acc[v] = fmaf(fmaf((float)mm_dwh<FULLC>(A.s0, A.s1, j, v), sx, 0.0f), (float)d[v], acc[v]);
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ void mm4_kloop(const uint8_t *E, const ZzTensor &T, int g, int l, int w,
+                                          const Mm4Stage &st, float (&acc)[4]) {
+    const int nb = T.I / ZZ_BLK, nch = (nb + 3) / 4;
+    const ZzWalk W = zz_walk(T, g, l & 15, 4 * ((l >> 2) & 3));   // piece 0 of row l%16
+#pragma unroll
+    for (int v = 0; v < 4; v++) acc[v] = 0.0f;
+    auto chunk = [&](const Mm4A &A, int c) {
+        if (c < W.nfull) mm4_chunk<FMT, true>(A, st, c, l, acc);
+        else if (c < nch) mm4_chunk<FMT, false>(A, st, c, l, acc);
+    };
+    // this wave's chunks w, w+4, ...: two register sets, each chunk's loads issued
+    // one chunk ahead (unconditional, clamped)
+    Mm4A a0 = mm4_load<FMT>(E, W, min(w, nch - 1)), a1;
+    for (int c = w; c < nch; c += 8) {
+        a1 = mm4_load<FMT>(E, W, min(c + 4, nch - 1));
+        chunk(a0, c);
+        a0 = mm4_load<FMT>(E, W, min(c + 8, nch - 1));
+        chunk(a1, c + 4);
+    }
+    if (FMT == ZZ_FMT_Q40)                       // the 16*(q - 8) weights
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[v] *= 0.0625f;
+}
+
+// the four waves' partial sums into res[row][token] (fixed order)
+__device__ __forceinline__ void mm4_reduce(Mm4Red &rd, const float (&acc)[4]) {
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+#pragma unroll
+    for (int v = 0; v < 4; v++) rd.part[w][l][v] = acc[v];
+    __syncthreads();
+    const int L = tid >> 2, v = tid & 3;
+    rd.res[4 * (L >> 2) + v][L & 3] = ((rd.part[0][L][v] + rd.part[1][L][v]) + rd.part[2][L][v]) + rd.part[3][L][v];
+    __syncthreads();
+}
+
+struct Mm4Shared {
+    Mm4Stage st;
+    Mm4Red rd;
+    float hb[4][ZZ_BLK];
+};
+
 // ------------------------------------------------------------------ up
 union MmUpShared {
     MmStage st[2];
+    Mm4Shared t4;
     struct {
         float u[32][MM_TN + 1];              // up values, [hidden row][token]
         float amax[2][MM_TN];
@@ -355,8 +494,9 @@ __device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &ite
 }
 
 // ------------------------------------------------------------------ down
-struct MmDownShared {
+union MmDownShared {
     MmStage st[2];
+    Mm4Shared t4;
 };
 
 template <int FMT, int NT>
@@ -399,6 +539,57 @@ __device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &i
     }
 }
 
+// Tiny items (<= 4 tokens): lanes 0..31 own gate rows 32rb.., lanes 32..63 the up rows
+// (gate and up in one format); then h = act(g, u) and its q8_0 quantisation per token.
+template <int FMT>
+__device__ __forceinline__ void mm4_up_body(const ZzFfnArgs &a, const ZzItem &item, int rb, Mm4Shared &sm) {
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = item.n, D = a.D, nb = D / ZZ_BLK;
+    const uint8_t *E = a.experts + (size_t)item.e * a.estride;
+    const int *ptok = a.ptok + item.p0;
+    mm4_stage(sm.st, [&](int t) { return a.xq + (size_t)ptok[min(t, n - 1)] * D; },
+              [&](int t) { return a.xs + (size_t)ptok[min(t, n - 1)] * nb; }, D);
+    const ZzTensor &T = l < 32 ? a.lay.gate : a.lay.up;
+    float acc[4];
+    mm4_kloop<FMT>(E, T, 2 * rb + ((l >> 4) & 1), l, w, sm.st, acc);
+    __syncthreads();                             // the stage is done with
+    mm4_reduce(sm.rd, acc);
+    if (tid < 4 * ZZ_BLK) {                      // token t, hidden row 32rb + r
+        const int t = tid >> 5, r = tid & 31;
+        sm.hb[t][r] = zz_act(a.act, sm.rd.res[r][t], sm.rd.res[32 + r][t], a.clamp);
+    }
+    __syncthreads();
+    if (tid < 32) {                              // q8_0 of each token's block (q40.h:124-138)
+        const int t = tid >> 3, m = tid & 7;
+        float d;
+        int qs;
+        const unsigned pk = zz_quant8(*(const float4 *)&sm.hb[t][4 * m], &d, &qs);
+        if (t < n) {
+            const size_t p = (size_t)item.p0 + t;
+            const int nbM = a.MI / ZZ_BLK;
+            *(unsigned *)(a.hq + p * a.MI + rb * ZZ_BLK + 4 * m) = pk;
+            if (m == 0) {
+                a.hs[p * nbM + rb] = d;
+                a.hsum[p * nbM + rb] = qs;
+            }
+        }
+    }
+}
+
+// Tiny items (<= 4 tokens), down: rows 64rt + l, the unweighted y of each token.
+template <int FMT>
+__device__ __forceinline__ void mm4_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, Mm4Shared &sm) {
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = item.n, MI = a.MI, nb = MI / ZZ_BLK;
+    const uint8_t *E = a.experts + (size_t)item.e * a.estride;
+    mm4_stage(sm.st, [&](int t) { return a.hq + ((size_t)item.p0 + min(t, n - 1)) * MI; },
+              [&](int t) { return a.hs + ((size_t)item.p0 + min(t, n - 1)) * nb; }, MI);
+    float acc[4];
+    mm4_kloop<FMT>(E, a.lay.down, 4 * rt + (l >> 4), l, w, sm.st, acc);
+    __syncthreads();
+    mm4_reduce(sm.rd, acc);
+    const int t = tid >> 6, r = tid & 63;
+    if (t < n) a.y[((size_t)item.p0 + t) * a.D + 64 * rt + r] = sm.rd.res[r][t];
+}
+
 // XCD-aware work order. Workgroup g of a launch runs on XCD g % 8 (round-robin
 // dispatch), and each XCD has its own L2. All tiles of one item read the same
 // activations, so they get workgroup ids of one residue mod 8: item i runs on XCD
@@ -423,7 +614,8 @@ __global__ __launch_bounds__(256) void zz_up_mma_kernel(ZzFfnArgs a) {
     __shared__ MmUpShared sm;
     __shared__ int tok[MM_TN];
     const int nt = (item.n + 15) / 16;
-    if (nt <= 1) mm_up_body<GF, UF, 1>(a, item, rb, sm, tok);
+    if (GF == UF && GF != ZZ_FMT_TQ2 && item.n <= 4 && a.D <= MM4_K) mm4_up_body<GF>(a, item, rb, sm.t4);
+    else if (nt <= 1) mm_up_body<GF, UF, 1>(a, item, rb, sm, tok);
     else if (nt <= 2) mm_up_body<GF, UF, 2>(a, item, rb, sm, tok);
     else mm_up_body<GF, UF, 4>(a, item, rb, sm, tok);
 }
@@ -436,7 +628,8 @@ __global__ __launch_bounds__(256) void zz_down_mma_kernel(ZzFfnArgs a) {
     const ZzItem item = a.items[it];
     __shared__ MmDownShared sm;
     const int nt = (item.n + 15) / 16;
-    if (nt <= 1) mm_down_body<FMT, 1>(a, item, rt, sm);
+    if (FMT != ZZ_FMT_TQ2 && item.n <= 4 && a.MI <= MM4_K) mm4_down_body<FMT>(a, item, rt, sm.t4);
+    else if (nt <= 1) mm_down_body<FMT, 1>(a, item, rt, sm);
     else if (nt <= 2) mm_down_body<FMT, 2>(a, item, rt, sm);
     else mm_down_body<FMT, 4>(a, item, rt, sm);
 }
