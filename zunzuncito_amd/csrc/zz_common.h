@@ -92,28 +92,41 @@ __host__ __device__ __forceinline__ int64_t zz_sidx(const ZzTensor &T, int g, in
 // A lane's walk over the chunks of one 16-row group of a q4_0 / q8_0 tensor, with
 // the offsets of zz_qlane / zz_sidx strength-reduced: a full chunk is chunk 0 plus c
 // strides, the short last chunk (if any) has its own offset. rr is the row of the
-// scale pointer within the group. Offsets are from the expert's base.
+// scale pointer within the group. Offsets are from the expert's base and fit 32
+// bits (an expert of the largest accepted shape, D = MI = 8192 in q8_0, is 214 MB),
+// so a load is the uniform base plus one 32-bit lane offset.
 struct ZzWalk {
-    int64_t qb, qs, sb, ss;
-    int nfull, qstep;
+    uint32_t qb, qs, sb, ss, qstep;
+    int nfull;
 };
 __device__ __forceinline__ ZzWalk zz_walk(const ZzTensor &T, int g, int lane, int rr) {
     ZzWalk w;
     const int nb = T.I / ZZ_BLK, lb = zz_lb(T);
     w.nfull = nb / 4;
     w.qstep = 256 * lb;
-    w.qb = zz_qlane(T, g, 0, lane);
-    w.sb = zz_sidx(T, g, 0, rr);
+    w.qb = (uint32_t)zz_qlane(T, g, 0, lane);
+    w.sb = (uint32_t)zz_sidx(T, g, 0, rr);
     const int bl = 4 * (w.nfull < (nb + 3) / 4 ? w.nfull : 0);     // the short chunk's first block
-    w.qs = zz_qlane(T, g, bl, lane);
-    w.ss = zz_sidx(T, g, bl, rr);
+    w.qs = (uint32_t)zz_qlane(T, g, bl, lane);
+    w.ss = (uint32_t)zz_sidx(T, g, bl, rr);
     return w;
 }
+__device__ __forceinline__ uint32_t zz_walk_qo(const ZzWalk &w, int c) {
+    return c < w.nfull ? w.qb + (uint32_t)c * w.qstep : w.qs;
+}
+__device__ __forceinline__ uint32_t zz_walk_so(const ZzWalk &w, int c) {
+    return c < w.nfull ? w.sb + (uint32_t)c * 128u : w.ss;
+}
 __device__ __forceinline__ const uint8_t *zz_walk_q(const uint8_t *E, const ZzWalk &w, int c) {
-    return E + (c < w.nfull ? w.qb + (int64_t)c * w.qstep : w.qs);
+    return E + zz_walk_qo(w, c);
 }
 __device__ __forceinline__ const uint8_t *zz_walk_s(const uint8_t *E, const ZzWalk &w, int c) {
-    return E + (c < w.nfull ? w.sb + (int64_t)c * 128 : w.ss);
+    return E + zz_walk_so(w, c);
+}
+// The wave's index in its workgroup, as a uniform value: what is derived from it
+// (the tensor a wave walks, its chunk counts) then stays in scalar registers.
+__device__ __forceinline__ int zz_wave_id() {
+    return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
 
 __host__ __device__ __forceinline__ int64_t zz_tq2off(const ZzTensor &T, int row, int gp) {

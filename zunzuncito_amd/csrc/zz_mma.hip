@@ -64,12 +64,11 @@ __device__ __forceinline__ MmA mm_load_a(const uint8_t *E, const ZzTensor &T, co
     // words per lane group; the extra bytes read stay inside the slot (the q plane
     // is followed by the scale plane) and belong to blocks the loop skips.
     const bool full = c < W.nfull;
-    const uint8_t *q = zz_walk_q(E, W, c);
-    const uint8_t *s = zz_walk_s(E, W, c);                    // 16-byte aligned
-    A.q = ld16(q);
-    if (FMT == ZZ_FMT_Q80) A.q2 = ld16(q + (full ? 16 : 0));
-    A.s0 = ld16(s);
-    A.s1 = ld16(s + (full ? 16 : 0));
+    const uint32_t qo = zz_walk_qo(W, c), so = zz_walk_so(W, c);    // so: 16-byte aligned
+    A.q = ld16(E + qo);
+    if (FMT == ZZ_FMT_Q80) A.q2 = ld16(E + (qo + (full ? 16u : 0u)));
+    A.s0 = ld16(E + so);
+    A.s1 = ld16(E + (so + (full ? 16u : 0u)));
     return A;
 }
 
@@ -147,9 +146,12 @@ struct MmX {
     float s[MM_SP];
 };
 
+// Rows are 32-bit byte offsets from uniform bases (the activation planes are far
+// below 4 GB), so each load is a scalar base plus one lane offset.
 struct MmSrc {
-    const int8_t *row[MM_XP];        // activation row of each piece's token
-    const float *srow[MM_SP];        // d_x row of each scale slot's token
+    const uint8_t *xb, *sb;          // the int8 activations and their f32 block scales
+    uint32_t row[MM_XP];             // byte offset of each piece's token row
+    uint32_t srow[MM_SP];            // byte offset of each scale slot's d_x row
     int seg[MM_XP], kb[MM_SP];
 };
 
@@ -160,9 +162,11 @@ struct MmSrc {
 template <int KP>
 __device__ __forceinline__ void mm_load_x(const MmSrc &src, int c, int cbs, MmX &x) {
 #pragma unroll
-    for (int k = 0; k < KP; k++) x.v[k] = ld16(src.row[k] + c * 4 * ZZ_BLK + 16 * min(src.seg[k], 2 * cbs - 1));
+    for (int k = 0; k < KP; k++)
+        x.v[k] = ld16(src.xb + (src.row[k] + (uint32_t)(c * 4 * ZZ_BLK + 16 * min(src.seg[k], 2 * cbs - 1))));
 #pragma unroll
-    for (int k = 0; k < MM_SP; k++) x.s[k] = src.srow[k][4 * c + min(src.kb[k], cbs - 1)];
+    for (int k = 0; k < MM_SP; k++)
+        x.s[k] = *(const float *)(src.sb + (src.srow[k] + (uint32_t)(4 * (4 * c + min(src.kb[k], cbs - 1)))));
 }
 
 template <int KP>
@@ -366,7 +370,7 @@ __device__ __forceinline__ void mm4_kloop(const uint8_t *E, const ZzTensor &T, i
 
 // the four waves' partial sums into res[row][token] (fixed order)
 __device__ __forceinline__ void mm4_reduce(Mm4Red &rd, const float (&acc)[4]) {
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63;
 #pragma unroll
     for (int v = 0; v < 4; v++) rd.part[w][l][v] = acc[v];
     __syncthreads();
@@ -396,23 +400,25 @@ union MmUpShared {
 template <int GF, int UF, int NT>
 __device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &item, int rb, MmUpShared &sm,
                                            int *tok) {
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, qq = l >> 4;
+    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, qq = l >> 4;
     const ZzTensor &T = w < 2 ? a.lay.gate : a.lay.up;
     const int g = 2 * rb + (w & 1), n = item.n, D = a.D, nb = D / ZZ_BLK;
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
     if (tid < MM_TN) tok[tid] = a.ptok[item.p0 + min(tid, n - 1)];
     __syncthreads();
     MmSrc src;
+    src.xb = (const uint8_t *)a.xq;
+    src.sb = (const uint8_t *)a.xs;
 #pragma unroll
     for (int k = 0; k < MM_XP; k++) {
         const int i = tid + 256 * k, t = i >> 3;
-        src.row[k] = a.xq + (size_t)tok[t] * D;          // tok[t >= n]: token n - 1
+        src.row[k] = (uint32_t)tok[t] * (uint32_t)D;     // tok[t >= n]: token n - 1
         src.seg[k] = i & 7;
     }
 #pragma unroll
     for (int k = 0; k < MM_SP; k++) {
         const int i = tid + 256 * k, t = i % MM_TN;
-        src.srow[k] = a.xs + (size_t)tok[t] * nb;
+        src.srow[k] = (uint32_t)tok[t] * (uint32_t)(4 * nb);
         src.kb[k] = i / MM_TN;
     }
 
@@ -501,21 +507,23 @@ union MmDownShared {
 
 template <int FMT, int NT>
 __device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, MmDownShared &sm) {
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, qq = l >> 4;
+    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, qq = l >> 4;
     const ZzTensor &T = a.lay.down;
     const int g = 4 * rt + w, n = item.n, MI = a.MI, nb = MI / ZZ_BLK;
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
     MmSrc src;
+    src.xb = (const uint8_t *)a.hq;
+    src.sb = (const uint8_t *)a.hs;
 #pragma unroll
     for (int k = 0; k < MM_XP; k++) {
         const int i = tid + 256 * k, t = i >> 3;
-        src.row[k] = a.hq + ((size_t)item.p0 + min(t, n - 1)) * MI;
+        src.row[k] = (uint32_t)(item.p0 + min(t, n - 1)) * (uint32_t)MI;
         src.seg[k] = i & 7;
     }
 #pragma unroll
     for (int k = 0; k < MM_SP; k++) {
         const int i = tid + 256 * k, t = i % MM_TN;
-        src.srow[k] = a.hs + ((size_t)item.p0 + min(t, n - 1)) * nb;
+        src.srow[k] = (uint32_t)(item.p0 + min(t, n - 1)) * (uint32_t)(4 * nb);
         src.kb[k] = i / MM_TN;
     }
 
@@ -543,7 +551,7 @@ __device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &i
 // (gate and up in one format); then h = act(g, u) and its q8_0 quantisation per token.
 template <int FMT>
 __device__ __forceinline__ void mm4_up_body(const ZzFfnArgs &a, const ZzItem &item, int rb, Mm4Shared &sm) {
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = item.n, D = a.D, nb = D / ZZ_BLK;
+    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, n = item.n, D = a.D, nb = D / ZZ_BLK;
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
     const int *ptok = a.ptok + item.p0;
     mm4_stage(sm.st, [&](int t) { return a.xq + (size_t)ptok[min(t, n - 1)] * D; },
@@ -578,7 +586,7 @@ __device__ __forceinline__ void mm4_up_body(const ZzFfnArgs &a, const ZzItem &it
 // Tiny items (<= 4 tokens), down: rows 64rt + l, the unweighted y of each token.
 template <int FMT>
 __device__ __forceinline__ void mm4_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, Mm4Shared &sm) {
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = item.n, MI = a.MI, nb = MI / ZZ_BLK;
+    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, n = item.n, MI = a.MI, nb = MI / ZZ_BLK;
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
     mm4_stage(sm.st, [&](int t) { return a.hq + ((size_t)item.p0 + min(t, n - 1)) * MI; },
               [&](int t) { return a.hs + ((size_t)item.p0 + min(t, n - 1)) * nb; }, MI);
