@@ -308,7 +308,7 @@ __device__ __forceinline__ float zz_dec_up_part(const ZzFfnArgs &a, const ZzDecS
 __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
     const ZzFfnArgs &f = a.f;
     const int K = a.tk.K, p = blockIdx.y, s = p / K, js = p - s * K;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, h = w >> 2, q = w & 3, j = blockIdx.x;
+    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, h = w >> 2, q = w & 3, j = blockIdx.x;
     extern __shared__ __attribute__((aligned(16))) char tk_lds[];
     __shared__ ZzDecStage st;
     __shared__ float part[2][4][16];                // [half][gate g0, g1, up g0, g1][row]
@@ -384,7 +384,7 @@ static inline size_t zz_dec_down_lds(int P, int MI) { return (size_t)P * MI + 8 
 template <int FMT>
 __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     const ZzFfnArgs &f = a.f;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r = l & 15, qq = l >> 4;
+    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, r = l & 15, qq = l >> 4;
     const int g = blockIdx.x;
     const ZzTensor &T = f.lay.down;
     const int MI = f.MI, nb = MI / ZZ_BLK, D = f.D, S = a.S, K = a.K, P = S * K;
