@@ -1,0 +1,63 @@
+/* zz_gemma.h -- the parts of gemma4.c's forward() around the MoE block, on the GPU
+ * (libzzmoe.so, MI355X gfx950): the feed-forward half of layer_fwd and the tied
+ * q4_0 embedding / lm_head with greedy selection. With attention as the identity,
+ * these and zz_moe.h make up the whole per-token path of gemma4.c:1184-1275.
+ *
+ * Conventions as zz_moe.h: 1 when done, 0 (or -1 for an id) to decline with the
+ * outputs untouched; single caller; _dev forms take device pointers and a
+ * hipStream_t (NULL = the library's stream) and are not waited for.
+ */
+#ifndef ZZ_GEMMA_H
+#define ZZ_GEMMA_H
+
+#include <stdint.h>
+#include <stddef.h>
+#include "zz_moe.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The feed-forward half of one gemma layer (gemma4.c:1003-1030):
+ *   res = H;  h2 = MoE(res)                        moe_start/moe_finish, 1010 + 1021
+ *   h1 = rmsnorm(dense_mlp(rmsnorm(res, pre_ffn_ln)), post_ffn_ln1)      1012-1020
+ *   H  = (res + rmsnorm(h1 + h2, post_ffn_ln)) * layer_scalar           1022-1030
+ * moe_layer is a ZZ_GATE_SOFTMAX_PES layer, dense_layer a ZZ_GATE_DENSE layer of
+ * the same D (its record: mlp_gate | mlp_up | mlp_down). The dense branch runs on
+ * a second stream while the MoE runs, as the reference overlaps them (1003-1009).
+ * Returns a block id >= 0, or -1. The layers stay owned by their creator and must
+ * outlive the block. */
+int zz_ffn_block_create(int moe_layer, int dense_layer, const float *post_ffn_ln,
+                        float layer_scalar);
+void zz_ffn_block_destroy(int block);
+
+/* H [S, D] in place. eidx/ewt [S*K] (may be NULL) receive the MoE routing. */
+int zz_ffn_block_forward_dev(int block, float *d_H, int S, int *d_eidx, float *d_ewt,
+                             void *stream);
+int zz_ffn_block_forward(int block, float *H, int S, int *eidx, float *ewt);
+
+/* The tied q4_0 embedding table [V, D] (reference layout, q40.h:9-18), which is
+ * also the lm_head (gemma4.c:353-354): embed_row scales by embed_scale
+ * (gemma4.c:1131-1145); logits are rmsnorm(H, final_norm) quantised q8_0 times the
+ * table, softcapped as tanh(v / cap) * cap when softcap > 0 (gemma4.c:1264-1275).
+ * V % 64 == 0. Returns a head id >= 0, or -1. */
+int zz_head_create(const uint8_t *table, int V, int D, const float *final_norm, float eps,
+                   float embed_scale, float softcap);
+void zz_head_destroy(int head);
+
+/* H[s] = embed_row(tok[s]) for S tokens (ids outside [0, V) read row 0). */
+int zz_head_embed_dev(int head, const int *d_tok, int S, float *d_H, void *stream);
+int zz_head_embed(int head, const int *tok, int S, float *H);
+
+/* logits [S, V] of S <= 4 rows of H, and (if argmax is not NULL) the greedy token of
+ * each row: the first index of the largest logit (sample at temp <= 0,
+ * gemma4.c:2149-2152). */
+int zz_head_logits_dev(int head, const float *d_H, int S, float *d_logits, int *d_argmax,
+                       void *stream);
+int zz_head_logits(int head, const float *H, int S, float *logits, int *argmax);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZZ_GEMMA_H */

@@ -29,6 +29,11 @@
 #define ZZ_GATE_SIGMOID_BIAS 1  /* lfm25.c:636-668: double logits, sigmoid, +bias for
                                    selection only, normalise, x routed_scaling      */
 #define ZZ_GATE_SOFTMAX_TOPK 2  /* maple.c:582-601: double logits, top-k, softmax    */
+#define ZZ_GATE_DENSE        3  /* gemma4.c:1012-1020: the dense MLP branch. No router:
+                                   E = K = 1 and every row goes through expert 0 with
+                                   weight 1 (its record holds mlp_gate|mlp_up|mlp_down);
+                                   pre_ln = pre_ffn_ln, post_ln = post_ffn_ln1, applied
+                                   as gemma's two ffn_ln2 norms are                    */
 
 /* activation between gate/up and down */
 #define ZZ_ACT_GEGLU_TANH   0   /* gemma4.c:432-434, 644 */

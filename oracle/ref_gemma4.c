@@ -138,6 +138,87 @@ int ref_g4_expert(int D, int MI, const uint8_t *blob, const float *X, const int 
     return 0;
 }
 
+/* The feed-forward half of layer_fwd (gemma4.c:1003-1030) with attention as the
+ * identity: the engine's own moe_start / moe_finish, rmsnorm, matvec and gelu_tanh,
+ * called in the order of those lines on its Buf (res = b->eout as there). The dense
+ * MLP record is mlp_gate [DI, D] | mlp_up [DI, D] | mlp_down [D, DI] in q4_0. */
+int ref_g4_ffn_block(int D, int MI, int E, int K, int DI, float eps, const float *router,
+                     const float *rscale, const float *pes, const float *pre_ln2,
+                     const float *post_ln2, const uint8_t *experts, int64_t esz,
+                     const uint8_t *mlp, const float *pre_ffn_ln, const float *post_ffn_ln1,
+                     const float *post_ffn_ln, float layer_scalar, float *H, int S,
+                     int *eidx, float *ewt) {
+    if (K > MAXTOPK || K > E || E > 128) return -1;
+    M *m = g4_model(D, MI, E, K, eps, router, rscale, pes, pre_ln2, post_ln2, experts, esz);
+    Buf b;
+    g4_buf(&b, D, MI, E, K, S);
+    const int IM = D > DI ? D : DI;
+    float *gate = zz_calloc(sizeof(float) * (size_t)DI), *up = zz_calloc(sizeof(float) * (size_t)DI);
+    float *act = zz_calloc(sizeof(float) * (size_t)DI), *tmp = zz_calloc(sizeof(float) * (size_t)D);
+    float *h2 = zz_calloc(sizeof(float) * (size_t)S * D);
+    int8_t *xq = zz_calloc((size_t)IM + 64);
+    float *sx = zz_calloc(sizeof(float) * (size_t)(IM / Q40_BLK + 8));
+    size_t gb = q40_tensor_bytes(DI, D);
+    W wg = {0, DI, D, mlp, NULL}, wu = {0, DI, D, mlp + gb, NULL}, wd = {0, D, DI, mlp + 2 * gb, NULL};
+    float *res = b.eout;
+    memcpy(res, H, sizeof(float) * (size_t)S * D);
+    moe_start(m, 0, res, h2, S, &b);
+    for (int s = 0; s < S; s++) {
+        rmsnorm(b.xn, res + (size_t)s * D, pre_ffn_ln, D, eps);
+        matvec(gate, &wg, b.xn, xq, sx);
+        matvec(up, &wu, b.xn, xq, sx);
+        for (int i = 0; i < DI; i++) act[i] = gelu_tanh(gate[i]) * up[i];
+        float *h1 = H + (size_t)s * D;
+        matvec(h1, &wd, act, xq, sx);
+        rmsnorm(h1, h1, post_ffn_ln1, D, eps);
+    }
+    moe_finish(m, 0, h2, S, &b);
+    for (int s = 0; s < S; s++) {
+        const float *r = res + (size_t)s * D;
+        float *h1 = H + (size_t)s * D, *hb = h2 + (size_t)s * D;
+        for (int i = 0; i < D; i++) tmp[i] = h1[i] + hb[i];
+        rmsnorm(tmp, tmp, post_ffn_ln, D, eps);
+        for (int i = 0; i < D; i++) h1[i] = (r[i] + tmp[i]) * layer_scalar;
+    }
+    if (eidx) memcpy(eidx, b.eidx, sizeof(int) * (size_t)S * K);
+    if (ewt) memcpy(ewt, b.ewt, sizeof(float) * (size_t)S * K);
+    free(gate); free(up); free(act); free(tmp); free(h2); free(xq); free(sx);
+    g4_free_buf(&b);
+    g4_free_model(m);
+    return 0;
+}
+
+/* embed_row (gemma4.c:1131-1145) from a q4_0 [V, D] table. */
+int ref_g4_embed(const uint8_t *table, int V, int D, float embed_scale, int tok, float *h) {
+    M *m = g4_model(D, 64, 1, 1, 1e-6f, NULL, NULL, NULL, NULL, NULL, NULL, 0);
+    m->c.embed_scale = embed_scale;
+    m->c.vocab = V;
+    m->L[MAXL - 1].q_proj.q = table;
+    m->L[MAXL - 1].q_proj.O = V;
+    m->L[MAXL - 1].q_proj.I = D;
+    embed_row(m, tok, h);
+    g4_free_model(m);
+    return 0;
+}
+
+/* The head of forward() for one row (gemma4.c:1264-1275: final rmsnorm, tied lm_head
+ * matvec, softcap) and the greedy token of sample() at temp 0 (gemma4.c:2149-2152). */
+int ref_g4_head(const uint8_t *table, int V, int D, const float *fnorm, float eps, float softcap,
+                const float *h, float *logits) {
+    float *xn = zz_calloc(sizeof(float) * (size_t)D);
+    int8_t *xq = zz_calloc((size_t)D + 64);
+    float *sx = zz_calloc(sizeof(float) * (size_t)(D / Q40_BLK + 8));
+    W we = {0, V, D, table, NULL};
+    rmsnorm(xn, h, fnorm, D, eps);
+    matvec(logits, &we, xn, xq, sx);
+    if (softcap > 0)
+        for (int i = 0; i < V; i++) logits[i] = tanhf(logits[i] / softcap) * softcap;
+    uint64_t rng = 1;
+    int tok = sample(logits, V, 0.0f, 1.0f, 0, NULL, &rng);
+    free(xn); free(xq); free(sx);
+    return tok;
+}
+
 void ref_g4_set_threads(int n) {
 #ifdef _OPENMP
     if (n > 0) omp_set_num_threads(n);

@@ -588,3 +588,88 @@ int orc_moe_layer(const orc_cfg *c, const orc_weights *w, const float *in, int S
     free(X); free(xq); free(xs); free(xt); free(offs); free(rows); free(rw); free(slot);
     return 0;
 }
+
+/* ------------------------------------------------- gemma around the MoE ---- */
+void orc_dense_mlp(const orc_dense *dn, int D, float eps, const float *r, int S, float *h1) {
+    const int DI = dn->DI;
+    const int64_t gb = orc_tensor_bytes(ORC_FMT_Q40, DI, D);
+    const uint8_t *G = dn->mlp, *U = dn->mlp + gb, *Dn = dn->mlp + 2 * gb;
+    #pragma omp parallel for schedule(static)
+    for (int s = 0; s < S; s++) {
+        float *xn = (float *)malloc(sizeof(float) * (size_t)D);
+        float *mlp = (float *)malloc(sizeof(float) * (size_t)DI);
+        int8_t *xq = (int8_t *)malloc((size_t)(D > DI ? D : DI));
+        float *sx = (float *)malloc(sizeof(float) * (size_t)((D > DI ? D : DI) / BLK));
+        /* gemma4.c:1014-1020: rmsnorm, matvec(gate), matvec(up), gelu*up, matvec(down),
+         * rmsnorm; every matvec quantises its input (gemma4.c:454-459) */
+        orc_rmsnorm(xn, r + (size_t)s * D, dn->pre_ffn_ln, D, eps);
+        orc_quant_act(xn, xq, sx, D);
+        for (int o = 0; o < DI; o++) {
+            float g = orc_q40_dot(G + (size_t)o * row_bytes(ORC_FMT_Q40, D), xq, sx, D);
+            float u = orc_q40_dot(U + (size_t)o * row_bytes(ORC_FMT_Q40, D), xq, sx, D);
+            mlp[o] = orc_act(ORC_ACT_GEGLU_TANH, g, u, 0.0f);
+        }
+        orc_quant_act(mlp, xq, sx, DI);
+        float *h = h1 + (size_t)s * D;
+        for (int o = 0; o < D; o++) h[o] = orc_q40_dot(Dn + (size_t)o * row_bytes(ORC_FMT_Q40, DI), xq, sx, DI);
+        orc_rmsnorm(h, h, dn->post_ffn_ln1, D, eps);
+        free(xn); free(mlp); free(xq); free(sx);
+    }
+}
+
+int orc_gemma_ffn_block(const orc_cfg *c, const orc_weights *w, const orc_dense *dn, float *H, int S,
+                        int *eidx, float *ewt) {
+    const int D = c->D;
+    if (c->gating != ORC_GATE_GEMMA || dn->DI % 64) return -1;
+    float *res = (float *)malloc(sizeof(float) * (size_t)S * D + 4);
+    float *h1 = (float *)malloc(sizeof(float) * (size_t)S * D + 4);
+    float *h2 = (float *)malloc(sizeof(float) * (size_t)S * D + 4);
+    int *uniq = (int *)malloc(sizeof(int) * (size_t)c->E);
+    int nu = 0, rc;
+    memcpy(res, H, sizeof(float) * (size_t)S * D);              /* gemma4.c:1008 */
+    rc = orc_moe_layer(c, w, res, S, h2, eidx, ewt, uniq, &nu, NULL);
+    if (rc == 0) {
+        orc_dense_mlp(dn, D, c->eps, res, S, h1);
+        /* gemma4.c:1022-1030 */
+        for (int s = 0; s < S; s++) {
+            float *t = h1 + (size_t)s * D, *hs = H + (size_t)s * D;
+            const float *a = h2 + (size_t)s * D, *r = res + (size_t)s * D;
+            for (int i = 0; i < D; i++) t[i] = t[i] + a[i];
+            orc_rmsnorm(t, t, dn->post_ffn_ln, D, c->eps);
+            for (int i = 0; i < D; i++) hs[i] = (r[i] + t[i]) * dn->layer_scalar;
+        }
+    }
+    free(res); free(h1); free(h2); free(uniq);
+    return rc;
+}
+
+void orc_embed_row(const uint8_t *table, int D, float embed_scale, int tok, float *h) {
+    const uint8_t *row = table + (size_t)tok * row_bytes(ORC_FMT_Q40, D);
+    for (int b = 0; b < D / BLK; b++) {
+        const uint8_t *bp = row + (size_t)b * 18;
+        float d = blk_scale(bp);
+        for (int j = 0; j < 16; j++) {
+            h[b * BLK + j] = d * (float)((bp[2 + j] & 15) - 8);
+            h[b * BLK + j + 16] = d * (float)((bp[2 + j] >> 4) - 8);
+        }
+    }
+    for (int i = 0; i < D; i++) h[i] *= embed_scale;
+}
+
+int orc_head(const uint8_t *table, int V, int D, const float *fnorm, float eps, float softcap,
+             const float *h, float *logits) {
+    float *xn = (float *)malloc(sizeof(float) * (size_t)D);
+    int8_t *xq = (int8_t *)malloc((size_t)D);
+    float *sx = (float *)malloc(sizeof(float) * (size_t)(D / BLK));
+    orc_rmsnorm(xn, h, fnorm, D, eps);
+    orc_quant_act(xn, xq, sx, D);
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < V; o++) {
+        float v = orc_q40_dot(table + (size_t)o * row_bytes(ORC_FMT_Q40, D), xq, sx, D);
+        logits[o] = softcap > 0 ? tanhf(v / softcap) * softcap : v;
+    }
+    int am = 0;
+    for (int i = 1; i < V; i++) if (logits[i] > logits[am]) am = i;
+    free(xn); free(xq); free(sx);
+    return am;
+}

@@ -131,6 +131,31 @@ int orc_moe_layer(const orc_cfg *c, const orc_weights *w, const float *in, int S
 void orc_dispatch(const int *eidx, const float *ewt, int S, int K, const int *uniq, int nu,
                   int *offs, int *rows, float *wts, int *slots);
 
+/* ---- gemma around the MoE block: the feed-forward half of layer_fwd
+ *      (gemma4.c:1003-1030) and the tied q4_0 embedding / lm_head ---- */
+typedef struct {
+    int DI;                         /* dense_inter                                  */
+    const uint8_t *mlp;             /* q4_0 mlp_gate [DI,D] | mlp_up [DI,D] | mlp_down [D,DI] */
+    const float *pre_ffn_ln;        /* [D] */
+    const float *post_ffn_ln1;      /* [D] */
+    const float *post_ffn_ln;       /* [D] */
+    float layer_scalar;
+} orc_dense;
+
+/* dense branch of S rows (gemma4.c:1012-1020): h1 = rmsnorm(mlp(rmsnorm(r, pre_ffn_ln)),
+ * post_ffn_ln1), q8_0 activations (matvec, gemma4.c:445-460) */
+void orc_dense_mlp(const orc_dense *dn, int D, float eps, const float *r, int S, float *h1);
+/* H [S, D] in place: H = (H + rmsnorm(dense(H) + moe(H), post_ffn_ln)) * layer_scalar.
+ * c must be gemma gating. Returns 0, or -1 on a bad config. */
+int orc_gemma_ffn_block(const orc_cfg *c, const orc_weights *w, const orc_dense *dn, float *H, int S,
+                        int *eidx, float *ewt);
+/* embed_row (gemma4.c:1131-1145) of a q4_0 [V, D] table */
+void orc_embed_row(const uint8_t *table, int D, float embed_scale, int tok, float *h);
+/* lm_head of one row (gemma4.c:1264-1275): logits[V] = softcap(table . q8_0(rmsnorm(h,
+ * fnorm))); returns the greedy token (gemma4.c:2149-2152) */
+int orc_head(const uint8_t *table, int V, int D, const float *fnorm, float eps, float softcap,
+             const float *h, float *logits);
+
 /* threads used by the parallel loops (OpenMP); 0 = runtime default */
 void orc_set_threads(int n);
 

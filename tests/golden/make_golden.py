@@ -103,8 +103,25 @@ def kernel_cases():
     print("kernels_lcg12345: q40", q40.nbytes, "B, dots", d40.size + d80.size + dtq.size)
 
 
+def gemma_cases():
+    """The feed-forward half of layer_fwd, embed_row, the tied head with greedy
+    selection, and a two-layer stack's prefill + greedy decode, from the compiled
+    reference (gemma4.c:1003-1030, 1131-1145, 1264-1275, 2149-2152)."""
+    L, dn, H, table, fnorm, st, H0 = Z.gemma_block_case()
+    D, MI, E, K, DI, V, seed = Z.GEMMA_SHAPE
+    Hb, eidx, ewt = Z.ref_block(L, dn, H)
+    emb = Z.ref_embed(table, V, D, np.float32(np.sqrt(np.float32(D))), Z.GEMMA_TOKS)
+    lg, am = Z.ref_head(table, V, D, fnorm, L.eps, 30.0, H[:3])
+    toks, Hp, lg_last = Z.ref_stack(st, H0, Z.GEMMA_STACK["steps"])
+    np.savez(os.path.join(HERE, "gemma_block_stack.npz"), digest=Z.gemma_digest(L, dn, H, table, fnorm, st, H0),
+             block_H=Hb, block_eidx=eidx, block_ewt=ewt, embed=emb, head_logits=lg, head_argmax=am,
+             stack_tokens=toks, stack_prefill=Hp, stack_logits=lg_last)
+    print("gemma_block_stack: tokens", toks.tolist(), "head argmax", am.tolist())
+
+
 if __name__ == "__main__":
     if Z.ref_lib("gemma4") is None:
         sys.exit("oracle/_ref is not built (needs /root/reference): run `make -C oracle`")
     kernel_cases()
     layer_cases()
+    gemma_cases()

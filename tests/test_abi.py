@@ -16,7 +16,9 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def declared_symbols():
     names = set()
-    for h in ("zz_gpu.h", "zz_moe.h"):
+    for h in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if not h.endswith(".h"):
+            continue
         text = open(os.path.join(ROOT, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b((?:gpu|zz)_\w+)\s*\(", text, flags=re.M):
@@ -38,7 +40,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_headers_compile_as_c():
-    src = '#include "zz_moe.h"\nint main(void){ return gpu_ready(); }\n'
+    src = '#include "zz_gemma.h"\nint main(void){ return gpu_ready(); }\n'
     r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-I",
                         os.path.join(ROOT, "include"), "-x", "c", "-"], input=src,
                        capture_output=True, text=True)
@@ -76,6 +78,19 @@ def test_decline_contract_without_device():
                             None, None) == 0
     assert np.all(out == 3.0)
     assert L.zz_moe_stats((C.c_uint * 4)()) == 0
+    ln = np.ones(64, np.float32)
+    assert L.zz_ffn_block_create(0, 1, ln.ctypes.data_as(zz._f32p), 1.0) == -1
+    assert L.zz_ffn_block_forward(0, out.ctypes.data_as(zz._f32p), 1, None, None) == 0
+    assert np.all(out == 3.0)
+    tab = np.zeros(64 * 2 * 18, np.uint8)
+    assert L.zz_head_create(tab.ctypes.data_as(zz._u8p), 64, 64, ln.ctypes.data_as(zz._f32p),
+                            1e-6, 8.0, 30.0) == -1
+    tok = np.zeros(1, np.int32)
+    assert L.zz_head_embed(0, tok.ctypes.data_as(zz._i32p), 1, out.ctypes.data_as(zz._f32p)) == 0
+    lg = np.full((1, 64), 5.0, np.float32)
+    assert L.zz_head_logits(0, x.ctypes.data_as(zz._f32p), 1, lg.ctypes.data_as(zz._f32p),
+                            tok.ctypes.data_as(zz._i32p)) == 0
+    assert np.all(out == 3.0) and np.all(lg == 5.0)
     L.gpu_shutdown()                             # safe when never initialised
 
 

@@ -330,3 +330,224 @@ def rel_l2(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+# ------------------------------------------- gemma around the MoE block
+class OrcDense(C.Structure):
+    _fields_ = [("DI", C.c_int), ("mlp", u8p), ("pre_ffn_ln", f32p), ("post_ffn_ln1", f32p),
+                ("post_ffn_ln", f32p), ("layer_scalar", C.c_float)]
+
+
+@dataclass
+class Dense:
+    """gemma's dense MLP branch and layer combine weights (gemma4.c:1003-1030)."""
+    D: int
+    DI: int
+    mlp: np.ndarray            # q4_0 mlp_gate [DI,D] | mlp_up [DI,D] | mlp_down [D,DI]
+    pre_ffn_ln: np.ndarray
+    post_ffn_ln1: np.ndarray
+    post_ffn_ln: np.ndarray
+    layer_scalar: float
+
+    def orc(self):
+        return OrcDense(self.DI, ptr(self.mlp), ptr(self.pre_ffn_ln), ptr(self.post_ffn_ln1),
+                        ptr(self.post_ffn_ln), self.layer_scalar)
+
+
+def make_dense(D, DI, seed):
+    rng = np.random.default_rng(20_000 + seed)
+    mlp = np.concatenate([make_expert_q(rng, FMT_Q40, DI, D), make_expert_q(rng, FMT_Q40, DI, D),
+                          make_expert_q(rng, FMT_Q40, D, DI)])
+    ln = lambda: (1 + 0.05 * rng.standard_normal(D)).astype(np.float32)   # noqa: E731
+    return Dense(D, DI, mlp, ln(), ln(), ln(), float(np.float32(0.5 + rng.random())))
+
+
+def make_table(V, D, seed):
+    """A seeded tied q4_0 embedding / lm_head [V, D] and its final norm."""
+    rng = np.random.default_rng(30_000 + seed)
+    table = make_expert_q(rng, FMT_Q40, V, D, sigma=0.05)
+    fnorm = (1 + 0.05 * rng.standard_normal(D)).astype(np.float32)
+    return table, fnorm
+
+
+def _bind_gemma(L):
+    L.orc_dense_mlp.argtypes = [C.POINTER(OrcDense), C.c_int, C.c_float, f32p, C.c_int, f32p]
+    L.orc_gemma_ffn_block.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.POINTER(OrcDense),
+                                      f32p, C.c_int, i32p, f32p]
+    L.orc_embed_row.argtypes = [u8p, C.c_int, C.c_float, C.c_int, f32p]
+    L.orc_head.argtypes = [u8p, C.c_int, C.c_int, f32p, C.c_float, C.c_float, f32p, f32p]
+    return L
+
+
+def oracle_dense(dn, eps, H):
+    L = _bind_gemma(oracle())
+    H = np.ascontiguousarray(H, np.float32)
+    out = np.zeros_like(H)
+    o = dn.orc()
+    L.orc_dense_mlp(C.byref(o), dn.D, C.c_float(eps), ptr(H), H.shape[0], ptr(out))
+    return out
+
+
+def oracle_block(L_, dn, H):
+    """(H', eidx, ewt) of orc_gemma_ffn_block."""
+    L = _bind_gemma(oracle())
+    H = np.array(H, np.float32, order="C", copy=True)
+    S = H.shape[0]
+    eidx = np.zeros(S * L_.K, np.int32)
+    ewt = np.zeros(S * L_.K, np.float32)
+    cfg, w, o = L_.cfg(), L_.weights(), dn.orc()
+    assert L.orc_gemma_ffn_block(C.byref(cfg), C.byref(w), C.byref(o), ptr(H), S, ptr(eidx), ptr(ewt)) == 0
+    return H, eidx, ewt
+
+
+def ref_block(L_, dn, H):
+    """The compiled reference's FFN half of layer_fwd, or None where unavailable."""
+    lib = ref_lib("gemma4")
+    if lib is None or L_.use_bias or L_.fmts != (FMT_Q40,) * 3:
+        return None
+    H = np.array(H, np.float32, order="C", copy=True)
+    S = H.shape[0]
+    eidx = np.zeros(S * L_.K, np.int32)
+    ewt = np.zeros(S * L_.K, np.float32)
+    rc = lib.ref_g4_ffn_block(L_.D, L_.MI, L_.E, L_.K, dn.DI, C.c_float(L_.eps), ptr(L_.router),
+                              ptr(L_.router_scale), ptr(L_.pes), ptr(L_.pre_ln), ptr(L_.post_ln),
+                              ptr(L_.experts), C.c_int64(L_.esz), ptr(dn.mlp), ptr(dn.pre_ffn_ln),
+                              ptr(dn.post_ffn_ln1), ptr(dn.post_ffn_ln), C.c_float(dn.layer_scalar),
+                              ptr(H), S, ptr(eidx), ptr(ewt))
+    assert rc == 0
+    return H, eidx, ewt
+
+
+def oracle_embed(table, D, scale, toks):
+    L = _bind_gemma(oracle())
+    out = np.zeros((len(toks), D), np.float32)
+    for i, t in enumerate(toks):
+        L.orc_embed_row(ptr(table), D, C.c_float(scale), int(t), ptr(out[i]))
+    return out
+
+
+def ref_embed(table, V, D, scale, toks):
+    lib = ref_lib("gemma4")
+    if lib is None:
+        return None
+    lib.ref_g4_embed.argtypes = [u8p, C.c_int, C.c_int, C.c_float, C.c_int, f32p]
+    out = np.zeros((len(toks), D), np.float32)
+    for i, t in enumerate(toks):
+        lib.ref_g4_embed(ptr(table), V, D, C.c_float(scale), int(t), ptr(out[i]))
+    return out
+
+
+def oracle_head(table, V, D, fnorm, eps, cap, H):
+    L = _bind_gemma(oracle())
+    H = np.ascontiguousarray(H, np.float32)
+    lg = np.zeros((H.shape[0], V), np.float32)
+    am = np.array([L.orc_head(ptr(table), V, D, ptr(fnorm), C.c_float(eps), C.c_float(cap),
+                              ptr(H[s]), ptr(lg[s])) for s in range(H.shape[0])], np.int32)
+    return lg, am
+
+
+def ref_head(table, V, D, fnorm, eps, cap, H):
+    lib = ref_lib("gemma4")
+    if lib is None:
+        return None
+    lib.ref_g4_head.argtypes = [u8p, C.c_int, C.c_int, f32p, C.c_float, C.c_float, f32p, f32p]
+    H = np.ascontiguousarray(H, np.float32)
+    lg = np.zeros((H.shape[0], V), np.float32)
+    am = np.array([lib.ref_g4_head(ptr(table), V, D, ptr(fnorm), C.c_float(eps), C.c_float(cap),
+                                   ptr(H[s]), ptr(lg[s])) for s in range(H.shape[0])], np.int32)
+    return lg, am
+
+
+@dataclass
+class Stack:
+    """A seeded gemma stack: per layer a MoE layer and a dense branch, plus the tied
+    head (BASELINE config 5 with attention as the identity)."""
+    layers: list
+    denses: list
+    table: np.ndarray
+    fnorm: np.ndarray
+    V: int
+    embed_scale: float
+    softcap: float = 30.0
+
+
+def make_stack(n_layers, D, MI, E, K, DI, V, seed, zipf=False):
+    layers = [make_layer("gemma", seed=100 * seed + l, E=E, D=D, MI=MI, K=K, zipf=zipf)
+              for l in range(n_layers)]
+    denses = [make_dense(D, DI, 100 * seed + l) for l in range(n_layers)]
+    table, fnorm = make_table(V, D, seed)
+    return Stack(layers, denses, table, fnorm, V, float(np.sqrt(np.float32(D))))
+
+
+def stack_run(st, H0, n_decode, block, head, embed):
+    """Prefill H0 through every layer, then n_decode greedy steps; the per-layer and
+    head functions are passed in (oracle or compiled reference). Returns the tokens,
+    the prefill output and the last decode step's logits."""
+    H = np.array(H0, np.float32, copy=True)
+    for L_, dn in zip(st.layers, st.denses):
+        H = block(L_, dn, H)[0]
+    Hp = H.copy()
+    lg, am = head(st.table, st.V, st.layers[0].D, st.fnorm, st.layers[0].eps, st.softcap, H[-1:])
+    toks = [int(am[0])]
+    for _ in range(n_decode):
+        H = embed(st.table, st.V, st.layers[0].D, st.embed_scale, toks[-1:])
+        for L_, dn in zip(st.layers, st.denses):
+            H = block(L_, dn, H)[0]
+        lg, am = head(st.table, st.V, st.layers[0].D, st.fnorm, st.layers[0].eps, st.softcap, H)
+        toks.append(int(am[0]))
+    return np.array(toks, np.int32), Hp, lg[0]
+
+
+def oracle_stack(st, H0, n_decode):
+    return stack_run(st, H0, n_decode, oracle_block, oracle_head,
+                     lambda t, V, D, s, tk: oracle_embed(t, D, s, tk))
+
+
+def ref_stack(st, H0, n_decode):
+    if ref_lib("gemma4") is None:
+        return None
+    return stack_run(st, H0, n_decode, ref_block, ref_head, ref_embed)
+
+
+# ---------------------------------------- the golden gemma fixture's case
+# (tests/golden/gemma_block_stack.npz, written by tests/golden/make_golden.py)
+def _input_digest(L, x):
+    import hashlib
+    h = hashlib.sha256()
+    for a in (L.router, L.router_scale, L.pes, L.bias, L.pre_ln, L.post_ln, L.experts, x):
+        if a is not None:
+            h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+# gemma around the MoE block: (D, MI, E, K, DI, V, seed), the block's S, the stack's
+# layers, prefill rows and greedy steps, and the embedding scale of the stack case
+GEMMA_SHAPE = (512, 256, 16, 4, 512, 1024, 3)
+GEMMA_BLOCK_S = 6
+GEMMA_STACK = dict(layers=2, S=6, steps=6, embed_scale=1.0)
+GEMMA_TOKS = [0, 1, 17, 511, 1023]
+
+
+def gemma_block_case():
+    """What the golden gemma fixture's inputs are, regenerated from seeds."""
+    D, MI, E, K, DI, V, seed = GEMMA_SHAPE
+    L = make_layer("gemma", seed=seed, E=E, D=D, MI=MI, K=K)
+    dn = make_dense(D, DI, seed)
+    H = make_input(L, GEMMA_BLOCK_S, seed)
+    table, fnorm = make_table(V, D, seed)
+    st = make_stack(GEMMA_STACK["layers"], D, MI, E, K, DI, V, seed)
+    st.embed_scale = GEMMA_STACK["embed_scale"]
+    H0 = make_input(L, GEMMA_STACK["S"], seed + 1)
+    return L, dn, H, table, fnorm, st, H0
+
+
+def gemma_digest(L, dn, H, table, fnorm, st, H0):
+    import hashlib
+    h = hashlib.sha256()
+    h.update(_input_digest(L, H).encode())
+    for a in (dn.mlp, dn.pre_ffn_ln, dn.post_ffn_ln1, dn.post_ffn_ln, table, fnorm, H0):
+        h.update(np.ascontiguousarray(a).tobytes())
+    for l_, d_ in zip(st.layers, st.denses):
+        h.update(_input_digest(l_, H0).encode())
+        h.update(np.ascontiguousarray(d_.mlp).tobytes())
+    return h.hexdigest()

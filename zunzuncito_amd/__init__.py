@@ -1,8 +1,9 @@
 """zunzuncito_amd -- MI355X-native MoE-layer hot path for the zunzuncito engines.
 
 The product is libzzmoe.so (HIP, gfx950), whose C ABI is include/zz_gpu.h (the
-engines' gpu.h, same symbols) and include/zz_moe.h (the whole MoE block with
-experts resident in HBM). This module is a thin ctypes binding of that ABI for
+engines' gpu.h, same symbols), include/zz_moe.h (the whole MoE block with
+experts resident in HBM) and include/zz_gemma.h (gemma's feed-forward block and
+tied embedding / lm_head around it). This module is a thin ctypes binding of that ABI for
 Python callers, tests and the benchmark. There is no CPU fallback here: when the
 library is missing or no gfx950 device is present, calls raise.
 """
@@ -15,7 +16,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libzzmoe.so")
 
 GPU_FMT_Q40, GPU_FMT_Q80, GPU_FMT_TQ2, GPU_FMT_Q4A = 1, 2, 3, 4
-ZZ_GATE_SOFTMAX_PES, ZZ_GATE_SIGMOID_BIAS, ZZ_GATE_SOFTMAX_TOPK = 0, 1, 2
+ZZ_GATE_SOFTMAX_PES, ZZ_GATE_SIGMOID_BIAS, ZZ_GATE_SOFTMAX_TOPK, ZZ_GATE_DENSE = 0, 1, 2, 3
 ZZ_ACT_GEGLU_TANH, ZZ_ACT_SWIGLU, ZZ_ACT_SWIGLU_CLAMP = 0, 1, 2
 
 # Every symbol include/zz_gpu.h and include/zz_moe.h declare.
@@ -27,6 +28,9 @@ ABI_SYMBOLS = (
     "zz_moe_blockdots", "zz_moe_stats", "zz_moe_profile", "zz_moe_profile_read",
     "zz_quantize",
     "zz_last_error",
+    "zz_ffn_block_create", "zz_ffn_block_destroy", "zz_ffn_block_forward_dev",
+    "zz_ffn_block_forward", "zz_head_create", "zz_head_destroy", "zz_head_embed_dev",
+    "zz_head_embed", "zz_head_logits_dev", "zz_head_logits",
 )
 KERNELS = ("prep", "logits", "topk", "dispatch", "ffn_up", "ffn_down", "combine", "dec_route",
            "dec_down")
@@ -97,6 +101,18 @@ def lib():
     L.zz_moe_profile_read.argtypes = [C.POINTER(C.c_double), C.POINTER(C.c_int), C.c_int]
     L.zz_quantize.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]
     L.zz_last_error.restype = C.c_char_p
+    L.zz_ffn_block_create.argtypes = [C.c_int, C.c_int, _f32p, C.c_float]
+    L.zz_ffn_block_destroy.argtypes = [C.c_int]
+    L.zz_ffn_block_forward_dev.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p,
+                                           C.c_void_p]
+    L.zz_ffn_block_forward.argtypes = [C.c_int, _f32p, C.c_int, _i32p, _f32p]
+    L.zz_head_create.argtypes = [_u8p, C.c_int, C.c_int, _f32p, C.c_float, C.c_float, C.c_float]
+    L.zz_head_destroy.argtypes = [C.c_int]
+    L.zz_head_embed_dev.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
+    L.zz_head_embed.argtypes = [C.c_int, _i32p, C.c_int, _f32p]
+    L.zz_head_logits_dev.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p,
+                                     C.c_void_p]
+    L.zz_head_logits.argtypes = [C.c_int, _f32p, C.c_int, _f32p, _i32p]
     _lib = L
     return L
 
@@ -244,3 +260,79 @@ def gpu_matmul(fmt, W_mapped, x, O, I):
     if not lib().gpu_matmul(fmt, _p(y, _f32p), _p(W_mapped, _u8p), _p(x, _f32p), O, I, S):
         raise RuntimeError(f"gpu_matmul declined: {last_error()}")
     return y
+
+
+class FfnBlock:
+    """gemma's feed-forward half of layer_fwd (zz_ffn_block_create): a MoE layer and a
+    ZZ_GATE_DENSE layer of the same D, combined with post_ffn_ln and layer_scalar."""
+
+    def __init__(self, moe, dense, post_ffn_ln, layer_scalar):
+        self._post = np.ascontiguousarray(post_ffn_ln, np.float32)
+        self.moe, self.dense, self.D, self.K = moe, dense, moe.D, moe.K
+        self.id = lib().zz_ffn_block_create(moe.id, dense.id, _p(self._post, _f32p),
+                                            float(layer_scalar))
+        if self.id < 0:
+            raise RuntimeError(f"zz_ffn_block_create declined: {last_error()}")
+
+    def forward(self, H):
+        """Host H [S, D] -> (new H, eidx, ewt); synchronous."""
+        H = np.array(H, np.float32, order="C", copy=True)
+        S = H.shape[0]
+        eidx = np.zeros(S * self.K, np.int32)
+        ewt = np.zeros(S * self.K, np.float32)
+        if not lib().zz_ffn_block_forward(self.id, _p(H, _f32p), S, _p(eidx, _i32p), _p(ewt, _f32p)):
+            raise RuntimeError(f"zz_ffn_block_forward declined: {last_error()}")
+        return H, eidx, ewt
+
+    def forward_dev(self, d_H, S, d_eidx=0, d_ewt=0, stream=0):
+        if not lib().zz_ffn_block_forward_dev(self.id, C.c_void_p(d_H), S, C.c_void_p(d_eidx or None),
+                                              C.c_void_p(d_ewt or None), C.c_void_p(stream or None)):
+            raise RuntimeError(f"zz_ffn_block_forward_dev declined: {last_error()}")
+
+    def close(self):
+        if self.id >= 0:
+            lib().zz_ffn_block_destroy(self.id)
+            self.id = -1
+
+
+class Head:
+    """Tied q4_0 embedding / lm_head (zz_head_create)."""
+
+    def __init__(self, table, V, D, final_norm, eps, embed_scale, softcap):
+        table = np.ascontiguousarray(table, np.uint8)
+        fn = np.ascontiguousarray(final_norm, np.float32)
+        self.V, self.D = V, D
+        self.id = lib().zz_head_create(_p(table, _u8p), V, D, _p(fn, _f32p), eps, embed_scale, softcap)
+        if self.id < 0:
+            raise RuntimeError(f"zz_head_create declined: {last_error()}")
+
+    def embed(self, tok):
+        tok = np.ascontiguousarray(tok, np.int32)
+        H = np.zeros((tok.size, self.D), np.float32)
+        if not lib().zz_head_embed(self.id, _p(tok, _i32p), tok.size, _p(H, _f32p)):
+            raise RuntimeError(f"zz_head_embed declined: {last_error()}")
+        return H
+
+    def logits(self, H):
+        H = np.ascontiguousarray(H, np.float32)
+        S = H.shape[0]
+        lg = np.zeros((S, self.V), np.float32)
+        am = np.zeros(S, np.int32)
+        if not lib().zz_head_logits(self.id, _p(H, _f32p), S, _p(lg, _f32p), _p(am, _i32p)):
+            raise RuntimeError(f"zz_head_logits declined: {last_error()}")
+        return lg, am
+
+    def embed_dev(self, d_tok, S, d_H, stream=0):
+        if not lib().zz_head_embed_dev(self.id, C.c_void_p(d_tok), S, C.c_void_p(d_H),
+                                       C.c_void_p(stream or None)):
+            raise RuntimeError(f"zz_head_embed_dev declined: {last_error()}")
+
+    def logits_dev(self, d_H, S, d_logits, d_argmax=0, stream=0):
+        if not lib().zz_head_logits_dev(self.id, C.c_void_p(d_H), S, C.c_void_p(d_logits),
+                                        C.c_void_p(d_argmax or None), C.c_void_p(stream or None)):
+            raise RuntimeError(f"zz_head_logits_dev declined: {last_error()}")
+
+    def close(self):
+        if self.id >= 0:
+            lib().zz_head_destroy(self.id)
+            self.id = -1

@@ -188,7 +188,7 @@ static std::vector<Layer *> g_layers;
 
 static int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
-static ZzTensor make_tensor(int fmt, int O, int I, int64_t *cursor) {
+ZzTensor zz_make_tensor(int fmt, int O, int I, int64_t *cursor) {
     ZzTensor t;
     t.fmt = fmt;
     t.O = O;
@@ -211,7 +211,8 @@ static int desc_ok(const zz_moe_desc *d) {
     if (!d) return 0;
     if (d->D <= 0 || d->MI <= 0 || d->D % 64 || d->MI % 64 || d->D > ZZ_MAXD || d->MI > ZZ_MAXD) return 0;
     if (d->E <= 0 || d->E > ZZ_MAXE || d->K < 1 || d->K > ZZ_MAXK || d->K > d->E) return 0;
-    if (d->gating < 0 || d->gating > 2 || d->act < 0 || d->act > 2) return 0;
+    if (d->gating < 0 || d->gating > 3 || d->act < 0 || d->act > 2) return 0;
+    if (d->gating == ZZ_GATE_DENSE && (d->E != 1 || d->K != 1 || d->use_bias)) return 0;
     int f[3] = {d->fmt_gate, d->fmt_up, d->fmt_down};
     for (int i = 0; i < 3; i++)
         if (f[i] != ZZ_FMT_Q40 && f[i] != ZZ_FMT_Q80 && f[i] != ZZ_FMT_TQ2) return 0;
@@ -245,29 +246,35 @@ static void free_layer(Layer *L) {
 
 extern "C" int zz_moe_layer_create(const zz_moe_desc *d, const zz_moe_weights *w) {
     if (!g_ready) { zz_set_error("zz_moe_layer_create: gpu_init first"); return -1; }
-    if (!desc_ok(d) || !w || !w->router) { zz_set_error("zz_moe_layer_create: bad descriptor"); return -1; }
+    const bool dense = desc_ok(d) && d->gating == ZZ_GATE_DENSE;
+    if (!desc_ok(d) || !w || (!dense && !w->router)) { zz_set_error("zz_moe_layer_create: bad descriptor"); return -1; }
     if (d->gating == ZZ_GATE_SOFTMAX_PES && (!w->router_scale || !w->pes || !w->pre_ln || !w->post_ln)) {
         zz_set_error("zz_moe_layer_create: gemma gating needs scale, pes and both norms");
         return -1;
     }
+    if (dense && (!w->pre_ln || !w->post_ln)) {
+        zz_set_error("zz_moe_layer_create: the dense branch needs both norms");
+        return -1;
+    }
+    const bool norms = d->gating == ZZ_GATE_SOFTMAX_PES || dense;
     if (d->use_bias && !w->bias) { zz_set_error("zz_moe_layer_create: use_bias without bias"); return -1; }
     Layer *L = new Layer();
     L->d = *d;
     int64_t cur = 0;
-    L->lay.gate = make_tensor(d->fmt_gate, d->MI, d->D, &cur);
-    L->lay.up = make_tensor(d->fmt_up, d->MI, d->D, &cur);
-    L->lay.down = make_tensor(d->fmt_down, d->D, d->MI, &cur);
+    L->lay.gate = zz_make_tensor(d->fmt_gate, d->MI, d->D, &cur);
+    L->lay.up = zz_make_tensor(d->fmt_up, d->MI, d->D, &cur);
+    L->lay.down = zz_make_tensor(d->fmt_down, d->D, d->MI, &cur);
     L->lay.bytes = cur;
     L->src_gate = 0;
     L->src_up = fmt_tensor_bytes(d->fmt_gate, d->MI, d->D);
     L->src_down = L->src_up + fmt_tensor_bytes(d->fmt_up, d->MI, d->D);
     L->rec_bytes = L->src_down + fmt_tensor_bytes(d->fmt_down, d->D, d->MI);
-    bool ok = upload_f32(&L->router, w->router, (size_t)d->E * d->D) &&
+    bool ok = upload_f32(&L->router, dense ? nullptr : w->router, (size_t)d->E * d->D) &&
               upload_f32(&L->rscale, d->gating == ZZ_GATE_SOFTMAX_PES ? w->router_scale : nullptr, d->D) &&
               upload_f32(&L->pes, d->gating == ZZ_GATE_SOFTMAX_PES ? w->pes : nullptr, d->E) &&
               upload_f32(&L->bias, d->use_bias ? w->bias : nullptr, d->E) &&
-              upload_f32(&L->pre_ln, d->gating == ZZ_GATE_SOFTMAX_PES ? w->pre_ln : nullptr, d->D) &&
-              upload_f32(&L->post_ln, d->gating == ZZ_GATE_SOFTMAX_PES ? w->post_ln : nullptr, d->D) &&
+              upload_f32(&L->pre_ln, norms ? w->pre_ln : nullptr, d->D) &&
+              upload_f32(&L->post_ln, norms ? w->post_ln : nullptr, d->D) &&
               hipMalloc(&L->slots, (size_t)d->E * L->lay.bytes) == hipSuccess &&
               hipMalloc(&L->staging, (size_t)L->rec_bytes) == hipSuccess;
     if (!ok) {
@@ -285,6 +292,15 @@ extern "C" int zz_moe_layer_create(const zz_moe_desc *d, const zz_moe_weights *w
 static Layer *get_layer(int id) {
     if (!g_ready || id < 0 || id >= (int)g_layers.size()) return nullptr;
     return g_layers[id];
+}
+
+// library internals shared with zz_gemma.hip
+hipStream_t zz_lib_stream() { return g_stream; }
+int zz_lib_ready() { return g_ready; }
+unsigned *zz_lib_diag() { return g_diag; }
+const zz_moe_desc *zz_layer_desc(int id) {
+    const Layer *L = get_layer(id);
+    return L ? &L->d : nullptr;
 }
 
 extern "C" void zz_moe_layer_destroy(int id) {
@@ -442,7 +458,8 @@ static bool takes_decode(const zz_moe_desc &d, int S) { return S <= g_dec_max_s 
 static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream_t st) {
     const zz_moe_desc &d = L->d;
     Workspace &w = L->ws;
-    const bool gemma = d.gating == ZZ_GATE_SOFTMAX_PES;
+    const bool dense = d.gating == ZZ_GATE_DENSE;   // gemma's norms, no router
+    const bool gemma = d.gating == ZZ_GATE_SOFTMAX_PES || dense;
     const bool tq_in = d.fmt_gate == ZZ_FMT_TQ2;
     const int P = S * d.K;
 
@@ -450,6 +467,7 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
     pa.D = d.D; pa.gemma = gemma; pa.eps = d.eps; pa.in = d_in;
     pa.router_scale = L->rscale; pa.pre_ln = L->pre_ln; pa.xn = w.xn;
     pa.xq = w.xq; pa.xs = w.xs; pa.xsum = w.xsum; pa.xt = tq_in ? w.xt : nullptr; pa.diag = g_diag;
+    pa.route_eidx = dense ? w.eidx : nullptr; pa.route_ewt = dense ? w.ewt : nullptr;
 
     ZzLogitArgs la;
     la.D = d.D; la.E = d.E; la.gating = d.gating; la.S = S; la.router = L->router; la.xn = w.xn; la.x = d_in;
@@ -472,12 +490,12 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
 
     if (dec) {
         ZzDecRouteArgs ra;
-        ra.prep = pa; ra.lg = la; ra.tk = ta; ra.dp = da; ra.S = S;
+        ra.prep = pa; ra.lg = la; ra.tk = ta; ra.dp = da; ra.S = S; ra.dense = dense;
         if (!(ProfScope(ZZ_K_DEC_ROUTE, st), zz_launch_dec_logits(ra, st))) ZZ_FAIL("decode router launch failed");
     } else {
         if (!(ProfScope(ZZ_K_PREP, st), zz_launch_prep(pa, S, st))) ZZ_FAIL("prep launch failed");
-        if (!(ProfScope(ZZ_K_LOGITS, st), zz_launch_logits(la, S, st))) ZZ_FAIL("logits launch failed");
-        if (!(ProfScope(ZZ_K_TOPK, st), zz_launch_topk(ta, S, st))) ZZ_FAIL("topk launch failed");
+        if (!dense && !(ProfScope(ZZ_K_LOGITS, st), zz_launch_logits(la, S, st))) ZZ_FAIL("logits launch failed");
+        if (!dense && !(ProfScope(ZZ_K_TOPK, st), zz_launch_topk(ta, S, st))) ZZ_FAIL("topk launch failed");
         if (!(ProfScope(ZZ_K_DISPATCH, st), zz_launch_dispatch(da, st))) ZZ_FAIL("dispatch launch failed");
     }
 
@@ -492,7 +510,7 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
         dd.f = fa; dd.S = S; dd.K = d.K; dd.E = d.E; dd.eidx = w.eidx; dd.ewt = w.ewt; dd.ppos = w.ppos;
         dd.out = d_out; dd.ss = gemma ? w.ss : nullptr;
         ZzDecUpArgs ua;
-        ua.f = fa; ua.tk = ta;
+        ua.f = fa; ua.tk = ta; ua.dense = dense;
         if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_dec_up(ua, S, st))) ZZ_FAIL("ffn_up launch failed");
         if (!(ProfScope(ZZ_K_DEC_DOWN, st), zz_launch_dec_down(dd, st))) ZZ_FAIL("decode down launch failed");
         if (gemma && !(ProfScope(ZZ_K_COMBINE, st), zz_launch_dec_norm(d_out, L->post_ln, w.ss, d.D, d.eps, S, st)))
@@ -688,9 +706,12 @@ extern "C" int zz_moe_stats(unsigned *c) {
 
 extern "C" const char *zz_last_error(void) { return g_err; }
 
+void zz_gemma_shutdown();   // zz_gemma.hip
+
 extern "C" void gpu_shutdown(void) {
     if (!g_ready) return;
     (void)hipStreamSynchronize(g_stream);
+    zz_gemma_shutdown();
     for (Layer *&L : g_layers) { free_layer(L); L = nullptr; }
     g_layers.clear();
     for (Mapping &m : g_maps) (void)hipFree(m.dev);

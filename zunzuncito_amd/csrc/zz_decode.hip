@@ -20,7 +20,8 @@
 // expert id kept inside the slot table whatever the router produced
 __device__ __forceinline__ int zz_clamp_e(int e, int E) { return e < 0 || e >= E ? 0 : e; }
 
-// Decode router, part 1: one workgroup per expert e. Gemma: per token, one set of
+// Decode router, part 1: one workgroup per expert e (the dense branch, which has
+// no router: 16 workgroups that only norm and quantise). Gemma: per token, one set of
 // loads (x row, router row e, router scale) gives both the rmsnorm factor and the
 // rounded products of the router logit. The mean square is certified to round to
 // the float of the reference's serial double sum (gemma4.c:425-428), else that sum
@@ -39,15 +40,18 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
     __shared__ float rr[DEC_MAXS];
     __shared__ float cert;
     const float rs = 1.0f / sqrtf((float)D);
+    if (a.dense && e == 0 && tid < S) {                      // one expert, weight 1
+        pp.route_eidx[tid] = 0;
+        pp.route_ewt[tid] = 1.0f;
+    }
     if (gem) {
         const int R = (D + 255) >> 8;                         // <= RB
-        const float *w = lg.router + (size_t)e * D;
         float wr[RB], sr[RB];
 #pragma unroll
         for (int j = 0; j < RB; j++) {                        // clamped: loads stay in range
             const int i = min(tid + 256 * j, D - 1);
-            wr[j] = w[i];
-            sr[j] = pp.router_scale[i];
+            wr[j] = a.dense ? 0.0f : lg.router[(size_t)e * D + i];
+            sr[j] = a.dense ? 0.0f : pp.router_scale[i];
         }
 #pragma unroll
         for (int j = 0; j < RB; j++) sr[j] = sr[j] * rs;
@@ -80,6 +84,7 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
             __syncthreads();
             const float r = 1.0f / sqrtf(cert + pp.eps);
             if (tid == 0) rr[s] = r;
+            if (a.dense) continue;                            // no router
 #pragma unroll
             for (int j = 0; j < RB; j++) {
                 const int i = tid + 256 * j;
@@ -167,44 +172,6 @@ __device__ __forceinline__ void zz_dec_stage_commit(const ZzFfnArgs &a, const Zz
     st.xs[min(tid, nb - 1)] = r.sv;
     st.xsum[min(tid, nb - 1)] = r.cv;
     __syncthreads();
-}
-
-// One lane-order chunk of a q4_0 / q8_0 row group: the lane's weight bytes (q4_0 in
-// .a, q8_0 in .a and .b) and its row's fp16 scales, for the chunk's 4 or 2 blocks.
-struct ZzChunk {
-    uint4 a, b;
-    uint2 s;
-};
-
-// Branch-free (only addresses are selected), so the load counters stay exact. A
-// short last chunk (2 blocks) has 8 (q4_0) or 16 (q8_0) bytes per lane and 2 scales
-// per row: the extra bytes read stay inside the slot (the q plane is followed by
-// the scale plane, which is preceded by the q plane) and are not used.
-template <int FMT>
-__device__ __forceinline__ ZzChunk zz_load_chunk(const uint8_t *E, const ZzWalk &W, int c) {
-    ZzChunk k;
-    const bool full = c < W.nfull;
-    const uint8_t *q = zz_walk_q(E, W, c);
-    const uint8_t *sp = zz_walk_s(E, W, c);
-    k.a = ld16(q);
-    k.b = FMT == ZZ_FMT_Q80 ? ld16(q + (full ? 16 : 0)) : make_uint4(0, 0, 0, 0);
-    k.s = *(const uint2 *)(sp - (full ? 0 : 4));   // short: the 2 scales in .y
-    return k;
-}
-
-// signed int8 weights k = 8qq..8qq+7 of block j of a chunk, and its scale
-template <int FMT>
-__device__ __forceinline__ uint2 zz_chunk_w(const ZzChunk &k, int j) {
-    if (FMT == ZZ_FMT_Q80) {
-        const uint4 v = j < 2 ? k.a : k.b;
-        return (j & 1) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y);
-    }
-    const unsigned w = j == 0 ? k.a.x : (j == 1 ? k.a.y : (j == 2 ? k.a.z : k.a.w));
-    return zz_q4_unpack16(w);                       // 16 * (q - 8): sums scaled by 1/16
-}
-__device__ __forceinline__ float zz_chunk_dw(const ZzChunk &k, int j, bool full) {
-    const unsigned v = j < 2 && full ? k.s.x : k.s.y;
-    return zz_h2f((uint16_t)((j & 1) ? v >> 16 : v & 0xffff));
 }
 
 // The dots of one batch of a wave's chunks (h + 2i). The activation operands of a
@@ -315,9 +282,9 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
     __shared__ float hb[ZZ_BLK];
     ZzDecStageRegs sr;
     zz_dec_stage_issue(f, s, sr);
-    if (w == 0) zz_topk_wave_any(a.tk, s, tk_lds, j == 0 && js == 0);
+    if (w == 0 && !a.dense) zz_topk_wave_any(a.tk, s, tk_lds, j == 0 && js == 0);
     __syncthreads();
-    const int e = zz_clamp_e(((const ZzTopkWaveHdr *)tk_lds)->idx[js], a.tk.E);
+    const int e = a.dense ? 0 : zz_clamp_e(((const ZzTopkWaveHdr *)tk_lds)->idx[js], a.tk.E);
     const ZzTensor &T = q >= 2 ? f.lay.up : f.lay.gate;
     const int g = 2 * j + (q & 1);
     const uint8_t *E = f.experts + (size_t)e * f.estride;
@@ -551,12 +518,13 @@ __global__ __launch_bounds__(256) void zz_dec_norm_kernel(float *out, const floa
 
 int zz_launch_dec_logits(const ZzDecRouteArgs &a, hipStream_t st) {
     const int R = (a.prep.D + 255) / 256;
-    if (R <= 4) hipLaunchKernelGGL(zz_dec_logits_kernel<4>, dim3(a.lg.E), dim3(256), 0, st, a);
-    else if (R <= 8) hipLaunchKernelGGL(zz_dec_logits_kernel<8>, dim3(a.lg.E), dim3(256), 0, st, a);
-    else if (R <= 12) hipLaunchKernelGGL(zz_dec_logits_kernel<12>, dim3(a.lg.E), dim3(256), 0, st, a);
-    else if (R <= 16) hipLaunchKernelGGL(zz_dec_logits_kernel<16>, dim3(a.lg.E), dim3(256), 0, st, a);
-    else if (R <= 24) hipLaunchKernelGGL(zz_dec_logits_kernel<24>, dim3(a.lg.E), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(zz_dec_logits_kernel<32>, dim3(a.lg.E), dim3(256), 0, st, a);
+    const dim3 g(a.dense ? 16 : a.lg.E);
+    if (R <= 4) hipLaunchKernelGGL(zz_dec_logits_kernel<4>, g, dim3(256), 0, st, a);
+    else if (R <= 8) hipLaunchKernelGGL(zz_dec_logits_kernel<8>, g, dim3(256), 0, st, a);
+    else if (R <= 12) hipLaunchKernelGGL(zz_dec_logits_kernel<12>, g, dim3(256), 0, st, a);
+    else if (R <= 16) hipLaunchKernelGGL(zz_dec_logits_kernel<16>, g, dim3(256), 0, st, a);
+    else if (R <= 24) hipLaunchKernelGGL(zz_dec_logits_kernel<24>, g, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(zz_dec_logits_kernel<32>, g, dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess;
 }
 

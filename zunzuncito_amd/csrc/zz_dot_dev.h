@@ -55,3 +55,41 @@ __device__ __forceinline__ uint4 ld16(const void *p) { return *(const uint4 *)p;
 __device__ __forceinline__ uint2 zz_q4_unpack16(unsigned w) {
     return make_uint2((w << 4) & 0xF0F0F0F0u, w & 0xF0F0F0F0u);
 }
+
+// One lane-order chunk of a q4_0 / q8_0 row group: the lane's weight bytes (q4_0 in
+// .a, q8_0 in .a and .b) and its row's fp16 scales, for the chunk's 4 or 2 blocks.
+struct ZzChunk {
+    uint4 a, b;
+    uint2 s;
+};
+
+// Branch-free (only addresses are selected), so the load counters stay exact. A
+// short last chunk (2 blocks) has 8 (q4_0) or 16 (q8_0) bytes per lane and 2 scales
+// per row: the extra bytes read stay inside the slot (the q plane is followed by
+// the scale plane, which is preceded by the q plane) and are not used.
+template <int FMT>
+__device__ __forceinline__ ZzChunk zz_load_chunk(const uint8_t *E, const ZzWalk &W, int c) {
+    ZzChunk k;
+    const bool full = c < W.nfull;
+    const uint8_t *q = zz_walk_q(E, W, c);
+    const uint8_t *sp = zz_walk_s(E, W, c);
+    k.a = ld16(q);
+    k.b = FMT == ZZ_FMT_Q80 ? ld16(q + (full ? 16 : 0)) : make_uint4(0, 0, 0, 0);
+    k.s = *(const uint2 *)(sp - (full ? 0 : 4));   // short: the 2 scales in .y
+    return k;
+}
+
+// signed int8 weights k = 8qq..8qq+7 of block j of a chunk, and its scale
+template <int FMT>
+__device__ __forceinline__ uint2 zz_chunk_w(const ZzChunk &k, int j) {
+    if (FMT == ZZ_FMT_Q80) {
+        const uint4 v = j < 2 ? k.a : k.b;
+        return (j & 1) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y);
+    }
+    const unsigned w = j == 0 ? k.a.x : (j == 1 ? k.a.y : (j == 2 ? k.a.z : k.a.w));
+    return zz_q4_unpack16(w);                       // 16 * (q - 8): sums scaled by 1/16
+}
+__device__ __forceinline__ float zz_chunk_dw(const ZzChunk &k, int j, bool full) {
+    const unsigned v = j < 2 && full ? k.s.x : k.s.y;
+    return zz_h2f((uint16_t)((j & 1) ? v >> 16 : v & 0xffff));
+}

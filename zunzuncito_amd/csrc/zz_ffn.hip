@@ -134,8 +134,10 @@ __global__ void zz_blockdots_kernel(const uint8_t *E, ZzTensor T, int row0, int 
 }
 
 // ------------------------------------------------------------------ launchers
-int zz_launch_repack(const ZzRepackArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(zz_repack_kernel, dim3(256, 3), dim3(256), 0, st, a);
+int zz_launch_repack(const ZzRepackArgs &a, hipStream_t st) { return zz_launch_repack_n(a, 3, st); }
+
+int zz_launch_repack_n(const ZzRepackArgs &a, int n, hipStream_t st) {
+    hipLaunchKernelGGL(zz_repack_kernel, dim3(256, n), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess;
 }
 

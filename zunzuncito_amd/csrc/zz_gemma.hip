@@ -1,0 +1,455 @@
+// zz_gemma.hip -- gemma4's forward() around the MoE block (include/zz_gemma.h):
+//   - the feed-forward half of layer_fwd (gemma4.c:1003-1030): the MoE layer and the
+//     dense MLP (a ZZ_GATE_DENSE layer) on two streams, then the layer combine;
+//   - the tied q4_0 embedding / lm_head (gemma4.c:1131-1145, 1264-1275) with the
+//     greedy token (gemma4.c:2149-2152).
+// The lm_head table is held in the slot-table lane order (zz_common.h), so its GEMV
+// streams one 16-byte load per lane and chunk like the expert kernels.
+#include "zz_common.h"
+#include "zz_kernels.h"
+#include "zz_dot_dev.h"
+#include "zz_route_dev.h"
+#include "../../include/zz_gemma.h"
+
+#include <math.h>
+#include <string.h>
+#include <vector>
+
+#define ZZ_FAIL(...)               \
+    do {                           \
+        zz_set_error(__VA_ARGS__); \
+        return 0;                  \
+    } while (0)
+
+// ------------------------------------------------------------------ kernels
+// H = (H + rmsnorm(h1 + h2, w)) * ls (gemma4.c:1022-1030): tmp = h1 + h2, its sum of
+// squares in double (gemma4.c:425-428), tmp*r*w left to right, then (res + tmp)*ls.
+// One workgroup per token.
+__global__ __launch_bounds__(256) void zz_block_combine_kernel(float *H, const float *h1, const float *h2,
+                                                               const float *w, float ls, float eps, int D) {
+    const int s = blockIdx.x, tid = threadIdx.x;
+    __shared__ __attribute__((aligned(16))) float row[ZZ_MAXD];
+    __shared__ double red[4];
+    float *hr = H + (size_t)s * D;
+    const float *a = h1 + (size_t)s * D, *b = h2 + (size_t)s * D;
+    double ss = 0.0;
+    for (int o = 4 * tid; o < D; o += 1024) {
+        const float4 x = *(const float4 *)(a + o), y = *(const float4 *)(b + o);
+        const float4 t = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+        *(float4 *)&row[o] = t;
+        ss += (double)t.x * t.x + (double)t.y * t.y + (double)t.z * t.z + (double)t.w * t.w;
+    }
+    ss = zz_block_sum(ss, red);
+    const float r = 1.0f / sqrtf((float)(ss / D) + eps);
+    for (int o = 4 * tid; o < D; o += 1024) {
+        const float4 t = *(const float4 *)&row[o], wv = *(const float4 *)(w + o), h = *(const float4 *)(hr + o);
+        *(float4 *)(hr + o) = make_float4((h.x + (t.x * r) * wv.x) * ls, (h.y + (t.y * r) * wv.y) * ls,
+                                          (h.z + (t.z * r) * wv.z) * ls, (h.w + (t.w * r) * wv.w) * ls);
+    }
+}
+
+// embed_row (gemma4.c:1131-1145): h = (d * (q - 8)) * embed_scale for row tok[s] of
+// the lane-order table. Thread u owns block u/4, weights k = 8(u%4)..+7: one 4-byte
+// word (byte m: nibbles k = 8qq+m and 8qq+m+4, stored as q ^ 8) and the block scale.
+__global__ __launch_bounds__(256) void zz_embed_kernel(const uint8_t *tb, ZzTensor T, const int *tok, float scale,
+                                                       float *H) {
+    const int s = blockIdx.x, D = T.I, nb = D / ZZ_BLK;
+    int t = tok[s];
+    t = t < 0 || t >= T.O ? 0 : t;
+    const int g = t >> 4, r = t & 15;
+    for (int u = threadIdx.x; u < 4 * nb; u += 256) {
+        const int b = u >> 2, qq = u & 3;
+        const unsigned w = *(const unsigned *)(tb + zz_qlane(T, g, b, 16 * qq + r));
+        const float d = zz_h2f(*(const uint16_t *)(tb + zz_sidx(T, g, b, r)));
+        float v[8];
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int n0 = (int)((w >> (8 * m)) & 15u) ^ 8, n1 = (int)((w >> (8 * m + 4)) & 15u) ^ 8;
+            v[m] = (d * (float)(n0 - 8)) * scale;
+            v[m + 4] = (d * (float)(n1 - 8)) * scale;
+        }
+        float *h = H + (size_t)s * D + b * ZZ_BLK + 8 * qq;
+        *(float4 *)h = make_float4(v[0], v[1], v[2], v[3]);
+        *(float4 *)(h + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
+__device__ __forceinline__ unsigned zz_ord_bits(float f) {       // order-preserving
+    const unsigned u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// lm_head GEMV: one wave per 16-row group of the table over the whole K range, lane
+// l = 16qq + r as in the slot table; HD_C chunks' loads are issued together. The
+// q8_0 rows of xn (S <= 4) are staged in LDS. Then the softcap, the logits, and the
+// row's (logit, -index) key into amax[s] by a 64-bit atomic max: the first index of
+// the largest logit wins, whatever the order the workgroups finish in.
+#define HD_C 8
+__global__ __launch_bounds__(256) void zz_head_kernel(const uint8_t *tb, ZzTensor T, const int8_t *xq,
+                                                      const float *xs, int S, float cap, float *logits,
+                                                      unsigned long long *amax) {
+    __shared__ __attribute__((aligned(16))) int8_t sx_q[ZZ_DEC_MAXS][ZZ_MAXD];
+    __shared__ float sx_s[ZZ_DEC_MAXS][ZZ_MAXD / ZZ_BLK];
+    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, r = l & 15, qq = l >> 4;
+    const int D = T.I, nb = D / ZZ_BLK, nch = (nb + 3) / 4, V = T.O, g = 4 * blockIdx.x + w;
+    for (int i = tid; i < S * (D / 16); i += 256) {
+        const int s = i / (D / 16), k = i - s * (D / 16);
+        *(uint4 *)&sx_q[s][16 * k] = ld16(xq + (size_t)s * D + 16 * k);
+    }
+    for (int i = tid; i < S * nb; i += 256) sx_s[i / nb][i % nb] = xs[i];
+    const ZzWalk W = zz_walk(T, g, l, r);
+    float acc[ZZ_DEC_MAXS] = {0.0f, 0.0f, 0.0f, 0.0f};
+    ZzChunk k[HD_C];
+#pragma unroll
+    for (int i = 0; i < HD_C; i++) k[i] = zz_load_chunk<ZZ_FMT_Q40>(tb, W, min(i, nch - 1));
+    __syncthreads();
+    for (int c0 = 0; c0 < nch; c0 += HD_C) {
+#pragma unroll
+        for (int i = 0; i < HD_C; i++) {
+            const int c = c0 + i;
+            if (c >= nch) break;
+            const bool full = c < W.nfull;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (j >= 2 && !full) break;
+                const int b = 4 * c + j;
+                const uint2 wv = zz_chunk_w<ZZ_FMT_Q40>(k[i], j);
+                const float dw = zz_chunk_dw(k[i], j, full);
+#pragma unroll
+                for (int s = 0; s < ZZ_DEC_MAXS; s++) {
+                    if (s >= S) break;
+                    const uint2 xv = *(const uint2 *)&sx_q[s][b * ZZ_BLK + 8 * qq];
+                    int d = zz_dot4(wv.x, xv.x, 0);
+                    d = zz_dot4(wv.y, xv.y, d);
+                    acc[s] = fmaf(dw * sx_s[s][b], (float)d, acc[s]);
+                }
+            }
+        }
+        if (c0 + HD_C < nch)
+#pragma unroll
+            for (int i = 0; i < HD_C; i++) k[i] = zz_load_chunk<ZZ_FMT_Q40>(tb, W, min(c0 + HD_C + i, nch - 1));
+    }
+    const int o = 16 * g + r;
+#pragma unroll
+    for (int s = 0; s < ZZ_DEC_MAXS; s++) {
+        if (s >= S) break;
+        float v = acc[s];
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        v *= 0.0625f;                                    // the 16*(q - 8) weights
+        if (cap > 0.0f) v = tanhf(v / cap) * cap;
+        if (qq == 0) logits[(size_t)s * V + o] = v;
+        unsigned long long key = ((unsigned long long)zz_ord_bits(v) << 32) | (0xffffffffu - (unsigned)o);
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) {
+            const unsigned long long k2 = __shfl_xor(key, m, 64);
+            key = k2 > key ? k2 : key;
+        }
+        if (l == 0) atomicMax(amax + s, key);
+    }
+}
+
+// argmax[s] from the keys, which are cleared for the next call
+__global__ void zz_head_argmax_kernel(unsigned long long *amax, int *argmax, int S) {
+    const int s = threadIdx.x;
+    if (s < S) {
+        const unsigned long long k = amax[s];
+        if (argmax) argmax[s] = (int)(0xffffffffu - (unsigned)(k & 0xffffffffu));
+        amax[s] = 0ull;
+    }
+}
+
+// ------------------------------------------------------------------ ffn blocks
+struct FfnBlock {
+    int moe, dense, D;
+    float ls, eps;
+    float *post_ln = nullptr;
+    float *h1 = nullptr, *h2 = nullptr, *hh = nullptr;   // hh: host-form staging of H
+    size_t cap = 0;                                    // tokens h1/h2/hh hold
+    hipStream_t ds = nullptr;                          // the dense branch's stream
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+static std::vector<FfnBlock *> g_blocks;
+
+static void free_block(FfnBlock *B) {
+    if (!B) return;
+    if (B->ds) (void)hipStreamSynchronize(B->ds);
+    void *ps[] = {B->post_ln, B->h1, B->h2, B->hh};
+    for (void *p : ps)
+        if (p) (void)hipFree(p);
+    if (B->fork) (void)hipEventDestroy(B->fork);
+    if (B->join) (void)hipEventDestroy(B->join);
+    if (B->ds) (void)hipStreamDestroy(B->ds);
+    delete B;
+}
+
+static FfnBlock *get_block(int id) {
+    if (!zz_lib_ready() || id < 0 || id >= (int)g_blocks.size()) return nullptr;
+    return g_blocks[id];
+}
+
+extern "C" int zz_ffn_block_create(int moe_layer, int dense_layer, const float *post_ffn_ln, float layer_scalar) {
+    const zz_moe_desc *m = zz_layer_desc(moe_layer), *d = zz_layer_desc(dense_layer);
+    if (!m || !d || !post_ffn_ln || m->gating != ZZ_GATE_SOFTMAX_PES || d->gating != ZZ_GATE_DENSE ||
+        m->D != d->D) {
+        zz_set_error("zz_ffn_block_create: needs a gemma MoE layer and a dense layer of one D, and post_ffn_ln");
+        return -1;
+    }
+    FfnBlock *B = new FfnBlock();
+    B->moe = moe_layer;
+    B->dense = dense_layer;
+    B->D = m->D;
+    B->ls = layer_scalar;
+    B->eps = m->eps;
+    bool ok = hipMalloc(&B->post_ln, sizeof(float) * m->D) == hipSuccess &&
+              hipMemcpy(B->post_ln, post_ffn_ln, sizeof(float) * m->D, hipMemcpyHostToDevice) == hipSuccess &&
+              hipStreamCreateWithFlags(&B->ds, hipStreamNonBlocking) == hipSuccess &&
+              hipEventCreateWithFlags(&B->fork, hipEventDisableTiming) == hipSuccess &&
+              hipEventCreateWithFlags(&B->join, hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+        zz_set_error("zz_ffn_block_create: device allocation failed");
+        free_block(B);
+        return -1;
+    }
+    for (size_t i = 0; i < g_blocks.size(); i++)
+        if (!g_blocks[i]) { g_blocks[i] = B; return (int)i; }
+    g_blocks.push_back(B);
+    return (int)g_blocks.size() - 1;
+}
+
+extern "C" void zz_ffn_block_destroy(int id) {
+    FfnBlock *B = get_block(id);
+    if (!B) return;
+    (void)hipStreamSynchronize(zz_lib_stream());
+    free_block(B);
+    g_blocks[id] = nullptr;
+}
+
+static int block_grow(FfnBlock *B, int S, hipStream_t st) {
+    if ((size_t)S <= B->cap) return 1;
+    ZZ_CHECK(hipStreamSynchronize(st));
+    ZZ_CHECK(hipStreamSynchronize(B->ds));
+    float **bufs[] = {&B->h1, &B->h2, &B->hh};
+    for (float **p : bufs) {
+        if (*p) (void)hipFree(*p);
+        *p = nullptr;
+    }
+    B->cap = 0;
+    const size_t n = sizeof(float) * (size_t)S * B->D;
+    ZZ_CHECK(hipMalloc(&B->h1, n));
+    ZZ_CHECK(hipMalloc(&B->h2, n));
+    ZZ_CHECK(hipMalloc(&B->hh, n));
+    B->cap = (size_t)S;
+    return 1;
+}
+
+static int block_forward(FfnBlock *B, float *d_H, int S, int *d_eidx, float *d_ewt, hipStream_t st) {
+    if (S <= 0 || !d_H) ZZ_FAIL("zz_ffn_block_forward: bad arguments");
+    if (!block_grow(B, S, st)) return 0;
+    // the dense branch forks off the caller's stream and joins before the combine
+    ZZ_CHECK(hipEventRecord(B->fork, st));
+    ZZ_CHECK(hipStreamWaitEvent(B->ds, B->fork, 0));
+    if (!zz_moe_forward_dev(B->moe, d_H, B->h2, S, d_eidx, d_ewt, st)) return 0;
+    if (!zz_moe_forward_dev(B->dense, d_H, B->h1, S, nullptr, nullptr, B->ds)) return 0;
+    ZZ_CHECK(hipEventRecord(B->join, B->ds));
+    ZZ_CHECK(hipStreamWaitEvent(st, B->join, 0));
+    hipLaunchKernelGGL(zz_block_combine_kernel, dim3(S), dim3(256), 0, st, d_H, B->h1, B->h2, B->post_ln, B->ls,
+                       B->eps, B->D);
+    if (hipGetLastError() != hipSuccess) ZZ_FAIL("zz_ffn_block_forward: combine launch failed");
+    return 1;
+}
+
+extern "C" int zz_ffn_block_forward_dev(int id, float *d_H, int S, int *d_eidx, float *d_ewt, void *stream) {
+    FfnBlock *B = get_block(id);
+    if (!B) ZZ_FAIL("zz_ffn_block_forward_dev: no such block");
+    return block_forward(B, d_H, S, d_eidx, d_ewt, stream ? (hipStream_t)stream : zz_lib_stream());
+}
+
+extern "C" int zz_ffn_block_forward(int id, float *H, int S, int *eidx, float *ewt) {
+    FfnBlock *B = get_block(id);
+    if (!B || !H || S <= 0) ZZ_FAIL("zz_ffn_block_forward: bad arguments");
+    const zz_moe_desc *m = zz_layer_desc(B->moe);
+    if (!m) ZZ_FAIL("zz_ffn_block_forward: the MoE layer is gone");
+    hipStream_t st = zz_lib_stream();
+    if (!block_grow(B, S, st)) return 0;
+    int *d_ix = nullptr;
+    float *d_wt = nullptr;
+    const size_t P = (size_t)S * m->K;
+    if ((eidx && hipMalloc(&d_ix, sizeof(int) * P) != hipSuccess) ||
+        (ewt && hipMalloc(&d_wt, sizeof(float) * P) != hipSuccess)) {
+        if (d_ix) (void)hipFree(d_ix);
+        ZZ_FAIL("zz_ffn_block_forward: allocation failed");
+    }
+    std::vector<float> h((size_t)S * B->D);
+    int ok = hipMemcpyAsync(B->hh, H, sizeof(float) * h.size(), hipMemcpyHostToDevice, st) == hipSuccess &&
+             block_forward(B, B->hh, S, d_ix, d_wt, st) &&
+             hipMemcpyAsync(h.data(), B->hh, sizeof(float) * h.size(), hipMemcpyDeviceToHost, st) == hipSuccess &&
+             hipStreamSynchronize(st) == hipSuccess &&
+             (!eidx || hipMemcpy(eidx, d_ix, sizeof(int) * P, hipMemcpyDeviceToHost) == hipSuccess) &&
+             (!ewt || hipMemcpy(ewt, d_wt, sizeof(float) * P, hipMemcpyDeviceToHost) == hipSuccess);
+    if (d_ix) (void)hipFree(d_ix);
+    if (d_wt) (void)hipFree(d_wt);
+    if (!ok) ZZ_FAIL("zz_ffn_block_forward: failed (%s)", hipGetErrorString(hipGetLastError()));
+    memcpy(H, h.data(), sizeof(float) * h.size());
+    return 1;
+}
+
+// ------------------------------------------------------------------ heads
+struct Head {
+    int V, D;
+    float eps, escale, cap;
+    ZzTensor T;
+    uint8_t *table = nullptr;       // lane-order q4_0 [V, D]
+    float *fnorm = nullptr;
+    int8_t *xq = nullptr;           // [4, D] q8_0 of rmsnorm(H, final_norm)
+    float *xs = nullptr;            // [4, D/32]
+    int *xsum = nullptr;            // [4, D/32]
+    unsigned long long *amax = nullptr;   // [4] argmax keys, kept at 0 between calls
+};
+static std::vector<Head *> g_heads;
+
+static void free_head(Head *h) {
+    if (!h) return;
+    void *ps[] = {h->table, h->fnorm, h->xq, h->xs, h->xsum, h->amax};
+    for (void *p : ps)
+        if (p) (void)hipFree(p);
+    delete h;
+}
+
+static Head *get_head(int id) {
+    if (!zz_lib_ready() || id < 0 || id >= (int)g_heads.size()) return nullptr;
+    return g_heads[id];
+}
+
+extern "C" int zz_head_create(const uint8_t *table, int V, int D, const float *final_norm, float eps,
+                              float embed_scale, float softcap) {
+    if (!zz_lib_ready() || !table || !final_norm || V <= 0 || V % 64 || D <= 0 || D % 64 || D > ZZ_MAXD) {
+        zz_set_error("zz_head_create: bad arguments (V %% 64 == 0, D %% 64 == 0, D <= %d)", ZZ_MAXD);
+        return -1;
+    }
+    Head *h = new Head();
+    h->V = V;
+    h->D = D;
+    h->eps = eps;
+    h->escale = embed_scale;
+    h->cap = softcap;
+    int64_t cur = 0;
+    h->T = zz_make_tensor(ZZ_FMT_Q40, V, D, &cur);
+    const size_t src_bytes = (size_t)V * (D / ZZ_BLK) * 18, nb = D / ZZ_BLK;
+    hipStream_t st = zz_lib_stream();
+    uint8_t *staging = nullptr;
+    bool ok = hipMalloc(&h->table, (size_t)cur) == hipSuccess && hipMalloc(&staging, src_bytes) == hipSuccess &&
+              hipMalloc(&h->fnorm, sizeof(float) * D) == hipSuccess &&
+              hipMalloc(&h->xq, (size_t)ZZ_DEC_MAXS * D) == hipSuccess &&
+              hipMalloc(&h->xs, sizeof(float) * ZZ_DEC_MAXS * nb) == hipSuccess &&
+              hipMalloc(&h->xsum, sizeof(int) * ZZ_DEC_MAXS * nb) == hipSuccess &&
+              hipMalloc(&h->amax, sizeof(unsigned long long) * ZZ_DEC_MAXS) == hipSuccess &&
+              hipMemset(h->amax, 0, sizeof(unsigned long long) * ZZ_DEC_MAXS) == hipSuccess &&
+              hipMemcpy(h->fnorm, final_norm, sizeof(float) * D, hipMemcpyHostToDevice) == hipSuccess &&
+              hipMemcpy(staging, table, src_bytes, hipMemcpyHostToDevice) == hipSuccess;
+    if (ok) {
+        ZzRepackArgs a;
+        memset(&a, 0, sizeof a);
+        a.src = staging;
+        a.dst = h->table;
+        a.lay.gate = h->T;
+        a.lay.bytes = cur;
+        ok = zz_launch_repack_n(a, 1, st) && hipStreamSynchronize(st) == hipSuccess;
+    }
+    if (staging) (void)hipFree(staging);
+    if (!ok) {
+        zz_set_error("zz_head_create: device allocation or upload failed");
+        free_head(h);
+        return -1;
+    }
+    for (size_t i = 0; i < g_heads.size(); i++)
+        if (!g_heads[i]) { g_heads[i] = h; return (int)i; }
+    g_heads.push_back(h);
+    return (int)g_heads.size() - 1;
+}
+
+extern "C" void zz_head_destroy(int id) {
+    Head *h = get_head(id);
+    if (!h) return;
+    (void)hipStreamSynchronize(zz_lib_stream());
+    free_head(h);
+    g_heads[id] = nullptr;
+}
+
+extern "C" int zz_head_embed_dev(int id, const int *d_tok, int S, float *d_H, void *stream) {
+    Head *h = get_head(id);
+    if (!h || !d_tok || !d_H || S <= 0) ZZ_FAIL("zz_head_embed_dev: bad arguments");
+    hipStream_t st = stream ? (hipStream_t)stream : zz_lib_stream();
+    hipLaunchKernelGGL(zz_embed_kernel, dim3(S), dim3(256), 0, st, h->table, h->T, d_tok, h->escale, d_H);
+    if (hipGetLastError() != hipSuccess) ZZ_FAIL("zz_head_embed_dev: launch failed");
+    return 1;
+}
+
+extern "C" int zz_head_embed(int id, const int *tok, int S, float *H) {
+    Head *h = get_head(id);
+    if (!h || !tok || !H || S <= 0) ZZ_FAIL("zz_head_embed: bad arguments");
+    hipStream_t st = zz_lib_stream();
+    int *d_tok = nullptr;
+    float *d_H = nullptr;
+    int ok = hipMalloc(&d_tok, sizeof(int) * S) == hipSuccess &&
+             hipMalloc(&d_H, sizeof(float) * (size_t)S * h->D) == hipSuccess &&
+             hipMemcpy(d_tok, tok, sizeof(int) * S, hipMemcpyHostToDevice) == hipSuccess &&
+             zz_head_embed_dev(id, d_tok, S, d_H, st) && hipStreamSynchronize(st) == hipSuccess &&
+             hipMemcpy(H, d_H, sizeof(float) * (size_t)S * h->D, hipMemcpyDeviceToHost) == hipSuccess;
+    if (d_tok) (void)hipFree(d_tok);
+    if (d_H) (void)hipFree(d_H);
+    if (!ok) ZZ_FAIL("zz_head_embed: failed");
+    return 1;
+}
+
+extern "C" int zz_head_logits_dev(int id, const float *d_H, int S, float *d_logits, int *d_argmax, void *stream) {
+    Head *h = get_head(id);
+    if (!h || !d_H || !d_logits || S <= 0 || S > ZZ_DEC_MAXS) ZZ_FAIL("zz_head_logits_dev: bad arguments (S <= %d)", ZZ_DEC_MAXS);
+    hipStream_t st = stream ? (hipStream_t)stream : zz_lib_stream();
+    // rmsnorm(H, final_norm) and its q8_0 rows, as matvec quantises xn (gemma4.c:445-460)
+    ZzPrepArgs pa;
+    memset(&pa, 0, sizeof pa);
+    pa.D = h->D;
+    pa.gemma = 1;
+    pa.eps = h->eps;
+    pa.in = d_H;
+    pa.pre_ln = h->fnorm;
+    pa.xq = h->xq;
+    pa.xs = h->xs;
+    pa.xsum = h->xsum;
+    pa.diag = zz_lib_diag();
+    if (!zz_launch_prep(pa, S, st)) ZZ_FAIL("zz_head_logits_dev: norm launch failed");
+    hipLaunchKernelGGL(zz_head_kernel, dim3(h->V / 64), dim3(256), 0, st, h->table, h->T, h->xq, h->xs, S, h->cap,
+                       d_logits, h->amax);
+    hipLaunchKernelGGL(zz_head_argmax_kernel, dim3(1), dim3(64), 0, st, h->amax, d_argmax, S);
+    if (hipGetLastError() != hipSuccess) ZZ_FAIL("zz_head_logits_dev: launch failed");
+    return 1;
+}
+
+extern "C" int zz_head_logits(int id, const float *H, int S, float *logits, int *argmax) {
+    Head *h = get_head(id);
+    if (!h || !H || !logits || S <= 0 || S > ZZ_DEC_MAXS) ZZ_FAIL("zz_head_logits: bad arguments");
+    hipStream_t st = zz_lib_stream();
+    float *d_H = nullptr, *d_l = nullptr;
+    int *d_a = nullptr;
+    int ok = hipMalloc(&d_H, sizeof(float) * (size_t)S * h->D) == hipSuccess &&
+             hipMalloc(&d_l, sizeof(float) * (size_t)S * h->V) == hipSuccess &&
+             hipMalloc(&d_a, sizeof(int) * S) == hipSuccess &&
+             hipMemcpy(d_H, H, sizeof(float) * (size_t)S * h->D, hipMemcpyHostToDevice) == hipSuccess &&
+             zz_head_logits_dev(id, d_H, S, d_l, d_a, st) && hipStreamSynchronize(st) == hipSuccess &&
+             hipMemcpy(logits, d_l, sizeof(float) * (size_t)S * h->V, hipMemcpyDeviceToHost) == hipSuccess &&
+             (!argmax || hipMemcpy(argmax, d_a, sizeof(int) * S, hipMemcpyDeviceToHost) == hipSuccess);
+    if (d_H) (void)hipFree(d_H);
+    if (d_l) (void)hipFree(d_l);
+    if (d_a) (void)hipFree(d_a);
+    if (!ok) ZZ_FAIL("zz_head_logits: failed");
+    return 1;
+}
+
+// released by gpu_shutdown (zz_api.hip)
+void zz_gemma_shutdown() {
+    for (FfnBlock *&B : g_blocks) { free_block(B); B = nullptr; }
+    g_blocks.clear();
+    for (Head *&h : g_heads) { free_head(h); h = nullptr; }
+    g_heads.clear();
+}

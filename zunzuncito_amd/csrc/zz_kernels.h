@@ -15,6 +15,8 @@ struct ZzPrepArgs {
     int *xsum;                  // [S, D/32]
     float *xt;                  // [S] tq2 Sx, or null
     unsigned *diag;             // diagnostics counters
+    int *route_eidx;            // dense branch: [S] set to expert 0, or null
+    float *route_ewt;           // dense branch: [S] set to weight 1
 };
 
 struct ZzLogitArgs {
@@ -97,12 +99,14 @@ struct ZzDecRouteArgs {
     ZzTopkArgs tk;              // top-k of all tokens
     ZzDispatchArgs dp;          // dispatch lists and work items
     int S;
+    int dense;                  // dense branch: norms and quantisation only, no logits
 };
 
 // Decode gate/up: the routing of each token and the expert GEMVs of its pairs.
 struct ZzDecUpArgs {
     ZzFfnArgs f;
     ZzTopkArgs tk;
+    int dense;                  // dense branch: expert 0 for every pair, no top-k
 };
 
 // Fused decode down projection + gate-weighted combine.
@@ -115,6 +119,15 @@ struct ZzDecDownArgs {
     float *out;                 // [S, D]
     double *ss;                 // [S, D/16] per-tile sums of squares of out (gemma), or null
 };
+
+// Host-side internals of the library (zz_api.hip), shared by its host files.
+struct zz_moe_desc;
+hipStream_t zz_lib_stream();
+int zz_lib_ready();
+unsigned *zz_lib_diag();
+const zz_moe_desc *zz_layer_desc(int id);
+// tensor in the slot-table layout at *cursor (advanced past it, 256-aligned)
+ZzTensor zz_make_tensor(int fmt, int O, int I, int64_t *cursor);
 
 struct ZzRepackArgs {
     const uint8_t *src;         // reference record [gate | up | down]
@@ -138,6 +151,8 @@ int zz_launch_up_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_down_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st);
 int zz_launch_combine(const ZzCombineArgs &a, int S, hipStream_t st);
 int zz_launch_repack(const ZzRepackArgs &a, hipStream_t st);
+// the first n tensors of a.lay only (gate, then up, then down)
+int zz_launch_repack_n(const ZzRepackArgs &a, int n, hipStream_t st);
 // y[S,O] = W[O,I] x[S,I] with f32 activations (gpu.h matmul contract)
 int zz_launch_matmul_f32(int fmt, float *y, const uint8_t *W, const float *x, int O, int I,
                          int S, hipStream_t st);

@@ -22,7 +22,8 @@
 // Prep: one workgroup per token. Gemma: the mean square is certified to round to
 // the float the reference's serial double sum gives (gemma4.c:425-428), else that
 // sum is replayed serially; then the router input xn = rmsnorm(x)*scale*D^-1/2
-// (gemma4.c:591-593). The expert input X (gemma: rmsnorm(x, pre_ffn_ln2),
+// (gemma4.c:591-593), unless there is no router (the dense branch, which routes
+// every row to its one expert with weight 1 here). The expert input X (gemma: rmsnorm(x, pre_ffn_ln2),
 // gemma4.c:763-764; lfm/maple: x) is quantised q8_0-style (q40.h:124-138), one
 // 32-block per thread, with per-block integer sums; for tq2 the Sx total
 // (tq2.h:98-108) is summed serially in the reference's order.
@@ -34,6 +35,10 @@ __global__ __launch_bounds__(256) void zz_prep_kernel(ZzPrepArgs a) {
     __shared__ int xsum_l[ZZ_MAXD / ZZ_BLK];
     __shared__ float cert;
     float r = 1.0f;
+    if (a.route_eidx && tid == 0) {                // dense branch: one expert, weight 1
+        a.route_eidx[s] = 0;
+        a.route_ewt[s] = 1.0f;
+    }
     if (a.gemma) {
         double sq = 0.0;
         for (int i = 4 * tid; i < D; i += 1024) {
@@ -60,7 +65,7 @@ __global__ __launch_bounds__(256) void zz_prep_kernel(ZzPrepArgs a) {
         __syncthreads();
         r = 1.0f / sqrtf(cert + a.eps);
         const float rs = 1.0f / sqrtf((float)D);
-        for (int i = 4 * tid; i < D; i += 1024) {
+        for (int i = 4 * tid; a.router_scale && i < D; i += 1024) {   // no router: no xn
             const float4 v = *(const float4 *)(x + i), sc = *(const float4 *)(a.router_scale + i);
             *(float4 *)(a.xn + (size_t)s * D + i) =
                 make_float4((v.x * r) * (sc.x * rs), (v.y * r) * (sc.y * rs), (v.z * r) * (sc.z * rs),
