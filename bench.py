@@ -7,7 +7,10 @@ router biased by a seeded Zipf(1.1) per-expert logit offset. A step is one
 zz_moe_forward_dev() call on one layer; steps rotate over --layers distinct
 layers (default 30, ~12.8 GB of experts) so the weights cannot sit in the 256 MB
 MALL. Inputs and weights are resident in HBM before timing starts. The S=1
-decode figure is reported under "decode".
+decode figure is reported under "decode", and the 30-layer stack
+(configs[4]: each MoE layer with gemma's dense MLP and layer combine, a tied q4_0
+head of 262144 rows, 512-token prefill then 256 greedy decode steps, attention as
+the identity) under "stack".
 
 Also reported: per-kernel durations from HIP events recorded by the library on
 the stream each kernel runs on (zz_moe_profile), the roofline of the dominant
@@ -203,6 +206,104 @@ def cpu_baseline(zz, torch, host, S_sample, seconds, seed):
                        f"OpenMP, experts preloaded in RAM")
 
 
+DI, V = 2112, 262144                     # Gemma-4 dense_inter and vocabulary
+DENSE_B = 2 * Q40_TENSOR(DI, D) + Q40_TENSOR(D, DI)
+TABLE_B = Q40_TENSOR(V, D)
+
+
+def device_q40(zz, torch, n, gen, sigma=0.02):
+    """n N(0, sigma) weights quantised to q4_0 on the device (bit-exact
+    q40_quant_row), as a uint8 tensor in the reference layout."""
+    f = torch.empty(n, dtype=torch.float32, device="cuda")
+    f.normal_(0.0, sigma, generator=gen)
+    q = torch.empty(n // 32 * 18, dtype=torch.uint8, device="cuda")
+    zz.quantize_dev(1, f.data_ptr(), q.data_ptr(), n, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.current_stream().synchronize()
+    return q
+
+
+def stack_bench(zz, torch, layers, seed, prefill_S, steps):
+    """the Gemma-4 stack of the MoE layers above, each with a q4_0
+    dense MLP (dense_inter 2112) and the layer combine, under a tied q4_0 embedding /
+    lm_head of Gemma-4's 262144 rows; attention is the identity. A prefill of
+    prefill_S N(0,1) rows, then greedy decode steps whose token ids stay on the
+    device, both timed with HIP events on the launching stream."""
+    rng = np.random.default_rng(seed + 500)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed * 7919)
+    objs, blocks = [], []
+    for li, m in enumerate(layers):
+        d = zz.MoeLayer(D, DI, 1, 1, zz.ZZ_GATE_DENSE, zz.ZZ_ACT_GEGLU_TANH, (1, 1, 1), None,
+                        pre_ln=(1 + 0.05 * rng.standard_normal(D)).astype(np.float32),
+                        post_ln=(1 + 0.05 * rng.standard_normal(D)).astype(np.float32), eps=1e-6)
+        q = device_q40(zz, torch, 3 * DI * D, gen)
+        d.upload_dev(0, q.data_ptr(), DENSE_B)
+        del q
+        b = zz.FfnBlock(m, d, (1 + 0.05 * rng.standard_normal(D)).astype(np.float32),
+                        float(np.float32(0.5 + 0.5 * rng.random())))
+        objs += [b, d]
+        blocks.append(b)
+    parts = []
+    for r0 in range(0, V, 16384):                        # 16384 rows per pass: 185 MB of f32
+        parts.append(device_q40(zz, torch, 16384 * D, gen).cpu().numpy())
+    table = np.concatenate(parts)
+    del parts
+    torch.cuda.empty_cache()
+    head = zz.Head(table, V, D, (1 + 0.05 * rng.standard_normal(D)).astype(np.float32), 1e-6,
+                   float(np.sqrt(np.float32(D))), 30.0)
+    del table
+    stack = zz.Stack(blocks, head)
+    objs += [stack, head]
+    st = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 99)
+    H0 = torch.randn(prefill_S, D, generator=g, device="cuda")
+    H = H0.clone()
+    tok = torch.zeros(steps + 1, dtype=torch.int32, device="cuda")
+    stack.prefill_dev(H.data_ptr(), prefill_S, tok.data_ptr(), st.cuda_stream)   # warm-up
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 3
+    e0.record(st)
+    for _ in range(reps):
+        H.copy_(H0)
+        stack.prefill_dev(H.data_ptr(), prefill_S, tok.data_ptr(), st.cuda_stream)
+    e1.record(st)
+    torch.cuda.synchronize()
+    copy_ms = prefill_S * D * 4 * 2 / 4e12 * 1e3                      # the H reset, ~3 us
+    prefill_s = (e0.elapsed_time(e1) / reps - copy_ms) / 1e3
+    out = {}
+    for graph in (False, True):
+        stack.decode_dev(tok.data_ptr(), 4, graph=graph, stream=st.cuda_stream)     # warm / capture
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(st)
+        stack.decode_dev(tok.data_ptr(), steps, graph=graph, stream=st.cuda_stream)
+        e1.record(st)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        out["graph" if graph else "eager"] = dict(tokens_per_s=steps / (e0.elapsed_time(e1) / 1e3),
+                                                  ms_per_token=e0.elapsed_time(e1) / steps,
+                                                  host_wall_ms_per_token=wall * 1e3 / steps)
+    toks = tok.cpu().numpy()
+    # algorithmic bytes of one decode token: per layer the 8 routed experts, the
+    # router, the dense MLP and the norm vectors; the head table once
+    per_layer = K * REC_B + E * D * 4 + DENSE_B + 8 * D * 4
+    step_bytes = len(layers) * per_layer + TABLE_B + D * 4
+    best = max(out.values(), key=lambda v: v["tokens_per_s"])
+    for o in objs:
+        o.close()
+    return dict(
+        workload=f"gemma4 stack: {len(layers)} layers x (MoE E={E} top-{K} MI={MI} + dense "
+                 f"MLP {DI}) q4_0, tied q4_0 head V={V}, attention = identity",
+        prefill=dict(tokens=prefill_S, ms=prefill_s * 1e3, tokens_per_s=prefill_S / prefill_s),
+        decode=dict(steps=steps, eager=out["eager"], graph=out["graph"],
+                    tokens_per_s=best["tokens_per_s"], hbm_bytes_per_token=step_bytes,
+                    hbm_GBs=step_bytes * best["tokens_per_s"] / 1e9,
+                    hbm_frac=step_bytes * best["tokens_per_s"] / 1e9 / HBM_PEAK_GBS,
+                    distinct_tokens=int(len(np.unique(toks)))))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -214,6 +315,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 30-layer stack (config 5)")
+    ap.add_argument("--stack-steps", type=int, default=256)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="only run one plain device-to-device copy of this many MiB (the "
                          "known-size kernel that scales FETCH_SIZE / WRITE_SIZE counters)")
@@ -304,6 +407,10 @@ def main():
         "kernels_us": r["kern"],
         "decode": decode,
     }
+    if not args.no_stack:
+        log("building and timing the gemma stack (config 5) ...")
+        line["stack"] = stack_bench(zz, torch, layers, args.seed, args.tokens, args.stack_steps)
+        log("stack:", json.dumps(line["stack"]))
     if not args.no_cpu:
         log("timing the CPU reference path ...")
         line["cpu_baseline"] = cpu_baseline(zz, torch, host, args.cpu_tokens, args.cpu_seconds,

@@ -56,6 +56,25 @@ int zz_head_logits_dev(int head, const float *d_H, int S, float *d_logits, int *
                        void *stream);
 int zz_head_logits(int head, const float *H, int S, float *logits, int *argmax);
 
+/* A stack of FFN blocks under one head: gemma4.c forward() (1184-1275) with the
+ * attention of every layer taken as the identity. Returns a stack id >= 0, or -1.
+ * The blocks and the head must outlive the stack. */
+int zz_stack_create(const int *blocks, int n_blocks, int head);
+void zz_stack_destroy(int stack);
+
+/* Prefill: S rows of H [S, D] through every block in order, in place; when d_tok is
+ * not NULL, d_tok[0] receives the greedy token of the last row (forward() with
+ * last_only, then sample at temp 0). */
+int zz_stack_prefill_dev(int stack, float *d_H, int S, int *d_tok, void *stream);
+
+/* Greedy decode: for i = 0 .. n-1, d_tok[i+1] = the greedy token of
+ * head(blocks(embed_row(d_tok[i]))). Token ids never leave the device. d_logits
+ * (may be NULL) receives the last step's logits [V]. use_graph != 0 replays one
+ * captured HIP graph per step (captured once per stack, on the first such call)
+ * instead of launching each kernel. */
+int zz_stack_decode_dev(int stack, int *d_tok, int n, float *d_logits, int use_graph,
+                        void *stream);
+
 #ifdef __cplusplus
 }
 #endif

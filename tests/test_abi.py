@@ -91,6 +91,9 @@ def test_decline_contract_without_device():
     assert L.zz_head_logits(0, x.ctypes.data_as(zz._f32p), 1, lg.ctypes.data_as(zz._f32p),
                             tok.ctypes.data_as(zz._i32p)) == 0
     assert np.all(out == 3.0) and np.all(lg == 5.0)
+    ids = np.zeros(2, np.int32)
+    assert L.zz_stack_create(ids.ctypes.data_as(zz._i32p), 2, 0) == -1
+    assert L.zz_stack_decode_dev(0, None, 4, None, 1, None) == 0
     L.gpu_shutdown()                             # safe when never initialised
 
 

@@ -233,3 +233,53 @@ def test_stack_prefill_and_greedy_decode_on_device(dev):
         say("stack tokens", toks, "reference fixture", g["stack_tokens"].tolist())
     finally:
         close_all(*objs)
+
+
+def test_stack_runner_graph_equals_eager(dev):
+    """zz_stack_*: prefill equals the blocks run one by one; greedy decode replayed
+    from a captured HIP graph equals eager launches bit for bit, on every step of
+    three calls with eager work and host synchronisations between the replays."""
+    import torch
+    *_, st, H0 = Z.gemma_block_case()
+    D, V = st.layers[0].D, st.V
+    blocks, objs = [], []
+    for L_, dn in zip(st.layers, st.denses):
+        B, m, d = gpu_block(L_, dn)
+        blocks.append(B)
+        objs += [B, m, d]
+    hd = zz.Head(st.table, V, D, st.fnorm, st.layers[0].eps, st.embed_scale, st.softcap)
+    stack = zz.Stack(blocks, hd)
+    objs += [stack, hd]
+    try:
+        s = torch.cuda.current_stream().cuda_stream
+        dH = torch.from_numpy(H0).cuda()
+        tok0 = torch.zeros(1, dtype=torch.int32, device="cuda")
+        stack.prefill_dev(dH.data_ptr(), H0.shape[0], tok0.data_ptr(), s)
+        ref = torch.from_numpy(H0).cuda()
+        for B in blocks:
+            B.forward_dev(ref.data_ptr(), H0.shape[0], stream=s)
+        torch.cuda.synchronize()
+        assert torch.equal(dH.view(torch.int32), ref.view(torch.int32))
+        n = 8
+        runs = []
+        for graph in (False, True, True, False, True):
+            toks = torch.zeros(n + 1, dtype=torch.int32, device="cuda")
+            toks[0] = tok0[0]
+            lg = torch.zeros(V, dtype=torch.float32, device="cuda")
+            stack.decode_dev(toks.data_ptr(), n, lg.data_ptr(), graph=graph, stream=s)
+            torch.cuda.synchronize()
+            runs.append((graph, toks.cpu().numpy(), lg.cpu().numpy()))
+            junk = torch.randn(1024, device="cuda") * 2          # eager work between replays
+            assert float(junk.abs().sum()) > 0
+        say("stack decode tokens", runs[0][1].tolist())
+        for graph, t, l in runs[1:]:
+            assert np.array_equal(t, runs[0][1]), (graph, t, runs[0][1])
+            assert np.array_equal(l.view(np.uint32), runs[0][2].view(np.uint32))
+        # prefill's greedy token is the head of the last prefill row
+        wl, wam = Z.oracle_head(st.table, V, D, st.fnorm, st.layers[0].eps, st.softcap,
+                                dH[-1:].cpu().numpy())
+        top2 = np.sort(wl[0])[-2:]
+        if top2[1] - top2[0] > LOGIT_TOL:
+            assert int(tok0.item()) == wam[0]
+    finally:
+        close_all(*objs)

@@ -30,7 +30,8 @@ ABI_SYMBOLS = (
     "zz_last_error",
     "zz_ffn_block_create", "zz_ffn_block_destroy", "zz_ffn_block_forward_dev",
     "zz_ffn_block_forward", "zz_head_create", "zz_head_destroy", "zz_head_embed_dev",
-    "zz_head_embed", "zz_head_logits_dev", "zz_head_logits",
+    "zz_head_embed", "zz_head_logits_dev", "zz_head_logits", "zz_stack_create",
+    "zz_stack_destroy", "zz_stack_prefill_dev", "zz_stack_decode_dev",
 )
 KERNELS = ("prep", "logits", "topk", "dispatch", "ffn_up", "ffn_down", "combine", "dec_route",
            "dec_down")
@@ -113,6 +114,10 @@ def lib():
     L.zz_head_logits_dev.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p,
                                      C.c_void_p]
     L.zz_head_logits.argtypes = [C.c_int, _f32p, C.c_int, _f32p, _i32p]
+    L.zz_stack_create.argtypes = [_i32p, C.c_int, C.c_int]
+    L.zz_stack_destroy.argtypes = [C.c_int]
+    L.zz_stack_prefill_dev.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
+    L.zz_stack_decode_dev.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p]
     _lib = L
     return L
 
@@ -335,4 +340,30 @@ class Head:
     def close(self):
         if self.id >= 0:
             lib().zz_head_destroy(self.id)
+            self.id = -1
+
+
+class Stack:
+    """FFN blocks under a tied head (zz_stack_create): prefill and greedy decode with
+    token ids kept on the device."""
+
+    def __init__(self, blocks, head):
+        ids = np.array([b.id for b in blocks], np.int32)
+        self.id = lib().zz_stack_create(_p(ids, _i32p), len(ids), head.id)
+        if self.id < 0:
+            raise RuntimeError(f"zz_stack_create declined: {last_error()}")
+
+    def prefill_dev(self, d_H, S, d_tok=0, stream=0):
+        if not lib().zz_stack_prefill_dev(self.id, C.c_void_p(d_H), S, C.c_void_p(d_tok or None),
+                                          C.c_void_p(stream or None)):
+            raise RuntimeError(f"zz_stack_prefill_dev declined: {last_error()}")
+
+    def decode_dev(self, d_tok, n, d_logits=0, graph=False, stream=0):
+        if not lib().zz_stack_decode_dev(self.id, C.c_void_p(d_tok), n, C.c_void_p(d_logits or None),
+                                         1 if graph else 0, C.c_void_p(stream or None)):
+            raise RuntimeError(f"zz_stack_decode_dev declined: {last_error()}")
+
+    def close(self):
+        if self.id >= 0:
+            lib().zz_stack_destroy(self.id)
             self.id = -1

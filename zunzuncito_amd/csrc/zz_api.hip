@@ -429,6 +429,13 @@ struct ProfScope {             // brackets one kernel launch with two events
     }
 };
 
+// internal: event timing off while a HIP graph is captured; returns the old state
+int zz_lib_prof_set(int on) {
+    const int was = g_prof;
+    g_prof = on;
+    return was;
+}
+
 extern "C" int zz_moe_profile(int on) {
     if (!g_ready) ZZ_FAIL("zz_moe_profile: not ready");
     (void)hipDeviceSynchronize();

@@ -446,8 +446,136 @@ extern "C" int zz_head_logits(int id, const float *H, int S, float *logits, int 
     return 1;
 }
 
+// ------------------------------------------------------------------ stacks
+struct Stack {
+    std::vector<int> blocks;
+    int head, D, V;
+    float *h = nullptr;             // [D] the decode row
+    float *logits = nullptr;        // [V]
+    int *cur = nullptr;             // the current token
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;  // one decode step, captured on first use
+};
+static std::vector<Stack *> g_stacks;
+
+static void free_stack(Stack *k) {
+    if (!k) return;
+    if (k->exec) (void)hipGraphExecDestroy(k->exec);
+    if (k->graph) (void)hipGraphDestroy(k->graph);
+    void *ps[] = {k->h, k->logits, k->cur};
+    for (void *p : ps)
+        if (p) (void)hipFree(p);
+    delete k;
+}
+
+static Stack *get_stack(int id) {
+    if (!zz_lib_ready() || id < 0 || id >= (int)g_stacks.size()) return nullptr;
+    return g_stacks[id];
+}
+
+extern "C" int zz_stack_create(const int *blocks, int n, int head) {
+    Head *h = get_head(head);
+    if (!blocks || n <= 0 || !h) {
+        zz_set_error("zz_stack_create: bad arguments");
+        return -1;
+    }
+    for (int i = 0; i < n; i++) {
+        FfnBlock *B = get_block(blocks[i]);
+        if (!B || B->D != h->D) {
+            zz_set_error("zz_stack_create: block %d is missing or not of the head's D", blocks[i]);
+            return -1;
+        }
+    }
+    Stack *k = new Stack();
+    k->blocks.assign(blocks, blocks + n);
+    k->head = head;
+    k->D = h->D;
+    k->V = h->V;
+    if (hipMalloc(&k->h, sizeof(float) * h->D) != hipSuccess ||
+        hipMalloc(&k->logits, sizeof(float) * h->V) != hipSuccess || hipMalloc(&k->cur, sizeof(int)) != hipSuccess) {
+        zz_set_error("zz_stack_create: device allocation failed");
+        free_stack(k);
+        return -1;
+    }
+    for (size_t i = 0; i < g_stacks.size(); i++)
+        if (!g_stacks[i]) { g_stacks[i] = k; return (int)i; }
+    g_stacks.push_back(k);
+    return (int)g_stacks.size() - 1;
+}
+
+extern "C" void zz_stack_destroy(int id) {
+    Stack *k = get_stack(id);
+    if (!k) return;
+    (void)hipDeviceSynchronize();
+    free_stack(k);
+    g_stacks[id] = nullptr;
+}
+
+static int stack_blocks(Stack *k, float *d_H, int S, hipStream_t st) {
+    for (int b : k->blocks) {
+        FfnBlock *B = get_block(b);
+        if (!B) ZZ_FAIL("zz_stack: block %d is gone", b);
+        if (!block_forward(B, d_H, S, nullptr, nullptr, st)) return 0;
+    }
+    return 1;
+}
+
+extern "C" int zz_stack_prefill_dev(int id, float *d_H, int S, int *d_tok, void *stream) {
+    Stack *k = get_stack(id);
+    if (!k || !d_H || S <= 0) ZZ_FAIL("zz_stack_prefill_dev: bad arguments");
+    hipStream_t st = stream ? (hipStream_t)stream : zz_lib_stream();
+    if (!stack_blocks(k, d_H, S, st)) return 0;
+    if (d_tok && !zz_head_logits_dev(k->head, d_H + (size_t)(S - 1) * k->D, 1, k->logits, d_tok, st)) return 0;
+    return 1;
+}
+
+// one decode step: cur -> embed -> blocks -> head -> cur
+static int stack_step(Stack *k, hipStream_t st) {
+    return zz_head_embed_dev(k->head, k->cur, 1, k->h, st) && stack_blocks(k, k->h, 1, st) &&
+           zz_head_logits_dev(k->head, k->h, 1, k->logits, k->cur, st);
+}
+
+extern "C" int zz_stack_decode_dev(int id, int *d_tok, int n, float *d_logits, int use_graph, void *stream) {
+    Stack *k = get_stack(id);
+    if (!k || !d_tok || n < 0) ZZ_FAIL("zz_stack_decode_dev: bad arguments");
+    hipStream_t st = stream ? (hipStream_t)stream : zz_lib_stream();
+    ZZ_CHECK(hipMemcpyAsync(k->cur, d_tok, sizeof(int), hipMemcpyDeviceToDevice, st));
+    for (int i = 0; i < n; i++) {
+        if (use_graph && i > 0 && !k->exec) {
+            // step 0 ran eagerly, so every workspace already holds one row: the
+            // captured step allocates nothing and waits on nothing
+            const int prof = zz_lib_prof_set(0);           // no timing events in the graph
+            const hipError_t b = hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed);
+            const int ok = b == hipSuccess && stack_step(k, st);
+            hipGraph_t g = nullptr;
+            const hipError_t e = b == hipSuccess ? hipStreamEndCapture(st, &g) : b;
+            zz_lib_prof_set(prof);
+            if (!ok || e != hipSuccess) {
+                if (g) (void)hipGraphDestroy(g);
+                ZZ_FAIL("zz_stack_decode_dev: capture failed (%s)", hipGetErrorString(e));
+            }
+            k->graph = g;
+            if (hipGraphInstantiate(&k->exec, g, nullptr, nullptr, 0) != hipSuccess) {
+                k->exec = nullptr;
+                ZZ_FAIL("zz_stack_decode_dev: graph instantiation failed");
+            }
+        }
+        if (use_graph && k->exec) {
+            ZZ_CHECK(hipGraphLaunch(k->exec, st));
+        } else if (!stack_step(k, st)) {
+            return 0;
+        }
+        ZZ_CHECK(hipMemcpyAsync(d_tok + i + 1, k->cur, sizeof(int), hipMemcpyDeviceToDevice, st));
+    }
+    if (d_logits && n > 0)
+        ZZ_CHECK(hipMemcpyAsync(d_logits, k->logits, sizeof(float) * k->V, hipMemcpyDeviceToDevice, st));
+    return 1;
+}
+
 // released by gpu_shutdown (zz_api.hip)
 void zz_gemma_shutdown() {
+    for (Stack *&k : g_stacks) { free_stack(k); k = nullptr; }
+    g_stacks.clear();
     for (FfnBlock *&B : g_blocks) { free_block(B); B = nullptr; }
     g_blocks.clear();
     for (Head *&h : g_heads) { free_head(h); h = nullptr; }

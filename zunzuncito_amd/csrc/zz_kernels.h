@@ -126,6 +126,7 @@ hipStream_t zz_lib_stream();
 int zz_lib_ready();
 unsigned *zz_lib_diag();
 const zz_moe_desc *zz_layer_desc(int id);
+int zz_lib_prof_set(int on);        // per-kernel event timing on/off; returns the old state
 // tensor in the slot-table layout at *cursor (advanced past it, 256-aligned)
 ZzTensor zz_make_tensor(int fmt, int O, int I, int64_t *cursor);
 
