@@ -75,6 +75,18 @@ int zz_stack_prefill_dev(int stack, float *d_H, int S, int *d_tok, void *stream)
 int zz_stack_decode_dev(int stack, int *d_tok, int n, float *d_logits, int use_graph,
                         void *stream);
 
+/* A gemma4 container directory (convert_gemma4.py: manifest.txt, dense.bin,
+ * experts.bin) made resident as a stack (gemma4.c:260-403 reads the same files):
+ * per layer the MoE layer (router_proj, router_scale, router_pes,
+ * pre/post_feedforward_layernorm_2 and the layer's experts), the dense branch
+ * (mlp_gate, mlp_up, mlp_down, pre_feedforward_layernorm,
+ * post_feedforward_layernorm_1) and the block (post_feedforward_layernorm,
+ * layer_scalar); the head from embed_tokens, norm, cfg embed_scale and
+ * final_logit_softcap. Attention weights are not read. Returns a stack id >= 0 that
+ * owns all of these (zz_stack_destroy frees them), or -1; *n_layers, *D, *V (each
+ * may be NULL) receive the model's shape. */
+int zz_gemma_stack_load(const char *dir, int *n_layers, int *D, int *V);
+
 #ifdef __cplusplus
 }
 #endif

@@ -83,6 +83,17 @@ int zz_moe_expert_upload(int layer, int eid, const uint8_t *rec, size_t n);
 /* Same from a device buffer (already in HBM). */
 int zz_moe_expert_upload_dev(int layer, int eid, const void *d_rec, size_t n);
 
+/* Fill every slot of `layer` from layer `li` of a zunzuncito container directory
+ * (convert_*.py output). dir/manifest.txt gives the record size -- gemma/maple
+ * `esz esz gate_b down_b` (gemma4.c:310-312), lfm `eszl li esz gate_b down_b fmt`
+ * (lfm25.c:328-330) -- and each record's offset, `expert li e off`
+ * (gemma4.c:326-329). The 4096-aligned [gate | up | down] records of
+ * dir/experts.bin (convert_gemma4.py:361-390) are read once and uploaded; the
+ * reference's slot/LRU tier and its I/O threads (gemma4.c:487-540) have no
+ * counterpart, every expert stays resident. Declines on a record size that is not
+ * the layer's zz_moe_record_bytes, a missing expert line or a short read. */
+int zz_moe_load_experts(int layer, const char *dir, int li);
+
 /* moe_start + moe_finish for S rows. in: gemma the residual [S, D], lfm/maple the
  * normed hidden X [S, D]. out [S, D]. eidx/ewt [S*K] (may be NULL) receive the
  * routing in route_row's order. Host pointers; synchronous. */

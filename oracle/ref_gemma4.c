@@ -219,6 +219,30 @@ int ref_g4_head(const uint8_t *table, int V, int D, const float *fnorm, float ep
     return tok;
 }
 
+/* The engine's own container reader, manifest() (gemma4.c:260-403), on a directory:
+ * the record size, every expert offset (n_layers * n_experts), layer 0's router,
+ * each layer's layer_scalar, the final norm, embed_tokens row 0, and the bytes of
+ * expert (li, e) read at the engine's offset. Returns n_layers, or -1. */
+int ref_g4_manifest_probe(const char *dir, int64_t *esz3, int64_t *eoff, float *router0,
+                          float *scalars, float *fnorm, uint8_t *embed_row0, int li, int e,
+                          uint8_t *rec) {
+    M *m = zz_calloc(sizeof(M));
+    manifest(m, dir);
+    Cfg *c = &m->c;
+    esz3[0] = m->esz; esz3[1] = m->gate_b; esz3[2] = m->down_b;
+    memcpy(eoff, m->eoff, sizeof(int64_t) * (size_t)c->n_layers * c->n_experts);
+    memcpy(router0, m->L[0].router_proj.f, sizeof(float) * (size_t)c->n_experts * c->hidden);
+    for (int l = 0; l < c->n_layers; l++) scalars[l] = m->L[l].layer_scalar.f[0];
+    memcpy(fnorm, m->L[MAXL - 1].o_proj.f, sizeof(float) * (size_t)c->hidden);
+    memcpy(embed_row0, m->L[MAXL - 1].q_proj.q, q40_row_bytes(c->hidden));
+    int64_t off = m->eoff[(int64_t)li * c->n_experts + e], esz = m->esz;
+    ssize_t r = pread(m->efd, rec, (size_t)esz, off);
+    int nl = c->n_layers;
+    close(m->efd);
+    free(m->eoff); free(m->dense); free(m);
+    return r == (ssize_t)esz ? nl : -1;
+}
+
 void ref_g4_set_threads(int n) {
 #ifdef _OPENMP
     if (n > 0) omp_set_num_threads(n);

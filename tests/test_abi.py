@@ -94,6 +94,8 @@ def test_decline_contract_without_device():
     ids = np.zeros(2, np.int32)
     assert L.zz_stack_create(ids.ctypes.data_as(zz._i32p), 2, 0) == -1
     assert L.zz_stack_decode_dev(0, None, 4, None, 1, None) == 0
+    assert L.zz_moe_load_experts(0, b"/nonexistent", 0) == 0
+    assert L.zz_gemma_stack_load(b"/nonexistent", None, None, None) == -1
     L.gpu_shutdown()                             # safe when never initialised
 
 

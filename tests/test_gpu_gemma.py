@@ -283,3 +283,45 @@ def test_stack_runner_graph_equals_eager(dev):
             assert int(tok0.item()) == wam[0]
     finally:
         close_all(*objs)
+
+
+def test_container_load(dev, tmp_path):
+    """zz_gemma_stack_load / zz_moe_load_experts on a container directory written in
+    the converter's layout: the loaded stack decodes exactly as the stack built from
+    the same weights in memory, and its prefill matches the reference fixture."""
+    import torch
+    g = np.load(Z.os.path.join(Z.ROOT, "tests", "golden", "gemma_block_stack.npz"))
+    *_, st, H0 = Z.gemma_block_case()
+    Z.write_gemma_container(str(tmp_path), st)
+    loaded = zz.Stack.load(str(tmp_path))
+    objs = [loaded]
+    try:
+        assert (loaded.n_layers, loaded.D, loaded.V) == (len(st.layers), st.layers[0].D, st.V)
+        s = torch.cuda.current_stream().cuda_stream
+        dH = torch.from_numpy(H0).cuda()
+        tok = torch.zeros(Z.GEMMA_STACK["steps"] + 1, dtype=torch.int32, device="cuda")
+        loaded.prefill_dev(dH.data_ptr(), H0.shape[0], tok.data_ptr(), s)
+        loaded.decode_dev(tok.data_ptr(), Z.GEMMA_STACK["steps"], graph=True, stream=s)
+        torch.cuda.synchronize()
+        err = Z.rel_l2(dH.cpu().numpy(), g["stack_prefill"])
+        say(f"loaded stack prefill vs reference fixture: rel L2 {err:.2e}, tokens {tok.cpu().tolist()}")
+        assert err < 2 * OUT_TOL
+        assert np.array_equal(tok.cpu().numpy(), g["stack_tokens"])
+        # one layer's experts through zz_moe_load_experts into a fresh layer
+        L1 = st.layers[1]
+        m = zz.MoeLayer(L1.D, L1.MI, L1.E, L1.K, L1.gating, L1.act, L1.fmts, L1.router,
+                        L1.router_scale, L1.pes, None, L1.pre_ln, L1.post_ln, eps=L1.eps)
+        objs.append(m)
+        m.load_experts(str(tmp_path), 1)
+        x = Z.make_input(L1, 5, 77)
+        out, eidx, _ = m.forward(x)
+        want = Z.oracle_moe(L1, x)
+        assert np.array_equal(eidx, want.eidx) and Z.rel_l2(out, want.out) < OUT_TOL
+        # a record size that is not the layer's declines with the reason
+        bad = zz.MoeLayer(L1.D, L1.MI * 2, L1.E, L1.K, L1.gating, L1.act, L1.fmts, L1.router,
+                          L1.router_scale, L1.pes, None, L1.pre_ln, L1.post_ln, eps=L1.eps)
+        objs.append(bad)
+        with pytest.raises(RuntimeError, match="record"):
+            bad.load_experts(str(tmp_path), 1)
+    finally:
+        close_all(*objs)

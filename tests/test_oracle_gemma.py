@@ -150,3 +150,39 @@ def test_block_tolerance_is_discriminating():
     assert Z.rel_l2(Z.oracle_block(L, bad, H)[0], good) > 1e-2
     bad2 = Z.Dense(dn.D, dn.DI, dn.mlp, dn.pre_ffn_ln, dn.post_ffn_ln1, dn.post_ffn_ln, 1.0)
     assert Z.rel_l2(Z.oracle_block(L, bad2, H)[0], good) > 1e-2
+
+
+def test_container_writer_read_by_the_engine(tmp_path):
+    """The test-side container writer (zzref.write_gemma_container) produces what the
+    engine's own reader, manifest() (gemma4.c:260-403), parses back: record size,
+    every expert offset, the dense tensors by name, and the expert bytes at the
+    engine's offsets. The GPU loader is then tested against the same directories."""
+    lib = Z.ref_lib("gemma4")
+    if lib is None:
+        pytest.skip("oracle/_ref not built here")
+    *_, st, H0 = Z.gemma_block_case()
+    eoff = Z.write_gemma_container(str(tmp_path), st)
+    L0, NL = st.layers[0], len(st.layers)
+    D, E = L0.D, L0.E
+    lib.ref_g4_manifest_probe.argtypes = [C.c_char_p, C.POINTER(C.c_int64), C.POINTER(C.c_int64),
+                                          Z.f32p, Z.f32p, Z.f32p, Z.u8p, C.c_int, C.c_int, Z.u8p]
+    esz3 = np.zeros(3, np.int64)
+    eo = np.zeros(NL * E, np.int64)
+    r0 = np.zeros((E, D), np.float32)
+    sc = np.zeros(NL, np.float32)
+    fn = np.zeros(D, np.float32)
+    row0 = np.zeros(D // 32 * 18, np.uint8)
+    rec = np.zeros(L0.esz, np.uint8)
+    li, e = NL - 1, E - 3
+    nl = lib.ref_g4_manifest_probe(str(tmp_path).encode(), esz3.ctypes.data_as(C.POINTER(C.c_int64)),
+                                   eo.ctypes.data_as(C.POINTER(C.c_int64)), Z.ptr(r0), Z.ptr(sc),
+                                   Z.ptr(fn), Z.ptr(row0), li, e, Z.ptr(rec))
+    assert nl == NL
+    assert esz3.tolist() == [L0.esz, Z.tensor_bytes(1, L0.MI, D), Z.tensor_bytes(1, D, L0.MI)]
+    assert eo.tolist() == [eoff[(l, x)] for l in range(NL) for x in range(E)]
+    assert all(o % 4096 == 0 for o in eo)
+    assert np.array_equal(r0, st.layers[0].router)
+    assert np.array_equal(sc, np.array([d.layer_scalar for d in st.denses], np.float32))
+    assert np.array_equal(fn, st.fnorm)
+    assert np.array_equal(row0, st.table[:row0.size])
+    assert np.array_equal(rec, st.layers[li].experts[e * L0.esz:(e + 1) * L0.esz])

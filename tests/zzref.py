@@ -551,3 +551,89 @@ def gemma_digest(L, dn, H, table, fnorm, st, H0):
         h.update(_input_digest(l_, H0).encode())
         h.update(np.ascontiguousarray(d_.mlp).tobytes())
     return h.hexdigest()
+
+
+# ------------------------------------------------ zunzuncito container directories
+def write_gemma_container(path, st, head_dim=64, n_heads=2):
+    """Write stack `st` as a gemma4 container directory in the layout that
+    tools/convert_gemma4.py writes and gemma4.c:260-403 reads: manifest.txt (cfg
+    lines, `esz`, the dense index, `expert li e off`), dense.bin (tensors back to
+    back: q4_0 matrices, f32 vectors, shapes [O, I] with I = 1 for vectors) and
+    experts.bin ([gate | up | down] records at 4096-aligned offsets). Attention
+    tensors are small seeded placeholders: the engine's reader binds them, the GPU
+    loader skips them. Returns the per-(layer, expert) offsets."""
+    os.makedirs(path, exist_ok=True)
+    L0 = st.layers[0]
+    D, MI, E, K, NL = L0.D, L0.MI, L0.E, L0.K, len(st.layers)
+    DI = st.denses[0].DI
+    rng = np.random.default_rng(4242)
+    dense, off = [], 0
+    blob = open(os.path.join(path, "dense.bin"), "wb")
+
+    def add(name, arr, fmt, O, I):
+        nonlocal off
+        b = np.ascontiguousarray(arr).tobytes()
+        blob.write(b)
+        dense.append((name, off, len(b), fmt, O, I))
+        off += len(b)
+
+    def q40(O, I):
+        return make_expert_q(rng, FMT_Q40, O, I)
+
+    add("embed_tokens", st.table, 1, st.V, D)
+    add("norm", st.fnorm, 0, D, 1)
+    for l, (L_, dn) in enumerate(zip(st.layers, st.denses)):
+        o = f"layers.{l}."
+        ones = np.ones(D, np.float32)
+        for nm, v in (("input_layernorm", ones), ("post_attention_layernorm", ones),
+                      ("pre_feedforward_layernorm", dn.pre_ffn_ln),
+                      ("post_feedforward_layernorm", dn.post_ffn_ln),
+                      ("pre_feedforward_layernorm_2", L_.pre_ln),
+                      ("post_feedforward_layernorm_1", dn.post_ffn_ln1),
+                      ("post_feedforward_layernorm_2", L_.post_ln)):
+            add(o + nm, v, 0, D, 1)
+        add(o + "layer_scalar", np.array([dn.layer_scalar], np.float32), 0, 1, 1)
+        hd = head_dim
+        add(o + "q_proj", q40(n_heads * hd, D), 1, n_heads * hd, D)
+        add(o + "k_proj", q40(hd, D), 1, hd, D)
+        add(o + "v_proj", q40(hd, D), 1, hd, D)
+        add(o + "o_proj", q40(D, n_heads * hd), 1, D, n_heads * hd)
+        add(o + "q_norm", np.ones(hd, np.float32), 0, hd, 1)
+        add(o + "k_norm", np.ones(hd, np.float32), 0, hd, 1)
+        gb = tensor_bytes(FMT_Q40, DI, D)
+        add(o + "mlp_gate", dn.mlp[:gb], 1, DI, D)
+        add(o + "mlp_up", dn.mlp[gb:2 * gb], 1, DI, D)
+        add(o + "mlp_down", dn.mlp[2 * gb:], 1, D, DI)
+        add(o + "router_proj", L_.router, 0, E, D)
+        add(o + "router_scale", L_.router_scale, 0, D, 1)
+        add(o + "router_pes", L_.pes, 0, E, 1)
+    blob.close()
+    esz, gb, db = L0.esz, tensor_bytes(FMT_Q40, MI, D), tensor_bytes(FMT_Q40, D, MI)
+    eoff, off = {}, 0
+    with open(os.path.join(path, "experts.bin"), "wb") as f:
+        for l, L_ in enumerate(st.layers):
+            for e in range(E):
+                pad = (-off) % 4096
+                f.write(b"\0" * pad)
+                off += pad
+                f.write(L_.experts[e * esz:(e + 1) * esz].tobytes())
+                eoff[(l, e)] = off
+                off += esz
+    cfg = dict(hidden=D, n_layers=NL, n_heads=n_heads, head_dim=head_dim, global_head_dim=head_dim,
+               n_kv_heads=1, n_global_kv_heads=1, k_eq_v_global=False, n_experts=E, topk=K,
+               moe_inter=MI, dense_inter=DI, vocab=st.V, eps=L0.eps, sliding_window=128,
+               rope_theta_local=10000.0, rope_theta_global=1000000.0, rope_partial_global=1.0,
+               final_logit_softcap=st.softcap, embed_scale=st.embed_scale, ctx=256,
+               slots_per_layer=E)
+    with open(os.path.join(path, "manifest.txt"), "w") as m:
+        for k, v in cfg.items():
+            m.write(f"cfg {k} {v}\n")
+        m.write("cfg layer_types " + " ".join("0" for _ in range(NL)) + "\n")
+        m.write(f"esz {esz} {gb} {db}\n")
+        m.write(f"ndense {len(dense)}\n")
+        for name, o_, ln, fmt, O, I in dense:
+            m.write(f"dense {name} {o_} {ln} {fmt} {O} {I}\n")
+        m.write(f"nexpert {len(eoff)}\n")
+        for (l, e), o_ in eoff.items():
+            m.write(f"expert {l} {e} {o_}\n")
+    return eoff

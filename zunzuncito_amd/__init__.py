@@ -31,7 +31,8 @@ ABI_SYMBOLS = (
     "zz_ffn_block_create", "zz_ffn_block_destroy", "zz_ffn_block_forward_dev",
     "zz_ffn_block_forward", "zz_head_create", "zz_head_destroy", "zz_head_embed_dev",
     "zz_head_embed", "zz_head_logits_dev", "zz_head_logits", "zz_stack_create",
-    "zz_stack_destroy", "zz_stack_prefill_dev", "zz_stack_decode_dev",
+    "zz_stack_destroy", "zz_stack_prefill_dev", "zz_stack_decode_dev", "zz_moe_load_experts",
+    "zz_gemma_stack_load",
 )
 KERNELS = ("prep", "logits", "topk", "dispatch", "ffn_up", "ffn_down", "combine", "dec_route",
            "dec_down")
@@ -118,6 +119,8 @@ def lib():
     L.zz_stack_destroy.argtypes = [C.c_int]
     L.zz_stack_prefill_dev.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
     L.zz_stack_decode_dev.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p]
+    L.zz_moe_load_experts.argtypes = [C.c_int, C.c_char_p, C.c_int]
+    L.zz_gemma_stack_load.argtypes = [C.c_char_p, _i32p, _i32p, _i32p]
     _lib = L
     return L
 
@@ -194,6 +197,11 @@ class MoeLayer:
     def upload_all(self, experts):
         for e in range(self.E):
             self.upload(e, experts[e * self.record_bytes:(e + 1) * self.record_bytes])
+
+    def load_experts(self, path, li):
+        """Layer li's records from a container's experts.bin (zz_moe_load_experts)."""
+        if not lib().zz_moe_load_experts(self.id, os.fsencode(path), li):
+            raise RuntimeError(f"zz_moe_load_experts declined: {last_error()}")
 
     def upload_dev(self, eid, dev_ptr, nbytes):
         if not lib().zz_moe_expert_upload_dev(self.id, eid, C.c_void_p(dev_ptr), nbytes):
@@ -352,6 +360,17 @@ class Stack:
         self.id = lib().zz_stack_create(_p(ids, _i32p), len(ids), head.id)
         if self.id < 0:
             raise RuntimeError(f"zz_stack_create declined: {last_error()}")
+
+    @classmethod
+    def load(cls, path):
+        """A gemma4 container directory made resident (zz_gemma_stack_load)."""
+        self = cls.__new__(cls)
+        nl, D, V = (C.c_int(), C.c_int(), C.c_int())
+        self.id = lib().zz_gemma_stack_load(os.fsencode(path), C.byref(nl), C.byref(D), C.byref(V))
+        if self.id < 0:
+            raise RuntimeError(f"zz_gemma_stack_load declined: {last_error()}")
+        self.n_layers, self.D, self.V = nl.value, D.value, V.value
+        return self
 
     def prefill_dev(self, d_H, S, d_tok=0, stream=0):
         if not lib().zz_stack_prefill_dev(self.id, C.c_void_p(d_H), S, C.c_void_p(d_tok or None),

@@ -455,11 +455,20 @@ struct Stack {
     int *cur = nullptr;             // the current token
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;  // one decode step, captured on first use
+    // what a container load created for this stack, destroyed with it
+    std::vector<int> own_layers, own_blocks;
+    int own_head = -1;
 };
 static std::vector<Stack *> g_stacks;
 
-static void free_stack(Stack *k) {
+// owned: also destroy what the stack owns (not at shutdown, which frees everything)
+static void free_stack(Stack *k, bool owned = false) {
     if (!k) return;
+    if (owned) {
+        for (int b : k->own_blocks) zz_ffn_block_destroy(b);
+        for (int l : k->own_layers) zz_moe_layer_destroy(l);
+        if (k->own_head >= 0) zz_head_destroy(k->own_head);
+    }
     if (k->exec) (void)hipGraphExecDestroy(k->exec);
     if (k->graph) (void)hipGraphDestroy(k->graph);
     void *ps[] = {k->h, k->logits, k->cur};
@@ -507,8 +516,17 @@ extern "C" void zz_stack_destroy(int id) {
     Stack *k = get_stack(id);
     if (!k) return;
     (void)hipDeviceSynchronize();
-    free_stack(k);
     g_stacks[id] = nullptr;
+    free_stack(k, true);
+}
+
+int zz_stack_adopt(int id, const std::vector<int> &layers, const std::vector<int> &blocks, int head) {
+    Stack *k = get_stack(id);
+    if (!k) return 0;
+    k->own_layers = layers;
+    k->own_blocks = blocks;
+    k->own_head = head;
+    return 1;
 }
 
 static int stack_blocks(Stack *k, float *d_H, int S, hipStream_t st) {
