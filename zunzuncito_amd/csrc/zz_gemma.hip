@@ -80,30 +80,34 @@ __device__ __forceinline__ unsigned zz_ord_bits(float f) {       // order-preser
 }
 
 // lm_head GEMV: one wave per 16-row group of the table over the whole K range, lane
-// l = 16qq + r as in the slot table; HD_C chunks' loads are issued together. The
-// q8_0 rows of xn (S <= 4) are staged in LDS. Then the softcap, the logits, and the
-// row's (logit, -index) key into amax[s] by a 64-bit atomic max: the first index of
-// the largest logit wins, whatever the order the workgroups finish in.
+// l = 16qq + r as in the slot table. Weight chunks come in batches of HD_C, the next
+// batch requested before the current one is used. The q8_0 rows of xn (S <= 4) are
+// staged in LDS (S*D codes then S*D/32 scales, dynamic). Then the softcap, the
+// logits, and the workgroup's best (logit, -index) key per row into part[s][wg]: the
+// finish kernel picks the largest key, so the first index of the largest logit wins
+// whatever the order the workgroups run in.
 #define HD_C 8
 __global__ __launch_bounds__(256) void zz_head_kernel(const uint8_t *tb, ZzTensor T, const int8_t *xq,
                                                       const float *xs, int S, float cap, float *logits,
-                                                      unsigned long long *amax) {
-    __shared__ __attribute__((aligned(16))) int8_t sx_q[ZZ_DEC_MAXS][ZZ_MAXD];
-    __shared__ float sx_s[ZZ_DEC_MAXS][ZZ_MAXD / ZZ_BLK];
+                                                      unsigned long long *part) {
+    extern __shared__ __attribute__((aligned(16))) char hd_lds[];
+    __shared__ unsigned long long wkey[4][ZZ_DEC_MAXS];
     const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, r = l & 15, qq = l >> 4;
     const int D = T.I, nb = D / ZZ_BLK, nch = (nb + 3) / 4, V = T.O, g = 4 * blockIdx.x + w;
-    for (int i = tid; i < S * (D / 16); i += 256) {
-        const int s = i / (D / 16), k = i - s * (D / 16);
-        *(uint4 *)&sx_q[s][16 * k] = ld16(xq + (size_t)s * D + 16 * k);
-    }
-    for (int i = tid; i < S * nb; i += 256) sx_s[i / nb][i % nb] = xs[i];
+    int8_t *sq = (int8_t *)hd_lds;                          // [S][D]
+    float *ss = (float *)(hd_lds + (size_t)S * D);          // [S][nb]
     const ZzWalk W = zz_walk(T, g, l, r);
-    float acc[ZZ_DEC_MAXS] = {0.0f, 0.0f, 0.0f, 0.0f};
-    ZzChunk k[HD_C];
+    ZzChunk k[HD_C], kn[HD_C];
 #pragma unroll
     for (int i = 0; i < HD_C; i++) k[i] = zz_load_chunk<ZZ_FMT_Q40>(tb, W, min(i, nch - 1));
+    for (int i = tid; i < S * (D / 16); i += 256) *(uint4 *)(sq + 16 * i) = ld16(xq + 16 * (size_t)i);
+    for (int i = tid; i < S * nb; i += 256) ss[i] = xs[i];
     __syncthreads();
+    float acc[ZZ_DEC_MAXS] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int c0 = 0; c0 < nch; c0 += HD_C) {
+        if (c0 + HD_C < nch)
+#pragma unroll
+            for (int i = 0; i < HD_C; i++) kn[i] = zz_load_chunk<ZZ_FMT_Q40>(tb, W, min(c0 + HD_C + i, nch - 1));
 #pragma unroll
         for (int i = 0; i < HD_C; i++) {
             const int c = c0 + i;
@@ -118,16 +122,15 @@ __global__ __launch_bounds__(256) void zz_head_kernel(const uint8_t *tb, ZzTenso
 #pragma unroll
                 for (int s = 0; s < ZZ_DEC_MAXS; s++) {
                     if (s >= S) break;
-                    const uint2 xv = *(const uint2 *)&sx_q[s][b * ZZ_BLK + 8 * qq];
+                    const uint2 xv = *(const uint2 *)(sq + (size_t)s * D + b * ZZ_BLK + 8 * qq);
                     int d = zz_dot4(wv.x, xv.x, 0);
                     d = zz_dot4(wv.y, xv.y, d);
-                    acc[s] = fmaf(dw * sx_s[s][b], (float)d, acc[s]);
+                    acc[s] = fmaf(dw * ss[s * nb + b], (float)d, acc[s]);
                 }
             }
         }
-        if (c0 + HD_C < nch)
 #pragma unroll
-            for (int i = 0; i < HD_C; i++) k[i] = zz_load_chunk<ZZ_FMT_Q40>(tb, W, min(c0 + HD_C + i, nch - 1));
+        for (int i = 0; i < HD_C; i++) k[i] = kn[i];
     }
     const int o = 16 * g + r;
 #pragma unroll
@@ -145,17 +148,36 @@ __global__ __launch_bounds__(256) void zz_head_kernel(const uint8_t *tb, ZzTenso
             const unsigned long long k2 = __shfl_xor(key, m, 64);
             key = k2 > key ? k2 : key;
         }
-        if (l == 0) atomicMax(amax + s, key);
+        if (l == 0) wkey[w][s] = key;
+    }
+    __syncthreads();
+    if (tid < S) {
+        unsigned long long key = wkey[0][tid];
+        for (int q = 1; q < 4; q++) key = wkey[q][tid] > key ? wkey[q][tid] : key;
+        part[(size_t)tid * gridDim.x + blockIdx.x] = key;
     }
 }
 
-// argmax[s] from the keys, which are cleared for the next call
-__global__ void zz_head_argmax_kernel(unsigned long long *amax, int *argmax, int S) {
-    const int s = threadIdx.x;
-    if (s < S) {
-        const unsigned long long k = amax[s];
-        if (argmax) argmax[s] = (int)(0xffffffffu - (unsigned)(k & 0xffffffffu));
-        amax[s] = 0ull;
+// argmax[s] = the index of the largest of the n partial keys of row s
+__global__ __launch_bounds__(256) void zz_head_argmax_kernel(const unsigned long long *part, int n, int *argmax) {
+    __shared__ unsigned long long red[4];
+    const int s = blockIdx.x, tid = threadIdx.x;
+    unsigned long long key = 0ull;
+    for (int i = tid; i < n; i += 256) {
+        const unsigned long long k = part[(size_t)s * n + i];
+        key = k > key ? k : key;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const unsigned long long k2 = __shfl_xor(key, m, 64);
+        key = k2 > key ? k2 : key;
+    }
+    if ((tid & 63) == 0) red[tid >> 6] = key;
+    __syncthreads();
+    if (tid == 0) {
+        for (int q = 1; q < 4; q++) key = red[q] > key ? red[q] : key;
+        key = red[0] > key ? red[0] : key;
+        argmax[s] = (int)(0xffffffffu - (unsigned)(key & 0xffffffffu));
     }
 }
 
@@ -304,13 +326,13 @@ struct Head {
     int8_t *xq = nullptr;           // [4, D] q8_0 of rmsnorm(H, final_norm)
     float *xs = nullptr;            // [4, D/32]
     int *xsum = nullptr;            // [4, D/32]
-    unsigned long long *amax = nullptr;   // [4] argmax keys, kept at 0 between calls
+    unsigned long long *part = nullptr;   // [4][V/64] per-workgroup argmax keys
 };
 static std::vector<Head *> g_heads;
 
 static void free_head(Head *h) {
     if (!h) return;
-    void *ps[] = {h->table, h->fnorm, h->xq, h->xs, h->xsum, h->amax};
+    void *ps[] = {h->table, h->fnorm, h->xq, h->xs, h->xsum, h->part};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     delete h;
@@ -343,8 +365,7 @@ extern "C" int zz_head_create(const uint8_t *table, int V, int D, const float *f
               hipMalloc(&h->xq, (size_t)ZZ_DEC_MAXS * D) == hipSuccess &&
               hipMalloc(&h->xs, sizeof(float) * ZZ_DEC_MAXS * nb) == hipSuccess &&
               hipMalloc(&h->xsum, sizeof(int) * ZZ_DEC_MAXS * nb) == hipSuccess &&
-              hipMalloc(&h->amax, sizeof(unsigned long long) * ZZ_DEC_MAXS) == hipSuccess &&
-              hipMemset(h->amax, 0, sizeof(unsigned long long) * ZZ_DEC_MAXS) == hipSuccess &&
+              hipMalloc(&h->part, sizeof(unsigned long long) * ZZ_DEC_MAXS * (V / 64)) == hipSuccess &&
               hipMemcpy(h->fnorm, final_norm, sizeof(float) * D, hipMemcpyHostToDevice) == hipSuccess &&
               hipMemcpy(staging, table, src_bytes, hipMemcpyHostToDevice) == hipSuccess;
     if (ok) {
@@ -419,9 +440,11 @@ extern "C" int zz_head_logits_dev(int id, const float *d_H, int S, float *d_logi
     pa.xsum = h->xsum;
     pa.diag = zz_lib_diag();
     if (!zz_launch_prep(pa, S, st)) ZZ_FAIL("zz_head_logits_dev: norm launch failed");
-    hipLaunchKernelGGL(zz_head_kernel, dim3(h->V / 64), dim3(256), 0, st, h->table, h->T, h->xq, h->xs, S, h->cap,
-                       d_logits, h->amax);
-    hipLaunchKernelGGL(zz_head_argmax_kernel, dim3(1), dim3(64), 0, st, h->amax, d_argmax, S);
+    const size_t lds = (size_t)S * h->D + sizeof(float) * (size_t)S * (h->D / ZZ_BLK);
+    hipLaunchKernelGGL(zz_head_kernel, dim3(h->V / 64), dim3(256), lds, st, h->table, h->T, h->xq, h->xs, S, h->cap,
+                       d_logits, h->part);
+    if (d_argmax)
+        hipLaunchKernelGGL(zz_head_argmax_kernel, dim3(S), dim3(256), 0, st, h->part, h->V / 64, d_argmax);
     if (hipGetLastError() != hipSuccess) ZZ_FAIL("zz_head_logits_dev: launch failed");
     return 1;
 }
