@@ -325,3 +325,35 @@ def test_container_load(dev, tmp_path):
             bad.load_experts(str(tmp_path), 1)
     finally:
         close_all(*objs)
+
+
+@pytest.mark.parametrize("S", [1, 2, 4])
+def test_block_fused_decode_matches_two_stream_path(dev, S, layer_cache):
+    """Decode rows run the dense branch fused into the routed layer's four launches;
+    ZZ_BLOCK_FUSE=0 keeps it on its own stream. Both agree with the oracle (routing
+    exact, 1e-3) and with each other to float rounding (the dense down's chunks are
+    summed across waves in the fused path)."""
+    import os
+    L = layer_cache("gemma", seed=2, zipf=True)
+    dn = Z.make_dense(2816, 2112, 13)
+    H = Z.make_input(L, S, 13 + S)
+    want = Z.oracle_block(L, dn, H)
+    outs = []
+    for fuse in ("1", "0"):
+        os.environ["ZZ_BLOCK_FUSE"] = fuse
+        try:
+            B, m, d = gpu_block(L, dn)
+        finally:
+            os.environ.pop("ZZ_BLOCK_FUSE")
+        try:
+            Hb, eidx, ewt = B.forward(H)
+            Hb2, eidx2, _ = B.forward(H)           # repeatable
+            assert np.array_equal(Hb.view(np.uint32), Hb2.view(np.uint32))
+            assert np.array_equal(eidx, want[1])
+            err = Z.rel_l2(Hb, want[0])
+            say(f"block S={S} fuse={fuse}: rel L2 {err:.2e}")
+            assert err < OUT_TOL
+            outs.append(Hb)
+        finally:
+            close_all(B, m, d)
+    assert Z.rel_l2(outs[0], outs[1]) < 1e-5

@@ -462,25 +462,38 @@ extern "C" int zz_moe_profile_read(double *ms, int *launches, int n) {
 // path; larger ones the matrix cores
 static bool takes_decode(const zz_moe_desc &d, int S) { return S <= g_dec_max_s && zz_dec_fits(S, d.K, d.MI); }
 
-static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream_t st) {
+// Kernel arguments of one chunk of S <= chunk_tokens rows of layer L.
+struct ChunkArgs {
+    ZzPrepArgs pa;
+    ZzLogitArgs la;
+    ZzTopkArgs ta;
+    ZzDispatchArgs da;
+    ZzFfnArgs fa;
+    bool dense, gemma, dec;
+    int P, max_items;
+};
+
+static ChunkArgs chunk_args(Layer *L, const float *d_in, int S) {
     const zz_moe_desc &d = L->d;
     Workspace &w = L->ws;
-    const bool dense = d.gating == ZZ_GATE_DENSE;   // gemma's norms, no router
-    const bool gemma = d.gating == ZZ_GATE_SOFTMAX_PES || dense;
+    ChunkArgs c;
+    memset(&c, 0, sizeof c);
+    c.dense = d.gating == ZZ_GATE_DENSE;            // gemma's norms, no router
+    c.gemma = d.gating == ZZ_GATE_SOFTMAX_PES || c.dense;
     const bool tq_in = d.fmt_gate == ZZ_FMT_TQ2;
-    const int P = S * d.K;
+    c.P = S * d.K;
 
-    ZzPrepArgs pa;
-    pa.D = d.D; pa.gemma = gemma; pa.eps = d.eps; pa.in = d_in;
+    ZzPrepArgs &pa = c.pa;
+    pa.D = d.D; pa.gemma = c.gemma; pa.eps = d.eps; pa.in = d_in;
     pa.router_scale = L->rscale; pa.pre_ln = L->pre_ln; pa.xn = w.xn;
     pa.xq = w.xq; pa.xs = w.xs; pa.xsum = w.xsum; pa.xt = tq_in ? w.xt : nullptr; pa.diag = g_diag;
-    pa.route_eidx = dense ? w.eidx : nullptr; pa.route_ewt = dense ? w.ewt : nullptr;
+    pa.route_eidx = c.dense ? w.eidx : nullptr; pa.route_ewt = c.dense ? w.ewt : nullptr;
 
-    ZzLogitArgs la;
+    ZzLogitArgs &la = c.la;
     la.D = d.D; la.E = d.E; la.gating = d.gating; la.S = S; la.router = L->router; la.xn = w.xn; la.x = d_in;
-    la.bias = gemma && d.use_bias ? L->bias : nullptr; la.cen = w.cen; la.bnd = w.bnd; la.diag = g_diag;
+    la.bias = c.gemma && d.use_bias ? L->bias : nullptr; la.cen = w.cen; la.bnd = w.bnd; la.diag = g_diag;
 
-    ZzTopkArgs ta;
+    ZzTopkArgs &ta = c.ta;
     ta.D = d.D; ta.E = d.E; ta.K = d.K; ta.gating = d.gating; ta.norm_topk = d.norm_topk;
     ta.routed_scaling = d.routed_scaling; ta.cen = w.cen; ta.bnd = w.bnd; ta.router = L->router;
     ta.xn = w.xn; ta.bias = d.use_bias ? L->bias : nullptr; ta.pes = L->pes; ta.eidx = w.eidx;
@@ -488,49 +501,101 @@ static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream
 
     // decode-sized batches take the GEMV path; larger ones the matrix cores, on
     // work items of up to ZZ_MMA_TOKENS tokens of one expert
-    const bool dec = takes_decode(d, S);
-    const int tch = dec ? ZZ_DEC_MAXS : ZZ_MMA_TOKENS;
-    ZzDispatchArgs da;
-    da.P = P; da.E = d.E; da.K = d.K; da.tch = tch; da.eidx = w.eidx; da.ewt = w.ewt;
+    c.dec = takes_decode(d, S);
+    const int tch = c.dec ? ZZ_DEC_MAXS : ZZ_MMA_TOKENS;
+    ZzDispatchArgs &da = c.da;
+    da.P = c.P; da.E = d.E; da.K = d.K; da.tch = tch; da.eidx = w.eidx; da.ewt = w.ewt;
     da.ptok = w.ptok; da.pslot = w.pslot; da.pwt = w.pwt; da.ppos = w.ppos; da.uniq = w.uniq;
     da.uoff = w.uoff; da.ucnt = w.ucnt; da.items = w.items; da.meta = w.meta;
 
-    if (dec) {
-        ZzDecRouteArgs ra;
-        ra.prep = pa; ra.lg = la; ra.tk = ta; ra.dp = da; ra.S = S; ra.dense = dense;
-        if (!(ProfScope(ZZ_K_DEC_ROUTE, st), zz_launch_dec_logits(ra, st))) ZZ_FAIL("decode router launch failed");
-    } else {
-        if (!(ProfScope(ZZ_K_PREP, st), zz_launch_prep(pa, S, st))) ZZ_FAIL("prep launch failed");
-        if (!dense && !(ProfScope(ZZ_K_LOGITS, st), zz_launch_logits(la, S, st))) ZZ_FAIL("logits launch failed");
-        if (!dense && !(ProfScope(ZZ_K_TOPK, st), zz_launch_topk(ta, S, st))) ZZ_FAIL("topk launch failed");
-        if (!(ProfScope(ZZ_K_DISPATCH, st), zz_launch_dispatch(da, st))) ZZ_FAIL("dispatch launch failed");
-    }
-
-    ZzFfnArgs fa;
+    ZzFfnArgs &fa = c.fa;
     fa.D = d.D; fa.MI = d.MI; fa.K = d.K; fa.act = d.act; fa.clamp = d.clamp;
     fa.experts = L->slots; fa.estride = L->lay.bytes; fa.lay = L->lay; fa.items = w.items;
     fa.meta = w.meta; fa.ptok = w.ptok; fa.xq = w.xq; fa.xs = w.xs; fa.xsum = w.xsum; fa.xt = w.xt;
     fa.hq = w.hq; fa.hs = w.hs; fa.hsum = w.hsum; fa.y = w.y;
-    const int max_items = (P < d.E ? P : d.E) + (P + tch - 1) / tch;
-    if (dec) {
-        ZzDecDownArgs dd;
-        dd.f = fa; dd.S = S; dd.K = d.K; dd.E = d.E; dd.eidx = w.eidx; dd.ewt = w.ewt; dd.ppos = w.ppos;
-        dd.out = d_out; dd.ss = gemma ? w.ss : nullptr;
+    c.max_items = (c.P < d.E ? c.P : d.E) + (c.P + tch - 1) / tch;
+    return c;
+}
+
+static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream_t st) {
+    const zz_moe_desc &d = L->d;
+    Workspace &w = L->ws;
+    ChunkArgs c = chunk_args(L, d_in, S);
+
+    if (c.dec) {
+        ZzDecRouteArgs ra;
+        memset(&ra, 0, sizeof ra);
+        ra.prep = c.pa; ra.lg = c.la; ra.tk = c.ta; ra.dp = c.da; ra.S = S; ra.dense = c.dense;
+        if (!(ProfScope(ZZ_K_DEC_ROUTE, st), zz_launch_dec_logits(ra, st))) ZZ_FAIL("decode router launch failed");
         ZzDecUpArgs ua;
-        ua.f = fa; ua.tk = ta; ua.dense = dense;
+        memset(&ua, 0, sizeof ua);
+        ua.f = c.fa; ua.tk = c.ta; ua.dense = c.dense; ua.pk = c.P;
+        ZzDecDownArgs dd;
+        memset(&dd, 0, sizeof dd);
+        dd.f = c.fa; dd.S = S; dd.K = d.K; dd.E = d.E; dd.eidx = w.eidx; dd.ewt = w.ewt; dd.ppos = w.ppos;
+        dd.out = d_out; dd.ss = c.gemma ? w.ss : nullptr;
         if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_dec_up(ua, S, st))) ZZ_FAIL("ffn_up launch failed");
         if (!(ProfScope(ZZ_K_DEC_DOWN, st), zz_launch_dec_down(dd, st))) ZZ_FAIL("decode down launch failed");
-        if (gemma && !(ProfScope(ZZ_K_COMBINE, st), zz_launch_dec_norm(d_out, L->post_ln, w.ss, d.D, d.eps, S, st)))
+        if (c.gemma && !(ProfScope(ZZ_K_COMBINE, st), zz_launch_dec_norm(d_out, L->post_ln, w.ss, d.D, d.eps, S, st)))
             ZZ_FAIL("decode post-norm launch failed");
         return 1;
     }
-    if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_up_mfma(fa, max_items, st))) ZZ_FAIL("ffn_up launch failed");
-    if (!(ProfScope(ZZ_K_FFN_DOWN, st), zz_launch_down_mfma(fa, max_items, st))) ZZ_FAIL("ffn_down launch failed");
+    if (!(ProfScope(ZZ_K_PREP, st), zz_launch_prep(c.pa, S, st))) ZZ_FAIL("prep launch failed");
+    if (!c.dense && !(ProfScope(ZZ_K_LOGITS, st), zz_launch_logits(c.la, S, st))) ZZ_FAIL("logits launch failed");
+    if (!c.dense && !(ProfScope(ZZ_K_TOPK, st), zz_launch_topk(c.ta, S, st))) ZZ_FAIL("topk launch failed");
+    if (!(ProfScope(ZZ_K_DISPATCH, st), zz_launch_dispatch(c.da, st))) ZZ_FAIL("dispatch launch failed");
+    if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_up_mfma(c.fa, c.max_items, st))) ZZ_FAIL("ffn_up launch failed");
+    if (!(ProfScope(ZZ_K_FFN_DOWN, st), zz_launch_down_mfma(c.fa, c.max_items, st))) ZZ_FAIL("ffn_down launch failed");
 
     ZzCombineArgs ca;
-    ca.D = d.D; ca.K = d.K; ca.gemma = gemma; ca.eps = d.eps; ca.y = w.y; ca.ppos = w.ppos;
+    ca.D = d.D; ca.K = d.K; ca.gemma = c.gemma; ca.eps = d.eps; ca.y = w.y; ca.ppos = w.ppos;
     ca.ewt = w.ewt; ca.post_ln = L->post_ln; ca.out = d_out;
     if (!(ProfScope(ZZ_K_COMBINE, st), zz_launch_combine(ca, S, st))) ZZ_FAIL("combine launch failed");
+    return 1;
+}
+
+// The decode rows of a gemma FFN block (zz_gemma.hip) with the dense layer fused into
+// the routed layer's four launches: the router kernel also quantises the dense
+// branch's input, the gate/up kernel runs its rows as extra grid rows, the down
+// kernel its output rows beside the routed pairs', and one final kernel applies
+// both post-norms and the layer combine. H is updated in place; h1/h2 [S, D] hold
+// the dense and routed outputs before their norms. Returns 1 when done, 0 on a
+// failure, -1 when the layers or S do not take this path.
+int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_h2, const float *post_ln,
+                    float ls, int S, int *d_eidx, float *d_ewt, hipStream_t st) {
+    Layer *L = get_layer(moe_id), *N = get_layer(dense_id);
+    if (!L || !N || S <= 0) return -1;
+    const zz_moe_desc &d = L->d, &dn = N->d;
+    if (d.gating != ZZ_GATE_SOFTMAX_PES || dn.gating != ZZ_GATE_DENSE || d.D != dn.D || !takes_decode(d, S) ||
+        S > chunk_tokens(d) || d.fmt_down != dn.fmt_down || d.fmt_down == ZZ_FMT_TQ2 || dn.fmt_gate == ZZ_FMT_TQ2 ||
+        dn.fmt_up == ZZ_FMT_TQ2 || d.fmt_gate == ZZ_FMT_TQ2 || !zz_dec_fits2(S, d.K, d.MI, dn.MI))
+        return -1;
+    if (L->n_present != d.E || N->n_present != dn.E) ZZ_FAIL("block: experts not uploaded");
+    if (!ensure_ws(L, S) || !ensure_ws(N, S)) return 0;
+    ChunkArgs c = chunk_args(L, d_H, S), cn = chunk_args(N, d_H, S);
+    Workspace &w = L->ws, &wn = N->ws;
+
+    ZzDecRouteArgs ra;
+    memset(&ra, 0, sizeof ra);
+    ra.prep = c.pa; ra.lg = c.la; ra.tk = c.ta; ra.dp = c.da; ra.S = S; ra.dual = 1; ra.prep2 = cn.pa;
+    if (!(ProfScope(ZZ_K_DEC_ROUTE, st), zz_launch_dec_logits(ra, st))) ZZ_FAIL("block: router launch failed");
+    ZzDecUpArgs ua;
+    memset(&ua, 0, sizeof ua);
+    ua.f = c.fa; ua.tk = c.ta; ua.pk = c.P; ua.nd = S; ua.fd = cn.fa;
+    if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_dec_up(ua, S, st))) ZZ_FAIL("block: gate/up launch failed");
+    ZzDecDownArgs dd;
+    memset(&dd, 0, sizeof dd);
+    dd.f = c.fa; dd.S = S; dd.K = d.K; dd.E = d.E; dd.eidx = w.eidx; dd.ewt = w.ewt; dd.ppos = w.ppos;
+    dd.out = d_h2; dd.ss = w.ss; dd.nd = S; dd.fd = cn.fa; dd.yd = d_h1; dd.ssd = wn.ss;
+    if (!(ProfScope(ZZ_K_DEC_DOWN, st), zz_launch_dec_down(dd, st))) ZZ_FAIL("block: down launch failed");
+    ZzDecFinalArgs fa;
+    fa.D = d.D; fa.G = d.D / 16; fa.eps = d.eps; fa.ls = ls; fa.out = d_h2; fa.ss = w.ss; fa.post2 = L->post_ln;
+    fa.yd = d_h1; fa.ssd = wn.ss; fa.post1 = N->post_ln; fa.post = post_ln; fa.H = d_H;
+    if (!(ProfScope(ZZ_K_COMBINE, st), zz_launch_dec_final(fa, S, st))) ZZ_FAIL("block: final launch failed");
+    if (d_eidx) ZZ_CHECK(hipMemcpyAsync(d_eidx, w.eidx, sizeof(int) * S * d.K, hipMemcpyDeviceToDevice, st));
+    if (d_ewt) ZZ_CHECK(hipMemcpyAsync(d_ewt, w.ewt, sizeof(float) * S * d.K, hipMemcpyDeviceToDevice, st));
+    L->last_S = S;
+    N->last_S = S;
     return 1;
 }
 

@@ -101,32 +101,41 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
     } else if ((tid >> 6) < S) {
         zz_logit_wave_f64(lg, tid >> 6, e);
     }
-    // the expert input quantisation: block g on workgroup g % E, lanes 8(g / E)..+7
+    // the expert input quantisation: block g on workgroup g % E, lanes 8(g / E)..+7;
+    // dual: blocks S*nb.. are the dense branch's input (same rms factor, its own norm)
     __syncthreads();
-    for (int g0 = e + gridDim.x * (tid >> 3); g0 - (tid >> 3) * (int)gridDim.x < S * nb; g0 += gridDim.x * 32) {
-        const int g = min(g0, S * nb - 1), s = g / nb, b = g % nb, m = tid & 7;   // whole waves iterate
+    const int NQ = S * nb * (a.dual ? 2 : 1);
+    for (int g0 = e + gridDim.x * (tid >> 3); g0 - (tid >> 3) * (int)gridDim.x < NQ; g0 += gridDim.x * 32) {
+        const int g = min(g0, NQ - 1), m = tid & 7;               // whole waves iterate
+        const bool two = g >= S * nb;
+        const ZzPrepArgs &P = two ? a.prep2 : pp;
+        const int gg = two ? g - S * nb : g, s = gg / nb, b = gg % nb;
         float4 v = *(const float4 *)(pp.in + (size_t)s * D + b * ZZ_BLK + 4 * m);
         if (gem) {
             const float r = rr[s];
-            const float4 w = *(const float4 *)(pp.pre_ln + b * ZZ_BLK + 4 * m);
+            const float4 w = *(const float4 *)(P.pre_ln + b * ZZ_BLK + 4 * m);
             v = make_float4((v.x * r) * w.x, (v.y * r) * w.y, (v.z * r) * w.z, (v.w * r) * w.w);
         }
         float d;
         int qs;
         const unsigned pk = zz_quant8(v, &d, &qs);
-        if (g0 < S * nb) {
-            *(unsigned *)(pp.xq + (size_t)s * D + b * ZZ_BLK + 4 * m) = pk;
+        if (g0 < NQ) {
+            *(unsigned *)(P.xq + (size_t)s * D + b * ZZ_BLK + 4 * m) = pk;
             if (m == 0) {
-                pp.xs[(size_t)s * nb + b] = d;
-                pp.xsum[(size_t)s * nb + b] = qs;
+                P.xs[(size_t)s * nb + b] = d;
+                P.xsum[(size_t)s * nb + b] = qs;
             }
         }
+    }
+    if (a.dual && e == 0 && tid < S) {                          // the dense rows' routing
+        a.prep2.route_eidx[tid] = 0;
+        a.prep2.route_ewt[tid] = 1.0f;
     }
 }
 
 // ------------------------------------------------------------------ gate/up
-// grid (MI/32, S*K), 512 threads. Workgroup (j, p) owns hidden rows 32j..32j+31 of
-// (token, slot) pair p = s*K + slot. Wave 0 first runs the certified top-k of token
+// S*K*MI/32 workgroups (+ the fused dense branch's), 512 threads. Workgroup (p, j)
+// owns hidden rows 32j..32j+31 of (token, slot) pair p = s*K + slot. Wave 0 first runs the certified top-k of token
 // s (zz_topk_wave.h): every workgroup of the token repeats it, so no separate gating
 // launch or dispatch list stands between the router and the expert weights; the
 // token's first workgroup writes the routing outputs. Then wave w takes row group
@@ -273,18 +282,25 @@ __device__ __forceinline__ float zz_dec_up_part(const ZzFfnArgs &a, const ZzDecS
 }
 
 __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
-    const ZzFfnArgs &f = a.f;
-    const int K = a.tk.K, p = blockIdx.y, s = p / K, js = p - s * K;
-    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, h = w >> 2, q = w & 3, j = blockIdx.x;
+    // workgroup (p, j) of the routed pairs is number p*(MI/32) + j; the fused dense
+    // branch's rows (one per token, expert 0, no routing) follow, numbered the same way
+    const int nr = a.pk * (a.f.MI / ZZ_BLK);
+    const bool dn = (int)blockIdx.x >= nr;
+    const ZzFfnArgs &f = dn ? a.fd : a.f;
+    const int nbx = f.MI / ZZ_BLK, rel = dn ? (int)blockIdx.x - nr : (int)blockIdx.x;
+    const int p = rel / nbx, j = rel - p * nbx;
+    const int K = dn ? 1 : a.tk.K, s = p / K, js = p - s * K;
+    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, h = w >> 2, q = w & 3;
     extern __shared__ __attribute__((aligned(16))) char tk_lds[];
     __shared__ ZzDecStage st;
     __shared__ float part[2][4][16];                // [half][gate g0, g1, up g0, g1][row]
     __shared__ float hb[ZZ_BLK];
     ZzDecStageRegs sr;
     zz_dec_stage_issue(f, s, sr);
-    if (w == 0 && !a.dense) zz_topk_wave_any(a.tk, s, tk_lds, j == 0 && js == 0);
+    const bool routed = !a.dense && !dn;
+    if (w == 0 && routed) zz_topk_wave_any(a.tk, s, tk_lds, j == 0 && js == 0);
     __syncthreads();
-    const int e = a.dense ? 0 : zz_clamp_e(((const ZzTopkWaveHdr *)tk_lds)->idx[js], a.tk.E);
+    const int e = routed ? zz_clamp_e(((const ZzTopkWaveHdr *)tk_lds)->idx[js], a.tk.E) : 0;
     const ZzTensor &T = q >= 2 ? f.lay.up : f.lay.gate;
     const int g = 2 * j + (q & 1);
     const uint8_t *E = f.experts + (size_t)e * f.estride;
@@ -340,6 +356,7 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
 #define DD_W 8                        // waves
 #define DD_QB 4                       // hidden 16-byte segments per thread requested ahead
 #define DD_SB 2                       // hidden block scales per thread requested ahead
+#define DD_DN 4                       // fused dense-branch chunks per wave (its K <= 4096)
 
 struct ZzDecPairs {                 // per (token, slot) pair, flat order s*K + j
     int e[DEC_MAXS * ZZ_MAXK];      // expert (clamped into the table)
@@ -361,10 +378,16 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     __shared__ ZzDecPairs pr;
     __shared__ float yv[DEC_MAXS * ZZ_MAXK][16];
     __shared__ float htot[DEC_MAXS * ZZ_MAXK];
+    __shared__ float dpart[DD_W][DEC_MAXS][16];                 // fused dense branch, per wave
     extern __shared__ __attribute__((aligned(16))) char dd_lds[];
     int8_t *sh_q = (int8_t *)dd_lds;                            // [P][MI] by flat pair
     float *sh_s = (float *)(dd_lds + (size_t)P * MI);           // [P][nb]
     int *sh_c = (int *)(sh_s + P * nb);                         // [P][nb]
+    // fused dense branch (nd rows): its hidden [nd][MID] and scales [nd][MID/32]
+    constexpr bool DN = FMT != ZZ_FMT_TQ2;
+    const int nd = DN ? a.nd : 0, MID = a.fd.MI, nbd = MID / ZZ_BLK, nchd = (nbd + 3) / 4;
+    int8_t *sh_qd = (int8_t *)(sh_c + P * nb);
+    float *sh_sd = (float *)(sh_qd + (size_t)nd * MID);
     if (tid < P) {
         pr.e[tid] = zz_clamp_e(a.eidx[tid], a.E);
     }
@@ -443,6 +466,15 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     };
     __builtin_amdgcn_sched_barrier(0);                          // hidden loads issue first
     load_units(0);
+    // the fused dense branch's chunks of this wave (w, w+8, ...), requested after the
+    // routed pairs' first units so that waiting for those leaves these in flight
+    ZzChunk kd[DD_DN];
+    ZzWalk Wd;
+    if (nd) {
+        Wd = zz_walk(a.fd.lay.down, g, l, r);
+#pragma unroll
+        for (int i = 0; i < DD_DN; i++) kd[i] = zz_load_chunk<FMT>(a.fd.experts, Wd, min(w + DD_W * i, nchd - 1));
+    }
 #pragma unroll
     for (int k = 0; k < DD_QB; k++) *(uint4 *)(sh_q + 16 * (size_t)min(tid + 512 * k, nseg - 1)) = hv[k];
 #pragma unroll
@@ -456,6 +488,8 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
         sh_s[i] = f.hs[i];
         sh_c[i] = f.hsum[i];
     }
+    for (int i = tid; i < nd * MID / 16; i += 512) *(uint4 *)(sh_qd + 16 * (size_t)i) = ld16(a.fd.hq + 16 * (size_t)i);
+    for (int i = tid; i < nd * nbd; i += 512) sh_sd[i] = a.fd.hs[i];
     __syncthreads();
     if (FMT == ZZ_FMT_TQ2 && tid < P) {                         // tq2.h:101-106, serial
         double t = 0.0;
@@ -472,7 +506,50 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
         acc += __shfl_xor(acc, 32, 64);
         if (qq == 0) yv[cur][r] = FMT == ZZ_FMT_Q40 ? acc * 0.0625f : acc;   // 16*(q - 8) weights
     }
+    if (nd) {                                                   // this wave's dense chunks
+        float ad[DEC_MAXS] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < DD_DN; i++) {
+            const int cd = w + DD_W * i;
+            if (cd >= nchd) break;                              // wave-uniform
+            const int cbs = zz_cbs(a.fd.lay.down, 4 * cd);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (j >= cbs) break;
+                const int b = 4 * cd + j;
+                const uint2 wv = zz_chunk_w<FMT>(kd[i], j);
+                const float dw = zz_chunk_dw(kd[i], j, cbs == 4);
+#pragma unroll
+                for (int q = 0; q < DEC_MAXS; q++) {
+                    if (q >= nd) break;
+                    const uint2 xv = *(const uint2 *)(sh_qd + (size_t)q * MID + b * ZZ_BLK + 8 * qq);
+                    int d = zz_dot4(wv.x, xv.x, 0);
+                    d = zz_dot4(wv.y, xv.y, d);
+                    ad[q] = fmaf(dw * sh_sd[q * nbd + b], (float)d, ad[q]);
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < DEC_MAXS; q++) {
+            float v = ad[q];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            if (qq == 0 && q < nd) dpart[w][q][r] = v;
+        }
+    }
     __syncthreads();
+    if (nd && tid < nd * 16) {                                  // dense rows 16g.., waves in order
+        const int q = tid >> 4, rr = tid & 15;
+        float v = dpart[0][q][rr];
+#pragma unroll
+        for (int ww = 1; ww < DD_W; ww++) v += dpart[ww][q][rr];
+        if (FMT == ZZ_FMT_Q40) v *= 0.0625f;
+        a.yd[(size_t)q * D + g * 16 + rr] = v;
+        double t = (double)v * (double)v;
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) t += __shfl_xor(t, m, 64);
+        if (rr == 0) a.ssd[(size_t)q * gridDim.x + g] = t;
+    }
     if (tid < S * 16) {
         const int s = tid >> 4, rr = tid & 15, o = g * 16 + rr;
         float v = 0.0f;
@@ -529,16 +606,26 @@ int zz_launch_dec_logits(const ZzDecRouteArgs &a, hipStream_t st) {
 }
 
 int zz_launch_dec_up(const ZzDecUpArgs &a, int S, hipStream_t st) {
-    hipLaunchKernelGGL(zz_dec_up_kernel, dim3(a.f.MI / 32, S * a.tk.K), dim3(512), zz_topk_wave_bytes(a.tk.E), st, a);
+    const int n = S * a.tk.K * (a.f.MI / ZZ_BLK) + a.nd * (a.nd ? a.fd.MI / ZZ_BLK : 0);
+    hipLaunchKernelGGL(zz_dec_up_kernel, dim3(n), dim3(512), zz_topk_wave_bytes(a.tk.E), st, a);
     return hipGetLastError() == hipSuccess;
 }
 
 int zz_dec_fits(int S, int K, int MI) { return zz_dec_down_lds(S * K, MI) <= ZZ_DEC_LDS; }
 
+// a dense branch of intermediate MID fused in: its S hidden rows and scales beside the
+// routed pairs', and at most DD_DN of its chunks per wave
+static inline size_t zz_dec_dense_lds(int S, int MID) { return (size_t)S * MID + 4 * (size_t)S * (MID / ZZ_BLK); }
+int zz_dec_fits2(int S, int K, int MI, int MID) {
+    return zz_dec_down_lds(S * K, MI) + zz_dec_dense_lds(S, MID) <= ZZ_DEC_LDS &&
+           (MID / ZZ_BLK + 3) / 4 <= DD_W * DD_DN;
+}
+
 int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st) {
     const dim3 grid(a.f.D / 16);
-    const size_t lds = zz_dec_down_lds(a.S * a.K, a.f.MI);
-    if (!zz_dec_fits(a.S, a.K, a.f.MI)) return 0;
+    const int nd = a.nd && a.f.lay.down.fmt != ZZ_FMT_TQ2 ? a.nd : 0;
+    const size_t lds = zz_dec_down_lds(a.S * a.K, a.f.MI) + (nd ? zz_dec_dense_lds(nd, a.fd.MI) : 0);
+    if (nd ? !zz_dec_fits2(a.S, a.K, a.f.MI, a.fd.MI) : !zz_dec_fits(a.S, a.K, a.f.MI)) return 0;
     switch (a.f.lay.down.fmt) {
     case ZZ_FMT_Q40: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q40>, grid, dim3(512), lds, st, a); break;
     case ZZ_FMT_Q80: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q80>, grid, dim3(512), lds, st, a); break;
@@ -550,5 +637,51 @@ int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st) {
 
 int zz_launch_dec_norm(float *out, const float *post_ln, const double *ss, int D, float eps, int S, hipStream_t st) {
     hipLaunchKernelGGL(zz_dec_norm_kernel, dim3((D + 255) / 256, S), dim3(256), 0, st, out, post_ln, ss, D / 16, D, eps);
+    return hipGetLastError() == hipSuccess;
+}
+
+// The tail of a gemma FFN block whose dense branch ran fused into the routed layer's
+// decode kernels: the two post-norms from their per-tile sums (each formed as
+// zz_dec_norm_kernel forms it), then the layer combine as zz_block_combine_kernel
+// forms it (gemma4.c:807-808, 1020, 1022-1030). One workgroup per token.
+__global__ __launch_bounds__(256) void zz_dec_final_kernel(ZzDecFinalArgs a) {
+    const int s = blockIdx.x, tid = threadIdx.x, D = a.D, G = a.G;
+    __shared__ float rn[2];
+    __shared__ __attribute__((aligned(16))) float row[ZZ_MAXD];
+    __shared__ double red[4];
+    if (tid < 128) {                                 // wave 0: routed, wave 1: dense
+        const int which = tid >> 6, l = tid & 63;
+        const double *ss = (which ? a.ssd : a.ss) + (size_t)s * G;
+        double q = 0.0;
+        for (int k = l; k < G; k += 64) q += ss[k];
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+        if (l == 0) rn[which] = 1.0f / sqrtf((float)(q / D) + a.eps);
+    }
+    __syncthreads();
+    const float r2 = rn[0], r1 = rn[1];
+    const float *o2 = a.out + (size_t)s * D, *o1 = a.yd + (size_t)s * D;
+    double sq = 0.0;
+    for (int o = 4 * tid; o < D; o += 1024) {
+        const float4 y = *(const float4 *)(o2 + o), w2 = *(const float4 *)(a.post2 + o);
+        const float4 x = *(const float4 *)(o1 + o), w1 = *(const float4 *)(a.post1 + o);
+        const float4 h2 = make_float4((y.x * r2) * w2.x, (y.y * r2) * w2.y, (y.z * r2) * w2.z, (y.w * r2) * w2.w);
+        const float4 h1 = make_float4((x.x * r1) * w1.x, (x.y * r1) * w1.y, (x.z * r1) * w1.z, (x.w * r1) * w1.w);
+        const float4 t = make_float4(h1.x + h2.x, h1.y + h2.y, h1.z + h2.z, h1.w + h2.w);
+        *(float4 *)&row[o] = t;
+        sq += (double)t.x * t.x + (double)t.y * t.y + (double)t.z * t.z + (double)t.w * t.w;
+    }
+    sq = zz_block_sum(sq, red);
+    const float r = 1.0f / sqrtf((float)(sq / D) + a.eps);
+    float *hr = a.H + (size_t)s * D;
+    for (int o = 4 * tid; o < D; o += 1024) {
+        const float4 t = *(const float4 *)&row[o], wv = *(const float4 *)(a.post + o), h = *(const float4 *)(hr + o);
+        *(float4 *)(hr + o) = make_float4((h.x + (t.x * r) * wv.x) * a.ls, (h.y + (t.y * r) * wv.y) * a.ls,
+                                          (h.z + (t.z * r) * wv.z) * a.ls, (h.w + (t.w * r) * wv.w) * a.ls);
+    }
+}
+
+int zz_launch_dec_final(const ZzDecFinalArgs &a, int S, hipStream_t st) {
+    hipLaunchKernelGGL(zz_dec_final_kernel, dim3(S), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess;
 }

@@ -12,6 +12,7 @@
 #include "../../include/zz_gemma.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 #include <vector>
 
@@ -185,6 +186,7 @@ __global__ __launch_bounds__(256) void zz_head_argmax_kernel(const unsigned long
 struct FfnBlock {
     int moe, dense, D;
     float ls, eps;
+    int fuse = 1;                                      // fused decode path (ZZ_BLOCK_FUSE=0: off)
     float *post_ln = nullptr;
     float *h1 = nullptr, *h2 = nullptr, *hh = nullptr;   // hh: host-form staging of H
     size_t cap = 0;                                    // tokens h1/h2/hh hold
@@ -223,6 +225,8 @@ extern "C" int zz_ffn_block_create(int moe_layer, int dense_layer, const float *
     B->D = m->D;
     B->ls = layer_scalar;
     B->eps = m->eps;
+    const char *fz = getenv("ZZ_BLOCK_FUSE");
+    B->fuse = !(fz && fz[0] == '0');
     bool ok = hipMalloc(&B->post_ln, sizeof(float) * m->D) == hipSuccess &&
               hipMemcpy(B->post_ln, post_ffn_ln, sizeof(float) * m->D, hipMemcpyHostToDevice) == hipSuccess &&
               hipStreamCreateWithFlags(&B->ds, hipStreamNonBlocking) == hipSuccess &&
@@ -268,6 +272,11 @@ static int block_grow(FfnBlock *B, int S, hipStream_t st) {
 static int block_forward(FfnBlock *B, float *d_H, int S, int *d_eidx, float *d_ewt, hipStream_t st) {
     if (S <= 0 || !d_H) ZZ_FAIL("zz_ffn_block_forward: bad arguments");
     if (!block_grow(B, S, st)) return 0;
+    // decode rows: the dense branch rides in the routed layer's launches
+    if (B->fuse) {
+        const int r = zz_block_decode(B->moe, B->dense, d_H, B->h1, B->h2, B->post_ln, B->ls, S, d_eidx, d_ewt, st);
+        if (r >= 0) return r;
+    }
     // the dense branch forks off the caller's stream and joins before the combine
     ZZ_CHECK(hipEventRecord(B->fork, st));
     ZZ_CHECK(hipStreamWaitEvent(B->ds, B->fork, 0));

@@ -100,6 +100,8 @@ struct ZzDecRouteArgs {
     ZzDispatchArgs dp;          // dispatch lists and work items
     int S;
     int dense;                  // dense branch: norms and quantisation only, no logits
+    int dual;                   // also quantise the dense branch's input into prep2
+    ZzPrepArgs prep2;           // dual: the dense layer's pre-norm and input buffers
 };
 
 // Decode gate/up: the routing of each token and the expert GEMVs of its pairs.
@@ -107,6 +109,9 @@ struct ZzDecUpArgs {
     ZzFfnArgs f;
     ZzTopkArgs tk;
     int dense;                  // dense branch: expert 0 for every pair, no top-k
+    int pk;                     // routed pairs S*K: grid rows >= pk are dense-branch rows
+    int nd;                     // dense-branch rows (0, or S with a dense layer fused in)
+    ZzFfnArgs fd;               // the dense layer (nd > 0)
 };
 
 // Fused decode down projection + gate-weighted combine.
@@ -118,6 +123,25 @@ struct ZzDecDownArgs {
     const int *ppos;            // [S*K] -> sorted pair
     float *out;                 // [S, D]
     double *ss;                 // [S, D/16] per-tile sums of squares of out (gemma), or null
+    int nd;                     // dense-branch rows fused in (0 or S)
+    ZzFfnArgs fd;               // the dense layer (nd > 0)
+    float *yd;                  // [S, D] its down projection
+    double *ssd;                // [S, D/16] per-tile sums of squares of yd
+};
+
+// Decode tail of a gemma FFN block with the dense branch fused in: both post-norms
+// from their per-tile sums, then H = (H + rmsnorm(h1 + h2, post_ffn_ln)) * ls.
+struct ZzDecFinalArgs {
+    int D, G;                   // G = D/16 tiles
+    float eps, ls;
+    const float *out;           // [S, D] routed combine (before post_ffn_ln2)
+    const double *ss;
+    const float *post2;         // post_ffn_ln2
+    const float *yd;            // [S, D] dense down (before post_ffn_ln1)
+    const double *ssd;
+    const float *post1;         // post_ffn_ln1
+    const float *post;          // post_ffn_ln
+    float *H;                   // [S, D] in place
 };
 
 // Host-side internals of the library (zz_api.hip), shared by its host files.
@@ -127,6 +151,10 @@ int zz_lib_ready();
 unsigned *zz_lib_diag();
 const zz_moe_desc *zz_layer_desc(int id);
 int zz_lib_prof_set(int on);        // per-kernel event timing on/off; returns the old state
+// a gemma FFN block's decode rows with the dense branch fused into the routed layer's
+// launches: 1 done, 0 failed, -1 not applicable
+int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_h2, const float *post_ln,
+                    float ls, int S, int *d_eidx, float *d_ewt, hipStream_t st);
 // tensor in the slot-table layout at *cursor (advanced past it, 256-aligned)
 ZzTensor zz_make_tensor(int fmt, int O, int I, int64_t *cursor);
 
@@ -145,6 +173,8 @@ int zz_launch_dec_logits(const ZzDecRouteArgs &a, hipStream_t st);
 int zz_launch_dec_up(const ZzDecUpArgs &a, int S, hipStream_t st);
 int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st);
 int zz_dec_fits(int S, int K, int MI);   // the decode path's LDS holds S*K hidden rows
+int zz_dec_fits2(int S, int K, int MI, int MID);   // ... and S dense hidden rows of MID
+int zz_launch_dec_final(const ZzDecFinalArgs &a, int S, hipStream_t st);
 int zz_launch_dec_norm(float *out, const float *post_ln, const double *ss, int D, float eps, int S, hipStream_t st);
 // int8-MFMA grouped GEMM for work items of up to ZZ_MMA_TOKENS tokens
 #define ZZ_MMA_TOKENS 64
