@@ -15,6 +15,9 @@
 //      (gemma4.c:600-601), lfm flags the token (expf, lfm25.c:648);
 //   5. candidates are ranked by centre (disjoint intervals order as their
 //      values do; replayed ones are exact), and the gate weights are formed.
+// A register-only fast path settles the common case first: K rounds of a wave
+// maximum give the K largest keys, which are the answer, in order, when no other
+// expert's interval reaches the K-th lower bound and the K intervals are disjoint.
 #pragma once
 #include "zz_route_dev.h"
 
@@ -42,6 +45,27 @@ __device__ __forceinline__ float zz_round_down(double v) {
     if ((double)f > v) f = nextafterf(f, -INFINITY);
     return f;
 }
+// Wave maximum of an unsigned value through DPP: swaps within quads, the half-row
+// and row mirrors, then the row broadcasts (lane 15 into rows 1 and 3, lane 31 into
+// rows 2 and 3); lane 63 ends with the maximum. Lanes a step leaves out keep 0.
+__device__ __forceinline__ unsigned zz_wave_umax(unsigned v) {
+    v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+    v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+    v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
+    v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false));  // row_bcast:15
+    v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false));  // row_bcast:31
+    return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// a double held by lane q (q uniform)
+__device__ __forceinline__ double zz_readlane_f64(double v, int q) {
+    const unsigned long long u = __double_as_longlong(v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(u & 0xffffffffu), q);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(u >> 32), q);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
 __device__ __forceinline__ unsigned long long zz_lane_lt_mask() {
     const int l = threadIdx.x & 63;
     return l ? (~0ull >> (64 - l)) : 0ull;
@@ -120,6 +144,67 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
     }
     width = __ballot(width) != 0ull;
 
+    // Fast path, registers only: the K largest keys by K rounds of a wave maximum.
+    // It stands when no other expert's hi reaches the K-th key's lo (the K are the
+    // set) and, in key order, every interval lies strictly above all later ones (the
+    // key order is the true order). Otherwise the general passes below decide.
+    bool fast = false;
+    int contested = 0;                                   // lfm: a selection within expf's tolerance
+    {
+        // key order = (float part desc, expert asc): a DPP wave maximum of the float
+        // part, then the lowest expert holding it by ballot (e = lane + 64 j)
+        unsigned kh[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; j++) kh[j] = (unsigned)(key[j] >> 32);
+        int sel_e = 0;                                     // lane r < K: the r-th key's expert
+        unsigned top = 0u;
+        for (int r = 0; r < K; r++) {
+            unsigned m = 0u;
+#pragma unroll
+            for (int j = 0; j < EPL; j++) m = kh[j] > m ? kh[j] : m;
+            m = zz_wave_umax(m);
+            int e = -1;
+#pragma unroll
+            for (int j = 0; j < EPL; j++) {
+                const unsigned long long b = __ballot(kh[j] == m);
+                if (e < 0 && b) e = (int)__ffsll((long long)b) - 1 + 64 * j;
+            }
+            if (l == (e & 63)) kh[e >> 6] = 0u;            // taken (valid keys are > 0)
+            if (l == r) sel_e = e;
+            top = m;
+        }
+        const double lk0 = (double)zz_unord32(top);
+        int nc = 0;
+#pragma unroll
+        for (int j = 0; j < EPL; j++) nc += __popcll(__ballot(l + 64 * j < E && hi[j] >= lk0));
+        if (top != 0u && nc == K) {
+            // lane r < K fetches its expert's interval from the owning lane
+            double slo = 0.0, shi = 0.0;
+            const int own = sel_e & 63, jj = sel_e >> 6;
+#pragma unroll
+            for (int j = 0; j < EPL; j++) {
+                const double a = __shfl(lo[j], own, 64), b = __shfl(hi[j], own, 64);
+                if (jj == j) { slo = a; shi = b; }
+            }
+            // every interval strictly above all later ones: hi of rank q < lo of each
+            // earlier rank, i.e. a suffix maximum of hi against lo
+            double later = -INFINITY;
+            for (int q = K - 1; q >= 1; q--) {
+                const double hq = zz_readlane_f64(shi, q);
+                if (l < q) later = hq > later ? hq : later;
+            }
+            const bool ok = l >= K - 1 || later < slo;
+            if (__ballot(!ok) == 0ull) {
+                fast = true;
+                if (l < K) {
+                    h.idx[l] = sel_e;
+                    h.topv[l] = (float)(0.5 * (slo + shi));
+                }
+            }
+        }
+    }
+
+    if (!fast) {
     // 1. the k-th largest lane maximum (keys are distinct; empty lanes hold 0)
     unsigned long long mk = 0ull;
 #pragma unroll
@@ -186,7 +271,6 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
         any = __ballot(any) != 0ull;
         zz_wave_sync_lds();
     }
-    int contested = 0;
     if (any) {
         if (a.gating == ZZ_GATE_SOFTMAX_PES) {
             const float *xn = a.xn + (size_t)s * a.D;
@@ -226,6 +310,7 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
             h.topv[rk] = (float)me;
         }
     }
+    }                                                    // general passes
     zz_wave_sync_lds();
 
     // gate weights: per slot in parallel, their sum serially in slot order as the
