@@ -27,28 +27,45 @@
 // gemma4.c:763-764; lfm/maple: x) is quantised q8_0-style (q40.h:124-138), one
 // 32-block per thread, with per-block integer sums; for tq2 the Sx total
 // (tq2.h:98-108) is summed serially in the reference's order.
+#define PREP_R 8           // float4 per thread: D <= 8192
 __global__ __launch_bounds__(256) void zz_prep_kernel(ZzPrepArgs a) {
-    const int s = blockIdx.x, D = a.D, tid = threadIdx.x, nb = D / ZZ_BLK;
+    const int s = blockIdx.x, D = a.D, tid = threadIdx.x, nb = D / ZZ_BLK, n4 = D / 4;
     const float *x = a.in + (size_t)s * D;
     __shared__ double red[4];
     __shared__ float xs_l[ZZ_MAXD / ZZ_BLK];
     __shared__ int xsum_l[ZZ_MAXD / ZZ_BLK];
     __shared__ float cert;
-    float r = 1.0f;
+    // the row, its norm weights and router scale: every load issued first. Float4 i
+    // of the row is value 4i..4i+3: block i/8, lane i%8 of the block's 8 lanes.
+    const int R = (n4 + 255) >> 8;
+    float4 xv[PREP_R], wv[PREP_R], sv[PREP_R];
+#pragma unroll
+    for (int k = 0; k < PREP_R; k++) {
+        if (k >= R) break;
+        const int i = min(tid + 256 * k, n4 - 1);
+        xv[k] = *(const float4 *)(x + 4 * i);
+        if (a.gemma) wv[k] = *(const float4 *)(a.pre_ln + 4 * i);
+        if (a.gemma && a.router_scale) sv[k] = *(const float4 *)(a.router_scale + 4 * i);
+    }
     if (a.route_eidx && tid == 0) {                // dense branch: one expert, weight 1
         a.route_eidx[s] = 0;
         a.route_ewt[s] = 1.0f;
     }
+    float r = 1.0f;
     if (a.gemma) {
         double sq = 0.0;
-        for (int i = 4 * tid; i < D; i += 1024) {
-            const float4 v = *(const float4 *)(x + i);
-            sq += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+#pragma unroll
+        for (int k = 0; k < PREP_R; k++) {
+            if (k >= R) break;
+            if (tid + 256 * k < n4) {
+                const float4 v = xv[k];
+                sq += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+            }
         }
         sq = zz_block_sum(sq, red);
-        // GPU: each term in <= D/1024 + 12 roundings; reference: D - 1 in order.
+        // GPU: each term in <= R + 12 roundings; reference: D - 1 in order.
         // All terms are non-negative, so the exact sum is <= sq / (1 - g_m).
-        const double m = (double)(D / 1024 + 12);
+        const double m = (double)(R + 12);
         const double g = zz_gamma(D, ZZ_U64) + zz_gamma(m, ZZ_U64);
         const double b = g * sq / (1.0 - zz_gamma(m, ZZ_U64)) * 1.0000001 + 1e-300;
         const float lo = (float)((sq - b) / (double)D), hi = (float)((sq + b) / (double)D);
@@ -64,35 +81,44 @@ __global__ __launch_bounds__(256) void zz_prep_kernel(ZzPrepArgs a) {
         }
         __syncthreads();
         r = 1.0f / sqrtf(cert + a.eps);
-        const float rs = 1.0f / sqrtf((float)D);
-        for (int i = 4 * tid; a.router_scale && i < D; i += 1024) {   // no router: no xn
-            const float4 v = *(const float4 *)(x + i), sc = *(const float4 *)(a.router_scale + i);
-            *(float4 *)(a.xn + (size_t)s * D + i) =
-                make_float4((v.x * r) * (sc.x * rs), (v.y * r) * (sc.y * rs), (v.z * r) * (sc.z * rs),
-                            (v.w * r) * (sc.w * rs));
-        }
-    }
-    for (int b = tid; b < nb; b += 256) {
-        float v[ZZ_BLK];
+        if (a.router_scale) {                      // the router input (no router: no xn)
+            const float rs = 1.0f / sqrtf((float)D);
 #pragma unroll
-        for (int j = 0; j < ZZ_BLK; j += 4) {
-            const float4 t = *(const float4 *)(x + b * ZZ_BLK + j);
-            v[j] = t.x; v[j + 1] = t.y; v[j + 2] = t.z; v[j + 3] = t.w;
-        }
-        if (a.gemma) {
-#pragma unroll
-            for (int j = 0; j < ZZ_BLK; j += 4) {
-                const float4 w = *(const float4 *)(a.pre_ln + b * ZZ_BLK + j);
-                v[j] = (v[j] * r) * w.x; v[j + 1] = (v[j + 1] * r) * w.y;
-                v[j + 2] = (v[j + 2] * r) * w.z; v[j + 3] = (v[j + 3] * r) * w.w;
+            for (int k = 0; k < PREP_R; k++) {
+                if (k >= R) break;
+                const int i = tid + 256 * k;
+                if (i < n4) {
+                    const float4 v = xv[k], sc = sv[k];
+                    *(float4 *)(a.xn + (size_t)s * D + 4 * i) =
+                        make_float4((v.x * r) * (sc.x * rs), (v.y * r) * (sc.y * rs), (v.z * r) * (sc.z * rs),
+                                    (v.w * r) * (sc.w * rs));
+                }
             }
         }
+    }
+    // q8_0 of the expert input, 8 lanes per block (every lane of a wave takes part)
+#pragma unroll
+    for (int k = 0; k < PREP_R; k++) {
+        if (k >= R) break;
+        const int i = tid + 256 * k;
+        float4 v = xv[k];
+        if (a.gemma) {
+            const float4 w = wv[k];
+            v = make_float4((v.x * r) * w.x, (v.y * r) * w.y, (v.z * r) * w.z, (v.w * r) * w.w);
+        }
+        float d;
         int qs;
-        const float d = zz_quant_block(v, a.xq + (size_t)s * D + b * ZZ_BLK, &qs);
-        a.xs[(size_t)s * nb + b] = d;
-        a.xsum[(size_t)s * nb + b] = qs;
-        xs_l[b] = d;
-        xsum_l[b] = qs;
+        const unsigned pk = zz_quant8(v, &d, &qs);
+        if (i < n4) {
+            *(unsigned *)(a.xq + (size_t)s * D + 4 * i) = pk;
+            if ((i & 7) == 0) {
+                const int b = i >> 3;
+                a.xs[(size_t)s * nb + b] = d;
+                a.xsum[(size_t)s * nb + b] = qs;
+                xs_l[b] = d;
+                xsum_l[b] = qs;
+            }
+        }
     }
     if (a.xt) {
         __syncthreads();
