@@ -34,6 +34,10 @@
                                    weight 1 (its record holds mlp_gate|mlp_up|mlp_down);
                                    pre_ln = pre_ffn_ln, post_ln = post_ffn_ln1, applied
                                    as gemma's two ffn_ln2 norms are                    */
+#define ZZ_GATE_GROUPED      4  /* ling.c:705-789: 8-accumulator double logits, sigmoid,
+                                   +bias; groups of E/n_group ranked by their top-2 sum,
+                                   the best topk_group kept, top-k inside them; weights
+                                   the unbiased sigmoid, normalised, x routed_scaling   */
 
 /* activation between gate/up and down */
 #define ZZ_ACT_GEGLU_TANH   0   /* gemma4.c:432-434, 644 */
@@ -52,6 +56,7 @@ typedef struct zz_moe_desc {
     float eps;                /* gemma rmsnorm epsilon                                */
     float routed_scaling;     /* lfm                                                  */
     float clamp;              /* maple mlp_clamp                                      */
+    int n_group, topk_group;  /* ZZ_GATE_GROUPED: expert groups, groups kept          */
 } zz_moe_desc;
 
 typedef struct zz_moe_weights {   /* host pointers, copied at layer creation        */

@@ -450,6 +450,50 @@ void orc_route(const orc_cfg *c, const orc_weights *w, const float *x,
             for (int j = 0; j < K; j++) wts[j] /= (sum + 1e-6f);
         for (int j = 0; j < K; j++) wts[j] *= c->routed_scaling;
         free(sg);
+    } else if (c->gating == ORC_GATE_LING) {
+        /* ling.c:705-789: eight double accumulators (exact products), sigmoid, the bias
+         * for selection only; groups ranked by the sum of their two best biased scores,
+         * the best topk_group kept (strict '>', lower group on ties); top-K among their
+         * experts in ascending expert order; weights the unbiased sigmoid */
+        int NG = c->n_group, TG = c->topk_group, EG = E / NG;
+        float *rwt = (float *)malloc(sizeof(float) * (size_t)E);
+        float *rsel = (float *)malloc(sizeof(float) * (size_t)E);
+        for (int e = 0; e < E; e++) {
+            const float *r = w->router + (size_t)e * D;
+            double s8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            int i = 0;
+            for (; i + 8 <= D; i += 8)
+                for (int k = 0; k < 8; k++) s8[k] += (double)r[i + k] * x[i + k];
+            for (; i < D; i++) s8[0] += (double)r[i] * x[i];
+            double v = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+            rwt[e] = 1.0f / (1.0f + expf(-(float)v));
+            rsel[e] = rwt[e] + ((c->use_bias && w->bias) ? w->bias[e] : 0.0f);
+            if (logits_out) logits_out[e] = (float)v;
+        }
+        float gs[64], topg[64];
+        int keep[64];
+        unsigned char live[64] = {0};
+        for (int g = 0; g < NG; g++) {
+            float a = -INFINITY, bb = -INFINITY;
+            const float *sg = rsel + (size_t)g * EG;
+            for (int i = 0; i < EG; i++) {
+                if (sg[i] > a) { bb = a; a = sg[i]; }
+                else if (sg[i] > bb) bb = sg[i];
+            }
+            gs[g] = EG > 1 ? a + bb : a;
+        }
+        for (int j = 0; j < TG; j++) { keep[j] = -1; topg[j] = -INFINITY; }
+        for (int g = 0; g < NG; g++) topk_insert(gs[g], g, TG, topg, keep);
+        for (int j = 0; j < TG; j++) if (keep[j] >= 0) live[keep[j]] = 1;
+        for (int e = 0; e < E; e++)
+            if (live[e / EG]) topk_insert(rsel[e], e, K, topv, idx);
+        float sum = 0.0f;
+        for (int j = 0; j < K; j++) { wts[j] = rwt[idx[j]]; sum += wts[j]; }
+        if (c->norm_topk && K > 1)
+            for (int j = 0; j < K; j++) wts[j] /= (sum + 1e-20f);
+        for (int j = 0; j < K; j++) wts[j] *= c->routed_scaling;
+        free(rwt);
+        free(rsel);
     } else {
         /* maple.c:744 (w_dot_f32 logits, 400-410) + route_row 582-601 */
         for (int e = 0; e < E; e++) {
@@ -499,6 +543,9 @@ int orc_moe_layer(const orc_cfg *c, const orc_weights *w, const float *in, int S
                   float *out, int *eidx, float *ewt, int *uniq, int *nu_out, orc_dump *dump) {
     int D = c->D, MI = c->MI, E = c->E, K = c->K;
     if (D % 64 || MI % 64 || K < 1 || K > 64 || K > E || S < 0) return -1;
+    if (c->gating == ORC_GATE_LING && (c->n_group < 1 || c->n_group > 64 || E % c->n_group ||
+                                       c->topk_group < 1 || c->topk_group > c->n_group))
+        return -1;
     int64_t gb = orc_tensor_bytes(c->fmt_gate, MI, D), ub = orc_tensor_bytes(c->fmt_up, MI, D);
     int64_t db = orc_tensor_bytes(c->fmt_down, D, MI);
     if (gb < 0 || ub < 0 || db < 0 || gb + ub + db > w->esz) return -1;

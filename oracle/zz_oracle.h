@@ -33,6 +33,7 @@ extern "C" {
 #define ORC_GATE_GEMMA 0    /* gemma4.c:581-613  rmsnorm->scale->f32 logits->topk->softmax(K)*pes */
 #define ORC_GATE_LFM   1    /* lfm25.c:636-668   double logits->sigmoid->(+bias) topk->norm*scale  */
 #define ORC_GATE_MAPLE 2    /* maple.c:582-601   double logits->topk->softmax(K)                    */
+#define ORC_GATE_LING  4    /* ling.c:705-789    8-acc double logits->sigmoid(+bias)->groups->topk  */
 
 /* activation kinds */
 #define ORC_ACT_GEGLU_TANH 0   /* gemma4.c:432-434 */
@@ -49,6 +50,7 @@ typedef struct {
     float eps;              /* gemma rmsnorm epsilon                          */
     float routed_scaling;   /* lfm                                            */
     float clamp;            /* maple mlp_clamp                                */
+    int n_group, topk_group;/* ling: expert groups, groups kept               */
 } orc_cfg;
 
 typedef struct {

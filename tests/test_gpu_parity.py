@@ -38,7 +38,7 @@ def gpu_layer(L):
     m = zz.MoeLayer(L.D, L.MI, L.E, L.K, L.gating, L.act, L.fmts, L.router, L.router_scale,
                     L.pes, L.bias, L.pre_ln, L.post_ln, norm_topk=L.norm_topk,
                     use_bias=L.use_bias, eps=L.eps, routed_scaling=L.routed_scaling,
-                    clamp=L.clamp)
+                    clamp=L.clamp, n_group=L.n_group, topk_group=L.topk_group)
     m.upload_all(L.experts)
     return m
 
@@ -251,6 +251,22 @@ def test_config4_maple(dev, S, layer_cache):
     m = gpu_layer(L)
     try:
         check_layer(m, L, x, want)
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("S", [1, 4, 8, 64])
+def test_ling_grouped_router(dev, S, layer_cache):
+    """A13: Ling's grouped router (ling.c:705-789) on the decode (S <= 4), wave-logit
+    (S < 16) and exact-logit (S >= 16) paths: ids exact, weights 1e-4, outputs 1e-3."""
+    say("ling grouped S", S)
+    L = layer_cache("ling", seed=5)
+    x = Z.make_input(L, S, 60 + S)
+    want = Z.oracle_moe(L, x)
+    m = gpu_layer(L)
+    try:
+        _, _, _, err = check_layer(m, L, x, want)
+        say(f"  rel L2 {err:.2e}")
     finally:
         m.close()
 

@@ -356,7 +356,9 @@ def test_layer_golden_bit_exact(name, layer_cache):
 
 @pytest.mark.parametrize("kind,kw,S", [("gemma", dict(E=24, D=1024, MI=512), 33),
                                        ("lfm", dict(E=12, fmts=(2, 2, 2), D=1024, MI=768), 17),
-                                       ("maple", dict(E=40, D=1024, MI=512), 29)])
+                                       ("maple", dict(E=40, D=1024, MI=512), 29),
+                                       ("ling", dict(E=64, D=1024, MI=256), 40),
+                                       ("ling", dict(E=128, D=512, MI=128, fmts=(2, 2, 2)), 9)])
 def test_layer_vs_compiled_reference(kind, kw, S):
     """Live diff against oracle/_ref at shapes the fixtures do not cover."""
     if Z.ref_lib("gemma4") is None:
@@ -380,3 +382,25 @@ def test_fp32_tier_tolerance_is_discriminating(layer_cache):
     assert Z.rel_l2(bad, good) > 1e-2
     L3 = Z.make_layer("gemma", seed=2, E=16, K=7)
     assert Z.rel_l2(Z.oracle_moe(L3, x).out, good) > 1e-2
+
+
+def test_ling_grouped_router_keeps_only_live_groups():
+    """A13 (ling.c:705-789): every selected expert lies in one of topk_group groups,
+    and those groups are the ones with the largest top-2 biased scores (recomputed
+    here in numpy from the oracle's own logits, lower group on ties)."""
+    L = Z.make_layer("ling", seed=31, E=128, D=512, MI=128)
+    x = Z.make_input(L, 24, 31)
+    r = Z.oracle_moe(L, x, dump=True)
+    EG = L.E // L.n_group
+    for s_ in range(24):
+        v = r.dump["logits"][s_].astype(np.float32)
+        sg = (np.float32(1) / (np.float32(1) + np.exp(-v).astype(np.float32))).astype(np.float32)
+        sel = (sg + L.bias).astype(np.float32)
+        top2 = np.sort(sel.reshape(L.n_group, EG), axis=1)[:, -2:]
+        gs = (top2[:, 1] + top2[:, 0]).astype(np.float32)
+        keep = sorted(range(L.n_group), key=lambda g: (-gs[g], g))[:L.topk_group]
+        ids = r.eidx[s_ * L.K:(s_ + 1) * L.K]
+        assert set(int(e) // EG for e in ids) <= set(keep)
+        live = np.concatenate([np.arange(g * EG, (g + 1) * EG) for g in keep])
+        want = sorted(live, key=lambda e: (-sel[e], e))[:L.K]
+        assert list(ids) == want

@@ -14,7 +14,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_DIR = os.path.join(ROOT, "oracle")
 
 FMT_Q40, FMT_Q80, FMT_TQ2 = 1, 2, 3
-GATE_GEMMA, GATE_LFM, GATE_MAPLE = 0, 1, 2
+GATE_GEMMA, GATE_LFM, GATE_MAPLE, GATE_LING = 0, 1, 2, 4   # the library's ZZ_GATE_* codes
 ACT_GEGLU_TANH, ACT_SWIGLU, ACT_SWIGLU_CL = 0, 1, 2
 
 f32p = C.POINTER(C.c_float)
@@ -38,7 +38,8 @@ class OrcCfg(C.Structure):
                 ("gating", C.c_int), ("act", C.c_int),
                 ("fmt_gate", C.c_int), ("fmt_up", C.c_int), ("fmt_down", C.c_int),
                 ("norm_topk", C.c_int), ("use_bias", C.c_int),
-                ("eps", C.c_float), ("routed_scaling", C.c_float), ("clamp", C.c_float)]
+                ("eps", C.c_float), ("routed_scaling", C.c_float), ("clamp", C.c_float),
+                ("n_group", C.c_int), ("topk_group", C.c_int)]
 
 
 class OrcWeights(C.Structure):
@@ -156,6 +157,8 @@ class Layer:
     eps: float = 1e-6
     routed_scaling: float = 1.0
     clamp: float = 7.0
+    n_group: int = 1
+    topk_group: int = 1
     router: np.ndarray = None
     router_scale: np.ndarray = None
     pes: np.ndarray = None
@@ -170,7 +173,7 @@ class Layer:
     def cfg(self):
         return OrcCfg(self.D, self.MI, self.E, self.K, self.gating, self.act,
                       self.fmts[0], self.fmts[1], self.fmts[2], self.norm_topk, self.use_bias,
-                      self.eps, self.routed_scaling, self.clamp)
+                      self.eps, self.routed_scaling, self.clamp, self.n_group, self.topk_group)
 
     def weights(self):
         return OrcWeights(ptr(self.router), ptr(self.router_scale), ptr(self.pes),
@@ -229,6 +232,15 @@ def make_layer(kind, seed=1, E=None, D=None, MI=None, K=None, zipf=False, fmts=N
                   norm_topk=1, use_bias=1, routed_scaling=1.0)
         L.router = _normal(rng, (E, D))
         L.bias = (0.1 * rng.standard_normal(E)).astype(np.float32)
+    elif kind == "ling":
+        # Ling-3.0-tiny's router (ling.c:705-789): 128 experts in 8 groups, the best 4
+        # groups, top-8; SwiGLU experts of one format per layer
+        D, MI, E, K = D or 2048, MI or 512, E or 128, K or 8
+        L = Layer(D, MI, E, K, GATE_LING, ACT_SWIGLU, fmts or (FMT_Q40,) * 3, norm_topk=1,
+                  use_bias=1, routed_scaling=2.5, n_group=8 if E % 8 == 0 else 1,
+                  topk_group=4 if E % 8 == 0 else 1)
+        L.router = _normal(rng, (E, D), 0.05)
+        L.bias = (0.05 * rng.standard_normal(E)).astype(np.float32)
     elif kind == "maple":
         D, MI, E, K = D or 2048, MI or 768, E or 256, K or 8
         L = Layer(D, MI, E, K, GATE_MAPLE, ACT_SWIGLU_CL, (FMT_TQ2,) * 3, norm_topk=1, clamp=7.0)
@@ -315,6 +327,14 @@ def ref_moe(L, x):
                              C.c_float(L.routed_scaling), ptr(L.router), ptr(L.bias),
                              ptr(L.experts), C.c_int64(L.esz), ptr(x), S, ptr(out), ptr(eidx),
                              ptr(ewt), ptr(uniq), C.byref(nu))
+    elif L.gating == GATE_LING:
+        lib = ref_lib("ling")
+        if lib is None or len(set(L.fmts)) != 1:
+            return None
+        rc = lib.ref_ling_moe(L.D, L.MI, L.E, L.K, L.fmts[0], L.n_group, L.topk_group, L.norm_topk,
+                              C.c_float(L.routed_scaling), ptr(L.router), ptr(L.bias),
+                              ptr(L.experts), C.c_int64(L.esz), ptr(x), S, ptr(out), ptr(eidx),
+                              ptr(ewt), ptr(uniq), C.byref(nu))
     else:
         lib = ref_lib("maple")
         if lib is None:

@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(PKG_DIR, "libzzmoe.so")
 
 GPU_FMT_Q40, GPU_FMT_Q80, GPU_FMT_TQ2, GPU_FMT_Q4A = 1, 2, 3, 4
 ZZ_GATE_SOFTMAX_PES, ZZ_GATE_SIGMOID_BIAS, ZZ_GATE_SOFTMAX_TOPK, ZZ_GATE_DENSE = 0, 1, 2, 3
+ZZ_GATE_GROUPED = 4
 ZZ_ACT_GEGLU_TANH, ZZ_ACT_SWIGLU, ZZ_ACT_SWIGLU_CLAMP = 0, 1, 2
 
 # Every symbol include/zz_gpu.h and include/zz_moe.h declare.
@@ -48,7 +49,8 @@ class ZzMoeDesc(C.Structure):
                 ("gating", C.c_int), ("act", C.c_int),
                 ("fmt_gate", C.c_int), ("fmt_up", C.c_int), ("fmt_down", C.c_int),
                 ("norm_topk", C.c_int), ("use_bias", C.c_int),
-                ("eps", C.c_float), ("routed_scaling", C.c_float), ("clamp", C.c_float)]
+                ("eps", C.c_float), ("routed_scaling", C.c_float), ("clamp", C.c_float),
+                ("n_group", C.c_int), ("topk_group", C.c_int)]
 
 
 class ZzMoeWeights(C.Structure):
@@ -177,9 +179,9 @@ class MoeLayer:
 
     def __init__(self, D, MI, E, K, gating, act, fmts, router, router_scale=None, pes=None,
                  bias=None, pre_ln=None, post_ln=None, norm_topk=1, use_bias=0, eps=1e-6,
-                 routed_scaling=1.0, clamp=7.0):
+                 routed_scaling=1.0, clamp=7.0, n_group=1, topk_group=1):
         self.desc = ZzMoeDesc(D, MI, E, K, gating, act, fmts[0], fmts[1], fmts[2], norm_topk,
-                              use_bias, eps, routed_scaling, clamp)
+                              use_bias, eps, routed_scaling, clamp, n_group, topk_group)
         keep = [np.ascontiguousarray(a, np.float32) if a is not None else None
                 for a in (router, router_scale, pes, bias, pre_ln, post_ln)]
         w = ZzMoeWeights(*(_p(a, _f32p) for a in keep))

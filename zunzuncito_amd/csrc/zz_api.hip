@@ -211,8 +211,12 @@ static int desc_ok(const zz_moe_desc *d) {
     if (!d) return 0;
     if (d->D <= 0 || d->MI <= 0 || d->D % 64 || d->MI % 64 || d->D > ZZ_MAXD || d->MI > ZZ_MAXD) return 0;
     if (d->E <= 0 || d->E > ZZ_MAXE || d->K < 1 || d->K > ZZ_MAXK || d->K > d->E) return 0;
-    if (d->gating < 0 || d->gating > 3 || d->act < 0 || d->act > 2) return 0;
+    if (d->gating < 0 || d->gating > 4 || d->act < 0 || d->act > 2) return 0;
     if (d->gating == ZZ_GATE_DENSE && (d->E != 1 || d->K != 1 || d->use_bias)) return 0;
+    if (d->gating == ZZ_GATE_GROUPED &&                 // ling.c:352-353
+        (d->n_group < 1 || d->n_group > ZZ_MAXGROUP || d->E % d->n_group || d->topk_group < 1 ||
+         d->topk_group > d->n_group || d->K > d->topk_group * (d->E / d->n_group)))
+        return 0;
     int f[3] = {d->fmt_gate, d->fmt_up, d->fmt_down};
     for (int i = 0; i < 3; i++)
         if (f[i] != ZZ_FMT_Q40 && f[i] != ZZ_FMT_Q80 && f[i] != ZZ_FMT_TQ2) return 0;
@@ -495,6 +499,7 @@ static ChunkArgs chunk_args(Layer *L, const float *d_in, int S) {
 
     ZzTopkArgs &ta = c.ta;
     ta.D = d.D; ta.E = d.E; ta.K = d.K; ta.gating = d.gating; ta.norm_topk = d.norm_topk;
+    ta.n_group = d.n_group; ta.topk_group = d.topk_group;
     ta.routed_scaling = d.routed_scaling; ta.cen = w.cen; ta.bnd = w.bnd; ta.router = L->router;
     ta.xn = w.xn; ta.bias = d.use_bias ? L->bias : nullptr; ta.pes = L->pes; ta.eidx = w.eidx;
     ta.ewt = w.ewt; ta.topv = w.topv; ta.contested = w.contested; ta.diag = g_diag;

@@ -23,6 +23,8 @@
 #define ZZ_GATE_SIGMOID_BIAS 1  // lfm25.c:636-668
 #define ZZ_GATE_SOFTMAX_TOPK 2  // maple.c:582-601
 #define ZZ_GATE_DENSE 3         // gemma4.c:1012-1020: the dense MLP branch, no router
+#define ZZ_GATE_GROUPED 4       // ling.c:705-789: grouped sigmoid top-k
+#define ZZ_MAXGROUP 64          // expert groups of a grouped router
 
 #define ZZ_ACT_GEGLU_TANH 0     // gemma4.c:432-434
 #define ZZ_ACT_SWIGLU 1         // lfm25.c:456-458

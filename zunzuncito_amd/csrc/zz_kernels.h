@@ -31,6 +31,7 @@ struct ZzLogitArgs {
 
 struct ZzTopkArgs {
     int D, E, K, gating, norm_topk;
+    int n_group, topk_group;    // grouped router
     float routed_scaling;
     const double *cen, *bnd;    // [S, E]
     const float *router, *xn;   // gemma refinement

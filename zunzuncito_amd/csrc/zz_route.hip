@@ -150,7 +150,8 @@ __global__ __launch_bounds__(256) void zz_logits_kernel(ZzLogitArgs a) {
 //   gemma  v = v + fl(w_k * xn_k) in fp32, unfused (gemma4.c:600-601 as compiled:
 //          vmulps then in-order vaddss);
 //   lfm / maple  v = v + (double)w_k * x_k in double, then (float)v
-//          (lfm25.c:646-647, maple.c:400-410).
+//          (lfm25.c:646-647, maple.c:400-410);
+//   ling   eight double accumulators by k % 8, combined pairwise (ling.c:722-727).
 // A workgroup is 16 tokens x 16 experts; 64-wide K chunks of both operands are
 // staged in LDS so each router row and each input row is read once per tile.
 // Many independent chains (one per thread) hide the add latency.
@@ -185,6 +186,8 @@ __global__ __launch_bounds__(256) void zz_logits_exact_kernel(ZzLogitArgs a) {
     __syncthreads();
     float vf = 0.0f;
     double vd = 0.0;
+    double v8[8] = {0, 0, 0, 0, 0, 0, 0, 0};         // grouped: ling.c's 8 accumulators
+    const bool grp = a.gating == ZZ_GATE_GROUPED;
     int buf = 0;
     for (int k0 = 0; k0 < D; k0 += LG_K) {
         const int k1 = min(k0 + LG_K, D - LG_K);    // the last chunk reloads itself
@@ -202,6 +205,21 @@ __global__ __launch_bounds__(256) void zz_logits_exact_kernel(ZzLogitArgs a) {
                 vf = vf + w4.y * x4.y;
                 vf = vf + w4.z * x4.z;
                 vf = vf + w4.w * x4.w;
+            }
+        } else if (grp) {
+            // element k0 + k goes to accumulator k % 8 (k0 is a multiple of LG_K)
+#pragma unroll 16
+            for (int k = 0; k < LG_K; k += 8) {
+                const float4 xa = *(const float4 *)(xr + k), wa = *(const float4 *)(wr + k);
+                const float4 xb = *(const float4 *)(xr + k + 4), wb = *(const float4 *)(wr + k + 4);
+                v8[0] = v8[0] + (double)wa.x * (double)xa.x;
+                v8[1] = v8[1] + (double)wa.y * (double)xa.y;
+                v8[2] = v8[2] + (double)wa.z * (double)xa.z;
+                v8[3] = v8[3] + (double)wa.w * (double)xa.w;
+                v8[4] = v8[4] + (double)wb.x * (double)xb.x;
+                v8[5] = v8[5] + (double)wb.y * (double)xb.y;
+                v8[6] = v8[6] + (double)wb.z * (double)xb.z;
+                v8[7] = v8[7] + (double)wb.w * (double)xb.w;
             }
         } else {
 #pragma unroll 16
@@ -227,6 +245,7 @@ __global__ __launch_bounds__(256) void zz_logits_exact_kernel(ZzLogitArgs a) {
             if (a.bias) vf = vf + a.bias[e];       // harness logit offset, after the dot
             a.cen[o] = (double)vf;
         } else {
+            if (grp) vd = ((v8[0] + v8[1]) + (v8[2] + v8[3])) + ((v8[4] + v8[5]) + (v8[6] + v8[7]));
             a.cen[o] = (double)(float)vd;
         }
         a.bnd[o] = 0.0;                             // exact: no interval

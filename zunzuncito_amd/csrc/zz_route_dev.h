@@ -218,7 +218,14 @@ __device__ void zz_logit_wave_f64(const ZzLogitArgs &a, int s, int e) {
         float lo = (float)(c - b), hi = (float)(c + b), v = lo;
         if (lo != hi) {
             double r = 0.0;                      // serial replay, reference order
-            for (int i = 0; i < D; i++) r += (double)w[i] * (double)xv[i];
+            if (a.gating == ZZ_GATE_GROUPED) {   // ling.c:722-727: 8 accumulators, D % 8 == 0
+                double q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                for (int i = 0; i < D; i += 8)
+                    for (int k = 0; k < 8; k++) q[k] += (double)w[i + k] * (double)xv[i + k];
+                r = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+            } else {
+                for (int i = 0; i < D; i++) r += (double)w[i] * (double)xv[i];
+            }
             v = (float)r;
             atomicAdd(a.diag + 1, 1u);
         }

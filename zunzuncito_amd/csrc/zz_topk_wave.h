@@ -104,7 +104,7 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
     double *clo = (double *)(ck + E), *chi = clo + E;
     int *ci = (int *)(chi + E);
     const double *cen = a.cen + (size_t)s * E, *bnd = a.bnd + (size_t)s * E;
-    const bool sig = a.gating == ZZ_GATE_SIGMOID_BIAS;
+    const bool sig = a.gating == ZZ_GATE_SIGMOID_BIAS || a.gating == ZZ_GATE_GROUPED;
     const unsigned long long ltm = zz_lane_lt_mask();
 
     // intervals and keys; every load is issued before any is used
@@ -143,13 +143,78 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
         if (e >= E) lo[j] = hi[j] = -INFINITY;
     }
     width = __ballot(width) != 0ull;
+    int contested = 0;                                   // lfm: a selection within expf's tolerance
+
+    // Grouped router (ling.c:734-760): each group's top-2 sum as an interval (the two
+    // largest lo's, the two largest hi's, widened by the reference's float add), the
+    // best topk_group groups by that sum (ties to the lower group), then the experts of
+    // the other groups leave the running. A group set the intervals cannot fix is
+    // taken by centres and the token flagged, as lfm's near-ties are.
+    if (a.gating == ZZ_GATE_GROUPED) {
+        const int NG = a.n_group, TG = a.topk_group, EG = E / NG;
+#pragma unroll
+        for (int j = 0; j < EPL; j++) {
+            const int e = l + 64 * j;
+            if (e < E) {
+                clo[e] = lo[j];
+                chi[e] = hi[j];
+            }
+        }
+        zz_wave_sync_lds();
+        double glo = -INFINITY, ghi = -INFINITY;
+        if (l < NG) {
+            double a1 = -INFINITY, a2 = -INFINITY, b1 = -INFINITY, b2 = -INFINITY;
+            for (int i = 0; i < EG; i++) {
+                const double x = clo[l * EG + i], y = chi[l * EG + i];
+                if (x > a1) { a2 = a1; a1 = x; } else if (x > a2) a2 = x;
+                if (y > b1) { b2 = b1; b1 = y; } else if (y > b2) b2 = y;
+            }
+            glo = EG > 1 ? a1 + a2 : a1;
+            ghi = EG > 1 ? b1 + b2 : b1;
+            if (EG > 1) {                                // fl(a + b): half an ulp each way
+                const double u = (double)ulp_of((float)fmax(fabs(glo), fabs(ghi)));
+                if (u == u) {                            // not for infinite sums
+                    glo -= u;
+                    ghi += u;
+                }
+            }
+        }
+        // the TG-th largest lower bound (value desc, group asc)
+        int rk = 0;
+        for (int q = 0; q < NG; q++) {
+            const double gq = zz_readlane_f64(glo, q);
+            rk += (gq > glo) | ((gq == glo) & (q < l));
+        }
+        const unsigned long long at = __ballot(l < NG && rk == TG - 1);
+        const double lg = zz_readlane_f64(glo, (int)__ffsll((long long)at) - 1);
+        const unsigned long long cand = __ballot(l < NG && ghi >= lg);
+        unsigned long long live = cand;
+        if (__popcll(cand) != TG) {                      // not fixed: centres, flagged
+            const double gc = 0.5 * (glo + ghi);
+            int rc = 0;
+            for (int q = 0; q < NG; q++) {
+                const double cq = zz_readlane_f64(gc, q);
+                rc += (cq > gc) | ((cq == gc) & (q < l));
+            }
+            live = __ballot(l < NG && rc < TG);
+            contested = 1;
+        }
+#pragma unroll
+        for (int j = 0; j < EPL; j++) {
+            const int e = l + 64 * j;
+            if (e < E && !((live >> (e / EG)) & 1ull)) {
+                lo[j] = hi[j] = -INFINITY;
+                key[j] = 0ull;
+            }
+        }
+        zz_wave_sync_lds();                              // clo / chi are reused below
+    }
 
     // Fast path, registers only: the K largest keys by K rounds of a wave maximum.
     // It stands when no other expert's hi reaches the K-th key's lo (the K are the
     // set) and, in key order, every interval lies strictly above all later ones (the
     // key order is the true order). Otherwise the general passes below decide.
     bool fast = false;
-    int contested = 0;                                   // lfm: a selection within expf's tolerance
     {
         // key order = (float part desc, expert asc): a DPP wave maximum of the float
         // part, then the lowest expert holding it by ballot (e = lane + 64 j)
@@ -328,6 +393,10 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
         float out;
         if (a.gating == ZZ_GATE_SOFTMAX_PES) {                     // gemma4.c:609-612
             out = (wj / sum) * pj;
+        } else if (a.gating == ZZ_GATE_GROUPED) {                  // ling.c:783-788
+            float t = wj;
+            if (a.norm_topk && K > 1) t /= (sum + 1e-20f);
+            out = t * a.routed_scaling;
         } else if (sig) {                                          // lfm25.c:661-667
             float t = wj;
             if (a.norm_topk) t /= (sum + 1e-6f);
