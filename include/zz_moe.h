@@ -119,12 +119,16 @@ int zz_moe_forward_end(int layer, float *out, int *eidx, float *ewt);
  * xq/xs [S, D] / [S, D/32]: the int8 expert input; hq/hs [S*K, MI] / [S*K, MI/32]:
  * the int8 hidden by (token, slot); dispatch: uniq[E] union order (nu is set),
  * and for union entry u the tokens rows[offs[u] .. offs[u+1]) ascending with
- * their top-k slots (offs[nu+1], rows[S*K], slots[S*K]). */
+ * their top-k slots (offs[nu+1], rows[S*K], slots[S*K]); logits [S, E]: the
+ * router logits of the batched path (S > 4; the decode path keeps none), the
+ * reference's own values (gemma: after the bias) when S >= 16 and D % 64 == 0,
+ * interval centres otherwise. */
 typedef struct zz_moe_dump {
     int8_t *xq; float *xs;
     int8_t *hq; float *hs;
     int *uniq, *offs, *rows, *slots;
     int nu;
+    double *logits;
 } zz_moe_dump;
 int zz_moe_debug(int layer, zz_moe_dump *dump);
 

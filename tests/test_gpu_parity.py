@@ -89,6 +89,30 @@ def test_golden_layer(dev, name, layer_cache):
         m.close()
 
 
+# D % 256 == 0 takes 256-wide K chunks, other D % 64 == 0 the 64-wide ones
+@pytest.mark.parametrize("kind,kw,S", [
+    ("gemma", dict(), 64), ("gemma", dict(zipf=True, E=64), 37), ("gemma", dict(D=1088, E=64), 16),
+    ("lfm", dict(), 48), ("lfm", dict(D=1088), 20), ("maple", dict(E=16), 32),
+    ("ling", dict(), 64), ("ling", dict(D=1088, MI=256), 17)])
+def test_exact_router_logits(dev, kind, kw, S, layer_cache):
+    """At S >= 16 the batched router logits are the reference's own serial chains, bit
+    for bit: gemma's unfused fp32 chain (+ the bias), lfm/maple's double chain and
+    ling's eight double accumulators, each rounded to float as the reference does."""
+    L = layer_cache(kind, seed=3, **kw)
+    say("case", kind, kw, "S", S)
+    x = Z.make_input(L, S, 5)
+    m = gpu_layer(L)
+    try:
+        m.forward(x)
+        got = m.debug(S, logits=True)["logits"]
+        want = Z.oracle_moe(L, x, dump=True).dump["logits"]
+        assert np.array_equal(got.astype(np.float32).astype(np.float64), got), "not float-valued"
+        bad = got.astype(np.float32).view(np.uint32) != want.view(np.uint32)
+        assert not bad.any(), (int(bad.sum()), np.argwhere(bad)[:4])
+    finally:
+        m.close()
+
+
 @pytest.mark.parametrize("kind,kw", [("gemma", dict(E=8)), ("lfm", dict(E=8)),
                                      ("maple", dict(E=8, D=1024, MI=512))])
 def test_blockdots_bit_exact(dev, kind, kw, layer_cache):

@@ -61,7 +61,7 @@ class ZzMoeWeights(C.Structure):
 class ZzMoeDump(C.Structure):
     _fields_ = [("xq", _i8p), ("xs", _f32p), ("hq", _i8p), ("hs", _f32p),
                 ("uniq", _i32p), ("offs", _i32p), ("rows", _i32p), ("slots", _i32p),
-                ("nu", C.c_int)]
+                ("nu", C.c_int), ("logits", C.POINTER(C.c_double))]
 
 
 _lib = None
@@ -229,15 +229,20 @@ class MoeLayer:
         if not ok:
             raise RuntimeError(f"zz_moe_forward_dev declined: {last_error()}")
 
-    def debug(self, S):
+    def debug(self, S, logits=False):
+        """The last forward's dump (zz_moe_debug); logits=True adds the batched
+        path's router logits [S, E] as float64."""
         K, D, MI = self.K, self.D, self.MI
         d = dict(xq=np.zeros((S, D), np.int8), xs=np.zeros((S, D // 32), np.float32),
                  hq=np.zeros((S * K, MI), np.int8), hs=np.zeros((S * K, MI // 32), np.float32),
                  uniq=np.zeros(self.E, np.int32), offs=np.zeros(self.E + 1, np.int32),
                  rows=np.zeros(S * K, np.int32), slots=np.zeros(S * K, np.int32))
+        if logits:
+            d["logits"] = np.zeros((S, self.E), np.float64)
         dump = ZzMoeDump(_p(d["xq"], _i8p), _p(d["xs"], _f32p), _p(d["hq"], _i8p),
                          _p(d["hs"], _f32p), _p(d["uniq"], _i32p), _p(d["offs"], _i32p),
-                         _p(d["rows"], _i32p), _p(d["slots"], _i32p), 0)
+                         _p(d["rows"], _i32p), _p(d["slots"], _i32p), 0,
+                         _p(d["logits"], C.POINTER(C.c_double)) if logits else None)
         if not lib().zz_moe_debug(self.id, C.byref(dump)):
             raise RuntimeError(last_error())
         nu = dump.nu

@@ -707,6 +707,10 @@ extern "C" int zz_moe_debug(int id, zz_moe_dump *dp) {
         if (!zz_launch_dispatch(da, g_stream)) ZZ_FAIL("zz_moe_debug: dispatch launch failed");
     }
     ZZ_CHECK(hipStreamSynchronize(g_stream));
+    if (dp->logits) {
+        if (dec || d.gating == ZZ_GATE_DENSE) ZZ_FAIL("zz_moe_debug: no router logits on this path");
+        ZZ_CHECK(hipMemcpy(dp->logits, w.cen, sizeof(double) * S * d.E, hipMemcpyDeviceToHost));
+    }
     if (dp->xq) ZZ_CHECK(hipMemcpy(dp->xq, w.xq, (size_t)S * d.D, hipMemcpyDeviceToHost));
     if (dp->xs) ZZ_CHECK(hipMemcpy(dp->xs, w.xs, sizeof(float) * S * (d.D / ZZ_BLK), hipMemcpyDeviceToHost));
     std::vector<int> ptok(P), pslot(P), ppos(P), meta(2), uniq(d.E), uoff(d.E), ucnt(d.E);

@@ -146,110 +146,212 @@ __global__ __launch_bounds__(256) void zz_logits_kernel(ZzLogitArgs a) {
 
 // -------------------------------------------------------------------------------
 // Router logits for batches: the reference's own serial chains, exactly. One
-// thread owns one (token, expert) pair and walks k = 0..D-1 in order:
+// lane owns one (token, expert) pair and walks k = 0..D-1 in order:
 //   gemma  v = v + fl(w_k * xn_k) in fp32, unfused (gemma4.c:600-601 as compiled:
 //          vmulps then in-order vaddss);
 //   lfm / maple  v = v + (double)w_k * x_k in double, then (float)v
 //          (lfm25.c:646-647, maple.c:400-410);
 //   ling   eight double accumulators by k % 8, combined pairwise (ling.c:722-727).
-// A workgroup is 16 tokens x 16 experts; 64-wide K chunks of both operands are
-// staged in LDS so each router row and each input row is read once per tile.
-// Many independent chains (one per thread) hide the add latency.
-#define LG_T 16
-#define LG_E 16
-#define LG_K 64
-__global__ __launch_bounds__(256) void zz_logits_exact_kernel(ZzLogitArgs a) {
-    const int tid = threadIdx.x, tt = tid / LG_E, te = tid % LG_E;
-    const int s0 = blockIdx.x * LG_T, e0 = blockIdx.y * LG_E;
-    const int s = s0 + tt, e = e0 + te, D = a.D;
-    const bool gem = a.gating == ZZ_GATE_SOFTMAX_PES;
+// The double product of two floats is exact, so v + (double)w * x rounds once and
+// equals fma((double)w, (double)x, v): the double chains take one fma per element.
+// A workgroup is 4 tokens x 64 experts: wave w holds token s0 + w, lane l expert
+// e0 + l. The 64 router rows are staged in LDS in K chunks of KC (256 where D allows,
+// else 64), double buffered, and each lane reads its own row as float4. The token's
+// input is wave-uniform: a chunk sits in KC/16 VGPRs, 16 values each, lane l holding
+// element l % 16 (every 16-lane row alike), and element j reaches all lanes by the
+// DPP row broadcast (row_newbcast:j) folded into the multiply. The next chunk's
+// loads (router rows and input) are issued before this chunk is summed and land in
+// LDS after it: a chunk's 2 * KC VALU operations per wave are what hide the L2 / HBM
+// latency, so KC = 64 (~200 ns of work) left every chunk waiting and KC = 256 does
+// not. The chain is serial per lane, so the VALU time of one wave per SIMD
+// (S * E / 64 waves) is the floor; LDS carries only the router operand.
+#define LX_T 4
+#define LX_E 64
+#define LX_WARM 3      // warm-up sectors per thread and operand
+// lane (l & ~15) + J's value of v, in every lane of its 16-lane row
+template <int J>
+__device__ __forceinline__ float zz_row_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + J, 0xF, 0xF, false));
+}
+// 16 consecutive elements of one chain: w[J] (this lane's router row) times element
+// J of the row-broadcast input xq; CH as below, acc[0] the chain (acc[J % 8] for ling)
+typedef float zz_f4 __attribute__((ext_vector_type(4)));
+template <int CH, int J = 0>
+__device__ __forceinline__ void zz_chain16(float &vf, double *acc, const zz_f4 *w4, float xq) {
+    if constexpr (J < 16) {
+        const float xb = zz_row_bcast<J>(xq), w = w4[J / 4][J % 4];
+        if constexpr (CH == 1) acc[0] = __builtin_fma((double)w, (double)xb, acc[0]);
+        else acc[J % 8] = __builtin_fma((double)w, (double)xb, acc[J % 8]);
+        zz_chain16<CH, J + 1>(vf, acc, w4, xq);
+    }
+}
+// gemma's fp32 chain, 16 elements at a time: while the adds of group g run (in
+// order, one rounding each, as the reference), the products of group g + 1 are
+// formed between them, so the serial add chain never waits on its own multiply and
+// every multiply fills an add's latency. The compiler pairs each multiply with its
+// own add whatever the source order, so each step is written out: an unfused
+// v_mul_f32 with the row broadcast of the next group's input (the same product as
+// the reference's vmulps; operand order does not change a rounded product) and a
+// v_add_f32 of this group's product. The leading s_nop 1 gives the two wait states a
+// DPP read needs after a VALU write of its source.
+#define ZZ_MA(J, QI, WI, PI) \
+    "v_mul_f32_dpp %" #QI ", %[x], %" #WI " row_newbcast:" #J " row_mask:0xf bank_mask:0xf\n\t" \
+    "v_add_f32 %[v], %[v], %" #PI "\n\t"
+#define ZZ_MA4(J0, J1, J2, J3) \
+    asm volatile("s_nop 1\n\t" ZZ_MA(J0, 0, 6, 10) ZZ_MA(J1, 1, 7, 11) ZZ_MA(J2, 2, 8, 12) ZZ_MA(J3, 3, 9, 13) \
+                 : "=&v"(q[J0]), "=&v"(q[J1]), "=&v"(q[J2]), "=&v"(q[J3]), [v] "+v"(vf) \
+                 : [x] "v"(xnext), "v"(w[J0]), "v"(w[J1]), "v"(w[J2]), "v"(w[J3]), \
+                   "v"(p[J0]), "v"(p[J1]), "v"(p[J2]), "v"(p[J3]))
+// vf += p[0..15] in order, and q[j] = w[j] * (element j of xnext's row broadcast)
+__device__ __forceinline__ void zz_madd16(float &vf, const float *p, float *q, const float *w,
+                                          float xnext) {
+    ZZ_MA4(0, 1, 2, 3);
+    ZZ_MA4(4, 5, 6, 7);
+    ZZ_MA4(8, 9, 10, 11);
+    ZZ_MA4(12, 13, 14, 15);
+}
+#undef ZZ_MA4
+#undef ZZ_MA
+template <int J = 0>
+__device__ __forceinline__ void zz_prod16(float *p, const zz_f4 *w4, float xq) {
+    if constexpr (J < 16) {
+        p[J] = w4[J / 4][J % 4] * zz_row_bcast<J>(xq);
+        zz_prod16<J + 1>(p, w4, xq);
+    }
+}
+// CH: the chain kind -- 0 gemma's fp32 chain, 1 one double chain (lfm, maple),
+// 2 ling's eight double accumulators; one instantiation each, so a chain carries only
+// its own registers. KC: the K chunk (D % KC == 0).
+template <int CH, int KC>
+__global__ __launch_bounds__(256, 1) void zz_logits_exact_kernel(ZzLogitArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int s = blockIdx.x * LX_T + (tid >> 6), e0 = blockIdx.y * LX_E, e = e0 + lane, D = a.D;
+    constexpr bool gem = CH == 0, grp = CH == 2;
+    constexpr int NX = KC / 16;                       // input VGPRs per chunk
     const float *X = gem ? a.xn : a.x;
-    __shared__ float xs_t[2][LG_T][LG_K + 4];
-    __shared__ float ws_t[2][LG_E][LG_K + 4];
-    // staging: each thread moves LG_V float4 of each tile per chunk (rows clamped
-    // into range: a row past the end holds copies, its chains are not stored)
-    constexpr int LG_V = LG_T * LG_K / 4 / 256;
-    const int lr = tid / (LG_K / 4 / LG_V), lc = (tid % (LG_K / 4 / LG_V)) * 4 * LG_V;
-    const float *xsrc = X + (size_t)min(s0 + lr, a.S - 1) * D + lc;
-    const float *wsrc = a.router + (size_t)min(e0 + lr, a.E - 1) * D + lc;
-    float4 xv[LG_V], wv[LG_V];
+    // this lane's elements of the wave's input row (rows past the end read the last
+    // row; not stored)
+    const float *xrow = X + (size_t)min(s, a.S - 1) * D + (lane & 15);
+    __shared__ float ws_t[2][LX_E][KC + 4];
+    // staging: TPR threads per router row, RPP rows per pass, NV passes (rows clamped)
+    constexpr int TPR = KC / 4, RPP = 256 / TPR, NV = LX_E / RPP;
+    const int lr = tid / TPR, lc = (tid % TPR) * 4;
+    int woff[NV];                                     // element offsets into the router
 #pragma unroll
-    for (int v = 0; v < LG_V; v++) {
-        xv[v] = *(const float4 *)(xsrc + 4 * v);
-        wv[v] = *(const float4 *)(wsrc + 4 * v);
+    for (int v = 0; v < NV; v++) woff[v] = min(e0 + lr + RPP * v, a.E - 1) * D + lc;
+    const float *R = a.router;
+    zz_f4 wv4[NV];                                    // native vectors: kept in VGPRs
+    float xq[NX], xn[NX];
+#pragma unroll
+    for (int v = 0; v < NV; v++) wv4[v] = *(const zz_f4 *)(R + woff[v]);
+#pragma unroll
+    for (int i = 0; i < NX; i++) xq[i] = xrow[16 * i];
+    // L2 warm-up, issued behind chunk 0's loads: one dword per 64-byte sector of
+    // (a) this XCD's share of the workgroup's router rows (workgroups are dealt to the
+    // 8 XCDs round-robin, so those with the same blockIdx.x % 8 and blockIdx.y share
+    // an L2: each takes every J-th sector) and (b) the workgroup's own input rows. A
+    // layer's router and input are cold (the expert weights stream through every
+    // cache between layers); warmed, the later chunks' loads hit L2 instead of each
+    // chunk waiting out an HBM round trip. The values only pass through an empty asm.
+    float warm[2 * LX_WARM];
+    {
+        const int nr = min(LX_E, a.E - e0), J = ((int)gridDim.x + 7) >> 3, j = blockIdx.x >> 3;
+        const long ns = (long)nr * D / 16;
+        const float *rb = R + (size_t)e0 * D;
+        const int sx0 = blockIdx.x * LX_T, nx = min(LX_T, a.S - sx0);
+        const float *xb = X + (size_t)sx0 * D;
+        const int nsx = nx * D / 16;
+#pragma unroll
+        for (int r = 0; r < LX_WARM; r++) {
+            const long sr = j + (long)J * (tid + 256 * r);
+            warm[r] = sr < ns ? rb[16 * sr] : 0.0f;
+            const int sx = tid + 256 * r;
+            warm[LX_WARM + r] = sx < nsx ? xb[16 * sx] : 0.0f;
+        }
     }
 #pragma unroll
-    for (int v = 0; v < LG_V; v++) {
-        *(float4 *)&xs_t[0][lr][lc + 4 * v] = xv[v];
-        *(float4 *)&ws_t[0][lr][lc + 4 * v] = wv[v];
-    }
+    for (int v = 0; v < NV; v++) *(zz_f4 *)&ws_t[0][lr + RPP * v][lc] = wv4[v];
     __syncthreads();
     float vf = 0.0f;
-    double vd = 0.0;
-    double v8[8] = {0, 0, 0, 0, 0, 0, 0, 0};         // grouped: ling.c's 8 accumulators
-    const bool grp = a.gating == ZZ_GATE_GROUPED;
-    int buf = 0;
-    for (int k0 = 0; k0 < D; k0 += LG_K) {
-        const int k1 = min(k0 + LG_K, D - LG_K);    // the last chunk reloads itself
+    double acc[grp ? 8 : 1];                          // grouped: ling.c's 8 accumulators
 #pragma unroll
-        for (int v = 0; v < LG_V; v++) {
-            xv[v] = *(const float4 *)(xsrc + k1 + 4 * v);
-            wv[v] = *(const float4 *)(wsrc + k1 + 4 * v);
-        }
-        const float *xr = xs_t[buf][tt], *wr = ws_t[buf][te];
-        if (gem) {
-#pragma unroll 16
-            for (int k = 0; k < LG_K; k += 4) {
-                const float4 x4 = *(const float4 *)(xr + k), w4 = *(const float4 *)(wr + k);
-                vf = vf + w4.x * x4.x;
-                vf = vf + w4.y * x4.y;
-                vf = vf + w4.z * x4.z;
-                vf = vf + w4.w * x4.w;
-            }
-        } else if (grp) {
-            // element k0 + k goes to accumulator k % 8 (k0 is a multiple of LG_K)
-#pragma unroll 16
-            for (int k = 0; k < LG_K; k += 8) {
-                const float4 xa = *(const float4 *)(xr + k), wa = *(const float4 *)(wr + k);
-                const float4 xb = *(const float4 *)(xr + k + 4), wb = *(const float4 *)(wr + k + 4);
-                v8[0] = v8[0] + (double)wa.x * (double)xa.x;
-                v8[1] = v8[1] + (double)wa.y * (double)xa.y;
-                v8[2] = v8[2] + (double)wa.z * (double)xa.z;
-                v8[3] = v8[3] + (double)wa.w * (double)xa.w;
-                v8[4] = v8[4] + (double)wb.x * (double)xb.x;
-                v8[5] = v8[5] + (double)wb.y * (double)xb.y;
-                v8[6] = v8[6] + (double)wb.z * (double)xb.z;
-                v8[7] = v8[7] + (double)wb.w * (double)xb.w;
+    for (int k = 0; k < (grp ? 8 : 1); k++) acc[k] = 0.0;
+    int buf = 0;
+    for (int k0 = 0; k0 < D; k0 += KC) {
+        const int k1 = min(k0 + KC, D - KC);        // the last chunk reloads itself
+#pragma unroll
+        for (int v = 0; v < NV; v++) wv4[v] = *(const zz_f4 *)(R + (woff[v] + k1));
+#pragma unroll
+        for (int i = 0; i < NX; i++) xn[i] = xrow[k1 + 16 * i];
+        // keep those loads here, a whole chunk ahead of their LDS writes (the
+        // scheduler would otherwise sink each to just before its write, and wait)
+        __builtin_amdgcn_sched_barrier(0);
+        const float *wr = ws_t[buf][lane];
+        if constexpr (gem) {
+            zz_f4 w4[2][4];                         // the next group's row and the one after
+            float p[16], q[16];
+#pragma unroll
+            for (int r = 0; r < 4; r++) w4[0][r] = *(const zz_f4 *)(wr + 4 * r);
+            zz_prod16(p, w4[0], xq[0]);
+#pragma unroll
+            for (int r = 0; r < 4; r++) w4[1][r] = *(const zz_f4 *)(wr + 16 + 4 * r);
+#pragma unroll
+            for (int i = 0; i < NX; i++) {          // element k0 + 16i + j
+                if (i + 1 < NX) {
+                    float w[16];
+#pragma unroll
+                    for (int j = 0; j < 16; j++) w[j] = w4[(i + 1) & 1][j / 4][j % 4];
+                    if (i + 2 < NX) {
+#pragma unroll
+                        for (int r = 0; r < 4; r++) w4[i & 1][r] = *(const zz_f4 *)(wr + 16 * (i + 2) + 4 * r);
+                    }
+                    zz_madd16(vf, p, q, w, xq[i + 1]);
+#pragma unroll
+                    for (int j = 0; j < 16; j++) p[j] = q[j];
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 16; j++) vf = vf + p[j];
+                }
             }
         } else {
-#pragma unroll 16
-            for (int k = 0; k < LG_K; k += 4) {
-                const float4 x4 = *(const float4 *)(xr + k), w4 = *(const float4 *)(wr + k);
-                vd = vd + (double)w4.x * (double)x4.x;
-                vd = vd + (double)w4.y * (double)x4.y;
-                vd = vd + (double)w4.z * (double)x4.z;
-                vd = vd + (double)w4.w * (double)x4.w;
+#pragma unroll
+            for (int i = 0; i < NX; i++) {          // element k0 + 16i + j: acc j % 8
+                zz_f4 w4[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) w4[r] = *(const zz_f4 *)(wr + 16 * i + 4 * r);
+                zz_chain16<CH>(vf, acc, w4, xq[i]);
             }
         }
 #pragma unroll
-        for (int v = 0; v < LG_V; v++) {
-            *(float4 *)&xs_t[buf ^ 1][lr][lc + 4 * v] = xv[v];
-            *(float4 *)&ws_t[buf ^ 1][lr][lc + 4 * v] = wv[v];
-        }
+        for (int v = 0; v < NV; v++) *(zz_f4 *)&ws_t[buf ^ 1][lr + RPP * v][lc] = wv4[v];
+#pragma unroll
+        for (int i = 0; i < NX; i++) xq[i] = xn[i];
         __syncthreads();
         buf ^= 1;
     }
+#pragma unroll
+    for (int r = 0; r < 2 * LX_WARM; r++) asm volatile("" ::"v"(warm[r]));
     if (s < a.S && e < a.E) {
         const size_t o = (size_t)s * a.E + e;
-        if (gem) {
+        if constexpr (gem) {
             if (a.bias) vf = vf + a.bias[e];       // harness logit offset, after the dot
             a.cen[o] = (double)vf;
         } else {
-            if (grp) vd = ((v8[0] + v8[1]) + (v8[2] + v8[3])) + ((v8[4] + v8[5]) + (v8[6] + v8[7]));
+            double vd = acc[0];
+            if constexpr (grp)
+                vd = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
             a.cen[o] = (double)(float)vd;
         }
         a.bnd[o] = 0.0;                             // exact: no interval
     }
+}
+
+template <int KC>
+static void zz_launch_logits_exact(const ZzLogitArgs &b, int S, hipStream_t st) {
+    const dim3 g((S + LX_T - 1) / LX_T, (b.E + LX_E - 1) / LX_E);
+    if (b.gating == ZZ_GATE_SOFTMAX_PES) hipLaunchKernelGGL((zz_logits_exact_kernel<0, KC>), g, dim3(256), 0, st, b);
+    else if (b.gating == ZZ_GATE_GROUPED) hipLaunchKernelGGL((zz_logits_exact_kernel<2, KC>), g, dim3(256), 0, st, b);
+    else hipLaunchKernelGGL((zz_logits_exact_kernel<1, KC>), g, dim3(256), 0, st, b);
 }
 
 // Top-k gating, one wave per token (zz_topk_wave.h), four tokens per workgroup.
@@ -408,11 +510,11 @@ int zz_launch_prep(const ZzPrepArgs &a, int S, hipStream_t st) {
 }
 
 int zz_launch_logits(const ZzLogitArgs &a, int S, hipStream_t st) {
-    if (S >= 16 && a.D % LG_K == 0) {
+    if (S >= 16 && a.D % 64 == 0) {
         ZzLogitArgs b = a;
         b.S = S;
-        hipLaunchKernelGGL(zz_logits_exact_kernel, dim3((S + LG_T - 1) / LG_T, (a.E + LG_E - 1) / LG_E),
-                           dim3(256), 0, st, b);
+        if (a.D % 256 == 0) zz_launch_logits_exact<256>(b, S, st);
+        else zz_launch_logits_exact<64>(b, S, st);
     } else {
         hipLaunchKernelGGL(zz_logits_kernel, dim3((a.E + 3) / 4, S), dim3(256), 0, st, a);
     }
