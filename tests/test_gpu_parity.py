@@ -233,6 +233,28 @@ def test_gpu_matmul_declines_unmapped_and_q4a(dev):
     assert np.all(y == 5.0)
 
 
+def test_every_token_tile_count(dev, layer_cache):
+    """Work items of every shape against the oracle: gemma with 8 experts and top-2 at
+    S = 12 .. 300 puts 3 .. 80 tokens on an expert, so the <= 4-token path, items of
+    1, 2, 3 and 4 token tiles of 16, and experts split over two items all run."""
+    L = layer_cache("gemma", seed=11, E=8, K=2)
+    m = gpu_layer(L)
+    seen = set()
+    try:
+        for S in (12, 24, 100, 160, 200, 300):
+            x = Z.make_input(L, S, 7)
+            want = Z.oracle_moe(L, x)
+            for c in np.bincount(want.eidx, minlength=L.E):
+                for n in [64] * (c // 64) + [c % 64]:
+                    if n:
+                        seen.add("tiny" if n <= 4 else (n + 15) // 16)
+            out, eidx, ewt, err = check_layer(m, L, x, want)
+            say(f"  S={S} out rel L2 {err:.2e}")
+        assert seen >= {"tiny", 1, 2, 3, 4}, seen
+    finally:
+        m.close()
+
+
 # --------------------------------------------------------------- BASELINE configs
 def test_config2_gemma_zipf_s512(dev, layer_cache):
     """Config 2: S=512 prefill, Zipf(1.1) logit offsets (a harness extension that

@@ -625,6 +625,7 @@ __global__ __launch_bounds__(256) void zz_up_mma_kernel(ZzFfnArgs a) {
     if (GF == UF && GF != ZZ_FMT_TQ2 && item.n <= 4 && a.D <= MM4_K) mm4_up_body<GF>(a, item, rb, sm.t4);
     else if (nt <= 1) mm_up_body<GF, UF, 1>(a, item, rb, sm, tok);
     else if (nt <= 2) mm_up_body<GF, UF, 2>(a, item, rb, sm, tok);
+    else if (nt <= 3) mm_up_body<GF, UF, 3>(a, item, rb, sm, tok);
     else mm_up_body<GF, UF, 4>(a, item, rb, sm, tok);
 }
 
@@ -639,6 +640,7 @@ __global__ __launch_bounds__(256) void zz_down_mma_kernel(ZzFfnArgs a) {
     if (FMT != ZZ_FMT_TQ2 && item.n <= 4 && a.MI <= MM4_K) mm4_down_body<FMT>(a, item, rt, sm.t4);
     else if (nt <= 1) mm_down_body<FMT, 1>(a, item, rt, sm);
     else if (nt <= 2) mm_down_body<FMT, 2>(a, item, rt, sm);
+    else if (nt <= 3) mm_down_body<FMT, 3>(a, item, rt, sm);
     else mm_down_body<FMT, 4>(a, item, rt, sm);
 }
 
