@@ -219,6 +219,42 @@ int ref_g4_head(const uint8_t *table, int V, int D, const float *fnorm, float ep
     return tok;
 }
 
+/* The engine's FlashHead, flash_logits (gemma4.c:1055-1110), on one row: the model
+ * holds only the tied table and the four flash tensors, the buffers only what
+ * flash_logits touches. rmsnorm with the final norm first, as forward() does
+ * (gemma4.c:1239-1242); then the greedy token by sample at temp 0. */
+int ref_g4_flash(const uint8_t *table, int V, int D, const float *fnorm, float eps, float softcap,
+                 const uint8_t *cent, int NC, const int32_t *tmap, int CS, int NP,
+                 const float *cscale, int scaled, const int32_t *force, int nforce,
+                 const float *h, float *logits) {
+    M *m = zz_calloc(sizeof(M));
+    Cfg *c = &m->c;
+    c->hidden = D; c->vocab = V; c->eps = eps; c->final_logit_softcap = softcap;
+    c->flash_n_clusters = NC; c->flash_cluster_size = CS; c->flash_n_probes = NP;
+    c->flash_scaled_centroids = scaled; c->flash_n_force = nforce;
+    m->L[MAXL - 1].q_proj = (W){0, V, D, table, NULL};
+    m->flash_centroids = (W){0, NC, D, cent, NULL};
+    m->flash_token_map = (W){5, NC, CS, (const uint8_t *)tmap, NULL};
+    m->flash_cluster_scale = (W){0, 1, NC, NULL, cscale};
+    m->flash_force = (W){5, 1, nforce, (const uint8_t *)force, NULL};
+    m->use_flash = 1;
+    Buf b;
+    memset(&b, 0, sizeof b);
+    b.xn = zz_calloc(sizeof(float) * (size_t)D);
+    b.xq = zz_calloc((size_t)D + 64);
+    b.sx = zz_calloc(sizeof(float) * (size_t)(D / Q40_BLK + 8));
+    b.fsim = zz_calloc(sizeof(float) * ((size_t)NC + 64));
+    b.fsel = zz_calloc(sizeof(int) * ((size_t)NC + 64));
+    b.fids = zz_calloc(sizeof(int) * ((size_t)NP * CS + nforce + 64));
+    rmsnorm(b.xn, h, fnorm, D, eps);
+    flash_logits(m, b.xn, logits, &b);
+    uint64_t rng = 1;
+    int tok = sample(logits, V, 0.0f, 1.0f, 0, NULL, &rng);
+    free(b.xn); free(b.xq); free(b.sx); free(b.fsim); free(b.fsel); free(b.fids);
+    free(m);
+    return tok;
+}
+
 /* The engine's own container reader, manifest() (gemma4.c:260-403), on a directory:
  * the record size, every expert offset (n_layers * n_experts), layer 0's router,
  * each layer's layer_scalar, the final norm, embed_tokens row 0, and the bytes of

@@ -720,3 +720,71 @@ int orc_head(const uint8_t *table, int V, int D, const float *fnorm, float eps, 
     free(xn); free(xq); free(sx);
     return am;
 }
+
+/* The k best of v[] to the front of idx[] (gemma4.c:1112-1131). Only the set that
+ * ends in front matters to the caller, but where values tie at the boundary that set
+ * depends on the exact steps, so they are kept: the seeded 64-bit LCG, the pivot
+ * position it draws, the partition that moves strictly greater values left, and the
+ * narrowing on the pivot's final place. */
+static void flash_pick(const float *v, int *idx, int n, int k) {
+    uint64_t g = 0x9e3779b97f4a7c15ULL;
+    int lo = 0, hi = n - 1, t;
+    while (lo < hi) {
+        g = g * 6364136223846793005ULL + 1442695040888963407ULL;
+        const int p = lo + (int)((g >> 33) % (uint64_t)(hi - lo + 1));
+        const float pv = v[idx[p]];
+        t = idx[p]; idx[p] = idx[hi]; idx[hi] = t;
+        int st = lo;
+        for (int i = lo; i < hi; i++)
+            if (v[idx[i]] > pv) { t = idx[i]; idx[i] = idx[st]; idx[st] = t; st++; }
+        t = idx[st]; idx[st] = idx[hi]; idx[hi] = t;
+        if (st == k) break;
+        if (st < k) lo = st + 1;
+        else hi = st - 1;
+    }
+}
+
+static int cmp_int(const void *a, const void *b) {
+    const int x = *(const int *)a, y = *(const int *)b;
+    return (x > y) - (x < y);
+}
+
+int orc_flash_head(const uint8_t *table, int V, int D, const float *fnorm, float eps, float softcap,
+                   const uint8_t *cent, int NC, const int32_t *tmap, int CS, int NP,
+                   const float *cscale, int scaled, const int32_t *force, int nforce,
+                   const float *h, float *logits, int *sel) {
+    if (NP < 1 || NP > NC || CS < 1) return -1;
+    float *xn = (float *)malloc(sizeof(float) * (size_t)D);
+    int8_t *xq = (int8_t *)malloc((size_t)D);
+    float *sx = (float *)malloc(sizeof(float) * (size_t)(D / BLK));
+    float *fsim = (float *)malloc(sizeof(float) * (size_t)NC);
+    int *idx = (int *)malloc(sizeof(int) * (size_t)NC);
+    orc_rmsnorm(xn, h, fnorm, D, eps);
+    orc_quant_act(xn, xq, sx, D);
+    const size_t rb = row_bytes(ORC_FMT_Q40, D);
+    for (int i = 0; i < NC; i++) {
+        fsim[i] = orc_q40_dot(cent + (size_t)i * rb, xq, sx, D);
+        if (!scaled) fsim[i] *= cscale[i];
+        idx[i] = i;
+    }
+    flash_pick(fsim, idx, NC, NP);
+    for (int i = 0; i < V; i++) logits[i] = -INFINITY;
+    for (int i = 0; i < NP + (nforce > 0); i++) {
+        const int32_t *ids = i < NP ? tmap + (size_t)idx[i] * CS : force;
+        const int n = i < NP ? CS : nforce;
+        for (int j = 0; j < n; j++) {
+            const int id = ids[j];
+            if (id < 0 || id >= V) continue;           /* padding slot */
+            const float v = orc_q40_dot(table + (size_t)id * rb, xq, sx, D);
+            logits[id] = softcap > 0 ? tanhf(v / softcap) * softcap : v;
+        }
+    }
+    int am = 0;
+    for (int i = 1; i < V; i++) if (logits[i] > logits[am]) am = i;
+    if (sel) {
+        memcpy(sel, idx, sizeof(int) * (size_t)NP);
+        qsort(sel, (size_t)NP, sizeof(int), cmp_int);
+    }
+    free(xn); free(xq); free(sx); free(fsim); free(idx);
+    return am;
+}

@@ -158,6 +158,17 @@ void orc_embed_row(const uint8_t *table, int D, float embed_scale, int tok, floa
 int orc_head(const uint8_t *table, int V, int D, const float *fnorm, float eps, float softcap,
              const float *h, float *logits);
 
+/* FlashHead (gemma4.c:1055-1131), the approximate lm_head of one row: centroid scores
+ * fsim = q4_0 [NC, D] centroids . q8_0(rmsnorm(h, fnorm)) (times cluster_scale unless
+ * the scale is folded into the centroids, `scaled`), the NP best clusters by the
+ * reference's quickselect, their token_map rows [NC, CS] (-1 = padding) and the force
+ * list as candidates; logits[V] = -inf except the candidates' softcapped q4_0 logits.
+ * Returns the greedy token; sel (may be NULL) receives the NP chosen clusters, sorted. */
+int orc_flash_head(const uint8_t *table, int V, int D, const float *fnorm, float eps, float softcap,
+                   const uint8_t *cent, int NC, const int32_t *tmap, int CS, int NP,
+                   const float *cscale, int scaled, const int32_t *force, int nforce,
+                   const float *h, float *logits, int *sel);
+
 /* threads used by the parallel loops (OpenMP); 0 = runtime default */
 void orc_set_threads(int n);
 

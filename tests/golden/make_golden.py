@@ -119,9 +119,28 @@ def gemma_cases():
     print("gemma_block_stack: tokens", toks.tolist(), "head argmax", am.tolist())
 
 
+def flash_cases():
+    """FlashHead (gemma4.c:1055-1131 + sample at temp 0) from the compiled reference:
+    the plain case and the all-ties case of zzref.flash_case. The chosen clusters are
+    read off the logits: those whose members all came out finite."""
+    f = Z.FLASH_CASE
+    out = {}
+    for key, (scaled, tie_all) in (("plain", (1, False)), ("ties", (1, True))):
+        table, fnorm, F, H = Z.flash_case(scaled, tie_all)
+        lg, am = Z.ref_flash(table, f["V"], f["D"], fnorm, 1e-6, 30.0, F, H)
+        fin = np.isfinite(lg)
+        sel = np.array([[c for c in range(F.NC) if (F.tmap[c] >= 0).any() and fin[s][F.tmap[c][F.tmap[c] >= 0]].all()]
+                        for s in range(H.shape[0])], np.int32)
+        out.update({f"{key}_argmax": am, f"{key}_sel": sel, f"{key}_finite": fin,
+                    f"{key}_logits": lg[fin]})
+        print("gemma_flash_head", key, "argmax", am.tolist(), "clusters", sel[0].tolist())
+    np.savez(os.path.join(HERE, "gemma_flash_head.npz"), **out)
+
+
 if __name__ == "__main__":
     if Z.ref_lib("gemma4") is None:
         sys.exit("oracle/_ref is not built (needs /root/reference): run `make -C oracle`")
     kernel_cases()
     layer_cases()
     gemma_cases()
+    flash_cases()

@@ -186,3 +186,72 @@ def test_container_writer_read_by_the_engine(tmp_path):
     assert np.array_equal(fn, st.fnorm)
     assert np.array_equal(row0, st.table[:row0.size])
     assert np.array_equal(rec, st.layers[li].experts[e * L0.esz:(e + 1) * L0.esz])
+
+
+# ------------------------------------------------------------------- FlashHead
+FLASH = Z.FLASH_CASE
+FLASH_GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "gemma_flash_head.npz")
+flash_case = Z.flash_case
+
+
+def probed_ids(F, sel, V):
+    ids = set(int(i) for c in sel for i in F.tmap[c] if 0 <= i < V)
+    return ids | set(int(i) for i in F.force)
+
+
+@pytest.mark.parametrize("scaled,tie_all", [(1, False), (0, False), (1, True)])
+def test_flash_head_vs_compiled_reference(scaled, tie_all):
+    """orc_flash_head against the engine's own flash_logits + sample, bit for bit."""
+    table, fnorm, F, H = flash_case(scaled, tie_all)
+    V, D = FLASH["V"], FLASH["D"]
+    ref = Z.ref_flash(table, V, D, fnorm, 1e-6, 30.0, F, H)
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+    lg, am, sel = Z.oracle_flash(table, V, D, fnorm, 1e-6, 30.0, F, H)
+    assert np.array_equal(bits(lg), bits(ref[0]))
+    assert np.array_equal(am, ref[1])
+    for s in range(H.shape[0]):
+        fin = set(np.flatnonzero(np.isfinite(lg[s])).tolist())
+        assert fin == probed_ids(F, sel[s], V)
+
+
+def test_flash_head_probing_every_cluster_is_the_full_head():
+    """With every cluster probed (NP = NC) and no forced ids, the flash logits are the
+    full head's: same dots, same softcap, every id a member of some cluster."""
+    table, fnorm, F, H = flash_case()
+    V, D = FLASH["V"], FLASH["D"]
+    F.NP, F.force = F.NC, np.zeros(0, np.int32)
+    lg, am, sel = Z.oracle_flash(table, V, D, fnorm, 1e-6, 30.0, F, H)
+    full, fam = Z.oracle_head(table, V, D, fnorm, 1e-6, 30.0, H)
+    assert np.array_equal(bits(lg), bits(full)) and np.array_equal(am, fam)
+    assert np.array_equal(sel[0], np.arange(F.NC))
+
+
+def test_flash_head_picks_the_best_clusters():
+    """Without ties the probed set is the NP clusters of largest score, whatever the
+    quickselect's order: checked against a float64 score's ranking, away from ties."""
+    table, fnorm, F, H = flash_case()
+    V, D = FLASH["V"], FLASH["D"]
+    _, _, sel = Z.oracle_flash(table, V, D, fnorm, 1e-6, 30.0, F, H)
+    cent = Z.dequant_q40(F.cent, F.NC, D).astype(np.float64)
+    for s in range(H.shape[0]):
+        h = H[s].astype(np.float64)
+        xn = h / np.sqrt(np.mean(h * h) + 1e-6) * fnorm
+        score = cent @ xn
+        order = np.argsort(-score)
+        gap = score[order[F.NP - 1]] - score[order[F.NP]]
+        if gap > 1e-3 * np.abs(score).max():
+            assert np.array_equal(np.sort(order[:F.NP]), sel[s])
+
+
+def test_flash_head_golden():
+    """The fixture the compiled reference wrote (tests/golden/make_golden.py)."""
+    g = np.load(FLASH_GOLDEN)
+    for key, (scaled, tie_all) in (("plain", (1, False)), ("ties", (1, True))):
+        table, fnorm, F, H = flash_case(scaled, tie_all)
+        lg, am, sel = Z.oracle_flash(table, FLASH["V"], FLASH["D"], fnorm, 1e-6, 30.0, F, H)
+        assert np.array_equal(am, g[f"{key}_argmax"])
+        assert np.array_equal(sel, g[f"{key}_sel"])
+        fin = np.isfinite(lg)
+        assert np.array_equal(fin, g[f"{key}_finite"])
+        assert np.array_equal(bits(lg[fin]), bits(g[f"{key}_logits"]))

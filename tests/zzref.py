@@ -478,6 +478,120 @@ def ref_head(table, V, D, fnorm, eps, cap, H):
     return lg, am
 
 
+def dequant_q40(table, V, D):
+    """f32 [V, D] of a q4_0 [V, D] table (q40.h:9-18: fp16 d, then 16 bytes of
+    nibbles, low = weights 0..15, high = 16..31, value d * (q - 8))."""
+    b = np.frombuffer(np.ascontiguousarray(table), np.uint8).reshape(V, D // 32, 18)
+    d = b[:, :, :2].copy().view(np.float16)[:, :, 0].astype(np.float32)
+    q = b[:, :, 2:]
+    w = np.concatenate([(q & 15), (q >> 4)], axis=2).astype(np.float32) - 8.0
+    return (w * d[:, :, None]).reshape(V, D)
+
+
+@dataclass
+class Flash:
+    """A FlashHead for a tied table (tools/flashhead.py's tensors): q4_0 centroids
+    [NC, D], token_map [NC, CS] (-1 = padding), cluster_scale [NC], force ids."""
+    cent: np.ndarray
+    NC: int
+    tmap: np.ndarray
+    CS: int
+    NP: int
+    cscale: np.ndarray
+    scaled: int
+    force: np.ndarray
+
+    @property
+    def nforce(self):
+        return int(self.force.size)
+
+
+def make_flash(table, V, D, NC, CS, NP, nforce=3, seed=0, scaled=1, tie_all=False):
+    """A balanced clustering of the table's rows: a seeded permutation of the V ids in
+    NC rows of CS (NC * CS - V padding slots of -1 spread over them), each centroid the members' mean direction
+    times the largest member norm (the scale folded in when `scaled`, as the converter
+    does), quantised q4_0. tie_all: every centroid row the same bytes, so the choice
+    of clusters is decided by the quickselect's steps alone."""
+    assert NC * CS >= V
+    rng = np.random.default_rng(40_000 + seed)
+    ids = np.full(NC * CS, -1, np.int32)
+    ids[:V] = rng.permutation(V).astype(np.int32)
+    rng.shuffle(ids)                             # padding slots spread over the clusters
+    tmap = ids.reshape(NC, CS)
+    emb = dequant_q40(table, V, D)
+    cent = np.zeros((NC, D), np.float32)
+    cscale = np.zeros(NC, np.float32)
+    for c in range(NC):
+        m = tmap[c][tmap[c] >= 0]
+        rows = emb[m]
+        nrm = np.linalg.norm(rows, axis=1)
+        cscale[c] = nrm.max() if m.size else 1.0
+        u = (rows / np.maximum(nrm, 1e-12)[:, None]).mean(0) if m.size else np.ones(D, np.float32)
+        u = u / max(np.linalg.norm(u), 1e-12)
+        cent[c] = u * (cscale[c] if scaled else 1.0)
+    if tie_all:
+        cent[:] = cent[0]
+    force = rng.choice(V, nforce, replace=False).astype(np.int32) if nforce else np.zeros(0, np.int32)
+    return Flash(quant_rows(FMT_Q40, cent), NC, np.ascontiguousarray(tmap), CS, NP, cscale, scaled, force)
+
+
+def _flash_argtypes(extra_sel):
+    base = [u8p, C.c_int, C.c_int, f32p, C.c_float, C.c_float, u8p, C.c_int, i32p, C.c_int, C.c_int,
+            f32p, C.c_int, i32p, C.c_int, f32p, f32p]
+    return base + ([i32p] if extra_sel else [])
+
+
+# A FlashHead over a 4000-row table: 128 balanced clusters of 32 (96 padding slots),
+# 14 probed, 3 forced ids. tie_all makes every centroid the same bytes, so the probed
+# set is decided by the quickselect's steps alone (the case a plain top-k would get
+# wrong).
+FLASH_CASE = dict(V=4000, D=1024, NC=128, CS=32, NP=14, nforce=3)
+
+
+def flash_case(scaled=1, tie_all=False):
+    """(table, final norm, Flash, H [3, D]) of the FlashHead test case."""
+    f = FLASH_CASE
+    table, fnorm = make_table(f["V"], f["D"], 7)
+    F = make_flash(table, f["V"], f["D"], f["NC"], f["CS"], f["NP"], f["nforce"], seed=1,
+                   scaled=scaled, tie_all=tie_all)
+    L = make_layer("gemma", seed=1, E=8, D=f["D"], MI=64, K=2)
+    H = make_input(L, 3, 9)
+    return table, fnorm, F, H
+
+
+def oracle_flash(table, V, D, fnorm, eps, cap, F, H):
+    """(logits [S, V], greedy [S], chosen clusters [S, NP] sorted) of orc_flash_head."""
+    L = oracle()
+    L.orc_flash_head.argtypes = _flash_argtypes(True)
+    H = np.ascontiguousarray(H, np.float32)
+    S = H.shape[0]
+    lg = np.zeros((S, V), np.float32)
+    sel = np.zeros((S, F.NP), np.int32)
+    force = F.force if F.nforce else np.zeros(1, np.int32)
+    am = np.array([L.orc_flash_head(ptr(table), V, D, ptr(fnorm), C.c_float(eps), C.c_float(cap),
+                                    ptr(F.cent), F.NC, ptr(F.tmap), F.CS, F.NP, ptr(F.cscale), F.scaled,
+                                    ptr(force), F.nforce, ptr(H[s]), ptr(lg[s]), ptr(sel[s]))
+                   for s in range(S)], np.int32)
+    return lg, am, sel
+
+
+def ref_flash(table, V, D, fnorm, eps, cap, F, H):
+    """The compiled reference's flash_logits + sample, or None where it is unavailable."""
+    lib = ref_lib("gemma4")
+    if lib is None:
+        return None
+    lib.ref_g4_flash.argtypes = _flash_argtypes(False)
+    H = np.ascontiguousarray(H, np.float32)
+    S = H.shape[0]
+    lg = np.zeros((S, V), np.float32)
+    force = F.force if F.nforce else np.zeros(1, np.int32)
+    am = np.array([lib.ref_g4_flash(ptr(table), V, D, ptr(fnorm), C.c_float(eps), C.c_float(cap),
+                                    ptr(F.cent), F.NC, ptr(F.tmap), F.CS, F.NP, ptr(F.cscale), F.scaled,
+                                    ptr(force), F.nforce, ptr(H[s]), ptr(lg[s]))
+                   for s in range(S)], np.int32)
+    return lg, am
+
+
 @dataclass
 class Stack:
     """A seeded gemma stack: per layer a MoE layer and a dense branch, plus the tied
