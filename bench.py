@@ -222,6 +222,35 @@ def device_q40(zz, torch, n, gen, sigma=0.02):
     return q
 
 
+def flash_tensors(zz, torch, table, seed, cluster_size=32, probe_fraction=512 / 4748, n_force=2):
+    """A synthetic FlashHead for the tied table in tools/flashhead.py's shapes: V/32
+    balanced clusters (a seeded permutation of the ids), the probe count at the
+    builder's default fraction, each centroid the q4_0 of its members' mean row
+    (dequantised and averaged on the device). Arguments for Head.flash."""
+    Vt = table.shape[0] // (18 * (D // 32))
+    nc = Vt // cluster_size
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 4748)
+    perm = torch.randperm(Vt, generator=g, device="cuda")
+    cent = torch.empty(nc, D, dtype=torch.float32, device="cuda")
+    t = torch.from_numpy(table).cuda().view(Vt, D // 32, 18)
+    for c0 in range(0, nc, 1024):                 # 1024 clusters (32768 rows) per pass
+        ids = perm[c0 * cluster_size:(c0 + 1024) * cluster_size]
+        blk = t[ids]
+        dsc = blk[:, :, :2].contiguous().view(torch.float16).float()
+        q = blk[:, :, 2:]
+        w = (torch.cat([q & 15, q >> 4], dim=2).float() - 8.0) * dsc
+        cent[c0:c0 + 1024] = w.view(-1, cluster_size, D).mean(1)
+    del t
+    cq = torch.empty(nc * (D // 32) * 18, dtype=torch.uint8, device="cuda")
+    zz.quantize_dev(zz.GPU_FMT_Q40, cent.data_ptr(), cq.data_ptr(), nc * D, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    tmap = perm.view(nc, cluster_size).to(torch.int32).cpu().numpy()
+    n_probes = max(1, int(round(nc * probe_fraction)))
+    return (cq.cpu().numpy(), nc, tmap, cluster_size, n_probes, np.ones(nc, np.float32), 1,
+            np.arange(1, 1 + n_force, dtype=np.int32))
+
+
 def stack_bench(zz, torch, layers, seed, prefill_S, steps):
     """the Gemma-4 stack of the MoE layers above, each with a q4_0
     dense MLP (dense_inter 2112) and the layer combine, under a tied q4_0 embedding /
@@ -251,6 +280,7 @@ def stack_bench(zz, torch, layers, seed, prefill_S, steps):
     torch.cuda.empty_cache()
     head = zz.Head(table, V, D, (1 + 0.05 * rng.standard_normal(D)).astype(np.float32), 1e-6,
                    float(np.sqrt(np.float32(D))), 30.0)
+    flash = flash_tensors(zz, torch, table, seed)
     del table
     stack = zz.Stack(blocks, head)
     objs += [stack, head]
@@ -286,10 +316,27 @@ def stack_bench(zz, torch, layers, seed, prefill_S, steps):
                                                   ms_per_token=e0.elapsed_time(e1) / steps,
                                                   host_wall_ms_per_token=wall * 1e3 / steps)
     toks = tok.cpu().numpy()
+    # the same decode with FlashHead (gemma4.c:1055-1110) in place of the full head
+    head.flash(*flash)
+    stack.use_flash(True)
+    fl = {}
+    for graph in (False, True):
+        stack.decode_dev(tok.data_ptr(), 4, graph=graph, stream=st.cuda_stream)     # warm / capture
+        torch.cuda.synchronize()
+        e0.record(st)
+        stack.decode_dev(tok.data_ptr(), steps, graph=graph, stream=st.cuda_stream)
+        e1.record(st)
+        torch.cuda.synchronize()
+        fl["graph" if graph else "eager"] = dict(tokens_per_s=steps / (e0.elapsed_time(e1) / 1e3),
+                                                 ms_per_token=e0.elapsed_time(e1) / steps)
     # algorithmic bytes of one decode token: per layer the 8 routed experts, the
-    # router, the dense MLP and the norm vectors; the head table once
+    # router, the dense MLP and the norm vectors; the head table once (FlashHead: the
+    # centroids and the probed rows)
     per_layer = K * REC_B + E * D * 4 + DENSE_B + 8 * D * 4
     step_bytes = len(layers) * per_layer + TABLE_B + D * 4
+    NC, CS, NP, nforce = flash[1], flash[3], flash[4], len(flash[7])
+    flash_bytes = len(layers) * per_layer + Q40_TENSOR(NC, D) + Q40_TENSOR(NP * CS + nforce, D) + D * 4
+    fbest = max(fl.values(), key=lambda v: v["tokens_per_s"])
     best = max(out.values(), key=lambda v: v["tokens_per_s"])
     for o in objs:
         o.close()
@@ -301,7 +348,13 @@ def stack_bench(zz, torch, layers, seed, prefill_S, steps):
                     tokens_per_s=best["tokens_per_s"], hbm_bytes_per_token=step_bytes,
                     hbm_GBs=step_bytes * best["tokens_per_s"] / 1e9,
                     hbm_frac=step_bytes * best["tokens_per_s"] / 1e9 / HBM_PEAK_GBS,
-                    distinct_tokens=int(len(np.unique(toks)))))
+                    distinct_tokens=int(len(np.unique(toks)))),
+        flash_decode=dict(head=f"FlashHead: {NC} balanced clusters of {CS} (random permutation, "
+                               f"centroids the q4_0 member means), {NP} probed, {nforce} forced",
+                          eager=fl["eager"], graph=fl["graph"], tokens_per_s=fbest["tokens_per_s"],
+                          hbm_bytes_per_token=flash_bytes,
+                          hbm_GBs=flash_bytes * fbest["tokens_per_s"] / 1e9,
+                          hbm_frac=flash_bytes * fbest["tokens_per_s"] / 1e9 / HBM_PEAK_GBS))
 
 
 def main():

@@ -56,6 +56,30 @@ int zz_head_logits_dev(int head, const float *d_H, int S, float *d_logits, int *
                        void *stream);
 int zz_head_logits(int head, const float *H, int S, float *logits, int *argmax);
 
+/* FlashHead, the approximate lm_head of gemma4.c (flash_logits, 1055-1110, with
+ * flash_partition, 1112-1131), for a head: the tensors tools/flashhead.py writes into
+ * a container (gemma4.c:357-362) -- q4_0 centroids [n_clusters, D] (reference layout),
+ * token_map [n_clusters, cluster_size] (-1 = padding), cluster_scale [n_clusters]
+ * (read only when !scaled, i.e. when the scale is not folded into the centroids) and
+ * force [n_force] (ids always scored). n_clusters <= 16384, 1 <= n_probes <=
+ * n_clusters. Attaching keeps a reference-layout copy of the table on the device
+ * (V * D * 18/32 bytes) for the probed rows; a second call replaces the tensors.
+ * Returns 1, or 0. */
+int zz_head_flash(int head, const uint8_t *centroids, int n_clusters, const int32_t *token_map,
+                  int cluster_size, int n_probes, const float *cluster_scale, int scaled,
+                  const int32_t *force, int n_force);
+
+/* on != 0: zz_head_logits[_dev] and the stacks on this head take the FlashHead path
+ * (gemma4.c:1241-1242, `use_flash`): logits of the n_probes best clusters' members and
+ * the forced ids, -inf elsewhere, and the greedy token among them. The probed set is
+ * the reference's exactly (centroid scores in q40_dot's order; a tie at the boundary
+ * replays the reference's quickselect). on = 0 returns to the full head. */
+int zz_head_use_flash(int head, int on);
+
+/* *n = the number of rows whose probed set was decided by a quickselect replay (a tie
+ * at the boundary score) since zz_init. */
+int zz_head_flash_replays(unsigned *n);
+
 /* A stack of FFN blocks under one head: gemma4.c forward() (1184-1275) with the
  * attention of every layer taken as the identity. Returns a stack id >= 0, or -1.
  * The blocks and the head must outlive the stack. */
@@ -75,6 +99,9 @@ int zz_stack_prefill_dev(int stack, float *d_H, int S, int *d_tok, void *stream)
 int zz_stack_decode_dev(int stack, int *d_tok, int n, float *d_logits, int use_graph,
                         void *stream);
 
+/* zz_head_use_flash on the stack's head. */
+int zz_stack_use_flash(int stack, int on);
+
 /* A gemma4 container directory (convert_gemma4.py: manifest.txt, dense.bin,
  * experts.bin) made resident as a stack (gemma4.c:260-403 reads the same files):
  * per layer the MoE layer (router_proj, router_scale, router_pes,
@@ -82,7 +109,9 @@ int zz_stack_decode_dev(int stack, int *d_tok, int n, float *d_logits, int use_g
  * (mlp_gate, mlp_up, mlp_down, pre_feedforward_layernorm,
  * post_feedforward_layernorm_1) and the block (post_feedforward_layernorm,
  * layer_scalar); the head from embed_tokens, norm, cfg embed_scale and
- * final_logit_softcap. Attention weights are not read. Returns a stack id >= 0 that
+ * final_logit_softcap, with the container's FlashHead attached when it has one
+ * (cfg flash_*, gemma4.c:302-306, 357-362; off until zz_stack_use_flash). Attention
+ * weights are not read. Returns a stack id >= 0 that
  * owns all of these (zz_stack_destroy frees them), or -1; *n_layers, *D, *V (each
  * may be NULL) receive the model's shape. */
 int zz_gemma_stack_load(const char *dir, int *n_layers, int *D, int *V);

@@ -357,3 +357,113 @@ def test_block_fused_decode_matches_two_stream_path(dev, S, layer_cache):
         finally:
             close_all(B, m, d)
     assert Z.rel_l2(outs[0], outs[1]) < 1e-5
+
+
+# ------------------------------------------------------------------- FlashHead
+@pytest.mark.parametrize("scaled,tie_all,cap", [(1, False, 30.0), (0, False, 30.0), (1, True, 30.0),
+                                                (1, False, 0.0)])
+def test_flash_head_vs_oracle(dev, scaled, tie_all, cap):
+    """zz_head_flash + zz_head_use_flash against orc_flash_head (pinned to the
+    compiled reference's flash_logits): the same probed ids on every row (-inf
+    elsewhere), their logits bit for bit without a softcap and within the tanhf
+    ulp with one, the same greedy token away from near-ties. With every centroid the
+    same, the probed set comes from the quickselect replay, once per row."""
+    table, fnorm, F, H = Z.flash_case(scaled, tie_all)
+    V, D = Z.FLASH_CASE["V"], Z.FLASH_CASE["D"]
+    hd = zz.Head(table, V, D, fnorm, 1e-6, 1.0, cap)
+    try:
+        hd.flash(F.cent, F.NC, F.tmap, F.CS, F.NP, F.cscale, F.scaled, F.force)
+        r0 = zz.flash_replays()
+        hd.use_flash(True)
+        lg, am = hd.logits(H)
+        replays = zz.flash_replays() - r0
+        want, wam, sel = Z.oracle_flash(table, V, D, fnorm, 1e-6, cap, F, H)
+        fin = np.isfinite(want)
+        assert np.array_equal(np.isfinite(lg), fin)
+        assert np.all(lg[~fin] == -np.inf)
+        if cap == 0.0:
+            assert np.array_equal(lg[fin].view(np.uint32), want[fin].view(np.uint32))
+        else:
+            assert float(np.abs(lg[fin] - want[fin]).max()) < LOGIT_TOL
+        for s in range(H.shape[0]):
+            top2 = np.sort(want[s][fin[s]])[-2:]
+            if top2[1] - top2[0] > LOGIT_TOL:
+                assert am[s] == wam[s], (s, am[s], wam[s])
+        assert replays == (H.shape[0] if tie_all else 0), replays
+        hd.use_flash(False)                      # back to the full head
+        full, fam = hd.logits(H)
+        wf, wfam = Z.oracle_head(table, V, D, fnorm, 1e-6, cap, H)
+        assert float(np.abs(full - wf).max()) < LOGIT_TOL
+    finally:
+        hd.close()
+
+
+def test_flash_head_declines_bad_shapes(dev):
+    table, fnorm, F, H = Z.flash_case()
+    V, D = Z.FLASH_CASE["V"], Z.FLASH_CASE["D"]
+    hd = zz.Head(table, V, D, fnorm, 1e-6, 1.0, 30.0)
+    try:
+        with pytest.raises(RuntimeError, match="no FlashHead"):
+            hd.use_flash(True)
+        with pytest.raises(RuntimeError, match="n_probes"):
+            hd.flash(F.cent, F.NC, F.tmap, F.CS, F.NC + 1, F.cscale, F.scaled, F.force)
+    finally:
+        hd.close()
+
+
+def test_stack_decode_with_flash_head(dev, tmp_path):
+    """Greedy decode through the stack with the FlashHead on: eager and graph replays
+    agree bit for bit, a container carrying the FlashHead (convert_gemma4.py's
+    tensors, zz_gemma_stack_load) decodes the same tokens, and each step's token is
+    the oracle's flash head of the oracle's hidden from the GPU's previous token."""
+    import torch
+    *_, st, H0 = Z.gemma_block_case()
+    D, V = st.layers[0].D, st.V
+    F = Z.make_flash(st.table, V, D, 32, 32, 4, 2, seed=5)
+    blocks, objs = [], []
+    for L_, dn in zip(st.layers, st.denses):
+        B, m, d = gpu_block(L_, dn)
+        blocks.append(B)
+        objs += [B, m, d]
+    hd = zz.Head(st.table, V, D, st.fnorm, st.layers[0].eps, st.embed_scale, st.softcap)
+    hd.flash(F.cent, F.NC, F.tmap, F.CS, F.NP, F.cscale, F.scaled, F.force)
+    stack = zz.Stack(blocks, hd)
+    objs += [stack, hd]
+    Z.write_gemma_container(str(tmp_path), st, flash=F)
+    loaded = zz.Stack.load(str(tmp_path))
+    objs.append(loaded)
+    try:
+        s = torch.cuda.current_stream().cuda_stream
+        n = 6
+        runs = []
+        for stk, graph in ((stack, False), (stack, True), (loaded, True), (loaded, False)):
+            stk.use_flash(True)
+            dH = torch.from_numpy(H0).cuda()
+            toks = torch.zeros(n + 1, dtype=torch.int32, device="cuda")
+            stk.prefill_dev(dH.data_ptr(), H0.shape[0], toks.data_ptr(), s)
+            lg = torch.zeros(V, dtype=torch.float32, device="cuda")
+            stk.decode_dev(toks.data_ptr(), n, lg.data_ptr(), graph=graph, stream=s)
+            torch.cuda.synchronize()
+            runs.append((toks.cpu().numpy(), lg.cpu().numpy(), dH[-1:].cpu().numpy()))
+        say("flash stack tokens", runs[0][0].tolist())
+        for t, l, _ in runs[1:]:
+            assert np.array_equal(t, runs[0][0])
+            assert np.array_equal(l.view(np.uint32), runs[0][1].view(np.uint32))
+        toks = runs[0][0]
+        wl, wam, _ = Z.oracle_flash(st.table, V, D, st.fnorm, st.layers[0].eps, st.softcap, F, runs[0][2])
+        checks = [(wl, wam, toks[0])]
+        for i in range(n):
+            He = Z.oracle_embed(st.table, D, st.embed_scale, toks[i:i + 1])
+            for L_, dn in zip(st.layers, st.denses):
+                He = Z.oracle_block(L_, dn, He)[0]
+            wl, wam, _ = Z.oracle_flash(st.table, V, D, st.fnorm, st.layers[0].eps, st.softcap, F, He)
+            checks.append((wl, wam, toks[i + 1]))
+        for wl, wam, tok in checks:
+            fin = wl[0][np.isfinite(wl[0])]
+            top2 = np.sort(fin)[-2:]
+            if top2[1] - top2[0] > LOGIT_TOL:
+                assert tok == wam[0], (tok, wam[0])
+        # and off again: the full head's tokens
+        stack.use_flash(False)
+    finally:
+        close_all(*objs)

@@ -325,7 +325,7 @@ def test_dispatch_is_stable_counting_sort(layer_cache):
 # whole-MoE-layer fixtures (the kernel vectors and the gemma block/stack fixture have
 # their own tests)
 CASES = sorted(f[:-4] for f in os.listdir(GOLDEN)
-               if f.endswith(".npz") and not f.startswith(("kernels", "gemma_block")))
+               if f.endswith(".npz") and not f.startswith(("kernels", "gemma_block", "gemma_flash")))
 
 
 def load_case(name):

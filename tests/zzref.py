@@ -541,11 +541,11 @@ def _flash_argtypes(extra_sel):
     return base + ([i32p] if extra_sel else [])
 
 
-# A FlashHead over a 4000-row table: 128 balanced clusters of 32 (96 padding slots),
+# A FlashHead over a 4032-row table: 128 balanced clusters of 32 (64 padding slots),
 # 14 probed, 3 forced ids. tie_all makes every centroid the same bytes, so the probed
 # set is decided by the quickselect's steps alone (the case a plain top-k would get
 # wrong).
-FLASH_CASE = dict(V=4000, D=1024, NC=128, CS=32, NP=14, nforce=3)
+FLASH_CASE = dict(V=4032, D=1024, NC=128, CS=32, NP=14, nforce=3)
 
 
 def flash_case(scaled=1, tie_all=False):
@@ -688,14 +688,16 @@ def gemma_digest(L, dn, H, table, fnorm, st, H0):
 
 
 # ------------------------------------------------ zunzuncito container directories
-def write_gemma_container(path, st, head_dim=64, n_heads=2):
+def write_gemma_container(path, st, head_dim=64, n_heads=2, flash=None):
     """Write stack `st` as a gemma4 container directory in the layout that
     tools/convert_gemma4.py writes and gemma4.c:260-403 reads: manifest.txt (cfg
     lines, `esz`, the dense index, `expert li e off`), dense.bin (tensors back to
     back: q4_0 matrices, f32 vectors, shapes [O, I] with I = 1 for vectors) and
     experts.bin ([gate | up | down] records at 4096-aligned offsets). Attention
     tensors are small seeded placeholders: the engine's reader binds them, the GPU
-    loader skips them. Returns the per-(layer, expert) offsets."""
+    loader skips them. `flash` (a Flash) adds the FlashHead tensors and cfg keys as
+    convert_gemma4.py:315-327, 400 writes them. Returns the per-(layer, expert)
+    offsets."""
     os.makedirs(path, exist_ok=True)
     L0 = st.layers[0]
     D, MI, E, K, NL = L0.D, L0.MI, L0.E, L0.K, len(st.layers)
@@ -741,6 +743,12 @@ def write_gemma_container(path, st, head_dim=64, n_heads=2):
         add(o + "router_proj", L_.router, 0, E, D)
         add(o + "router_scale", L_.router_scale, 0, D, 1)
         add(o + "router_pes", L_.pes, 0, E, 1)
+    if flash is not None:
+        add("flash_centroids", flash.cent, 1, flash.NC, D)
+        add("flash_token_map", flash.tmap, 5, flash.NC, flash.CS)
+        add("flash_cluster_scale", flash.cscale, 0, 1, flash.NC)
+        fo = flash.force if flash.nforce else np.zeros(1, np.int32)
+        add("flash_force", fo.astype(np.int32), 5, 1, fo.size)
     blob.close()
     esz, gb, db = L0.esz, tensor_bytes(FMT_Q40, MI, D), tensor_bytes(FMT_Q40, D, MI)
     eoff, off = {}, 0
@@ -759,6 +767,9 @@ def write_gemma_container(path, st, head_dim=64, n_heads=2):
                rope_theta_local=10000.0, rope_theta_global=1000000.0, rope_partial_global=1.0,
                final_logit_softcap=st.softcap, embed_scale=st.embed_scale, ctx=256,
                slots_per_layer=E)
+    if flash is not None:
+        cfg.update(flash_n_clusters=flash.NC, flash_cluster_size=flash.CS, flash_n_probes=flash.NP,
+                   flash_scaled_centroids=flash.scaled, flash_n_force=flash.nforce)
     with open(os.path.join(path, "manifest.txt"), "w") as m:
         for k, v in cfg.items():
             m.write(f"cfg {k} {v}\n")

@@ -33,7 +33,8 @@ ABI_SYMBOLS = (
     "zz_ffn_block_forward", "zz_head_create", "zz_head_destroy", "zz_head_embed_dev",
     "zz_head_embed", "zz_head_logits_dev", "zz_head_logits", "zz_stack_create",
     "zz_stack_destroy", "zz_stack_prefill_dev", "zz_stack_decode_dev", "zz_moe_load_experts",
-    "zz_gemma_stack_load",
+    "zz_gemma_stack_load", "zz_head_flash", "zz_head_use_flash", "zz_head_flash_replays",
+    "zz_stack_use_flash",
 )
 KERNELS = ("prep", "logits", "topk", "dispatch", "ffn_up", "ffn_down", "combine", "dec_route",
            "dec_down")
@@ -123,6 +124,11 @@ def lib():
     L.zz_stack_decode_dev.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p]
     L.zz_moe_load_experts.argtypes = [C.c_int, C.c_char_p, C.c_int]
     L.zz_gemma_stack_load.argtypes = [C.c_char_p, _i32p, _i32p, _i32p]
+    L.zz_head_flash.argtypes = [C.c_int, _u8p, C.c_int, _i32p, C.c_int, C.c_int, _f32p, C.c_int, _i32p,
+                                C.c_int]
+    L.zz_head_use_flash.argtypes = [C.c_int, C.c_int]
+    L.zz_head_flash_replays.argtypes = [C.POINTER(C.c_uint)]
+    L.zz_stack_use_flash.argtypes = [C.c_int, C.c_int]
     _lib = L
     return L
 
@@ -151,6 +157,14 @@ def stats():
     if not lib().zz_moe_stats(c):
         raise RuntimeError(last_error())
     return list(c)
+
+
+def flash_replays():
+    """Rows whose FlashHead probe set a quickselect replay decided (a boundary tie)."""
+    n = C.c_uint(0)
+    if not lib().zz_head_flash_replays(C.byref(n)):
+        raise RuntimeError(last_error())
+    return n.value
 
 
 def quantize_dev(fmt, d_w, d_out, n, stream=0):
@@ -342,6 +356,22 @@ class Head:
             raise RuntimeError(f"zz_head_logits declined: {last_error()}")
         return lg, am
 
+    def flash(self, centroids, n_clusters, token_map, cluster_size, n_probes, cluster_scale, scaled,
+              force=None):
+        """Attach a FlashHead (zz_head_flash): q4_0 centroids [NC, D], token_map [NC, CS]
+        int32 (-1 = padding), cluster_scale [NC] f32, force ids int32."""
+        cent = np.ascontiguousarray(centroids, np.uint8)
+        tm = np.ascontiguousarray(token_map, np.int32)
+        cs = np.ascontiguousarray(cluster_scale, np.float32)
+        fo = np.ascontiguousarray(force if force is not None else np.zeros(0, np.int32), np.int32)
+        if not lib().zz_head_flash(self.id, _p(cent, _u8p), n_clusters, _p(tm, _i32p), cluster_size, n_probes,
+                                   _p(cs, _f32p), int(scaled), _p(fo, _i32p) if fo.size else None, fo.size):
+            raise RuntimeError(f"zz_head_flash declined: {last_error()}")
+
+    def use_flash(self, on=True):
+        if not lib().zz_head_use_flash(self.id, int(bool(on))):
+            raise RuntimeError(f"zz_head_use_flash declined: {last_error()}")
+
     def embed_dev(self, d_tok, S, d_H, stream=0):
         if not lib().zz_head_embed_dev(self.id, C.c_void_p(d_tok), S, C.c_void_p(d_H),
                                        C.c_void_p(stream or None)):
@@ -367,6 +397,11 @@ class Stack:
         self.id = lib().zz_stack_create(_p(ids, _i32p), len(ids), head.id)
         if self.id < 0:
             raise RuntimeError(f"zz_stack_create declined: {last_error()}")
+
+    def use_flash(self, on=True):
+        """The head's FlashHead on or off for this stack (zz_stack_use_flash)."""
+        if not lib().zz_stack_use_flash(self.id, int(bool(on))):
+            raise RuntimeError(f"zz_stack_use_flash declined: {last_error()}")
 
     @classmethod
     def load(cls, path):

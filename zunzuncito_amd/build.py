@@ -15,7 +15,7 @@ LIB = os.path.join(PKG, "libzzmoe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["zz_api.hip", "zz_route.hip", "zz_ffn.hip", "zz_matmul.hip", "zz_quant.hip", "zz_mma.hip", "zz_decode.hip",
-           "zz_gemma.hip", "zz_container.hip"]
+           "zz_gemma.hip", "zz_container.hip", "zz_flash.hip"]
 
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",

@@ -55,7 +55,10 @@ extern "C" int gpu_init(void) {
     ZZ_CHECK(hipGetDeviceProperties(&p, 0));
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0) ZZ_FAIL("device %s is not gfx950", p.gcnArchName);
     snprintf(g_name, sizeof g_name, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
-    ZZ_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    // the library's stream, what a NULL stream argument means: a blocking stream, so it
+    // is ordered with the legacy default stream both ways, as a caller passing the
+    // default stream's handle (0, e.g. torch's current stream) expects
+    ZZ_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamDefault));
     ZZ_CHECK(hipMalloc(&g_diag, 16 * sizeof(unsigned)));
     ZZ_CHECK(hipMemset(g_diag, 0, 16 * sizeof(unsigned)));
     const char *dm = getenv("ZZ_DECODE_MAX_S");

@@ -253,6 +253,19 @@ extern "C" int zz_gemma_stack_load(const char *dir_c, int *n_layers_out, int *D_
         return fail();
     head = zz_head_create(table.data(), V, D, (const float *)fnorm.data(), eps, escale, cap);
     if (head < 0) return fail();
+    const int NC = m.geti("flash_n_clusters", 0);
+    if (NC > 0) {                                // a FlashHead: gemma4.c:302-306, 357-362
+        const int CS = m.geti("flash_cluster_size"), NP = m.geti("flash_n_probes");
+        const int nf = m.geti("flash_n_force", 0), scaled = m.geti("flash_scaled_centroids", 0);
+        std::vector<uint8_t> cent, tmap, cs, fo;
+        if (CS <= 0 || NP <= 0 || nf < 0 || !dense_read(f.fd, m, "flash_centroids", 1, qbytes(NC, D), cent) ||
+            !dense_read(f.fd, m, "flash_token_map", 5, (int64_t)NC * CS * 4, tmap) ||
+            !dense_read(f.fd, m, "flash_cluster_scale", 0, (int64_t)NC * 4, cs) ||
+            !dense_read(f.fd, m, "flash_force", 5, (int64_t)(nf > 0 ? nf : 1) * 4, fo) ||
+            !zz_head_flash(head, cent.data(), NC, (const int32_t *)tmap.data(), CS, NP, (const float *)cs.data(),
+                           scaled, (const int32_t *)fo.data(), nf))
+            return fail();
+    }
     const int stack = zz_stack_create(blocks.data(), (int)blocks.size(), head);
     if (stack < 0 || !zz_stack_adopt(stack, layers, blocks, head)) return fail();
     if (n_layers_out) *n_layers_out = NL;

@@ -336,14 +336,30 @@ struct Head {
     float *xs = nullptr;            // [4, D/32]
     int *xsum = nullptr;            // [4, D/32]
     unsigned long long *part = nullptr;   // [4][V/64] per-workgroup argmax keys
+    // FlashHead (zz_flash.hip), once attached; use_flash routes the logits through it
+    bool use_flash = false;
+    ZzFlashArgs fl{};               // its device tensors and buffers (fl.rtab: the
+                                    // table in reference layout, [V, D])
 };
 static std::vector<Head *> g_heads;
+
+static void free_flash(ZzFlashArgs &f, bool keep_table) {
+    void *ps[] = {(void *)f.cent, (void *)f.tmap, (void *)f.cscale, (void *)f.force,
+                  f.fsim, f.sel, f.part};
+    for (void *p : ps)
+        if (p) (void)hipFree(p);
+    uint8_t *rtab = (uint8_t *)f.rtab;
+    if (rtab && !keep_table) (void)hipFree(rtab);
+    f = ZzFlashArgs{};
+    if (keep_table) f.rtab = rtab;
+}
 
 static void free_head(Head *h) {
     if (!h) return;
     void *ps[] = {h->table, h->fnorm, h->xq, h->xs, h->xsum, h->part};
     for (void *p : ps)
         if (p) (void)hipFree(p);
+    free_flash(h->fl, false);
     delete h;
 }
 
@@ -449,6 +465,19 @@ extern "C" int zz_head_logits_dev(int id, const float *d_H, int S, float *d_logi
     pa.xsum = h->xsum;
     pa.diag = zz_lib_diag();
     if (!zz_launch_prep(pa, S, st)) ZZ_FAIL("zz_head_logits_dev: norm launch failed");
+    if (h->use_flash) {                          // gemma4.c:1241-1242
+        ZzFlashArgs fa = h->fl;
+        fa.xq = h->xq;
+        fa.xs = h->xs;
+        fa.logits = d_logits;
+        fa.diag = zz_lib_diag();
+        if (!zz_launch_flash(fa, S, st)) ZZ_FAIL("zz_head_logits_dev: FlashHead launch failed");
+        if (d_argmax)
+            hipLaunchKernelGGL(zz_head_argmax_kernel, dim3(S), dim3(256), 0, st, fa.part, zz_flash_probe_groups(fa),
+                               d_argmax);
+        if (hipGetLastError() != hipSuccess) ZZ_FAIL("zz_head_logits_dev: launch failed");
+        return 1;
+    }
     const size_t lds = (size_t)S * h->D + sizeof(float) * (size_t)S * (h->D / ZZ_BLK);
     hipLaunchKernelGGL(zz_head_kernel, dim3(h->V / 64), dim3(256), lds, st, h->table, h->T, h->xq, h->xs, S, h->cap,
                        d_logits, h->part);
@@ -479,6 +508,72 @@ extern "C" int zz_head_logits(int id, const float *H, int S, float *logits, int 
 }
 
 // ------------------------------------------------------------------ stacks
+extern "C" int zz_head_flash(int id, const uint8_t *centroids, int n_clusters, const int32_t *token_map,
+                             int cluster_size, int n_probes, const float *cluster_scale, int scaled,
+                             const int32_t *force, int n_force) {
+    Head *h = get_head(id);
+    if (!h || !centroids || !token_map || n_clusters < 1 || n_clusters > ZZ_FLASH_MAXNC || cluster_size < 1 ||
+        n_probes < 1 || n_probes > n_clusters || n_force < 0 || (n_force > 0 && !force) || (!scaled && !cluster_scale))
+        ZZ_FAIL("zz_head_flash: bad arguments (1 <= n_probes <= n_clusters <= %d)", ZZ_FLASH_MAXNC);
+    hipStream_t st = zz_lib_stream();
+    ZZ_CHECK(hipStreamSynchronize(st));
+    free_flash(h->fl, true);                     // a new attachment replaces the old one
+    h->use_flash = false;
+    ZzFlashArgs &f = h->fl;
+    const int nb = h->D / ZZ_BLK;
+    const size_t rb = (size_t)18 * nb;
+    f.V = h->V; f.D = h->D; f.NC = n_clusters; f.CS = cluster_size; f.NP = n_probes; f.nforce = n_force;
+    f.scaled = scaled ? 1 : 0; f.cap = h->cap;
+    const int groups = zz_flash_probe_groups(f);
+    uint8_t *rtab = (uint8_t *)f.rtab, *cent = nullptr;
+    int *tmap = nullptr, *fo = nullptr;
+    float *cs = nullptr;
+    bool ok = true;
+    if (!rtab) {                                 // the table in reference layout, once
+        ok = hipMalloc(&rtab, rb * h->V) == hipSuccess && zz_launch_flash_unpack(h->table, h->T, rtab, st);
+        f.rtab = rtab;
+    }
+    ok = ok && hipMalloc(&cent, rb * n_clusters) == hipSuccess &&
+         hipMalloc(&tmap, sizeof(int) * (size_t)n_clusters * cluster_size) == hipSuccess &&
+         hipMalloc(&cs, sizeof(float) * n_clusters) == hipSuccess &&
+         hipMalloc(&fo, sizeof(int) * (size_t)(n_force > 0 ? n_force : 1)) == hipSuccess;
+    f.cent = cent; f.tmap = tmap; f.cscale = cs; f.force = fo;
+    ok = ok && hipMalloc(&f.fsim, sizeof(float) * ZZ_DEC_MAXS * n_clusters) == hipSuccess &&
+         hipMalloc(&f.sel, sizeof(int) * ZZ_DEC_MAXS * n_probes) == hipSuccess &&
+         hipMalloc(&f.part, sizeof(unsigned long long) * ZZ_DEC_MAXS * groups) == hipSuccess &&
+         hipMemcpy(cent, centroids, rb * n_clusters, hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(tmap, token_map, sizeof(int) * (size_t)n_clusters * cluster_size, hipMemcpyHostToDevice) ==
+             hipSuccess &&
+         (scaled || hipMemcpy(cs, cluster_scale, sizeof(float) * n_clusters, hipMemcpyHostToDevice) == hipSuccess) &&
+         (n_force == 0 || hipMemcpy(fo, force, sizeof(int) * n_force, hipMemcpyHostToDevice) == hipSuccess) &&
+         hipStreamSynchronize(st) == hipSuccess;
+    if (!ok) {
+        free_flash(h->fl, false);
+        ZZ_FAIL("zz_head_flash: device allocation or upload failed");
+    }
+    return 1;
+}
+
+static void drop_graphs_of_head(int head);
+
+extern "C" int zz_head_use_flash(int id, int on) {
+    Head *h = get_head(id);
+    if (!h || (on && !h->fl.cent)) ZZ_FAIL("zz_head_use_flash: no such head, or no FlashHead attached");
+    if (h->use_flash != (on != 0)) {
+        (void)hipStreamSynchronize(zz_lib_stream());
+        drop_graphs_of_head(id);                 // captured steps hold the other path
+    }
+    h->use_flash = on != 0;
+    return 1;
+}
+
+extern "C" int zz_head_flash_replays(unsigned *n) {
+    unsigned *d = zz_lib_diag();
+    if (!n || !d) ZZ_FAIL("zz_head_flash_replays: not ready");
+    ZZ_CHECK(hipMemcpy(n, d + 4, sizeof(unsigned), hipMemcpyDeviceToHost));
+    return 1;
+}
+
 struct Stack {
     std::vector<int> blocks;
     int head, D, V;
@@ -512,6 +607,22 @@ static void free_stack(Stack *k, bool owned = false) {
 static Stack *get_stack(int id) {
     if (!zz_lib_ready() || id < 0 || id >= (int)g_stacks.size()) return nullptr;
     return g_stacks[id];
+}
+
+static void drop_graphs_of_head(int head) {
+    for (Stack *k : g_stacks)
+        if (k && k->head == head) {
+            if (k->exec) (void)hipGraphExecDestroy(k->exec);
+            if (k->graph) (void)hipGraphDestroy(k->graph);
+            k->exec = nullptr;
+            k->graph = nullptr;
+        }
+}
+
+extern "C" int zz_stack_use_flash(int id, int on) {
+    Stack *k = get_stack(id);
+    if (!k) ZZ_FAIL("zz_stack_use_flash: no such stack");
+    return zz_head_use_flash(k->head, on);
 }
 
 extern "C" int zz_stack_create(const int *blocks, int n, int head) {

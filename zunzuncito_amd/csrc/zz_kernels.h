@@ -145,6 +145,29 @@ struct ZzDecFinalArgs {
     float *H;                   // [S, D] in place
 };
 
+// FlashHead (zz_flash.hip): the tensors of tools/flashhead.py on the device, and one
+// step's working buffers
+#define ZZ_FLASH_MAXNC 16384    // clusters held by the select kernel's LDS
+struct ZzFlashArgs {
+    int V, D, NC, CS, NP, nforce, scaled;
+    float cap;                  // final_logit_softcap (0: none)
+    const uint8_t *rtab;        // [V, D] q4_0 table, reference layout
+    const uint8_t *cent;        // [NC, D] q4_0 centroids, reference layout
+    const int *tmap;            // [NC, CS] token ids, -1 = padding
+    const float *cscale;        // [NC] (read when !scaled)
+    const int *force;           // [nforce]
+    const int8_t *xq;           // [S, D] q8_0 of rmsnorm(H, final_norm)
+    const float *xs;            // [S, D/32]
+    float *fsim;                // [S, NC] centroid scores
+    int *sel;                   // [S, NP] chosen clusters
+    float *logits;              // [S, V] or null
+    unsigned long long *part;   // [S, probe groups] argmax keys
+    unsigned *diag;             // [4]: quickselect replays
+};
+int zz_launch_flash(const ZzFlashArgs &a, int S, hipStream_t st);
+int zz_flash_probe_groups(const ZzFlashArgs &a);
+int zz_launch_flash_unpack(const uint8_t *src, const ZzTensor &T, uint8_t *dst, hipStream_t st);
+
 // Host-side internals of the library (zz_api.hip), shared by its host files.
 struct zz_moe_desc;
 hipStream_t zz_lib_stream();
