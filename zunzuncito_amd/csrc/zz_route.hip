@@ -363,13 +363,13 @@ __global__ __launch_bounds__(256) void zz_topk_kernel(ZzTopkArgs a, int S) {
 }
 
 // -------------------------------------------------------------------------------
-// Dispatch, one workgroup of 512 threads. Each expert gets a bitmask over tokens;
+// Dispatch, one workgroup of 1024 threads. Each expert gets a bitmask over tokens;
 // a pair's place in its expert's list is the expert's start plus the number of
 // earlier tokens that chose it (a popcount) -- the stable counting sort that gives
 // exactly rows[] of gemma4.c:779-786, ascending tokens. The smallest pair index
 // of each expert orders the union as first-seen (gemma4.c:756-761). Also emits
 // the FFN work list: per expert in union order, chunks of at most `tch` pairs.
-// exclusive prefix sum over the 512 threads of a workgroup: a shuffle scan per wave,
+// exclusive prefix sum over the threads of a workgroup (up to 1024): a shuffle scan per wave,
 // then the wave totals (two barriers)
 __device__ __forceinline__ int zz_block_excl_scan(int v, int *tmp) {
     const int t = threadIdx.x, l = t & 63, w = t >> 6;
@@ -387,46 +387,47 @@ __device__ __forceinline__ int zz_block_excl_scan(int v, int *tmp) {
     return base + x - v;
 }
 
-#define DP_PT 16                      // pairs per thread: S*K <= 8192 = 512 * DP_PT
+#define DP_T 1024                     // threads
+#define DP_PT 8                       // pairs per thread: S*K <= 8192 = DP_T * DP_PT
 // One workgroup: the per-expert token bitmasks give each expert's count, its pairs'
 // positions (a stable counting sort by expert, gemma4.c:779-786) and its first pair;
 // the union order is the order of first pairs (gemma4.c:756-761), read off a bitmap
 // over the pairs by prefix popcounts.
 // LDS: mask and word prefixes [E][W] (W = S/32 words), first-pair bitmap [P/32],
 // pair experts [P] (then the inverse permutation) and weights by position [P].
-__global__ __launch_bounds__(512) void zz_dispatch_kernel(ZzDispatchArgs a) {
+__global__ __launch_bounds__(DP_T) void zz_dispatch_kernel(ZzDispatchArgs a) {
     extern __shared__ unsigned dsm[];
     __shared__ int cnt[ZZ_MAXE], start[ZZ_MAXE], first[ZZ_MAXE], order[ZZ_MAXE], tmp[16];
-    __shared__ int fbase[DP_PT * 512 / 32];      // first pairs before each bitmap word
+    __shared__ int fbase[DP_PT * DP_T / 32];      // first pairs before each bitmap word
     const int P = a.P, E = a.E, K = a.K, S = P / K, W = (S + 31) / 32, PW = (P + 31) / 32, t = threadIdx.x;
     unsigned *mask = dsm, *wpre = dsm + E * W, *fb = wpre + E * W;
     int *pe = (int *)(fb + PW);                  // pair -> expert, later position -> pair
     float *pwl = (float *)(pe + P);              // position -> weight
-    for (int i = t; i < E * W; i += 512) mask[i] = 0u;
-    for (int i = t; i < PW; i += 512) fb[i] = 0u;
+    for (int i = t; i < E * W; i += DP_T) mask[i] = 0u;
+    for (int i = t; i < PW; i += DP_T) fb[i] = 0u;
     // every pair's expert and weight in registers first: one round of loads
     int ev[DP_PT];
     float wv[DP_PT];
 #pragma unroll
     for (int k = 0; k < DP_PT; k++) {
-        const int p = min(t + 512 * k, P - 1);
+        const int p = min(t + DP_T * k, P - 1);
         const int e = a.eidx[p];
         ev[k] = e < 0 || e >= E ? 0 : e;            // never index past the expert tables
         wv[k] = a.ewt[p];
     }
 #pragma unroll
     for (int k = 0; k < DP_PT; k++)
-        if (t + 512 * k < P) pe[t + 512 * k] = ev[k];
+        if (t + DP_T * k < P) pe[t + DP_T * k] = ev[k];
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < DP_PT; k++) {
-        const int p = t + 512 * k, s = p / K;
+        const int p = t + DP_T * k, s = p / K;
         if (p < P) atomicOr(&mask[ev[k] * W + (s >> 5)], 1u << (s & 31));
     }
     __syncthreads();
     // per expert: word prefix counts, the count, and the first pair that routes to
     // it (its lowest token, that token's slot holding e)
-    for (int e = t; e < E; e += 512) {
+    for (int e = t; e < E; e += DP_T) {
         int run = 0, s0 = -1;
         for (int w = 0; w < W; w++) {
             const unsigned m = mask[e * W + w];
@@ -454,7 +455,7 @@ __global__ __launch_bounds__(512) void zz_dispatch_kernel(ZzDispatchArgs a) {
     // through the inverse permutation, which reuses the pair-expert array
 #pragma unroll
     for (int k = 0; k < DP_PT; k++) {
-        const int p = t + 512 * k;
+        const int p = t + DP_T * k;
         if (p < P) {
             const int e = ev[k], s = p / K, w = s >> 5, bit = s & 31;
             const int pos = start[e] + wpre[e * W + w] + __popc(mask[e * W + w] & ((1u << bit) - 1u));
@@ -466,7 +467,7 @@ __global__ __launch_bounds__(512) void zz_dispatch_kernel(ZzDispatchArgs a) {
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < DP_PT; k++) {
-        const int i = t + 512 * k;
+        const int i = t + DP_T * k;
         if (i < P) {
             const int p = pe[i], s = p / K;
             a.ptok[i] = s;
@@ -529,6 +530,6 @@ int zz_launch_topk(const ZzTopkArgs &a, int S, hipStream_t st) {
 int zz_launch_dispatch(const ZzDispatchArgs &a, hipStream_t st) {
     const int W = (a.P / a.K + 31) / 32, PW = (a.P + 31) / 32;
     const size_t lds = sizeof(unsigned) * (2 * (size_t)a.E * W + PW) + 8 * (size_t)a.P;
-    hipLaunchKernelGGL(zz_dispatch_kernel, dim3(1), dim3(512), lds, st, a);
+    hipLaunchKernelGGL(zz_dispatch_kernel, dim3(1), dim3(DP_T), lds, st, a);
     return hipGetLastError() == hipSuccess;
 }
