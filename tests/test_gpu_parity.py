@@ -438,3 +438,29 @@ def test_device_quantiser_bit_exact(dev, fmt):
     torch.cuda.synchronize()
     zz.lib().gpu_init()
     assert np.array_equal(out.cpu().numpy(), want)
+
+
+def test_null_stream_orders_with_the_default_stream(dev):
+    """A NULL stream argument (the library's stream) is ordered after work the caller
+    queued on the legacy default stream, and before work queued there afterwards, with
+    no synchronisation in between: torch fills a large buffer, the library quantises
+    it at once, torch overwrites the buffer at once. The output is the quantisation of
+    the first fill (a non-blocking library stream read the buffer before it was
+    written, and every FlashHead score came out tied)."""
+    import torch
+    n = 32 * (1 << 20)
+    torch.cuda.synchronize()
+    f = torch.empty(n, dtype=torch.float32, device="cuda")
+    q = torch.zeros(n // 32 * 18, dtype=torch.uint8, device="cuda")
+    for _ in range(3):                              # several rounds, fresh values each
+        f.fill_(0.25)
+        f.mul_(torch.arange(n, device="cuda", dtype=torch.float32).remainder_(7.0).add_(1.0))
+        zz.quantize_dev(zz.GPU_FMT_Q40, f.data_ptr(), q.data_ptr(), n, 0)
+        f.fill_(float("nan"))                       # must land after the library read
+        torch.cuda.synchronize()
+        first = (0.25 * (np.arange(64, dtype=np.float32) % 7 + 1)).astype(np.float32)
+        want = Z.quant_rows(Z.FMT_Q40, first.reshape(1, -1))
+        got = q[:2 * 18].cpu().numpy()
+        assert np.array_equal(got, want)
+        tail = q[-18:].cpu().numpy()
+        assert np.isfinite(Z.dequant_q40(tail, 1, 32)).all()
