@@ -377,7 +377,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py runs on one GPU only: the MoE layer is measured on a single "
-              "MI355X (expert-parallel sharding is described in DESIGN.md, not built).",
+              "MI355X (expert-parallel sharding across GPUs is designed, not built).",
               file=sys.stderr)
         sys.exit(2)
 
