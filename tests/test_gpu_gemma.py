@@ -467,3 +467,32 @@ def test_stack_decode_with_flash_head(dev, tmp_path):
         stack.use_flash(False)
     finally:
         close_all(*objs)
+
+
+def test_flash_head_every_cluster_no_forced_ids(dev):
+    """FlashHead with no forced ids, and with every cluster probed: the probed ids are
+    then the whole vocabulary (every id is in some cluster), and the logits are the
+    full head's; both against the oracle as above."""
+    table, fnorm, F, H = Z.flash_case()
+    V, D = Z.FLASH_CASE["V"], Z.FLASH_CASE["D"]
+    hd = zz.Head(table, V, D, fnorm, 1e-6, 1.0, 30.0)
+    try:
+        for NP in (F.NP, F.NC):
+            F.NP, F.force = NP, np.zeros(0, np.int32)
+            hd.flash(F.cent, F.NC, F.tmap, F.CS, F.NP, F.cscale, F.scaled, None)
+            hd.use_flash(True)
+            lg, am = hd.logits(H)
+            want, wam, _ = Z.oracle_flash(table, V, D, fnorm, 1e-6, 30.0, F, H)
+            fin = np.isfinite(want)
+            assert np.array_equal(np.isfinite(lg), fin)
+            assert float(np.abs(lg[fin] - want[fin]).max()) < LOGIT_TOL
+            if NP == F.NC:
+                assert fin.all()
+                full, _ = Z.oracle_head(table, V, D, fnorm, 1e-6, 30.0, H)
+                assert float(np.abs(lg - full).max()) < LOGIT_TOL
+            for s in range(H.shape[0]):
+                top2 = np.sort(want[s][fin[s]])[-2:]
+                if top2[1] - top2[0] > LOGIT_TOL:
+                    assert am[s] == wam[s]
+    finally:
+        hd.close()
