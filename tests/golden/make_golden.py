@@ -97,10 +97,25 @@ def kernel_cases():
     for o in range(O):
         dtq[o] = R.ref_tq2_dot(Z.ptr(cb[o * (It // 4):]), C.c_float(alpha[o]), Z.ptr(tq_q),
                                Z.ptr(tq_s), C.c_float(tot), It)
+    # the exact-activation dots (q40.h:290-305, 443-455, tq2.h:235-252) on the same
+    # rows and the unquantised x
+    for n in ("ref_q40_dot_f32", "ref_q80_dot_f32", "ref_tq2_dot_f32"):
+        getattr(R, n).restype = C.c_float
+    d40f = np.zeros((4, O), np.float32)
+    d80f = np.zeros((4, O), np.float32)
+    for t in range(4):
+        xt_ = np.ascontiguousarray(x[t])
+        for o in range(O):
+            d40f[t, o] = R.ref_q40_dot_f32(Z.ptr(q40[o * (I // 32) * 18:]), Z.ptr(xt_), I)
+            d80f[t, o] = R.ref_q80_dot_f32(Z.ptr(q80[o * (I // 32) * 34:]), Z.ptr(xt_), I)
+    dtqf = np.zeros(O, np.float32)
+    for o in range(O):
+        dtqf[o] = R.ref_tq2_dot_f32(Z.ptr(cb[o * (It // 4):]), C.c_float(alpha[o]), Z.ptr(xt), It)
     np.savez(os.path.join(HERE, "kernels_lcg12345.npz"), w=w, q40=q40, q80=q80, x=x, xq=xq,
              xs=xs, d40=d40, d80=d80, codes=codes, alpha=alpha, tq=tq, xt=xt, tq_q=tq_q,
-             tq_s=tq_s, tq_tot=np.float32(tot), dtq=dtq)
-    print("kernels_lcg12345: q40", q40.nbytes, "B, dots", d40.size + d80.size + dtq.size)
+             tq_s=tq_s, tq_tot=np.float32(tot), dtq=dtq, d40f=d40f, d80f=d80f, dtqf=dtqf)
+    print("kernels_lcg12345: q40", q40.nbytes, "B, dots", d40.size + d80.size + dtq.size,
+          "f32 dots", d40f.size + d80f.size + dtqf.size)
 
 
 def gemma_cases():

@@ -234,6 +234,133 @@ def test_blockdots_brute_force():
     assert np.array_equal(out, ((codes[0].astype(np.int64) - 1) * xq).reshape(-1, 32).sum(1))
 
 
+# ------------------------------------------- f32-activation dots (A6, A9)
+def _f32_rows(rng, fmt, O, I, specials=False):
+    """Random q4_0 / q8_0 rows; with specials, some fp16 scales are NaN, +-inf, -0
+    or subnormal (q40.h:46-60 decodes them all)."""
+    q = Z.quant_rows(fmt, (rng.standard_normal((O, I)) * 0.05).astype(np.float32))
+    if specials:
+        bb = 18 if fmt == Z.FMT_Q40 else 34
+        blk = q.reshape(-1, bb)
+        pick = rng.choice(blk.shape[0], size=min(12, blk.shape[0]), replace=False)
+        for k, b in enumerate(pick):
+            h = [0x7e00, 0x7c00, 0xfc00, 0x8000, 0x0001, 0x03ff][k % 6]
+            blk[b, 0], blk[b, 1] = h & 255, h >> 8
+    return q
+
+
+def _dequant64(fmt, q, O, I):
+    """Closed form: the weights as float64, read from the block description."""
+    if fmt == Z.FMT_TQ2:
+        alpha = q[:O * 4].view(np.float32).astype(np.float64)
+        c = q[O * 4:].reshape(O, I // 64, 16)
+        w = np.concatenate([((c >> (2 * k)) & 3) for k in range(4)], axis=2).astype(np.float64) - 1
+        return w.reshape(O, I) * alpha[:, None]
+    bb = 18 if fmt == Z.FMT_Q40 else 34
+    blk = q.reshape(O * (I // 32), bb)
+    d = blk[:, :2].copy().view(np.float16).astype(np.float64)
+    if fmt == Z.FMT_Q40:
+        v = np.concatenate([blk[:, 2:] & 15, blk[:, 2:] >> 4], axis=1).astype(np.float64) - 8
+    else:
+        v = blk[:, 2:].view(np.int8).astype(np.float64)
+    return (v * d).reshape(O, I)
+
+
+def _matmul(fmt, W, x, O, I):
+    L = Z.oracle()
+    S = x.shape[0]
+    y = np.zeros((S, O), np.float32)
+    L.orc_matmul_f32(fmt, Z.ptr(y), Z.ptr(W), Z.ptr(np.ascontiguousarray(x, np.float32)), O, I, S)
+    return y
+
+
+def _bits_equal(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return bool(np.array_equal(np.isnan(a), np.isnan(b)) and
+                np.array_equal(a[~np.isnan(a)].view(np.uint32), b[~np.isnan(b)].view(np.uint32)))
+
+
+def test_f32_dots_golden():
+    """orc_q40/q80/tq2_dot_f32 and orc_matmul_f32 (tq2: alphas first, gpu.h:78-83)
+    against the compiled reference's q40_dot_f32 / q80_dot_f32 / tq2_dot_f32
+    (q40.h:290-305, 443-455, tq2.h:235-252) on the test_q40.c LCG stream."""
+    g = np.load(os.path.join(GOLDEN, "kernels_lcg12345.npz"))
+    L = Z.oracle()
+    O, I, It = 16, 2816, 2048
+    x = g["x"]
+    for t in range(4):
+        xt = np.ascontiguousarray(x[t])
+        a = [L.orc_q40_dot_f32(Z.ptr(g["q40"][o * 88 * 18:]), Z.ptr(xt), I) for o in range(O)]
+        b = [L.orc_q80_dot_f32(Z.ptr(g["q80"][o * 88 * 34:]), Z.ptr(xt), I) for o in range(O)]
+        assert _bits_equal(a, g["d40f"][t]) and _bits_equal(b, g["d80f"][t])
+    assert _bits_equal(_matmul(Z.FMT_Q40, g["q40"], x, O, I), g["d40f"])
+    assert _bits_equal(_matmul(Z.FMT_Q80, g["q80"], x, O, I), g["d80f"])
+    cb = g["tq"][O * 4:]
+    c = [L.orc_tq2_dot_f32(Z.ptr(cb[o * (It // 4):]), C.c_float(g["alpha"][o]), Z.ptr(g["xt"]), It)
+         for o in range(O)]
+    assert _bits_equal(c, g["dtqf"])
+    assert _bits_equal(_matmul(Z.FMT_TQ2, g["tq"], g["xt"].reshape(1, It), O, It)[0], g["dtqf"])
+
+
+@pytest.mark.parametrize("fmt", [Z.FMT_Q40, Z.FMT_Q80, Z.FMT_TQ2])
+def test_f32_dots_closed_form(fmt):
+    """The same dots against float64 dequant . x: every product is exact in
+    double, so the two differ only by the summation order, far below one float
+    ulp of the result plus the sum of magnitudes times 2^-50."""
+    rng = np.random.default_rng(11 + fmt)
+    O, S = 24, 3
+    for I in (64, 704, 2048):
+        if fmt == Z.FMT_TQ2:
+            codes = rng.integers(0, 3, size=(O, I)).astype(np.int8)
+            W = Z.tq2_tensor(codes, (rng.random(O) * 0.05 + 0.001).astype(np.float32))
+        else:
+            W = _f32_rows(rng, fmt, O, I)
+        x = rng.standard_normal((S, I)).astype(np.float32)
+        x[1] *= np.float32(1e3)
+        w64 = _dequant64(fmt, W, O, I)
+        ref = x.astype(np.float64) @ w64.T
+        mag = np.abs(x.astype(np.float64)) @ np.abs(w64).T
+        got = _matmul(fmt, W, x, O, I).astype(np.float64)
+        ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+        assert np.all(np.abs(got - ref) <= ulp + mag * 2.0 ** -50), (fmt, I)
+
+
+def test_f32_dots_vs_compiled_reference():
+    """Live against the reference's own *_dot_f32 (oracle/_ref), on random rows whose
+    fp16 scales include NaN, +-inf, -0 and subnormals, bit for bit."""
+    R = Z.ref_lib("kernels")
+    if R is None:
+        pytest.skip("oracle/_ref not built (needs /root/reference)")
+    for n in ("ref_q40_dot_f32", "ref_q80_dot_f32", "ref_tq2_dot_f32"):
+        getattr(R, n).restype = C.c_float
+    L = Z.oracle()
+    rng = np.random.default_rng(29)
+    for I in (32, 96, 2816):
+        O = 16
+        x = (rng.standard_normal((2, I)) * np.float32(3.0)).astype(np.float32)
+        for fmt, bb, fo, fr in ((Z.FMT_Q40, 18, L.orc_q40_dot_f32, R.ref_q40_dot_f32),
+                                (Z.FMT_Q80, 34, L.orc_q80_dot_f32, R.ref_q80_dot_f32)):
+            W = _f32_rows(rng, fmt, O, I, specials=True)
+            want = np.array([[fr(Z.ptr(W[o * (I // 32) * bb:]), Z.ptr(x[s]), I) for o in range(O)]
+                             for s in range(2)], np.float32)
+            got = np.array([[fo(Z.ptr(W[o * (I // 32) * bb:]), Z.ptr(x[s]), I) for o in range(O)]
+                            for s in range(2)], np.float32)
+            assert _bits_equal(got, want), (fmt, I)
+            assert _bits_equal(_matmul(fmt, W, x, O, I), want), (fmt, I)
+            assert np.isnan(want).any()
+    for I in (64, 2048):
+        O = 8
+        codes = rng.integers(0, 3, size=(O, I)).astype(np.int8)
+        alpha = (rng.standard_normal(O) * 0.05).astype(np.float32)
+        alpha[0], alpha[1] = np.inf, 0.0
+        W = Z.tq2_tensor(codes, alpha)
+        x = rng.standard_normal((1, I)).astype(np.float32)
+        cb = W[O * 4:]
+        want = np.array([R.ref_tq2_dot_f32(Z.ptr(cb[o * (I // 4):]), C.c_float(alpha[o]), Z.ptr(x[0]), I)
+                         for o in range(O)], np.float32)
+        assert _bits_equal(_matmul(Z.FMT_TQ2, W, x, O, I)[0], want)
+
+
 def test_tq2_layout_from_description():
     """tests/test_tq2.c:28-35: code j lives in byte j%16 of group j/64 at bit
     2*((j/16)%4); the oracle's packer and dequant must agree with that reading."""
