@@ -3,16 +3,24 @@
  *
  * Same symbols, format codes and decline contract as the reference's gpu.h
  * (gpu.h:35-109), so an engine built against this header links against
- * libzzmoe.so instead of metal.o with no source change. Every entry point is
- * fallible: 0 means "not done, run the CPU path" and leaves every output
- * untouched (gpu.h:31-33, 76-79; maple.c:621-624 relies on that).
+ * libzzmoe.so instead of metal.o. Every entry point is fallible: 0 means "not
+ * done, run the CPU path" and leaves every output untouched (gpu.h:31-33, 76-79;
+ * maple.c:621-624 relies on that).
  *
  * Differences forced by a discrete GPU, all inside the same contract:
  *  - gpu_map() cannot wrap host pages without a copy (gpu.h:66-69 "NO copy" is a
- *    unified-memory property). It uploads the range into HBM once. Mapping a range
- *    inside an existing mapping re-uploads those bytes (the refresh an engine needs
- *    after rewriting a mapped buffer, e.g. an expert slot filled by pread); a range
- *    that only overlaps older mappings replaces them (the host memory was reused).
+ *    unified-memory property). It uploads the range into HBM when called, and
+ *    bytes written to the host range afterwards are not seen until that range is
+ *    mapped again: mapping a range inside an existing mapping re-uploads those
+ *    bytes; a range that only overlaps older mappings replaces them (the host
+ *    memory was reused).
+ *    The engines map each expert slot once, while it is still empty
+ *    (gemma4.c:2051-2058, lfm25.c:1894, maple.c:1322, ling.c:1873), and then pread
+ *    other experts into it (gemma4.c:484-491). Linked unchanged, their per-row
+ *    expert matmuls (gemma4.c:670-684) would read the bytes the slot held at map
+ *    time. Each engine therefore needs one added line: gpu_map(slot->buf, esz) on
+ *    the main thread after a slot is refilled and before its first matmul. The
+ *    dense blob (gemma4.c:348), mapped once after it is read, needs nothing.
  *  - gpu_matmul() copies x in and y out per call (PCIe), then runs a dequantising
  *    GEMV with f32 activations: the *_dot_f32 semantics (gpu.h:25-27), checked to
  *    < 1e-4 relative like gemma4.c:2315-2368.

@@ -285,6 +285,54 @@ def test_stack_runner_graph_equals_eager(dev):
         close_all(*objs)
 
 
+def test_stack_graph_recaptured_after_longer_prefill(dev):
+    """A captured decode step holds raw pointers to the layers' workspaces and the
+    blocks' rows. A longer prefill reallocates both, so the next graph decode must
+    capture again: prefill 2 rows, graph decode, prefill 8 rows, graph decode, and
+    the second graph decode must equal an eager decode from the same token bit for
+    bit (tokens and last logits)."""
+    import torch
+    *_, st, H0 = Z.gemma_block_case()
+    D, V = st.layers[0].D, st.V
+    blocks, objs = [], []
+    for L_, dn in zip(st.layers, st.denses):
+        B, m, d = gpu_block(L_, dn)
+        blocks.append(B)
+        objs += [B, m, d]
+    hd = zz.Head(st.table, V, D, st.fnorm, st.layers[0].eps, st.embed_scale, st.softcap)
+    stack = zz.Stack(blocks, hd)
+    objs += [stack, hd]
+    n = 4
+    try:
+        s = torch.cuda.current_stream().cuda_stream
+
+        def decode(tok, graph):
+            toks = torch.zeros(n + 1, dtype=torch.int32, device="cuda")
+            toks[0] = tok
+            lg = torch.zeros(V, dtype=torch.float32, device="cuda")
+            stack.decode_dev(toks.data_ptr(), n, lg.data_ptr(), graph=graph, stream=s)
+            torch.cuda.synchronize()
+            return toks.cpu().numpy(), lg.cpu().numpy()
+
+        tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+        dH = torch.from_numpy(np.ascontiguousarray(H0[:2])).cuda()
+        stack.prefill_dev(dH.data_ptr(), 2, tok.data_ptr(), s)
+        t_short, _ = decode(int(tok.item()), True)
+        H8 = np.random.default_rng(8).standard_normal((8, D)).astype(np.float32)
+        dH8 = torch.from_numpy(H8).cuda()
+        stack.prefill_dev(dH8.data_ptr(), 8, tok.data_ptr(), s)
+        t8 = int(tok.item())
+        tg, lgg = decode(t8, True)
+        te, lge = decode(t8, False)
+        say("tokens after the short prefill", t_short.tolist(), "after the long one", tg.tolist())
+        assert np.array_equal(tg, te), (tg, te)
+        assert np.array_equal(lgg.view(np.uint32), lge.view(np.uint32))
+        tg2, lgg2 = decode(t8, True)                  # the recaptured graph, replayed
+        assert np.array_equal(tg2, te) and np.array_equal(lgg2.view(np.uint32), lge.view(np.uint32))
+    finally:
+        close_all(*objs)
+
+
 def test_container_load(dev, tmp_path):
     """zz_gemma_stack_load / zz_moe_load_experts on a container directory written in
     the converter's layout: the loaded stack decodes exactly as the stack built from

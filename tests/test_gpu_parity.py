@@ -220,6 +220,37 @@ def test_gpu_matmul_other_formats(dev, fmt):
     assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-4
 
 
+def test_gpu_map_slot_refill_needs_a_remap(dev):
+    """The engines map an expert slot once, while empty (gemma4.c:2051-2058), then
+    pread other experts into the same bytes (gemma4.c:484-491). A discrete GPU
+    copies at map time, so gpu_matmul keeps using the bytes of the last upload until
+    the rewritten range is mapped again; mapping a sub-range of an existing mapping
+    re-uploads just that range."""
+    rng = np.random.default_rng(43)
+    O, I = 256, 512
+    rb = O * (I // 32) * 18
+    slot = np.zeros(2 * rb, np.uint8)               # two tensors in one mapped slot
+    A = Z.quant_rows(Z.FMT_Q40, (rng.standard_normal((O, I)) * 0.02).astype(np.float32))
+    Bw = Z.quant_rows(Z.FMT_Q40, (rng.standard_normal((O, I)) * 0.02).astype(np.float32))
+    slot[:rb] = A
+    Wm = zz.gpu_map(slot)
+    x = rng.standard_normal((1, I)).astype(np.float32)
+
+    def ref(W):
+        y = np.zeros((1, O), np.float32)
+        Z.oracle().orc_matmul_f32(Z.FMT_Q40, Z.ptr(y), Z.ptr(np.ascontiguousarray(W)), Z.ptr(x), O, I, 1)
+        return y
+
+    ya = zz.gpu_matmul(Z.FMT_Q40, Wm[:rb], x, O, I)
+    assert np.abs(ya - ref(A)).max() / np.abs(ref(A)).max() < 1e-4
+    Wm[:rb] = Bw                                    # the "pread" of another expert
+    stale = zz.gpu_matmul(Z.FMT_Q40, Wm[:rb], x, O, I)
+    assert np.array_equal(stale, ya)                # not re-mapped: the old bytes
+    assert zz.lib().gpu_map(C.c_void_p(Wm.ctypes.data), rb) == 1   # refresh the sub-range
+    yb = zz.gpu_matmul(Z.FMT_Q40, Wm[:rb], x, O, I)
+    assert np.abs(yb - ref(Bw)).max() / np.abs(ref(Bw)).max() < 1e-4
+
+
 def test_gpu_matmul_declines_unmapped_and_q4a(dev):
     x = np.ones((1, 64), np.float32)
     y = np.full((1, 8), 5.0, np.float32)

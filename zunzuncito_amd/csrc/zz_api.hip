@@ -35,6 +35,7 @@ static int g_dec_max_s = ZZ_DEC_MAXS;
 static char g_name[128] = "none";
 static hipStream_t g_stream = nullptr;
 static unsigned *g_diag = nullptr;          // device counters, see zz_moe_stats
+static unsigned long long g_mem_gen = 1;    // see zz_lib_mem_gen
 
 struct Mapping {
     const uint8_t *host;
@@ -244,6 +245,7 @@ static int upload_f32(float **dst, const float *src, size_t n) {
 
 static void free_layer(Layer *L) {
     if (!L) return;
+    zz_lib_mem_bump();
     void *ps[] = {L->router, L->rscale, L->pes, L->bias, L->pre_ln, L->post_ln, L->slots,
                   L->staging, L->ws.block};
     for (void *p : ps)
@@ -304,6 +306,8 @@ static Layer *get_layer(int id) {
 // library internals shared with zz_gemma.hip
 hipStream_t zz_lib_stream() { return g_stream; }
 int zz_lib_ready() { return g_ready; }
+unsigned long long zz_lib_mem_gen() { return g_mem_gen; }
+void zz_lib_mem_bump() { g_mem_gen++; }
 unsigned *zz_lib_diag() { return g_diag; }
 const zz_moe_desc *zz_layer_desc(int id) {
     const Layer *L = get_layer(id);
@@ -380,6 +384,7 @@ static int ensure_ws(Layer *L, int S) {
     ZZ_CHECK(hipStreamSynchronize(g_stream));
     ZZ_CHECK(hipMalloc(&blk, off));
     if (w.block) (void)hipFree(w.block);
+    zz_lib_mem_bump();
     char *b = (char *)blk;
     w.block = blk;
     w.S = S;

@@ -197,6 +197,7 @@ static std::vector<FfnBlock *> g_blocks;
 
 static void free_block(FfnBlock *B) {
     if (!B) return;
+    zz_lib_mem_bump();
     if (B->ds) (void)hipStreamSynchronize(B->ds);
     void *ps[] = {B->post_ln, B->h1, B->h2, B->hh};
     for (void *p : ps)
@@ -261,6 +262,7 @@ static int block_grow(FfnBlock *B, int S, hipStream_t st) {
         *p = nullptr;
     }
     B->cap = 0;
+    zz_lib_mem_bump();
     const size_t n = sizeof(float) * (size_t)S * B->D;
     ZZ_CHECK(hipMalloc(&B->h1, n));
     ZZ_CHECK(hipMalloc(&B->h2, n));
@@ -344,6 +346,7 @@ struct Head {
 static std::vector<Head *> g_heads;
 
 static void free_flash(ZzFlashArgs &f, bool keep_table) {
+    zz_lib_mem_bump();
     void *ps[] = {(void *)f.cent, (void *)f.tmap, (void *)f.cscale, (void *)f.force,
                   f.fsim, f.sel, f.part};
     for (void *p : ps)
@@ -356,6 +359,7 @@ static void free_flash(ZzFlashArgs &f, bool keep_table) {
 
 static void free_head(Head *h) {
     if (!h) return;
+    zz_lib_mem_bump();
     void *ps[] = {h->table, h->fnorm, h->xq, h->xs, h->xsum, h->part};
     for (void *p : ps)
         if (p) (void)hipFree(p);
@@ -582,6 +586,8 @@ struct Stack {
     int *cur = nullptr;             // the current token
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;  // one decode step, captured on first use
+    unsigned long long gen = 0;     // zz_lib_mem_gen() the graph was captured at
+    unsigned long long warm = 0;    // zz_lib_mem_gen() after the last eager step
     // what a container load created for this stack, destroyed with it
     std::vector<int> own_layers, own_blocks;
     int own_head = -1;
@@ -609,14 +615,17 @@ static Stack *get_stack(int id) {
     return g_stacks[id];
 }
 
+static void drop_graph(Stack *k) {
+    if (k->exec) (void)hipGraphExecDestroy(k->exec);
+    if (k->graph) (void)hipGraphDestroy(k->graph);
+    k->exec = nullptr;
+    k->graph = nullptr;
+}
+
 static void drop_graphs_of_head(int head) {
     for (Stack *k : g_stacks)
-        if (k && k->head == head) {
-            if (k->exec) (void)hipGraphExecDestroy(k->exec);
-            if (k->graph) (void)hipGraphDestroy(k->graph);
-            k->exec = nullptr;
-            k->graph = nullptr;
-        }
+        if (k && k->head == head) drop_graph(k);
+    zz_lib_mem_bump();
 }
 
 extern "C" int zz_stack_use_flash(int id, int on) {
@@ -702,29 +711,37 @@ extern "C" int zz_stack_decode_dev(int id, int *d_tok, int n, float *d_logits, i
     hipStream_t st = stream ? (hipStream_t)stream : zz_lib_stream();
     ZZ_CHECK(hipMemcpyAsync(k->cur, d_tok, sizeof(int), hipMemcpyDeviceToDevice, st));
     for (int i = 0; i < n; i++) {
-        if (use_graph && i > 0 && !k->exec) {
-            // step 0 ran eagerly, so every workspace already holds one row: the
-            // captured step allocates nothing and waits on nothing
+        // a graph holds raw device pointers: once any buffer it may reference was
+        // freed or reallocated (a longer prefill grows the workspaces, a FlashHead is
+        // attached or switched), it is dropped and captured again
+        if (k->exec && k->gen != zz_lib_mem_gen()) drop_graph(k);
+        if (use_graph && !k->exec && k->warm == zz_lib_mem_gen()) {
+            // an eager step ran on the current buffers, so every workspace already
+            // holds one row: the captured step allocates nothing and waits on nothing
+            const unsigned long long gen = zz_lib_mem_gen();
             const int prof = zz_lib_prof_set(0);           // no timing events in the graph
             const hipError_t b = hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed);
             const int ok = b == hipSuccess && stack_step(k, st);
             hipGraph_t g = nullptr;
             const hipError_t e = b == hipSuccess ? hipStreamEndCapture(st, &g) : b;
             zz_lib_prof_set(prof);
-            if (!ok || e != hipSuccess) {
+            if (!ok || e != hipSuccess || zz_lib_mem_gen() != gen) {
                 if (g) (void)hipGraphDestroy(g);
-                ZZ_FAIL("zz_stack_decode_dev: capture failed (%s)", hipGetErrorString(e));
+                ZZ_FAIL("zz_stack_decode_dev: capture failed (%s%s)", hipGetErrorString(e),
+                        zz_lib_mem_gen() != gen ? ", buffers reallocated during capture" : "");
             }
             k->graph = g;
             if (hipGraphInstantiate(&k->exec, g, nullptr, nullptr, 0) != hipSuccess) {
-                k->exec = nullptr;
+                drop_graph(k);
                 ZZ_FAIL("zz_stack_decode_dev: graph instantiation failed");
             }
+            k->gen = gen;
         }
         if (use_graph && k->exec) {
             ZZ_CHECK(hipGraphLaunch(k->exec, st));
-        } else if (!stack_step(k, st)) {
-            return 0;
+        } else {
+            if (!stack_step(k, st)) return 0;
+            k->warm = zz_lib_mem_gen();
         }
         ZZ_CHECK(hipMemcpyAsync(d_tok + i + 1, k->cur, sizeof(int), hipMemcpyDeviceToDevice, st));
     }

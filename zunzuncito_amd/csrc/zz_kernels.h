@@ -175,6 +175,12 @@ int zz_lib_ready();
 unsigned *zz_lib_diag();
 const zz_moe_desc *zz_layer_desc(int id);
 int zz_lib_prof_set(int on);        // per-kernel event timing on/off; returns the old state
+// Generation of the library's device buffers: bumped whenever a buffer that a
+// captured HIP graph may hold (a layer, its workspace, a block's rows, a head or its
+// FlashHead tensors) is freed or reallocated. A captured graph is valid only while
+// the generation it was captured at is current.
+unsigned long long zz_lib_mem_gen();
+void zz_lib_mem_bump();
 // a gemma FFN block's decode rows with the dense branch fused into the routed layer's
 // launches: 1 done, 0 failed, -1 not applicable
 int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_h2, const float *post_ln,
