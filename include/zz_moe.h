@@ -109,6 +109,19 @@ int zz_moe_forward(int layer, const float *in, float *out, int S, int *eidx, flo
 int zz_moe_forward_dev(int layer, const float *d_in, float *d_out, int S, int *d_eidx,
                        float *d_ewt, void *stream);
 
+/* zz_moe_forward_dev without any device allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The layer's
+ * workspace is replaced by a fixed 64 MiB scratch array that the library's code
+ * object brings with it, one per device, held until the process ends. A chunk of
+ * min(S, the layer's chunk size) tokens must fit it: Gemma-4's layer (D 2816,
+ * E 128, K 8) takes up to 580 tokens per call, LFM2.5's 1239, Maple's 751.
+ * Larger S is declined with a message naming the limit, outputs untouched. No
+ * per-kernel timing is recorded. Every call on a device shares the one array:
+ * calls that overlap on one device (two streams, two threads) race. */
+int zz_moe_forward_dev_noalloc(int layer, const float *d_in, float *d_out, int S, int *d_eidx,
+                               float *d_ewt, void *stream);
+
 /* Split form for overlap (gemma runs its dense MLP between moe_start and
  * moe_finish, gemma4.c:1012-1021): begin uploads `in` and enqueues the layer;
  * end waits and writes out/eidx/ewt. One begin may be outstanding. */

@@ -34,7 +34,7 @@ ABI_SYMBOLS = (
     "zz_head_embed", "zz_head_logits_dev", "zz_head_logits", "zz_stack_create",
     "zz_stack_destroy", "zz_stack_prefill_dev", "zz_stack_decode_dev", "zz_moe_load_experts",
     "zz_gemma_stack_load", "zz_head_flash", "zz_head_use_flash", "zz_head_flash_replays",
-    "zz_stack_use_flash",
+    "zz_stack_use_flash", "zz_moe_forward_dev_noalloc",
 )
 KERNELS = ("prep", "logits", "topk", "dispatch", "ffn_up", "ffn_down", "combine", "dec_route",
            "dec_down")
@@ -97,6 +97,8 @@ def lib():
     L.zz_moe_forward.argtypes = [C.c_int, _f32p, _f32p, C.c_int, _i32p, _f32p]
     L.zz_moe_forward_dev.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
                                      C.c_void_p, C.c_void_p]
+    L.zz_moe_forward_dev_noalloc.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                                             C.c_void_p, C.c_void_p]
     L.zz_moe_forward_begin.argtypes = [C.c_int, _f32p, C.c_int]
     L.zz_moe_forward_end.argtypes = [C.c_int, _f32p, _i32p, _f32p]
     L.zz_moe_debug.argtypes = [C.c_int, C.POINTER(ZzMoeDump)]
@@ -242,6 +244,13 @@ class MoeLayer:
                                       C.c_void_p(stream or None))
         if not ok:
             raise RuntimeError(f"zz_moe_forward_dev declined: {last_error()}")
+
+    def forward_dev_noalloc(self, d_in, d_out, S, d_eidx=0, d_ewt=0, stream=0):
+        """forward_dev on the library's fixed scratch array: allocates nothing.
+        Returns False (with last_error()) when the batch does not fit the scratch."""
+        return bool(lib().zz_moe_forward_dev_noalloc(self.id, C.c_void_p(d_in), C.c_void_p(d_out), S,
+                                                     C.c_void_p(d_eidx or None), C.c_void_p(d_ewt or None),
+                                                     C.c_void_p(stream or None)))
 
     def debug(self, S, logits=False):
         """The last forward's dump (zz_moe_debug); logits=True adds the batched

@@ -37,6 +37,17 @@ static hipStream_t g_stream = nullptr;
 static unsigned *g_diag = nullptr;          // device counters, see zz_moe_stats
 static unsigned long long g_mem_gen = 1;    // see zz_lib_mem_gen
 
+// Scratch of zz_moe_forward_dev_noalloc: the workspace of one chunk, in a
+// file-scope device array that the code object brings with it (zero at load, held
+// by each device until the process ends). In host code `scratch` names a host-side
+// stand-in, not device memory: gpu_init takes the array's device address on each
+// device once with hipGetSymbolAddress, and only that address is used.
+#define ZZ_SCRATCH_BYTES ((size_t)64 << 20)
+#define ZZ_MAX_DEVICES 16
+static __device__ __align__(256) unsigned char scratch[ZZ_SCRATCH_BYTES];
+static char *g_scratch[ZZ_MAX_DEVICES];     // scratch's address on device i
+static hipError_t g_scratch_err = hipSuccess;
+
 struct Mapping {
     const uint8_t *host;
     size_t n;
@@ -56,6 +67,13 @@ extern "C" int gpu_init(void) {
     ZZ_CHECK(hipGetDeviceProperties(&p, 0));
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0) ZZ_FAIL("device %s is not gfx950", p.gcnArchName);
     snprintf(g_name, sizeof g_name, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    // the scratch array's address on this device (device 0, current since above);
+    // without it only zz_moe_forward_dev_noalloc declines, with this error
+    if (!g_scratch[0]) {
+        void *sp = nullptr;
+        g_scratch_err = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+        if (g_scratch_err == hipSuccess && sp) g_scratch[0] = (char *)sp;
+    }
     // the library's stream, what a NULL stream argument means: a blocking stream, so it
     // is ordered with the legacy default stream both ways, as a caller passing the
     // default stream's handle (0, e.g. torch's current stream) expects
@@ -359,45 +377,49 @@ static int chunk_tokens(const zz_moe_desc &d) {
     return by_pairs < by_masks ? by_pairs : by_masks;
 }
 
-static int ensure_ws(Layer *L, int S) {
-    Workspace &w = L->ws;
-    if (S <= w.S) return 1;
-    const zz_moe_desc &d = L->d;
+// Lays the workspace of S tokens of layer d out from `base` (nullptr: only
+// measures). host_io adds the in/out staging rows that only the host-pointer
+// forms use. Returns the bytes the layout spans.
+static size_t ws_layout(const zz_moe_desc &d, int S, bool host_io, char *base, Workspace *w) {
     const size_t P = (size_t)S * d.K, nbD = d.D / ZZ_BLK, nbM = d.MI / ZZ_BLK;
     const size_t nitems = (size_t)d.E + P / 8 + 8;
     size_t off = 0;
     auto take = [&](size_t bytes) {
         size_t o = off;
         off = (off + bytes + 255) & ~(size_t)255;
-        return o;
+        return base ? base + o : nullptr;
     };
-    size_t o_in = take(4 * S * (size_t)d.D), o_out = take(4 * S * (size_t)d.D), o_xn = take(4 * S * (size_t)d.D);
-    size_t o_xq = take(S * (size_t)d.D), o_xs = take(4 * S * nbD), o_xsum = take(4 * S * nbD), o_xt = take(4 * (size_t)S);
-    size_t o_cen = take(8 * S * (size_t)d.E), o_bnd = take(8 * S * (size_t)d.E);
-    size_t o_eidx = take(4 * P), o_ewt = take(4 * P), o_topv = take(4 * P), o_cont = take(4 * (size_t)S);
-    size_t o_ptok = take(4 * P), o_pslot = take(4 * P), o_ppos = take(4 * P), o_pwt = take(4 * P);
-    size_t o_uniq = take(4 * (size_t)d.E), o_uoff = take(4 * (size_t)d.E), o_ucnt = take(4 * (size_t)d.E);
-    size_t o_meta = take(64), o_items = take(sizeof(ZzItem) * nitems);
-    size_t o_hq = take(P * d.MI), o_hs = take(4 * P * nbM), o_hsum = take(4 * P * nbM);
-    size_t o_y = take(4 * P * d.D), o_ss = take(8 * S * (size_t)(d.D / 16));
+    Workspace v;
+    v.S = S;
+    v.in = (float *)take(host_io ? 4 * S * (size_t)d.D : 0);
+    v.out = (float *)take(host_io ? 4 * S * (size_t)d.D : 0);
+    v.xn = (float *)take(4 * S * (size_t)d.D);
+    v.xq = (int8_t *)take(S * (size_t)d.D); v.xs = (float *)take(4 * S * nbD); v.xsum = (int *)take(4 * S * nbD);
+    v.xt = (float *)take(4 * (size_t)S);
+    v.cen = (double *)take(8 * S * (size_t)d.E); v.bnd = (double *)take(8 * S * (size_t)d.E);
+    v.eidx = (int *)take(4 * P); v.ewt = (float *)take(4 * P); v.topv = (float *)take(4 * P);
+    v.contested = (int *)take(4 * (size_t)S);
+    v.ptok = (int *)take(4 * P); v.pslot = (int *)take(4 * P); v.ppos = (int *)take(4 * P); v.pwt = (float *)take(4 * P);
+    v.uniq = (int *)take(4 * (size_t)d.E); v.uoff = (int *)take(4 * (size_t)d.E); v.ucnt = (int *)take(4 * (size_t)d.E);
+    v.meta = (int *)take(64); v.items = (ZzItem *)take(sizeof(ZzItem) * nitems);
+    v.hq = (int8_t *)take(P * d.MI); v.hs = (float *)take(4 * P * nbM); v.hsum = (int *)take(4 * P * nbM);
+    v.y = (float *)take(4 * P * d.D); v.ss = (double *)take(8 * S * (size_t)(d.D / 16));
+    if (!host_io) v.in = v.out = nullptr;
+    if (w) *w = v;
+    return off;
+}
+
+static int ensure_ws(Layer *L, int S) {
+    Workspace &w = L->ws;
+    if (S <= w.S) return 1;
+    const size_t bytes = ws_layout(L->d, S, true, nullptr, nullptr);
     void *blk = nullptr;
     ZZ_CHECK(hipStreamSynchronize(g_stream));
-    ZZ_CHECK(hipMalloc(&blk, off));
+    ZZ_CHECK(hipMalloc(&blk, bytes));
     if (w.block) (void)hipFree(w.block);
     zz_lib_mem_bump();
-    char *b = (char *)blk;
+    ws_layout(L->d, S, true, (char *)blk, &w);
     w.block = blk;
-    w.S = S;
-    w.in = (float *)(b + o_in); w.out = (float *)(b + o_out); w.xn = (float *)(b + o_xn);
-    w.xq = (int8_t *)(b + o_xq); w.xs = (float *)(b + o_xs); w.xsum = (int *)(b + o_xsum);
-    w.xt = (float *)(b + o_xt); w.cen = (double *)(b + o_cen); w.bnd = (double *)(b + o_bnd);
-    w.eidx = (int *)(b + o_eidx); w.ewt = (float *)(b + o_ewt); w.topv = (float *)(b + o_topv);
-    w.contested = (int *)(b + o_cont); w.ptok = (int *)(b + o_ptok); w.pslot = (int *)(b + o_pslot);
-    w.ppos = (int *)(b + o_ppos); w.pwt = (float *)(b + o_pwt); w.uniq = (int *)(b + o_uniq);
-    w.uoff = (int *)(b + o_uoff); w.ucnt = (int *)(b + o_ucnt); w.meta = (int *)(b + o_meta);
-    w.items = (ZzItem *)(b + o_items); w.hq = (int8_t *)(b + o_hq); w.hs = (float *)(b + o_hs);
-    w.hsum = (int *)(b + o_hsum); w.y = (float *)(b + o_y);
-    w.ss = (double *)(b + o_ss);
     ZZ_CHECK(hipStreamSynchronize(g_stream));
     return 1;
 }
@@ -485,9 +507,8 @@ struct ChunkArgs {
     int P, max_items;
 };
 
-static ChunkArgs chunk_args(Layer *L, const float *d_in, int S) {
+static ChunkArgs chunk_args(Layer *L, Workspace &w, const float *d_in, int S) {
     const zz_moe_desc &d = L->d;
-    Workspace &w = L->ws;
     ChunkArgs c;
     memset(&c, 0, sizeof c);
     c.dense = d.gating == ZZ_GATE_DENSE;            // gemma's norms, no router
@@ -530,10 +551,9 @@ static ChunkArgs chunk_args(Layer *L, const float *d_in, int S) {
     return c;
 }
 
-static int run_chunk(Layer *L, const float *d_in, float *d_out, int S, hipStream_t st) {
+static int run_chunk(Layer *L, Workspace &w, const float *d_in, float *d_out, int S, hipStream_t st) {
     const zz_moe_desc &d = L->d;
-    Workspace &w = L->ws;
-    ChunkArgs c = chunk_args(L, d_in, S);
+    ChunkArgs c = chunk_args(L, w, d_in, S);
 
     if (c.dec) {
         ZzDecRouteArgs ra;
@@ -585,8 +605,8 @@ int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_
         return -1;
     if (L->n_present != d.E || N->n_present != dn.E) ZZ_FAIL("block: experts not uploaded");
     if (!ensure_ws(L, S) || !ensure_ws(N, S)) return 0;
-    ChunkArgs c = chunk_args(L, d_H, S), cn = chunk_args(N, d_H, S);
     Workspace &w = L->ws, &wn = N->ws;
+    ChunkArgs c = chunk_args(L, w, d_H, S), cn = chunk_args(N, wn, d_H, S);
 
     ZzDecRouteArgs ra;
     memset(&ra, 0, sizeof ra);
@@ -612,6 +632,19 @@ int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_
     return 1;
 }
 
+// the chunks of a device-pointer forward, on workspace w (chunks of <= CH tokens)
+static int run_chunks(Layer *L, Workspace &w, int CH, const float *d_in, float *d_out, int S, int *d_eidx,
+                      float *d_ewt, hipStream_t st) {
+    const zz_moe_desc &d = L->d;
+    for (int s0 = 0; s0 < S; s0 += CH) {
+        int n = S - s0 < CH ? S - s0 : CH;
+        if (!run_chunk(L, w, d_in + (size_t)s0 * d.D, d_out + (size_t)s0 * d.D, n, st)) return 0;
+        if (d_eidx) ZZ_CHECK(hipMemcpyAsync(d_eidx + (size_t)s0 * d.K, w.eidx, sizeof(int) * n * d.K, hipMemcpyDeviceToDevice, st));
+        if (d_ewt) ZZ_CHECK(hipMemcpyAsync(d_ewt + (size_t)s0 * d.K, w.ewt, sizeof(float) * n * d.K, hipMemcpyDeviceToDevice, st));
+    }
+    return 1;
+}
+
 static int forward_dev(Layer *L, const float *d_in, float *d_out, int S, int *d_eidx, float *d_ewt,
                        hipStream_t st) {
     const zz_moe_desc &d = L->d;
@@ -619,13 +652,8 @@ static int forward_dev(Layer *L, const float *d_in, float *d_out, int S, int *d_
     if (L->n_present != d.E) ZZ_FAIL("forward: %d of %d experts uploaded", L->n_present, d.E);
     const int CH = chunk_tokens(d);
     if (!ensure_ws(L, S < CH ? S : CH)) return 0;
-    for (int s0 = 0; s0 < S; s0 += CH) {
-        int n = S - s0 < CH ? S - s0 : CH;
-        if (!run_chunk(L, d_in + (size_t)s0 * d.D, d_out + (size_t)s0 * d.D, n, st)) return 0;
-        if (d_eidx) ZZ_CHECK(hipMemcpyAsync(d_eidx + (size_t)s0 * d.K, L->ws.eidx, sizeof(int) * n * d.K, hipMemcpyDeviceToDevice, st));
-        if (d_ewt) ZZ_CHECK(hipMemcpyAsync(d_ewt + (size_t)s0 * d.K, L->ws.ewt, sizeof(float) * n * d.K, hipMemcpyDeviceToDevice, st));
-        if (s0 == 0) L->last_S = n;
-    }
+    if (!run_chunks(L, L->ws, CH, d_in, d_out, S, d_eidx, d_ewt, st)) return 0;
+    L->last_S = S < CH ? S : CH;
     return 1;
 }
 
@@ -634,6 +662,36 @@ extern "C" int zz_moe_forward_dev(int id, const float *d_in, float *d_out, int S
     Layer *L = get_layer(id);
     if (!L || !d_in || !d_out) ZZ_FAIL("zz_moe_forward_dev: bad arguments");
     return forward_dev(L, d_in, d_out, S, d_eidx, d_ewt, stream ? (hipStream_t)stream : g_stream);
+}
+
+// The device-pointer forward on the scratch array instead of the layer's workspace:
+// no allocation at any point. Every call on a device shares its one array, which
+// keeps the last call's contents; no kernel reads workspace memory it has not
+// written in the same call, so nothing is cleared. Calls that overlap on one device
+// (two streams, two threads) race on it.
+extern "C" int zz_moe_forward_dev_noalloc(int id, const float *d_in, float *d_out, int S, int *d_eidx,
+                                          float *d_ewt, void *stream) {
+    Layer *L = get_layer(id);
+    if (!L || !d_in || !d_out || S <= 0) ZZ_FAIL("zz_moe_forward_dev_noalloc: bad arguments");
+    const zz_moe_desc &d = L->d;
+    if (L->n_present != d.E) ZZ_FAIL("forward: %d of %d experts uploaded", L->n_present, d.E);
+    int dev = -1;
+    ZZ_CHECK(hipGetDevice(&dev));
+    char *base = dev >= 0 && dev < ZZ_MAX_DEVICES ? g_scratch[dev] : nullptr;
+    if (!base)
+        ZZ_FAIL("zz_moe_forward_dev_noalloc: no scratch address on device %d (%s)", dev,
+                hipGetErrorString(g_scratch_err));
+    const int CH = chunk_tokens(d), S1 = S < CH ? S : CH;
+    const size_t need = ws_layout(d, S1, false, nullptr, nullptr);
+    if (need > ZZ_SCRATCH_BYTES)
+        ZZ_FAIL("zz_moe_forward_dev_noalloc: %d tokens of this layer need %zu bytes of scratch, above its %zu: "
+                "pass fewer tokens per call", S1, need, ZZ_SCRATCH_BYTES);
+    Workspace w;
+    ws_layout(d, S1, false, base, &w);
+    const int prof = zz_lib_prof_set(0);           // its timing events would be created on demand
+    const int ok = run_chunks(L, w, CH, d_in, d_out, S, d_eidx, d_ewt, stream ? (hipStream_t)stream : g_stream);
+    zz_lib_prof_set(prof);
+    return ok;
 }
 
 // Host-pointer forward: stage through the workspace chunk by chunk.
@@ -650,7 +708,7 @@ static int forward_host(Layer *L, const float *in, float *out, int S, int *eidx,
     for (int s0 = 0; s0 < S; s0 += CH) {
         int n = S - s0 < CH ? S - s0 : CH;
         ZZ_CHECK(hipMemcpyAsync(w.in, in + (size_t)s0 * d.D, sizeof(float) * n * d.D, hipMemcpyHostToDevice, g_stream));
-        if (!run_chunk(L, w.in, w.out, n, g_stream)) return 0;
+        if (!run_chunk(L, w, w.in, w.out, n, g_stream)) return 0;
         ZZ_CHECK(hipMemcpyAsync(o.data() + (size_t)s0 * d.D, w.out, sizeof(float) * n * d.D, hipMemcpyDeviceToHost, g_stream));
         ZZ_CHECK(hipMemcpyAsync(ix.data() + (size_t)s0 * d.K, w.eidx, sizeof(int) * n * d.K, hipMemcpyDeviceToHost, g_stream));
         ZZ_CHECK(hipMemcpyAsync(wt.data() + (size_t)s0 * d.K, w.ewt, sizeof(float) * n * d.K, hipMemcpyDeviceToHost, g_stream));
@@ -678,7 +736,7 @@ extern "C" int zz_moe_forward_begin(int id, const float *in, int S) {
     if (L->n_present != d.E) ZZ_FAIL("forward: %d of %d experts uploaded", L->n_present, d.E);
     if (!ensure_ws(L, S)) return 0;
     ZZ_CHECK(hipMemcpyAsync(L->ws.in, in, sizeof(float) * S * d.D, hipMemcpyHostToDevice, g_stream));
-    if (!run_chunk(L, L->ws.in, L->ws.out, S, g_stream)) return 0;
+    if (!run_chunk(L, L->ws, L->ws.in, L->ws.out, S, g_stream)) return 0;
     L->pending_S = S;
     L->last_S = S;
     return 1;
