@@ -418,7 +418,7 @@ def main():
             f"-> {ev / steps * 1e6:.1f} us/step, nu {nu:.1f}; kernels (us): "
             + ", ".join(f"{k} {v:.1f}" for k, v in kern.items()))
 
-    log("router fallback counters (rms, logit, gemma exact, lfm contested):", zz.stats())
+    log("router counters (rms replays, logit replays, gemma exact replays, exact ties):", zz.stats())
     S = args.tokens
     r = res[S]
     step_s = r["ev"] / r["steps"]

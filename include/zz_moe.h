@@ -157,10 +157,18 @@ int zz_moe_blockdots(int layer, int eid, int tensor, int row0, int nrows,
  * Device pointers, enqueued on `stream` (NULL = the library's stream). */
 int zz_quantize(int fmt, const float *d_w, uint8_t *d_out, int64_t n, void *stream);
 
-/* Counters since gpu_init: [0] rmsnorm serial replays, [1] lfm/maple logit serial
- * replays, [2] gemma tokens that needed the exact router replay, [3] lfm tokens
- * whose selection was within the expf tolerance of a tie (contested). */
+/* Counters since gpu_init: [0] rmsnorm serial replays, [1] lfm/maple/ling logit
+ * serial replays, [2] gemma tokens that needed the exact router replay, [3] tokens
+ * whose selection met an exact tie (equal scores at or above the k-th, or ling
+ * groups tied at the kept/dropped boundary), decided by the lower index as the
+ * reference's strict '>' insertion does (gemma4.c:604-607, lfm25.c:656-660). */
 int zz_moe_stats(unsigned *counters4);
+
+/* Diagnostic: the expf that the sigmoid routers evaluate on the device, which is
+ * glibc's bit for bit (the reference's libm: lfm25.c:654, ling.c:731), on n floats
+ * of device memory d_x -> d_y, enqueued on `stream` (NULL = the library's stream).
+ * For checking the device's bits against the host's expf. */
+int zz_router_expf(const float *d_x, float *d_y, int64_t n, void *stream);
 
 /* Per-kernel timing with HIP events recorded on the stream each kernel is
  * launched on. zz_moe_profile(1) clears and starts recording, (0) stops.

@@ -23,6 +23,13 @@ void orc_set_threads(int n) {
 #endif
 }
 
+/* The host libm's expf on n values: glibc's, the function the reference's sigmoid
+ * routers call (lfm25.c:654, ling.c:731), for checking the device's expf. */
+void orc_expf(const float *x, float *y, long long n) {
+    #pragma omp parallel for schedule(static)
+    for (long long i = 0; i < n; i++) y[i] = expf(x[i]);
+}
+
 /* ------------------------------------------------------------------ A1 ----
  * IEEE binary16 <-> binary32, round half to even, subnormals kept.
  * Follows q40.h:46-80, including its NaN encoding (quiet, payload dropped).

@@ -172,6 +172,9 @@ int orc_flash_head(const uint8_t *table, int V, int D, const float *fnorm, float
 /* threads used by the parallel loops (OpenMP); 0 = runtime default */
 void orc_set_threads(int n);
 
+/* the host libm's expf (glibc) on n values */
+void orc_expf(const float *x, float *y, long long n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -444,12 +444,6 @@ def test_declines_until_all_experts_resident(dev, layer_cache):
         m.close()
 
 
-def test_router_fallback_counters(dev):
-    s = zz.stats()
-    say("fallback counters (rms, logit, gemma exact, lfm contested):", s)
-    assert s[3] == 0
-
-
 @pytest.mark.parametrize("fmt", [Z.FMT_Q40, Z.FMT_Q80])
 def test_device_quantiser_bit_exact(dev, fmt):
     """zz_quantize equals q40_quant_row / q80_quant_row (through the oracle, pinned to

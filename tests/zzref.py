@@ -86,6 +86,7 @@ def oracle():
                                     f32p, i32p, f32p, i32p, i32p, C.POINTER(OrcDump)]
         L.orc_route.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), f32p, i32p, f32p, f32p]
         L.orc_set_threads.argtypes = [C.c_int]
+        L.orc_expf.argtypes = [f32p, f32p, C.c_longlong]
         L.orc_blockdots.argtypes = [C.c_int, u8p, i8p, C.c_int, i32p]
         L.orc_matmul_f32.argtypes = [C.c_int, f32p, u8p, f32p, C.c_int, C.c_int, C.c_int]
         L.orc_dispatch.argtypes = [i32p, f32p, C.c_int, C.c_int, i32p, C.c_int, i32p, i32p,

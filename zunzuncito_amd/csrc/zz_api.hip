@@ -179,7 +179,6 @@ struct Workspace {
     double *cen = nullptr, *bnd = nullptr;
     int *eidx = nullptr;
     float *ewt = nullptr, *topv = nullptr;
-    int *contested = nullptr;
     int *ptok = nullptr, *pslot = nullptr, *ppos = nullptr;
     float *pwt = nullptr;
     int *uniq = nullptr, *uoff = nullptr, *ucnt = nullptr, *meta = nullptr;
@@ -398,7 +397,6 @@ static size_t ws_layout(const zz_moe_desc &d, int S, bool host_io, char *base, W
     v.xt = (float *)take(4 * (size_t)S);
     v.cen = (double *)take(8 * S * (size_t)d.E); v.bnd = (double *)take(8 * S * (size_t)d.E);
     v.eidx = (int *)take(4 * P); v.ewt = (float *)take(4 * P); v.topv = (float *)take(4 * P);
-    v.contested = (int *)take(4 * (size_t)S);
     v.ptok = (int *)take(4 * P); v.pslot = (int *)take(4 * P); v.ppos = (int *)take(4 * P); v.pwt = (float *)take(4 * P);
     v.uniq = (int *)take(4 * (size_t)d.E); v.uoff = (int *)take(4 * (size_t)d.E); v.ucnt = (int *)take(4 * (size_t)d.E);
     v.meta = (int *)take(64); v.items = (ZzItem *)take(sizeof(ZzItem) * nitems);
@@ -531,7 +529,7 @@ static ChunkArgs chunk_args(Layer *L, Workspace &w, const float *d_in, int S) {
     ta.n_group = d.n_group; ta.topk_group = d.topk_group;
     ta.routed_scaling = d.routed_scaling; ta.cen = w.cen; ta.bnd = w.bnd; ta.router = L->router;
     ta.xn = w.xn; ta.bias = d.use_bias ? L->bias : nullptr; ta.pes = L->pes; ta.eidx = w.eidx;
-    ta.ewt = w.ewt; ta.topv = w.topv; ta.contested = w.contested; ta.diag = g_diag;
+    ta.ewt = w.ewt; ta.topv = w.topv; ta.diag = g_diag;
 
     // decode-sized batches take the GEMV path; larger ones the matrix cores, on
     // work items of up to ZZ_MMA_TOKENS tokens of one expert
@@ -841,6 +839,12 @@ extern "C" int zz_quantize(int fmt, const float *d_w, uint8_t *d_out, int64_t n,
     if (fmt != ZZ_FMT_Q40 && fmt != ZZ_FMT_Q80) ZZ_FAIL("zz_quantize: fmt %d declined", fmt);
     if (!zz_launch_quantize(fmt, d_w, d_out, n / ZZ_BLK, stream ? (hipStream_t)stream : g_stream))
         ZZ_FAIL("zz_quantize: launch failed");
+    return 1;
+}
+
+extern "C" int zz_router_expf(const float *d_x, float *d_y, int64_t n, void *stream) {
+    if (!g_ready || !d_x || !d_y || n <= 0) ZZ_FAIL("zz_router_expf: bad arguments");
+    if (!zz_launch_expf(d_x, d_y, n, stream ? (hipStream_t)stream : g_stream)) ZZ_FAIL("zz_router_expf: launch failed");
     return 1;
 }
 

@@ -40,7 +40,6 @@ struct ZzTopkArgs {
     int *eidx;                  // [S, K]
     float *ewt;                 // [S, K]
     float *topv;                // [S, K] selected scores (debug), or null
-    int *contested;             // [S] lfm near-tie flags, or null
     unsigned *diag;
 };
 
@@ -198,6 +197,7 @@ struct ZzRepackArgs {
 int zz_launch_prep(const ZzPrepArgs &a, int S, hipStream_t st);
 int zz_launch_logits(const ZzLogitArgs &a, int S, hipStream_t st);
 int zz_launch_topk(const ZzTopkArgs &a, int S, hipStream_t st);
+int zz_launch_expf(const float *x, float *y, int64_t n, hipStream_t st);
 int zz_launch_dispatch(const ZzDispatchArgs &a, hipStream_t st);
 int zz_launch_dec_logits(const ZzDecRouteArgs &a, hipStream_t st);
 int zz_launch_dec_up(const ZzDecUpArgs &a, int S, hipStream_t st);

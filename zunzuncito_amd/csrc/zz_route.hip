@@ -533,3 +533,15 @@ int zz_launch_dispatch(const ZzDispatchArgs &a, hipStream_t st) {
     hipLaunchKernelGGL(zz_dispatch_kernel, dim3(1), dim3(DP_T), lds, st, a);
     return hipGetLastError() == hipSuccess;
 }
+
+// the routers' expf on n values (a diagnostic: the device's bits against the host's)
+__global__ void __launch_bounds__(256) zz_expf_kernel(const float *x, float *y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        y[i] = zz_expf(x[i]);
+}
+
+int zz_launch_expf(const float *x, float *y, int64_t n, hipStream_t st) {
+    const int64_t want = (n + 255) / 256;
+    hipLaunchKernelGGL(zz_expf_kernel, dim3((unsigned)(want < 8192 ? want : 8192)), dim3(256), 0, st, x, y, n);
+    return hipGetLastError() == hipSuccess;
+}

@@ -12,13 +12,16 @@
 //   3. candidates are the experts with hi >= lk -- a superset of the top k;
 //   4. a candidate whose interval meets another candidate's is contested; gemma
 //      replays contested logits with the reference's serial fp32 chain
-//      (gemma4.c:600-601), lfm flags the token (expf, lfm25.c:648);
+//      (gemma4.c:600-601). lfm/maple/ling scores are exact points: their logits
+//      are exact floats and the sigmoid uses glibc's expf bit for bit (zz_expf.h);
 //   5. candidates are ranked by centre (disjoint intervals order as their
-//      values do; replayed ones are exact), and the gate weights are formed.
+//      values do; replayed ones are exact; equal values go to the lower expert,
+//      counted in diag[3]), and the gate weights are formed.
 // A register-only fast path settles the common case first: K rounds of a wave
 // maximum give the K largest keys, which are the answer, in order, when no other
 // expert's interval reaches the K-th lower bound and the K intervals are disjoint.
 #pragma once
+#include "zz_expf.h"
 #include "zz_route_dev.h"
 
 struct ZzTopkWaveHdr {
@@ -71,12 +74,11 @@ __device__ __forceinline__ unsigned long long zz_lane_lt_mask() {
     return l ? (~0ull >> (64 - l)) : 0ull;
 }
 
-// lfm sigmoid score of a logit: 1/(1+expf(-v)) with the exponential evaluated in
-// double and rounded once; glibc's expf is within 1 ulp of that
+// sigmoid score of an exact float logit, as lfm25.c:654 / ling.c:731 form it:
+// 1.0f / (1.0f + expf(-v)), bit for bit
 __device__ __forceinline__ float zz_sigmoid_score(double logit) {
     const float v = (float)logit;
-    const float ex = (float)exp(-(double)v);
-    return 1.0f / (1.0f + ex);
+    return 1.0f / (1.0f + zz_expf(-v));
 }
 
 // The reference's gemma logit of expert e for router input xn: in-order fp32 sum
@@ -94,8 +96,8 @@ __device__ float zz_gemma_chain(const float *w, const float *xn, int D, const fl
     return v;
 }
 
-// write: store the routing outputs (eidx, ewt, topv, contested, counters); the
-// result is in the header's idx / wt either way
+// write: store the routing outputs (eidx, ewt, topv, counters); the result is in
+// the header's idx / wt either way
 template <int EPL>
 __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) {
     ZzTopkWaveHdr &h = *(ZzTopkWaveHdr *)lds;
@@ -119,17 +121,15 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
     }
     double lo[EPL], hi[EPL];
     unsigned long long key[EPL];
-    int width = sig;
+    int width = 0;
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
         const int e = l + 64 * j;
         if (sig) {
-            // sel = s + bias within 2 ulp(s) + ulp(sel) of the reference's
+            // the reference's selection score s + bias, exactly (lfm25.c:654-655)
             const float sg = zz_sigmoid_score(cv[j]);
             const float sel = a.bias ? sg + bi[j] : sg;
-            const double sl = 2.0 * (double)ulp_of(sg) + (double)ulp_of(sel);
-            lo[j] = (double)sel - sl;
-            hi[j] = (double)sel + sl;
+            lo[j] = hi[j] = (double)sel;
         } else {
             lo[j] = cv[j] - bv[j];
             hi[j] = cv[j] + bv[j];
@@ -143,61 +143,42 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
         if (e >= E) lo[j] = hi[j] = -INFINITY;
     }
     width = __ballot(width) != 0ull;
-    int contested = 0;                                   // lfm: a selection within expf's tolerance
+    int ties = 0;                                        // an exact tie decided by index
 
-    // Grouped router (ling.c:734-760): each group's top-2 sum as an interval (the two
-    // largest lo's, the two largest hi's, widened by the reference's float add), the
-    // best topk_group groups by that sum (ties to the lower group), then the experts of
-    // the other groups leave the running. A group set the intervals cannot fix is
-    // taken by centres and the token flagged, as lfm's near-ties are.
+    // Grouped router (ling.c:734-760), on the exact selection scores: each group's
+    // score is the float sum of its two best, the best topk_group groups are kept by
+    // the reference's strict-'>' insertion (score desc, group asc; a score of -inf
+    // or NaN is never kept), and the experts of the other groups leave the running.
     if (a.gating == ZZ_GATE_GROUPED) {
         const int NG = a.n_group, TG = a.topk_group, EG = E / NG;
 #pragma unroll
         for (int j = 0; j < EPL; j++) {
             const int e = l + 64 * j;
-            if (e < E) {
-                clo[e] = lo[j];
-                chi[e] = hi[j];
-            }
+            if (e < E) clo[e] = lo[j];
         }
         zz_wave_sync_lds();
-        double glo = -INFINITY, ghi = -INFINITY;
+        float gs = -INFINITY;
         if (l < NG) {
-            double a1 = -INFINITY, a2 = -INFINITY, b1 = -INFINITY, b2 = -INFINITY;
+            float a1 = -INFINITY, a2 = -INFINITY;
             for (int i = 0; i < EG; i++) {
-                const double x = clo[l * EG + i], y = chi[l * EG + i];
+                const float x = (float)clo[l * EG + i];
                 if (x > a1) { a2 = a1; a1 = x; } else if (x > a2) a2 = x;
-                if (y > b1) { b2 = b1; b1 = y; } else if (y > b2) b2 = y;
             }
-            glo = EG > 1 ? a1 + a2 : a1;
-            ghi = EG > 1 ? b1 + b2 : b1;
-            if (EG > 1) {                                // fl(a + b): half an ulp each way
-                const double u = (double)ulp_of((float)fmax(fabs(glo), fabs(ghi)));
-                if (u == u) {                            // not for infinite sums
-                    glo -= u;
-                    ghi += u;
-                }
-            }
+            gs = EG > 1 ? a1 + a2 : a1;
         }
-        // the TG-th largest lower bound (value desc, group asc)
+        const bool valid = l < NG && gs > -INFINITY;
         int rk = 0;
         for (int q = 0; q < NG; q++) {
-            const double gq = zz_readlane_f64(glo, q);
-            rk += (gq > glo) | ((gq == glo) & (q < l));
+            const float gq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gs), q));
+            rk += (gq > gs) | ((gq == gs) & (q < l));
         }
-        const unsigned long long at = __ballot(l < NG && rk == TG - 1);
-        const double lg = zz_readlane_f64(glo, (int)__ffsll((long long)at) - 1);
-        const unsigned long long cand = __ballot(l < NG && ghi >= lg);
-        unsigned long long live = cand;
-        if (__popcll(cand) != TG) {                      // not fixed: centres, flagged
-            const double gc = 0.5 * (glo + ghi);
-            int rc = 0;
-            for (int q = 0; q < NG; q++) {
-                const double cq = zz_readlane_f64(gc, q);
-                rc += (cq > gc) | ((cq == gc) & (q < l));
-            }
-            live = __ballot(l < NG && rc < TG);
-            contested = 1;
+        const unsigned long long live = __ballot(valid && rk < TG);
+        // a tie across the boundary: the last kept group's score equals the first dropped one's
+        const unsigned long long at = __ballot(valid && rk == TG - 1), nx = __ballot(valid && rk == TG);
+        if (at && nx) {
+            const float g0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gs), (int)__ffsll((long long)at) - 1));
+            const float g1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gs), (int)__ffsll((long long)nx) - 1));
+            ties |= g0 == g1;
         }
 #pragma unroll
         for (int j = 0; j < EPL; j++) {
@@ -322,10 +303,10 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
     }
     zz_wave_sync_lds();
 
-    // 4. contested candidates (exact logits can only tie, which the index order
-    // below resolves as the reference does)
+    // 4. contested candidates. Only gemma's bounded logits have width: exact values
+    // can only tie, which the index order below resolves as the reference does
     int any = 0;
-    if (width) {
+    if (width && a.gating == ZZ_GATE_SOFTMAX_PES) {
         for (int i = l; i < nc; i += 64) {
             const double li = clo[i], hi_ = chi[i];
             int cf = 0;
@@ -337,44 +318,42 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
         zz_wave_sync_lds();
     }
     if (any) {
-        if (a.gating == ZZ_GATE_SOFTMAX_PES) {
-            const float *xn = a.xn + (size_t)s * a.D;
-            for (int i = 0; i < nc; i++) {                     // wave-uniform
-                const int ce = ci[i];
-                if (ce >= 0) continue;
-                const int e = -1 - ce;
-                const float v = zz_gemma_chain(a.router + (size_t)e * a.D, xn, a.D, a.bias, e);
-                zz_wave_sync_lds();
-                if (l == 0) {
-                    clo[i] = chi[i] = (double)v;
-                    ci[i] = e;
-                }
-                zz_wave_sync_lds();
+        const float *xn = a.xn + (size_t)s * a.D;
+        for (int i = 0; i < nc; i++) {                         // wave-uniform
+            const int ce = ci[i];
+            if (ce >= 0) continue;
+            const int e = -1 - ce;
+            const float v = zz_gemma_chain(a.router + (size_t)e * a.D, xn, a.D, a.bias, e);
+            zz_wave_sync_lds();
+            if (l == 0) {
+                clo[i] = chi[i] = (double)v;
+                ci[i] = e;
             }
-            if (l == 0 && write) atomicAdd(a.diag + 2, 1u);
-        } else {
-            for (int i = l; i < nc; i += 64)
-                if (ci[i] < 0) ci[i] = -1 - ci[i];
-            contested = sig;
             zz_wave_sync_lds();
         }
+        if (l == 0 && write) atomicAdd(a.diag + 2, 1u);
     }
 
-    // 5. rank candidates by (centre desc, index asc)
+    // 5. rank candidates by (centre desc, index asc); after step 4 two equal centres
+    // are two equal exact values, whose order the lower index decides
+    int tie = 0;
     for (int i = l; i < nc; i += 64) {
         const int e = ci[i];
         const double me = 0.5 * (clo[i] + chi[i]);
-        int rk = 0;
+        int rk = 0, eq = 0;
         for (int q = 0; q < nc; q++) {
             const int f = ci[q];
             const double mf = 0.5 * (clo[q] + chi[q]);
             rk += (f != e) & ((mf > me) | ((mf == me) & (f < e)));
+            eq |= (f != e) & (mf == me);
         }
         if (rk < K) {
             h.idx[rk] = e;
             h.topv[rk] = (float)me;
+            tie |= eq;
         }
     }
+    ties |= __ballot(tie) != 0ull;
     }                                                    // general passes
     zz_wave_sync_lds();
 
@@ -384,7 +363,7 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
     int ej = 0;
     if (l < K) {
         ej = h.idx[l];
-        wj = sig ? zz_sigmoid_score(cen[ej]) : expf(h.topv[l] - h.topv[0]);
+        wj = sig ? zz_sigmoid_score(cen[ej]) : zz_expf(h.topv[l] - h.topv[0]);
         if (a.gating == ZZ_GATE_SOFTMAX_PES) pj = a.pes[ej];
     }
     float sum = 0.0f;
@@ -414,10 +393,7 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
         }
     }
     zz_wave_sync_lds();
-    if (l == 0 && sig && write) {
-        if (a.contested) a.contested[s] = contested;
-        if (contested) atomicAdd(a.diag + 3, 1u);
-    }
+    if (l == 0 && ties && write) atomicAdd(a.diag + 3, 1u);
 }
 
 // experts per lane of zz_topk_wave for E experts
