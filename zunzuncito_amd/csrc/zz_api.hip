@@ -376,12 +376,32 @@ static int chunk_tokens(const zz_moe_desc &d) {
     return by_pairs < by_masks ? by_pairs : by_masks;
 }
 
+// Rows of the FFN work-item grid (slots per XCD): enough for the items of S tokens
+// in chunks of <= tch (one expert's items may all sit on one XCD), so that the XCD
+// placement of the dispatch kernel always fits.
+static int zz_item_slots(int E, int P, int S, int tch) {
+    const int items = (P < E ? P : E) + (P + tch - 1) / tch;
+    return (items + 7) / 8 + (S + tch - 1) / tch;
+}
+
+// An expert's gate + up weight stream expressed in token columns of the FFN's
+// epilogue work (the dispatch kernel's XCD balance): ~29 for q4_0, where 2.2 MB of
+// weights take as long at HBM speed as 29 columns of 3 VALU operations per weight
+// row and 32-weight block take on the XCD's SIMDs.
+static int zz_weight_cost(const ZzLayout &lay, const zz_moe_desc &d) {
+    const double bytes = (double)(lay.gate.fmt == ZZ_FMT_Q80 ? 34 : lay.gate.fmt == ZZ_FMT_TQ2 ? 8.125 : 18) / 32.0 +
+                         (double)(lay.up.fmt == ZZ_FMT_Q80 ? 34 : lay.up.fmt == ZZ_FMT_TQ2 ? 8.125 : 18) / 32.0;
+    const int c = (int)(29.0 * bytes / 1.125 + 0.5);
+    return c < 1 ? 1 : c;
+}
+
 // Lays the workspace of S tokens of layer d out from `base` (nullptr: only
 // measures). host_io adds the in/out staging rows that only the host-pointer
 // forms use. Returns the bytes the layout spans.
 static size_t ws_layout(const zz_moe_desc &d, int S, bool host_io, char *base, Workspace *w) {
     const size_t P = (size_t)S * d.K, nbD = d.D / ZZ_BLK, nbM = d.MI / ZZ_BLK;
-    const size_t nitems = (size_t)d.E + P / 8 + 8;
+    // FFN work-item slots: 8 per row of the XCD-placed item grid (zz_item_slots)
+    const size_t nitems = 8 * (size_t)zz_item_slots(d.E, (int)P, S, 4) + 8;
     size_t off = 0;
     auto take = [&](size_t bytes) {
         size_t o = off;
@@ -537,6 +557,8 @@ static ChunkArgs chunk_args(Layer *L, Workspace &w, const float *d_in, int S) {
     const int tch = c.dec ? ZZ_DEC_MAXS : ZZ_MMA_TOKENS;
     ZzDispatchArgs &da = c.da;
     da.P = c.P; da.E = d.E; da.K = d.K; da.tch = tch; da.eidx = w.eidx; da.ewt = w.ewt;
+    da.xslots = zz_item_slots(d.E, c.P, S, tch);
+    da.wcost = zz_weight_cost(L->lay, d);
     da.ptok = w.ptok; da.pslot = w.pslot; da.pwt = w.pwt; da.ppos = w.ppos; da.uniq = w.uniq;
     da.uoff = w.uoff; da.ucnt = w.ucnt; da.items = w.items; da.meta = w.meta;
 
@@ -545,7 +567,7 @@ static ChunkArgs chunk_args(Layer *L, Workspace &w, const float *d_in, int S) {
     fa.experts = L->slots; fa.estride = L->lay.bytes; fa.lay = L->lay; fa.items = w.items;
     fa.meta = w.meta; fa.ptok = w.ptok; fa.xq = w.xq; fa.xs = w.xs; fa.xsum = w.xsum; fa.xt = w.xt;
     fa.hq = w.hq; fa.hs = w.hs; fa.hsum = w.hsum; fa.y = w.y;
-    c.max_items = (c.P < d.E ? c.P : d.E) + (c.P + tch - 1) / tch;
+    c.max_items = 8 * da.xslots;
     return c;
 }
 
@@ -766,6 +788,7 @@ extern "C" int zz_moe_debug(int id, zz_moe_dump *dp) {
         // flat pair: the dispatch lists are built here, from its routing outputs
         ZzDispatchArgs da;
         da.P = P; da.E = d.E; da.K = d.K; da.tch = ZZ_DEC_MAXS; da.eidx = w.eidx; da.ewt = w.ewt;
+        da.xslots = zz_item_slots(d.E, P, S, ZZ_DEC_MAXS); da.wcost = zz_weight_cost(L->lay, d);
         da.ptok = w.ptok; da.pslot = w.pslot; da.pwt = w.pwt; da.ppos = w.ppos; da.uniq = w.uniq;
         da.uoff = w.uoff; da.ucnt = w.ucnt; da.items = w.items; da.meta = w.meta;
         if (!zz_launch_dispatch(da, g_stream)) ZZ_FAIL("zz_moe_debug: dispatch launch failed");

@@ -49,14 +49,16 @@ struct ZzItem {                 // one FFN work unit: <= tch pairs of one expert
 
 struct ZzDispatchArgs {
     int P, E, K, tch;
+    int xslots;                 // work-item slots per XCD the FFN grids hold
+    int wcost;                  // an expert's weight stream, in token columns of FFN work
     const int *eidx;            // [P]
     const float *ewt;           // [P]
     int *ptok, *pslot;          // [P] sorted pair -> token, slot
     float *pwt;                 // [P] sorted pair -> weight
     int *ppos;                  // [P] flat (token*K + slot) -> sorted position
     int *uniq, *uoff, *ucnt;    // [E] union order
-    ZzItem *items;              // [<= E + P/tch]
-    int *meta;                  // [0] = nu, [1] = n_items
+    ZzItem *items;              // [8 * xslots]: XCD x's j-th item at j*8 + x; n = 0: none
+    int *meta;                  // [0] = nu, [1] = item slots used (a multiple of 8)
 };
 
 struct ZzFfnArgs {

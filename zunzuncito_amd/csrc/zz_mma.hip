@@ -600,9 +600,11 @@ __device__ __forceinline__ void mm4_down_body(const ZzFfnArgs &a, const ZzItem &
 
 // XCD-aware work order. Workgroup g of a launch runs on XCD g % 8 (round-robin
 // dispatch), and each XCD has its own L2. All tiles of one item read the same
-// activations, so they get workgroup ids of one residue mod 8: item i runs on XCD
-// i % 8 as that XCD's (i / 8)-th item, its tiles back to back. Ids past the last
-// item exit.
+// activations, so they get workgroup ids of one residue mod 8: item slot i runs on
+// XCD i % 8 as that XCD's (i / 8)-th item, its tiles back to back. The dispatch
+// kernel fills the slots so that all items of one expert share an XCD (its weights
+// then come from HBM once) with the XCDs' loads balanced; empty slots (n = 0) and
+// ids past the last slot exit.
 #define ZZ_XCDS 8
 __device__ __forceinline__ void zz_xcd_tile(int ntiles, int *item, int *tile) {
     const int g = blockIdx.x, x = g % ZZ_XCDS, k = g / ZZ_XCDS;
@@ -619,6 +621,7 @@ __global__ __launch_bounds__(256) void zz_up_mma_kernel(ZzFfnArgs a) {
     zz_xcd_tile(a.MI / 32, &it, &rb);
     if (it >= a.meta[1]) return;
     const ZzItem item = a.items[it];
+    if (item.n <= 0) return;
     __shared__ MmUpShared sm;
     __shared__ int tok[MM_TN];
     const int nt = (item.n + 15) / 16;
@@ -635,6 +638,7 @@ __global__ __launch_bounds__(256) void zz_down_mma_kernel(ZzFfnArgs a) {
     zz_xcd_tile(a.D / 64, &it, &rt);
     if (it >= a.meta[1]) return;
     const ZzItem item = a.items[it];
+    if (item.n <= 0) return;
     __shared__ MmDownShared sm;
     const int nt = (item.n + 15) / 16;
     if (FMT != ZZ_FMT_TQ2 && item.n <= 4 && a.MI <= MM4_K) mm4_down_body<FMT>(a, item, rt, sm.t4);

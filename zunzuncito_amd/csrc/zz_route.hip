@@ -387,6 +387,25 @@ __device__ __forceinline__ int zz_block_excl_scan(int v, int *tmp) {
     return base + x - v;
 }
 
+__device__ __forceinline__ unsigned zz_uni(unsigned v) { return (unsigned)__builtin_amdgcn_readfirstlane((int)v); }
+
+// exclusive prefix sum of a 64-bit value over the workgroup (tmp: 16 entries of LDS)
+__device__ __forceinline__ unsigned long long zz_block_excl_scan64(unsigned long long v, unsigned long long *tmp) {
+    const int t = threadIdx.x, l = t & 63, w = t >> 6;
+    unsigned long long x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const unsigned long long n = __shfl_up(x, off, 64);
+        if (l >= off) x += n;
+    }
+    if (l == 63) tmp[w] = x;
+    __syncthreads();
+    unsigned long long base = 0;
+    for (int q = 0; q < w; q++) base += tmp[q];
+    __syncthreads();
+    return base + x - v;
+}
+
 #define DP_T 1024                     // threads
 #define DP_PT 8                       // pairs per thread: S*K <= 8192 = DP_T * DP_PT
 // One workgroup: the per-expert token bitmasks give each expert's count, its pairs'
@@ -394,15 +413,17 @@ __device__ __forceinline__ int zz_block_excl_scan(int v, int *tmp) {
 // the union order is the order of first pairs (gemma4.c:756-761), read off a bitmap
 // over the pairs by prefix popcounts.
 // LDS: mask and word prefixes [E][W] (W = S/32 words), first-pair bitmap [P/32],
-// pair experts [P] (then the inverse permutation) and weights by position [P].
+// pair experts [P].
 __global__ __launch_bounds__(DP_T) void zz_dispatch_kernel(ZzDispatchArgs a) {
     extern __shared__ unsigned dsm[];
     __shared__ int cnt[ZZ_MAXE], start[ZZ_MAXE], first[ZZ_MAXE], order[ZZ_MAXE], tmp[16];
+    __shared__ int xcost[ZZ_MAXE], xof[ZZ_MAXE], xjb[ZZ_MAXE], xslot[9];
+    __shared__ unsigned long long tmp64[16];
+    __shared__ int xtotal;
     __shared__ int fbase[DP_PT * DP_T / 32];      // first pairs before each bitmap word
     const int P = a.P, E = a.E, K = a.K, S = P / K, W = (S + 31) / 32, PW = (P + 31) / 32, t = threadIdx.x;
     unsigned *mask = dsm, *wpre = dsm + E * W, *fb = wpre + E * W;
-    int *pe = (int *)(fb + PW);                  // pair -> expert, later position -> pair
-    float *pwl = (float *)(pe + P);              // position -> weight
+    int *pe = (int *)(fb + PW);                  // pair -> expert
     for (int i = t; i < E * W; i += DP_T) mask[i] = 0u;
     for (int i = t; i < PW; i += DP_T) fb[i] = 0u;
     // every pair's expert and weight in registers first: one round of loads
@@ -451,30 +472,6 @@ __global__ __launch_bounds__(DP_T) void zz_dispatch_kernel(ZzDispatchArgs a) {
     const int fpre = zz_block_excl_scan(fw, tmp);
     if (t < PW) fbase[t] = fpre;
     __syncthreads();
-    // positions; the sorted lists are then written in position order (coalesced)
-    // through the inverse permutation, which reuses the pair-expert array
-#pragma unroll
-    for (int k = 0; k < DP_PT; k++) {
-        const int p = t + DP_T * k;
-        if (p < P) {
-            const int e = ev[k], s = p / K, w = s >> 5, bit = s & 31;
-            const int pos = start[e] + wpre[e * W + w] + __popc(mask[e * W + w] & ((1u << bit) - 1u));
-            a.ppos[p] = pos;
-            pe[pos] = p;
-            pwl[pos] = wv[k];
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < DP_PT; k++) {
-        const int i = t + DP_T * k;
-        if (i < P) {
-            const int p = pe[i], s = p / K;
-            a.ptok[i] = s;
-            a.pslot[i] = p - s * K;
-            a.pwt[i] = pwl[i];
-        }
-    }
     const bool present = t < E && cnt[t] != 0;
     if (present) {
         const int f = first[t];
@@ -484,6 +481,93 @@ __global__ __launch_bounds__(DP_T) void zz_dispatch_kernel(ZzDispatchArgs a) {
     const int ce = t < nu ? cnt[order[t]] : 0;
     const int nit = (ce + a.tch - 1) / a.tch;
     const int i0 = zz_block_excl_scan(nit, tmp);
+    // XCD placement of the work items. Workgroup g of an FFN launch runs on XCD g % 8
+    // and each XCD has its own L2, so all items of one expert go to one XCD, where
+    // they run back to back and read the expert's weights from HBM once. In union
+    // order (first seen, which puts the popular experts first), each expert goes to
+    // the least loaded XCD, lowest on ties, its load the weight stream (wcost) plus
+    // the token columns of its items (16 per started tile of 16, 4 for an item of <= 4
+    // tokens). Consecutive experts thus land on different XCDs and each XCD runs its
+    // items in union order, which keeps heavy and light experts interleaved in time
+    // (a balanced placement that runs each XCD's heavy experts first, or one that
+    // deals experts in a fixed order, measured slower). Item slot j*8 + x is XCD x's
+    // j-th item. Without an expert of several items the items keep union order, item
+    // i on XCD i % 8.
+    int cost = 0;
+    if (t < nu) {
+        cost = a.wcost;
+        for (int c = 0; c < nit; c++) {
+            const int n = min(a.tch, ce - c * a.tch);
+            cost += n <= 4 ? 4 : 16 * ((n + 15) >> 4);
+        }
+        xcost[t] = cost;
+    }
+    const int nm = __syncthreads_count(t < nu && nit > 1);
+    if (t < 64 && nm > 0) {
+        // One wave, while the others write the sorted lists below. XCD x's key
+        // (load << 3) | x is a uniform value held in a scalar register (readfirstlane
+        // keeps it there); the keys are distinct, so the least one names the XCD.
+        // Lane i holds the batch's i-th entry.
+        unsigned k0 = 0, k1 = 1, k2 = 2, k3 = 3, k4 = 4, k5 = 5, k6 = 6, k7 = 7;
+        for (int r0 = 0; r0 < nu; r0 += 64) {
+            const int ec = r0 + t < nu ? xcost[r0 + t] : 0;
+            const int rn = min(64, nu - r0);
+            int xo = 0;
+            for (int i = 0; i < rn; i++) {
+                const unsigned c = (unsigned)__builtin_amdgcn_readlane(ec, i) << 3;
+                const unsigned m = zz_uni(min(min(min(k0, k1), min(k2, k3)), min(min(k4, k5), min(k6, k7))));
+                k0 = zz_uni(k0 + (m == k0 ? c : 0u));
+                k1 = zz_uni(k1 + (m == k1 ? c : 0u));
+                k2 = zz_uni(k2 + (m == k2 ? c : 0u));
+                k3 = zz_uni(k3 + (m == k3 ? c : 0u));
+                k4 = zz_uni(k4 + (m == k4 ? c : 0u));
+                k5 = zz_uni(k5 + (m == k5 ? c : 0u));
+                k6 = zz_uni(k6 + (m == k6 ? c : 0u));
+                k7 = zz_uni(k7 + (m == k7 ? c : 0u));
+                if (t == i) xo = (int)(m & 7u);
+            }
+            if (t < rn) xof[r0 + t] = xo;
+        }
+    }
+    // positions of the pairs (a stable counting sort), each thread its own pairs,
+    // with the sorted lists written straight to their positions
+#pragma unroll
+    for (int k = 0; k < DP_PT; k++) {
+        const int p = t + DP_T * k;
+        if (p < P) {
+            const int e = ev[k], s = p / K, w = s >> 5, bit = s & 31;
+            const int pos = start[e] + wpre[e * W + w] + __popc(mask[e * W + w] & ((1u << bit) - 1u));
+            a.ppos[p] = pos;
+            a.ptok[pos] = s;
+            a.pslot[pos] = p - s * K;
+            a.pwt[pos] = wv[k];
+        }
+    }
+    __syncthreads();                             // wave 0's placement is done
+    // slot of each expert's first item: the items of earlier experts on its XCD, from
+    // one exclusive scan of per-XCD item counts packed a byte per XCD
+    if (t == nu - 1) xtotal = i0 + nit;                 // all items
+    const int xe = t < nu ? xof[t] : 0;
+    const unsigned long long cnt8 = t < nu ? (unsigned long long)min(nit, 255) << (8 * xe) : 0ull;
+    const unsigned long long pre8 = zz_block_excl_scan64(cnt8, tmp64);
+    if (t < nu) xjb[t] = (int)((pre8 >> (8 * xe)) & 255u);
+    if (t == DP_T - 1) {
+        const unsigned long long tot8 = pre8 + cnt8;
+        int mx = 0, sum = 0;
+        for (int x = 0; x < 8; x++) {
+            const int c = (int)((tot8 >> (8 * x)) & 255u);
+            mx = max(mx, c);
+            sum += c;
+            xslot[x] = c;
+        }
+        // a count above 255 carries into the next byte (or out) and breaks the sum
+        xslot[8] = sum == xtotal && nm > 0 ? mx : 1 << 30;
+    }
+    __syncthreads();
+    // a placement past the grid's slots per XCD (never at realistic routings): items
+    // in union order instead, item i on XCD i % 8, which always fits
+    const int ms = xslot[8];
+    const bool placed = ms <= a.xslots;
     if (t < nu) {
         const int e = order[t];
         a.uniq[t] = e;
@@ -495,12 +579,18 @@ __global__ __launch_bounds__(DP_T) void zz_dispatch_kernel(ZzDispatchArgs a) {
             it.u = t;
             it.p0 = start[e] + c * a.tch;
             it.n = min(a.tch, ce - c * a.tch);
-            a.items[i0 + c] = it;
+            a.items[placed ? (xjb[t] + c) * 8 + xof[t] : i0 + c] = it;
         }
+    }
+    const int total = placed ? 8 * ms : (i0 + nit + 7) / 8 * 8;     // (unplaced: read at t = nu - 1)
+    if (placed) {
+        for (int i = t; i < 8 * ms; i += DP_T)
+            if (i / 8 >= xslot[i & 7]) a.items[i].n = 0;
     }
     if (t == nu - 1 || (nu == 0 && t == 0)) {
         a.meta[0] = nu;
-        a.meta[1] = i0 + nit;
+        a.meta[1] = total;
+        for (int i = i0 + nit; !placed && i < total; i++) a.items[i].n = 0;
     }
 }
 
@@ -529,7 +619,7 @@ int zz_launch_topk(const ZzTopkArgs &a, int S, hipStream_t st) {
 
 int zz_launch_dispatch(const ZzDispatchArgs &a, hipStream_t st) {
     const int W = (a.P / a.K + 31) / 32, PW = (a.P + 31) / 32;
-    const size_t lds = sizeof(unsigned) * (2 * (size_t)a.E * W + PW) + 8 * (size_t)a.P;
+    const size_t lds = sizeof(unsigned) * (2 * (size_t)a.E * W + PW) + 4 * (size_t)a.P;
     hipLaunchKernelGGL(zz_dispatch_kernel, dim3(1), dim3(DP_T), lds, st, a);
     return hipGetLastError() == hipSuccess;
 }
