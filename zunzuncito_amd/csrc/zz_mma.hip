@@ -124,13 +124,17 @@ __device__ __forceinline__ void mm_chunk(const MmA &A, int l, float (&acc)[NT][4
             B[t] = X(t, j);
             sx[t] = SX(t, j);
         }
+        // all tiles' products first, into distinct registers, so that each epilogue
+        // finds its matrix-core result ready instead of waiting on it
+        zz_v4i r[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) r[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa, B[t], zero, 0, 0, 0);
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            const zz_v4i r = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa, B[t], zero, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const float s = FMT == ZZ_FMT_TQ2 ? sx[t] : fmaf((float)mm_dwh<FULL>(A.s0, A.s1, j, i), sx[t], 0.0f);
-                acc[t][i] = fmaf(s, (float)r[i], acc[t][i]);
+                acc[t][i] = fmaf(s, (float)r[t][i], acc[t][i]);
             }
         }
         // one block at a time: the next block's LDS reads hoisted over this one
@@ -343,25 +347,55 @@ __device__ __forceinline__ void mm4_chunk(const Mm4A &A, const Mm4Stage &st, int
     }
 }
 
+// This wave's chunks c = w, w+4, ... of the tensor, in a ring of three register sets
+// (two chunks in flight while one is multiplied; q8_0: two sets): the work per chunk
+// is far shorter than a memory latency, so the depth of the ring sets the pace. The caller issues
+// the first two chunks (mm4_first) before it stages the activations, so those loads
+// overlap the staging.
 template <int FMT>
-__device__ __forceinline__ void mm4_kloop(const uint8_t *E, const ZzTensor &T, int g, int l, int w,
-                                          const Mm4Stage &st, float (&acc)[4]) {
-    const int nb = T.I / ZZ_BLK, nch = (nb + 3) / 4;
-    const ZzWalk W = zz_walk(T, g, l & 15, 4 * ((l >> 2) & 3));   // piece 0 of row l%16
+struct Mm4Ring {
+    ZzWalk W;
+    int nch;
+    Mm4A r0, r1, r2;
+};
+
+template <int FMT>
+__device__ __forceinline__ void mm4_first(Mm4Ring<FMT> &R, const uint8_t *E, const ZzTensor &T, int g, int l, int w) {
+    R.nch = (T.I / ZZ_BLK + 3) / 4;
+    R.W = zz_walk(T, g, l & 15, 4 * ((l >> 2) & 3));    // piece 0 of row l%16
+    R.r0 = mm4_load<FMT>(E, R.W, min(w, R.nch - 1));
+    R.r1 = mm4_load<FMT>(E, R.W, min(w + 4, R.nch - 1));
+}
+
+// acc[v]: row 4(l/4)+v of the 64, token l%4, over this wave's chunks. Every load is
+// unconditional (clamped past the end) so the compiler's load counters stay exact.
+template <int FMT>
+__device__ __forceinline__ void mm4_kloop(Mm4Ring<FMT> &R, const uint8_t *E, int l, int w, const Mm4Stage &st,
+                                          float (&acc)[4]) {
+    const int nch = R.nch;
 #pragma unroll
     for (int v = 0; v < 4; v++) acc[v] = 0.0f;
     auto chunk = [&](const Mm4A &A, int c) {
-        if (c < W.nfull) mm4_chunk<FMT, true>(A, st, c, l, acc);
+        if (c < R.W.nfull) mm4_chunk<FMT, true>(A, st, c, l, acc);
         else if (c < nch) mm4_chunk<FMT, false>(A, st, c, l, acc);
     };
-    // this wave's chunks w, w+4, ...: two register sets, each chunk's loads issued
-    // one chunk ahead (unconditional, clamped)
-    Mm4A a0 = mm4_load<FMT>(E, W, min(w, nch - 1)), a1;
-    for (int c = w; c < nch; c += 8) {
-        a1 = mm4_load<FMT>(E, W, min(c + 4, nch - 1));
-        chunk(a0, c);
-        a0 = mm4_load<FMT>(E, W, min(c + 8, nch - 1));
-        chunk(a1, c + 4);
+    if (FMT == ZZ_FMT_Q80) {
+        // q8_0 chunks are twice the registers: two sets, one chunk in flight
+        for (int c = w; c < nch; c += 8) {
+            chunk(R.r0, c);
+            R.r0 = mm4_load<FMT>(E, R.W, min(c + 8, nch - 1));
+            chunk(R.r1, c + 4);
+            R.r1 = mm4_load<FMT>(E, R.W, min(c + 12, nch - 1));
+        }
+    } else {
+        for (int c = w; c < nch; c += 12) {
+            R.r2 = mm4_load<FMT>(E, R.W, min(c + 8, nch - 1));
+            chunk(R.r0, c);
+            R.r0 = mm4_load<FMT>(E, R.W, min(c + 12, nch - 1));
+            chunk(R.r1, c + 4);
+            R.r1 = mm4_load<FMT>(E, R.W, min(c + 16, nch - 1));
+            chunk(R.r2, c + 8);
+        }
     }
     if (FMT == ZZ_FMT_Q40)                       // the 16*(q - 8) weights
 #pragma unroll
@@ -554,11 +588,13 @@ __device__ __forceinline__ void mm4_up_body(const ZzFfnArgs &a, const ZzItem &it
     const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, n = item.n, D = a.D, nb = D / ZZ_BLK;
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
     const int *ptok = a.ptok + item.p0;
+    const ZzTensor &T = l < 32 ? a.lay.gate : a.lay.up;
+    Mm4Ring<FMT> R;
+    mm4_first<FMT>(R, E, T, 2 * rb + ((l >> 4) & 1), l, w);       // weights first
     mm4_stage(sm.st, [&](int t) { return a.xq + (size_t)ptok[min(t, n - 1)] * D; },
               [&](int t) { return a.xs + (size_t)ptok[min(t, n - 1)] * nb; }, D);
-    const ZzTensor &T = l < 32 ? a.lay.gate : a.lay.up;
     float acc[4];
-    mm4_kloop<FMT>(E, T, 2 * rb + ((l >> 4) & 1), l, w, sm.st, acc);
+    mm4_kloop<FMT>(R, E, l, w, sm.st, acc);
     __syncthreads();                             // the stage is done with
     mm4_reduce(sm.rd, acc);
     if (tid < 4 * ZZ_BLK) {                      // token t, hidden row 32rb + r
@@ -588,10 +624,12 @@ template <int FMT>
 __device__ __forceinline__ void mm4_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, Mm4Shared &sm) {
     const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, n = item.n, MI = a.MI, nb = MI / ZZ_BLK;
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
+    Mm4Ring<FMT> R;
+    mm4_first<FMT>(R, E, a.lay.down, 4 * rt + (l >> 4), l, w);     // weights first
     mm4_stage(sm.st, [&](int t) { return a.hq + ((size_t)item.p0 + min(t, n - 1)) * MI; },
               [&](int t) { return a.hs + ((size_t)item.p0 + min(t, n - 1)) * nb; }, MI);
     float acc[4];
-    mm4_kloop<FMT>(E, a.lay.down, 4 * rt + (l >> 4), l, w, sm.st, acc);
+    mm4_kloop<FMT>(R, E, l, w, sm.st, acc);
     __syncthreads();
     mm4_reduce(sm.rd, acc);
     const int t = tid >> 6, r = tid & 63;
@@ -616,7 +654,7 @@ static unsigned zz_xcd_grid(int max_items, int ntiles) {
 }
 
 template <int GF, int UF>
-__global__ __launch_bounds__(256) void zz_up_mma_kernel(ZzFfnArgs a) {
+__global__ __launch_bounds__(256, 4) void zz_up_mma_kernel(ZzFfnArgs a) {
     int it, rb;
     zz_xcd_tile(a.MI / 32, &it, &rb);
     if (it >= a.meta[1]) return;
@@ -633,7 +671,7 @@ __global__ __launch_bounds__(256) void zz_up_mma_kernel(ZzFfnArgs a) {
 }
 
 template <int FMT>
-__global__ __launch_bounds__(256) void zz_down_mma_kernel(ZzFfnArgs a) {
+__global__ __launch_bounds__(256, 4) void zz_down_mma_kernel(ZzFfnArgs a) {
     int it, rt;
     zz_xcd_tile(a.D / 64, &it, &rt);
     if (it >= a.meta[1]) return;
