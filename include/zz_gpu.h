@@ -36,7 +36,7 @@
 #define GPU_FMT_Q40 1
 #define GPU_FMT_Q80 2
 #define GPU_FMT_TQ2 3
-#define GPU_FMT_Q4A 4   /* declined: q4a is Maple's embedding/lm_head format */
+#define GPU_FMT_Q4A 4   /* gpu_matmul only: Maple's lm_head / FlashHead centroid format */
 
 #ifdef __cplusplus
 extern "C" {
@@ -58,8 +58,9 @@ int  gpu_map(const void *p, size_t n);
 /* gpu.h:74. y[S,O] = W[O,I] (q4_0) x[S,I] (f32), I % 32 == 0, W inside a mapping. */
 int  gpu_q40_matmul(float *y, const uint8_t *W, const float *x, int O, int I, int S);
 
-/* gpu.h:83-84. Any GPU_FMT_* except Q4A. For TQ2, W is the whole tensor (alphas then
- * code rows) and I % 64 == 0. */
+/* gpu.h:83-84. Any GPU_FMT_*. For TQ2, W is the whole tensor (alphas then code rows)
+ * and I % 64 == 0; for Q4A (tq2.h:269-292), rows of I/64 groups of 36 bytes and
+ * I % 64 == 0. */
 int  gpu_matmul(int fmt, float *y, const uint8_t *W, const float *x, int O, int I, int S);
 
 #ifdef __cplusplus

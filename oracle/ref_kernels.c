@@ -24,6 +24,7 @@ float ref_tq2_dot(const uint8_t *c, float a, const int8_t *q, const float *s, fl
 float ref_q40_dot_f32(const uint8_t *w, const float *x, int I) { return q40_dot_f32(w, x, I); }
 float ref_q80_dot_f32(const uint8_t *w, const float *x, int I) { return q80_dot_f32(w, x, I); }
 float ref_tq2_dot_f32(const uint8_t *c, float a, const float *x, int I) { return tq2_dot_f32(c, a, x, I); }
+float ref_q4a_dot_f32(const uint8_t *w, const float *x, int I) { return q4a_dot_f32(w, x, I); }
 void ref_tq2_dequant_row(const uint8_t *c, float a, float *w, int I) { tq2_dequant_row(c, a, w, I); }
 int ref_simd_variant(void) {
 #if defined(__AVX2__)

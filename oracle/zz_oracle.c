@@ -345,16 +345,42 @@ float orc_tq2_dot_f32(const uint8_t *codes, float alpha, const float *x, int I) 
     return (float)((double)alpha * acc);
 }
 
+/* tq2.h:405-427: a Q4A group is 64 weights in 36 bytes -- fp16 d, fp16 m, then two
+ * 16-byte halves, byte j of half h holding q[32h + j] (low nibble) and q[32h + j + 16]
+ * (high); w = d q + m. Per half, sum q u and sum u in double, then add d s + m t. */
+float orc_q4a_dot_f32(const uint8_t *w, const float *x, int I) {
+    double acc = 0.0;
+    for (int g = 0; g < I / 64; g++) {
+        const uint8_t *grp = w + (size_t)g * 36;
+        const double d = orc_h2f((uint16_t)(grp[0] | grp[1] << 8));
+        const double m = orc_h2f((uint16_t)(grp[2] | grp[3] << 8));
+        for (int h = 0; h < 2; h++) {
+            const uint8_t *nib = grp + 4 + 16 * h;
+            const float *u = x + (size_t)g * 64 + 32 * h;
+            double s = 0.0, t = 0.0;
+            for (int j = 0; j < 16; j++) {
+                s += (double)(nib[j] & 15) * u[j];
+                s += (double)(nib[j] >> 4) * u[j + 16];
+                t += (double)u[j] + (double)u[j + 16];
+            }
+            acc += d * s + m * t;
+        }
+    }
+    return (float)acc;
+}
+
 int64_t orc_tensor_bytes(int fmt, int O, int I) {
     if (fmt == ORC_FMT_Q40) return (int64_t)O * (I / BLK) * 18;
     if (fmt == ORC_FMT_Q80) return (int64_t)O * (I / BLK) * 34;
     if (fmt == ORC_FMT_TQ2) return (int64_t)O * 4 + (int64_t)O * (I / 4);
+    if (fmt == ORC_FMT_Q4A) return (int64_t)O * (I / 64) * 36;      /* tq2.h:287-292 */
     return -1;
 }
 
 static inline int64_t row_bytes(int fmt, int I) {
     return fmt == ORC_FMT_Q40 ? (int64_t)(I / BLK) * 18
-         : fmt == ORC_FMT_Q80 ? (int64_t)(I / BLK) * 34 : (int64_t)I / 4;
+         : fmt == ORC_FMT_Q80 ? (int64_t)(I / BLK) * 34
+         : fmt == ORC_FMT_Q4A ? (int64_t)(I / 64) * 36 : (int64_t)I / 4;
 }
 
 void orc_matmul_f32(int fmt, float *y, const uint8_t *W, const float *x, int O, int I, int S) {
@@ -369,6 +395,8 @@ void orc_matmul_f32(int fmt, float *y, const uint8_t *W, const float *x, int O, 
                 v = orc_tq2_dot_f32(codes + (size_t)o * (I / 4), alpha[o], xs, I);
             } else if (fmt == ORC_FMT_Q80) {
                 v = orc_q80_dot_f32(W + (size_t)o * row_bytes(fmt, I), xs, I);
+            } else if (fmt == ORC_FMT_Q4A) {
+                v = orc_q4a_dot_f32(W + (size_t)o * row_bytes(fmt, I), xs, I);
             } else {
                 v = orc_q40_dot_f32(W + (size_t)o * row_bytes(fmt, I), xs, I);
             }

@@ -28,6 +28,7 @@ extern "C" {
 #define ORC_FMT_Q40 1
 #define ORC_FMT_Q80 2
 #define ORC_FMT_TQ2 3
+#define ORC_FMT_Q4A 4   /* f32-activation matmul only (tq2.h:269-292) */
 
 /* gating kinds */
 #define ORC_GATE_GEMMA 0    /* gemma4.c:581-613  rmsnorm->scale->f32 logits->topk->softmax(K)*pes */
@@ -103,10 +104,11 @@ float orc_tq2_dot(const uint8_t *codes, float alpha, const int8_t *xq,
 void orc_blockdots(int fmt, const uint8_t *row, const int8_t *xq, int I, int32_t *out);
 
 /* ---- A6/A9: f32-activation dots, double accumulation (q40.h:290-305,
- *      443-455, tq2.h:235-252) -- the gpu.h matmul contract ---- */
+ *      443-455, tq2.h:235-252, 405-427) -- the gpu.h matmul contract ---- */
 float orc_q40_dot_f32(const uint8_t *w, const float *x, int I);
 float orc_q80_dot_f32(const uint8_t *w, const float *x, int I);
 float orc_tq2_dot_f32(const uint8_t *codes, float alpha, const float *x, int I);
+float orc_q4a_dot_f32(const uint8_t *w, const float *x, int I);
 /* y[S,O] = W[O,I] x[S,I] for any format (gpu.h:71-84 semantics) */
 void  orc_matmul_f32(int fmt, float *y, const uint8_t *W, const float *x, int O, int I, int S);
 

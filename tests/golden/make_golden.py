@@ -111,11 +111,30 @@ def kernel_cases():
     dtqf = np.zeros(O, np.float32)
     for o in range(O):
         dtqf[o] = R.ref_tq2_dot_f32(Z.ptr(cb[o * (It // 4):]), C.c_float(alpha[o]), Z.ptr(xt), It)
+    # q4a (tq2.h:269-292, 405-427): nibble bytes from the LCG's mantissas, d and m in
+    # maple.c:1790-1796's ranges, against the same four x rows
+    R.ref_q4a_dot_f32.restype = C.c_float
+    R.ref_f32_to_fp16.restype = C.c_uint16
+    ng = O * (I // 64)
+    q4a = np.zeros((ng, 36), np.uint8)
+    bits = (vals.view(np.uint32)[:ng * 32] >> np.uint32(7)).astype(np.uint8)
+    q4a[:, 4:] = bits.reshape(ng, 32)
+    for g in range(ng):
+        hd = R.ref_f32_to_fp16(C.c_float(0.002 + 0.01 * abs(float(vals[-1 - g]))))
+        hm = R.ref_f32_to_fp16(C.c_float(0.05 * float(vals[-1 - ng - g])))
+        q4a[g, :4] = [hd & 255, hd >> 8, hm & 255, hm >> 8]
+    q4a = q4a.reshape(-1)
+    dq4af = np.zeros((4, O), np.float32)
+    for t in range(4):
+        xt_ = np.ascontiguousarray(x[t])
+        for o in range(O):
+            dq4af[t, o] = R.ref_q4a_dot_f32(Z.ptr(q4a[o * (I // 64) * 36:]), Z.ptr(xt_), I)
     np.savez(os.path.join(HERE, "kernels_lcg12345.npz"), w=w, q40=q40, q80=q80, x=x, xq=xq,
              xs=xs, d40=d40, d80=d80, codes=codes, alpha=alpha, tq=tq, xt=xt, tq_q=tq_q,
-             tq_s=tq_s, tq_tot=np.float32(tot), dtq=dtq, d40f=d40f, d80f=d80f, dtqf=dtqf)
+             tq_s=tq_s, tq_tot=np.float32(tot), dtq=dtq, d40f=d40f, d80f=d80f, dtqf=dtqf,
+             q4a=q4a, dq4af=dq4af)
     print("kernels_lcg12345: q40", q40.nbytes, "B, dots", d40.size + d80.size + dtq.size,
-          "f32 dots", d40f.size + d80f.size + dtqf.size)
+          "f32 dots", d40f.size + d80f.size + dtqf.size + dq4af.size)
 
 
 def gemma_cases():

@@ -204,12 +204,14 @@ def test_check_gpu_shapes(dev, t, O, I):
     assert rel < 1e-4
 
 
-@pytest.mark.parametrize("fmt", [Z.FMT_Q80, Z.FMT_TQ2])
+@pytest.mark.parametrize("fmt", [Z.FMT_Q80, Z.FMT_TQ2, Z.FMT_Q4A])
 def test_gpu_matmul_other_formats(dev, fmt):
     rng = np.random.default_rng(41)
     O, I, S = 1792, 2048, 3
     if fmt == Z.FMT_TQ2:
         W = Z.make_expert_tq2(rng, O, I)
+    elif fmt == Z.FMT_Q4A:
+        W = Z.q4a_rows(rng, O, I)
     else:
         W = Z.quant_rows(fmt, (rng.standard_normal((O, I)) * 0.02).astype(np.float32))
     Wm = zz.gpu_map(W)
@@ -251,7 +253,9 @@ def test_gpu_map_slot_refill_needs_a_remap(dev):
     assert np.abs(yb - ref(Bw)).max() / np.abs(ref(Bw)).max() < 1e-4
 
 
-def test_gpu_matmul_declines_unmapped_and_q4a(dev):
+def test_gpu_matmul_declines_unmapped_and_bad_shapes(dev):
+    """A refused call leaves y untouched: W outside every mapping, an unknown format,
+    and a Q4A / TQ2 row length that is not a whole number of 64-groups."""
     x = np.ones((1, 64), np.float32)
     y = np.full((1, 8), 5.0, np.float32)
     W = np.zeros(8 * 2 * 18, np.uint8)               # never gpu_map'd
@@ -259,9 +263,45 @@ def test_gpu_matmul_declines_unmapped_and_q4a(dev):
     assert L.gpu_matmul(1, y.ctypes.data_as(zz._f32p), W.ctypes.data_as(zz._u8p),
                         x.ctypes.data_as(zz._f32p), 8, 64, 1) == 0
     Wm = zz.gpu_map(np.zeros(8 * 64, np.uint8))
-    assert L.gpu_matmul(4, y.ctypes.data_as(zz._f32p), Wm.ctypes.data_as(zz._u8p),
-                        x.ctypes.data_as(zz._f32p), 8, 64, 1) == 0
+    for fmt, I in ((5, 64), (Z.FMT_Q4A, 32), (Z.FMT_TQ2, 32)):
+        assert L.gpu_matmul(fmt, y.ctypes.data_as(zz._f32p), Wm.ctypes.data_as(zz._u8p),
+                            x.ctypes.data_as(zz._f32p), 8, I, 1) == 0
     assert np.all(y == 5.0)
+
+
+def _unit(v):
+    """maple.c:1781 UNIT(): (float)((int64)(r >> 40) - 2^23) / 2^23."""
+    return ((v >> np.uint64(40)).astype(np.int64) - 8388608).astype(np.float32) / np.float32(8388608.0)
+
+
+@pytest.mark.parametrize("t,fmt,O,I", [(0, Z.FMT_TQ2, 2048, 2048), (1, Z.FMT_TQ2, 512, 2048),
+                                       (3, Z.FMT_TQ2, 2048, 512), (4, Z.FMT_Q4A, 4096, 2048),
+                                       (5, Z.FMT_Q4A, 4736, 2048)])
+def test_maple_check_gpu_shapes(dev, t, fmt, O, I):
+    """maple.c:1756-1826 --check-gpu: gpu_matmul vs the reference's w_dot_f32
+    (tq2_dot_f32, q4a_dot_f32) at the engine's shapes, max|d| / max|ref| < 1e-4.
+    Weights from the same 64-bit LCG: random bytes, then tq2 row scales or q4a
+    group scales and biases overwritten, then x."""
+    say("maple check_gpu", fmt, O, I)
+    wb = Z.tensor_bytes(fmt, O, I)
+    nsc = O if fmt == Z.FMT_TQ2 else 2 * O * (I // 64)
+    st = lcg64_stream((0x243f6a8885a308d3 ^ t) % 2 ** 64, wb + nsc + I)
+    W = ((st[:wb] >> np.uint64(40)) & np.uint64(0xff)).astype(np.uint8)
+    u = _unit(st[wb:wb + nsc])
+    if fmt == Z.FMT_TQ2:
+        W[:4 * O] = (np.float32(0.01) + np.float32(0.04) * np.abs(u)).astype(np.float32).view(np.uint8)
+    else:
+        g = W.reshape(-1, 36)
+        g[:, 0:2] = (np.float32(0.002) + np.float32(0.01) * np.abs(u[0::2])).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        g[:, 2:4] = (np.float32(0.05) * u[1::2]).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    x = _unit(st[wb + nsc:]).reshape(1, I)
+    Wm = zz.gpu_map(W)
+    y = zz.gpu_matmul(fmt, Wm, x, O, I)
+    ref = np.zeros((1, O), np.float32)
+    Z.oracle().orc_matmul_f32(fmt, Z.ptr(ref), Z.ptr(Wm), Z.ptr(x), O, I, 1)
+    rel = np.abs(y - ref).max() / (np.abs(ref).max() + 1e-9)
+    say(f"  max rel err {rel:.3e}")
+    assert rel < 1e-4
 
 
 def test_every_token_tile_count(dev, layer_cache):

@@ -256,6 +256,13 @@ def _dequant64(fmt, q, O, I):
         c = q[O * 4:].reshape(O, I // 64, 16)
         w = np.concatenate([((c >> (2 * k)) & 3) for k in range(4)], axis=2).astype(np.float64) - 1
         return w.reshape(O, I) * alpha[:, None]
+    if fmt == Z.FMT_Q4A:                            # tq2.h:269-282: w = d q + m
+        grp = q.reshape(O * (I // 64), 36)
+        d = grp[:, 0:2].copy().view(np.float16).astype(np.float64)
+        m = grp[:, 2:4].copy().view(np.float16).astype(np.float64)
+        h0, h1 = grp[:, 4:20], grp[:, 20:36]
+        v = np.concatenate([h0 & 15, h0 >> 4, h1 & 15, h1 >> 4], axis=1).astype(np.float64)
+        return (v * d + m).reshape(O, I)
     bb = 18 if fmt == Z.FMT_Q40 else 34
     blk = q.reshape(O * (I // 32), bb)
     d = blk[:, :2].copy().view(np.float16).astype(np.float64)
@@ -300,9 +307,15 @@ def test_f32_dots_golden():
          for o in range(O)]
     assert _bits_equal(c, g["dtqf"])
     assert _bits_equal(_matmul(Z.FMT_TQ2, g["tq"], g["xt"].reshape(1, It), O, It)[0], g["dtqf"])
+    qa = g["q4a"]                                   # q4a_dot_f32, tq2.h:405-427
+    for t in range(4):
+        xt = np.ascontiguousarray(x[t])
+        a = [L.orc_q4a_dot_f32(Z.ptr(qa[o * 44 * 36:]), Z.ptr(xt), I) for o in range(O)]
+        assert _bits_equal(a, g["dq4af"][t])
+    assert _bits_equal(_matmul(Z.FMT_Q4A, qa, x, O, I), g["dq4af"])
 
 
-@pytest.mark.parametrize("fmt", [Z.FMT_Q40, Z.FMT_Q80, Z.FMT_TQ2])
+@pytest.mark.parametrize("fmt", [Z.FMT_Q40, Z.FMT_Q80, Z.FMT_TQ2, Z.FMT_Q4A])
 def test_f32_dots_closed_form(fmt):
     """The same dots against float64 dequant . x: every product is exact in
     double, so the two differ only by the summation order, far below one float
@@ -313,6 +326,8 @@ def test_f32_dots_closed_form(fmt):
         if fmt == Z.FMT_TQ2:
             codes = rng.integers(0, 3, size=(O, I)).astype(np.int8)
             W = Z.tq2_tensor(codes, (rng.random(O) * 0.05 + 0.001).astype(np.float32))
+        elif fmt == Z.FMT_Q4A:
+            W = Z.q4a_rows(rng, O, I)
         else:
             W = _f32_rows(rng, fmt, O, I)
         x = rng.standard_normal((S, I)).astype(np.float32)
@@ -331,7 +346,7 @@ def test_f32_dots_vs_compiled_reference():
     R = Z.ref_lib("kernels")
     if R is None:
         pytest.skip("oracle/_ref not built (needs /root/reference)")
-    for n in ("ref_q40_dot_f32", "ref_q80_dot_f32", "ref_tq2_dot_f32"):
+    for n in ("ref_q40_dot_f32", "ref_q80_dot_f32", "ref_tq2_dot_f32", "ref_q4a_dot_f32"):
         getattr(R, n).restype = C.c_float
     L = Z.oracle()
     rng = np.random.default_rng(29)
@@ -359,6 +374,14 @@ def test_f32_dots_vs_compiled_reference():
         want = np.array([R.ref_tq2_dot_f32(Z.ptr(cb[o * (I // 4):]), C.c_float(alpha[o]), Z.ptr(x[0]), I)
                          for o in range(O)], np.float32)
         assert _bits_equal(_matmul(Z.FMT_TQ2, W, x, O, I)[0], want)
+    for I in (64, 2048, 2816):
+        O = 16
+        W = Z.q4a_rows(rng, O, I, specials=True)
+        x = (rng.standard_normal((2, I)) * np.float32(3.0)).astype(np.float32)
+        want = np.array([[R.ref_q4a_dot_f32(Z.ptr(W[o * (I // 64) * 36:]), Z.ptr(x[s]), I)
+                          for o in range(O)] for s in range(2)], np.float32)
+        assert _bits_equal(_matmul(Z.FMT_Q4A, W, x, O, I), want), I
+        assert np.isnan(want).any()
 
 
 def test_tq2_layout_from_description():
@@ -531,3 +554,16 @@ def test_ling_grouped_router_keeps_only_live_groups():
         live = np.concatenate([np.arange(g * EG, (g + 1) * EG) for g in keep])
         want = sorted(live, key=lambda e: (-sel[e], e))[:L.K]
         assert list(ids) == want
+
+
+def test_tensor_sizes():
+    """tests/test_tq2.c size arithmetic, with q40.h:313-314 / 461-462 for the block
+    formats: the byte counts gpu_matmul checks a tensor's mapping against."""
+    L = Z.oracle()
+    for I in (64, 128, 512, 1792, 2048, 2816):
+        assert L.orc_tensor_bytes(Z.FMT_TQ2, 7, I) == 7 * 4 + 7 * (I // 4)
+        assert L.orc_tensor_bytes(Z.FMT_Q4A, 7, I) == 7 * (I // 64) * 36
+        assert L.orc_tensor_bytes(Z.FMT_Q40, 7, I) == 7 * (I // 32) * 18
+        assert L.orc_tensor_bytes(Z.FMT_Q80, 7, I) == 7 * (I // 32) * 34
+        for f in (Z.FMT_Q40, Z.FMT_Q80, Z.FMT_TQ2, Z.FMT_Q4A):
+            assert L.orc_tensor_bytes(f, 7, I) == Z.tensor_bytes(f, 7, I)

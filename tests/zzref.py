@@ -13,7 +13,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_DIR = os.path.join(ROOT, "oracle")
 
-FMT_Q40, FMT_Q80, FMT_TQ2 = 1, 2, 3
+FMT_Q40, FMT_Q80, FMT_TQ2, FMT_Q4A = 1, 2, 3, 4
 GATE_GEMMA, GATE_LFM, GATE_MAPLE, GATE_LING = 0, 1, 2, 4   # the library's ZZ_GATE_* codes
 ACT_GEGLU_TANH, ACT_SWIGLU, ACT_SWIGLU_CL = 0, 1, 2
 
@@ -80,6 +80,8 @@ def oracle():
             getattr(L, n).argtypes = [u8p, f32p, C.c_int]
         L.orc_tq2_dot_f32.restype = C.c_float
         L.orc_tq2_dot_f32.argtypes = [u8p, C.c_float, f32p, C.c_int]
+        L.orc_q4a_dot_f32.restype = C.c_float
+        L.orc_q4a_dot_f32.argtypes = [u8p, f32p, C.c_int]
         L.orc_tensor_bytes.restype = C.c_int64
         L.orc_tensor_bytes.argtypes = [C.c_int, C.c_int, C.c_int]
         L.orc_moe_layer.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), f32p, C.c_int,
@@ -139,7 +141,27 @@ def tensor_bytes(fmt, O, I):
         return O * (I // 32) * 18
     if fmt == FMT_Q80:
         return O * (I // 32) * 34
+    if fmt == FMT_Q4A:
+        return O * (I // 64) * 36
     return O * 4 + O * (I // 4)
+
+
+def q4a_rows(rng, O, I, specials=False):
+    """Random Q4A rows (tq2.h:269-292): per 64-group an fp16 scale d > 0 and an fp16
+    bias m of either sign (the ranges of maple.c:1790-1796), then random nibbles.
+    With specials, some groups' d or m is NaN, +-inf, -0 or subnormal."""
+    W = rng.integers(0, 256, size=(O * (I // 64), 36), dtype=np.uint8)
+    d = (0.002 + 0.01 * np.abs(rng.standard_normal(W.shape[0]))).astype(np.float16)
+    m = (0.05 * rng.standard_normal(W.shape[0])).astype(np.float16)
+    W[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    W[:, 2:4] = m.view(np.uint8).reshape(-1, 2)
+    if specials:
+        pick = rng.choice(W.shape[0], size=min(12, W.shape[0]), replace=False)
+        for k, g in enumerate(pick):
+            h = [0x7e00, 0x7c00, 0xfc00, 0x8000, 0x0001, 0x03ff][k % 6]
+            off = 0 if k % 2 == 0 else 2
+            W[g, off], W[g, off + 1] = h & 255, h >> 8
+    return W.reshape(-1)
 
 
 # ------------------------------------------------------------ synthetic layers

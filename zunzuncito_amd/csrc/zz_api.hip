@@ -133,6 +133,7 @@ static int64_t fmt_tensor_bytes(int fmt, int O, int I) {
     if (fmt == ZZ_FMT_Q40) return (int64_t)O * (I / ZZ_BLK) * 18;
     if (fmt == ZZ_FMT_Q80) return (int64_t)O * (I / ZZ_BLK) * 34;
     if (fmt == ZZ_FMT_TQ2) return (int64_t)O * 4 + (int64_t)O * (I / 4);
+    if (fmt == ZZ_FMT_Q4A) return (int64_t)O * (I / 64) * 36;        // tq2.h:287-292
     return -1;
 }
 
@@ -152,8 +153,10 @@ static int grow(float **p, size_t *cap, size_t n) {
 
 extern "C" int gpu_matmul(int fmt, float *y, const uint8_t *W, const float *x, int O, int I, int S) {
     if (!g_ready) ZZ_FAIL("gpu_matmul: not ready");
-    if (fmt != ZZ_FMT_Q40 && fmt != ZZ_FMT_Q80 && fmt != ZZ_FMT_TQ2) ZZ_FAIL("gpu_matmul: fmt %d declined", fmt);
-    if (O <= 0 || I <= 0 || S <= 0 || I % (fmt == ZZ_FMT_TQ2 ? 64 : 32)) ZZ_FAIL("gpu_matmul: bad shape");
+    if (fmt != ZZ_FMT_Q40 && fmt != ZZ_FMT_Q80 && fmt != ZZ_FMT_TQ2 && fmt != ZZ_FMT_Q4A)
+        ZZ_FAIL("gpu_matmul: fmt %d declined", fmt);
+    const int grp = fmt == ZZ_FMT_TQ2 || fmt == ZZ_FMT_Q4A ? 64 : 32;
+    if (O <= 0 || I <= 0 || S <= 0 || I % grp) ZZ_FAIL("gpu_matmul: bad shape");
     const Mapping *m = find_map(W, (size_t)fmt_tensor_bytes(fmt, O, I));
     if (!m) ZZ_FAIL("gpu_matmul: W not inside a gpu_map'd range");
     const uint8_t *dW = m->dev + (W - m->host);

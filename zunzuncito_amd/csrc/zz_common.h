@@ -17,6 +17,7 @@
 #define ZZ_FMT_Q40 1
 #define ZZ_FMT_Q80 2
 #define ZZ_FMT_TQ2 3
+#define ZZ_FMT_Q4A 4           // gpu_matmul only: maple's lm_head / centroid format
 
 // gating and activation kinds, mirrored in include/zz_moe.h
 #define ZZ_GATE_SOFTMAX_PES 0   // gemma4.c:581-613
