@@ -101,6 +101,39 @@ int ref_g4_moe(int D, int MI, int E, int K, float eps, const float *router,
     return 0;
 }
 
+/* The same call on a layer set up once (the engine's steady state: model and Buf
+ * live across calls, as in gemma4.c's decode loop), for timing. Buf is sized for
+ * Smax tokens. */
+typedef struct { M *m; Buf b; int Smax; } G4Layer;
+
+void *ref_g4_layer_new(int D, int MI, int E, int K, float eps, const float *router,
+                       const float *rscale, const float *pes, const float *pre_ln,
+                       const float *post_ln, const uint8_t *experts, int64_t esz, int Smax) {
+    if (K > MAXTOPK || K > E || E > 128 || Smax < 1) return NULL;
+    G4Layer *h = zz_calloc(sizeof *h);
+    h->m = g4_model(D, MI, E, K, eps, router, rscale, pes, pre_ln, post_ln, experts, esz);
+    g4_buf(&h->b, D, MI, E, K, Smax);
+    h->Smax = Smax;
+    return h;
+}
+
+int ref_g4_layer_call(void *hp, const float *residual, int S, float *out, int *nu) {
+    G4Layer *h = hp;
+    if (!h || S < 1 || S > h->Smax) return -1;
+    moe_start(h->m, 0, residual, out, S, &h->b);
+    moe_finish(h->m, 0, out, S, &h->b);
+    if (nu) *nu = h->b.moe_nu;
+    return 0;
+}
+
+void ref_g4_layer_free(void *hp) {
+    G4Layer *h = hp;
+    if (!h) return;
+    g4_free_buf(&h->b);
+    g4_free_model(h->m);
+    free(h);
+}
+
 /* route_row alone (gemma4.c:581-613), one token. */
 int ref_g4_route(int D, int E, int K, float eps, const float *router, const float *rscale,
                  const float *pes, const float *residual, int *idx, float *wts) {

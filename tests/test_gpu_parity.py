@@ -529,3 +529,31 @@ def test_null_stream_orders_with_the_default_stream(dev):
         assert np.array_equal(got, want)
         tail = q[-18:].cpu().numpy()
         assert np.isfinite(Z.dequant_q40(tail, 1, 32)).all()
+
+
+def test_profile_sessions_do_not_share_events(dev, layer_cache):
+    """zz_moe_profile: records stay readable after switching off, and a new session
+    reuses their events only after dropping them. Three sessions in a row, each with
+    a batched and a decode forward: every kernel time is positive and their sum stays
+    within the host's wall time of the forwards."""
+    import time
+    L = layer_cache("gemma", 0)
+    m = zz.MoeLayer(L.D, L.MI, L.E, L.K, L.gating, L.act, L.fmts, L.router, L.router_scale,
+                    L.pes, None, L.pre_ln, L.post_ln, eps=L.eps)
+    try:
+        m.upload_all(L.experts)
+        xb, x1 = Z.make_input(L, 64, 3), Z.make_input(L, 1, 4)
+        for session in range(3):
+            zz.profile(True)
+            t0 = time.perf_counter()
+            m.forward(xb)
+            m.forward(x1)
+            wall_ms = (time.perf_counter() - t0) * 1e3
+            zz.profile(False)
+            prof = zz.profile_read()
+            say(f"session {session}: " + ", ".join(f"{k} {ms:.3f}/{n}" for k, (ms, n) in prof.items() if n))
+            assert prof["ffn_down"][1] == 1 and prof["dec_down"][1] == 1
+            assert all(ms > 0 for ms, n in prof.values() if n)
+            assert sum(ms for ms, _ in prof.values()) <= wall_ms
+    finally:
+        m.close()

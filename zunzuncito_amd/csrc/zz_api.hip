@@ -494,8 +494,13 @@ int zz_lib_prof_set(int on) {
 extern "C" int zz_moe_profile(int on) {
     if (!g_ready) ZZ_FAIL("zz_moe_profile: not ready");
     (void)hipDeviceSynchronize();
-    for (ProfRec &r : g_prof_recs) { g_event_pool.push_back(r.a); g_event_pool.push_back(r.b); }
-    if (on) g_prof_recs.clear();
+    // switching off keeps the records (and their events) for zz_moe_profile_read;
+    // only a new session recycles them, so no event is ever in the pool and in a
+    // record at once
+    if (on) {
+        for (ProfRec &r : g_prof_recs) { g_event_pool.push_back(r.a); g_event_pool.push_back(r.b); }
+        g_prof_recs.clear();
+    }
     g_prof = on;
     return 1;
 }
