@@ -133,9 +133,10 @@ int zz_moe_forward_end(int layer, float *out, int *eidx, float *ewt);
  * the int8 hidden by (token, slot); dispatch: uniq[E] union order (nu is set),
  * and for union entry u the tokens rows[offs[u] .. offs[u+1]) ascending with
  * their top-k slots (offs[nu+1], rows[S*K], slots[S*K]); logits [S, E]: the
- * router logits of the batched path (S > 4; the decode path keeps none), the
- * reference's own values (gemma: after the bias) when S >= 16 and D % 64 == 0,
- * interval centres otherwise. */
+ * router logits, the reference's own float values for the lfm, maple and ling
+ * routers at every S, and for gemma (after the bias) when S >= 16 and D % 64 == 0;
+ * gemma's other batched logits are interval centres, and its decode path (S <= 4)
+ * keeps none. */
 typedef struct zz_moe_dump {
     int8_t *xq; float *xs;
     int8_t *hq; float *hs;

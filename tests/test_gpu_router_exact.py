@@ -257,3 +257,42 @@ def test_logit_serial_replay(dev, kind, S):
     say(f"  counters {ds.tolist()}  ids {got[1][:L.K].tolist()}")
     check(L, got, want, exact_weights=True)
     assert ds[1] >= S
+
+
+# ------------------------------------------------------- certified double logits
+def _cancelling_layer(kind, seed):
+    """Router rows whose dot with the input nearly cancels: two large equal and
+    opposite terms dwarf the rest, so the exact-order prefix sums are large against
+    the logit and many logits sit near a float rounding boundary of their bound."""
+    L = small_layer(kind, seed=seed)
+    rng = np.random.default_rng(seed)
+    L.router[:, 3] = (rng.standard_normal(L.E) * 300).astype(np.float32)
+    L.router[:, 7] = -L.router[:, 3]
+    return L
+
+
+@pytest.mark.parametrize("kind", ["lfm", "maple", "ling"])
+@pytest.mark.parametrize("S", [1, 3, 5, 8, 15])
+@pytest.mark.parametrize("cancel", [False, True])
+def test_certified_double_logits(dev, kind, S, cancel):
+    """Below S = 16 the lfm / maple / ling logits come from the wave-parallel sum with
+    the prefix-sum bound of the reference's serial double chain (and a replay where
+    the bound spans a float rounding boundary): they equal the reference's floats bit
+    for bit, and the routing follows."""
+    L = _cancelling_layer(kind, 11 + S) if cancel else small_layer(kind, seed=11 + S)
+    x = Z.make_input(L, S, 40 + S)
+    if cancel:
+        x[:, 3] = x[:, 7] = 1.0
+    m = gpu_layer(L)
+    try:
+        s0 = np.array(zz.stats(), np.int64)
+        out, eidx, ewt = m.forward(x)
+        ds = np.array(zz.stats(), np.int64) - s0
+        got = m.debug(S, logits=True)["logits"]
+    finally:
+        m.close()
+    want = Z.oracle_moe(L, x, dump=True)
+    say(f"  {kind} S={S} cancel={cancel}: logit replays {ds[1]}")
+    bad = got.astype(np.float32).view(np.uint32) != want.dump["logits"].view(np.uint32)
+    assert not bad.any(), (int(bad.sum()), np.argwhere(bad)[:4])
+    check(L, (out, eidx, ewt), want, exact_weights=True)

@@ -254,8 +254,8 @@ class MoeLayer:
                                                      C.c_void_p(stream or None)))
 
     def debug(self, S, logits=False):
-        """The last forward's dump (zz_moe_debug); logits=True adds the batched
-        path's router logits [S, E] as float64."""
+        """The last forward's dump (zz_moe_debug); logits=True adds the router
+        logits [S, E] as float64 (none for gemma's decode path)."""
         K, D, MI = self.K, self.D, self.MI
         d = dict(xq=np.zeros((S, D), np.int8), xs=np.zeros((S, D // 32), np.float32),
                  hq=np.zeros((S * K, MI), np.int8), hs=np.zeros((S * K, MI // 32), np.float32),

@@ -803,7 +803,9 @@ extern "C" int zz_moe_debug(int id, zz_moe_dump *dp) {
     }
     ZZ_CHECK(hipStreamSynchronize(g_stream));
     if (dp->logits) {
-        if (dec || d.gating == ZZ_GATE_DENSE) ZZ_FAIL("zz_moe_debug: no router logits on this path");
+        // the decode path keeps gemma's logits as centres with bounds only
+        if ((dec && d.gating == ZZ_GATE_SOFTMAX_PES) || d.gating == ZZ_GATE_DENSE)
+            ZZ_FAIL("zz_moe_debug: no router logits on this path");
         ZZ_CHECK(hipMemcpy(dp->logits, w.cen, sizeof(double) * S * d.E, hipMemcpyDeviceToHost));
     }
     if (dp->xq) ZZ_CHECK(hipMemcpy(dp->xq, w.xq, (size_t)S * d.D, hipMemcpyDeviceToHost));

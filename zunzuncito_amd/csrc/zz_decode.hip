@@ -35,7 +35,12 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
     const ZzLogitArgs &lg = a.lg;
     const int S = a.S, D = pp.D, nb = D / ZZ_BLK, tid = threadIdx.x, e = blockIdx.x;
     const bool gem = pp.gemma;
-    __shared__ __attribute__((aligned(16))) float buf[ZZ_MAXD + ZZ_MAXD / 32];
+    // gemma: the D rounded products (padded); lfm/maple/ling: one product buffer per
+    // token's wave
+    __shared__ __attribute__((aligned(16))) char sbuf[(ZZ_MAXD + ZZ_MAXD / 32) * 4 > DEC_MAXS * ZZ_DBUF * 8
+                                                          ? (ZZ_MAXD + ZZ_MAXD / 32) * 4
+                                                          : DEC_MAXS * ZZ_DBUF * 8];
+    float *buf = (float *)sbuf;
     __shared__ double red[12];
     __shared__ float rr[DEC_MAXS];
     __shared__ float cert;
@@ -99,7 +104,7 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
                                 lg.bnd + (size_t)s * lg.E + e);
         }
     } else if ((tid >> 6) < S) {
-        zz_logit_wave_f64(lg, tid >> 6, e);
+        zz_logit_wave_f64(lg, tid >> 6, e, (double *)sbuf + (tid >> 6) * ZZ_DBUF);
     }
     // the expert input quantisation: block g on workgroup g % E, lanes 8(g / E)..+7;
     // dual: blocks S*nb.. are the dense branch's input (same rms factor, its own norm)

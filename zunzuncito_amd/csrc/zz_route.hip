@@ -130,17 +130,18 @@ __global__ __launch_bounds__(256) void zz_prep_kernel(ZzPrepArgs a) {
     }
 }
 
+#define ZZ_WAVE_LDS (4 * ZZ_TBUF > 8 * ZZ_DBUF ? 4 * ZZ_TBUF : 8 * ZZ_DBUF)   // bytes per wave
 __global__ __launch_bounds__(256) void zz_logits_kernel(ZzLogitArgs a) {
-    __shared__ __attribute__((aligned(16))) float buf[4 * ZZ_TBUF];
+    __shared__ __attribute__((aligned(16))) char buf[4 * ZZ_WAVE_LDS];
     const int s = blockIdx.y, e = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (e >= a.E) return;
+    char *wb = buf + (threadIdx.x >> 6) * ZZ_WAVE_LDS;
     if (a.gating == ZZ_GATE_SOFTMAX_PES) {
         const size_t o = (size_t)s * a.E + e;
         zz_tight_wave<1, false>(a.router + (size_t)e * a.D, a.xn + (size_t)s * a.D, nullptr, nullptr,
-                                1.0f, a.D, a.bias, e, buf + (threadIdx.x >> 6) * ZZ_TBUF, a.cen + o,
-                                a.bnd + o, a.E, nullptr);
+                                1.0f, a.D, a.bias, e, (float *)wb, a.cen + o, a.bnd + o, a.E, nullptr);
     } else {
-        zz_logit_wave_f64(a, s, e);
+        zz_logit_wave_f64(a, s, e, (double *)wb);
     }
 }
 

@@ -185,50 +185,125 @@ __device__ void zz_tight_block_scan(const float *buf, int D, const float *bias, 
     __syncthreads();
 }
 
-// lfm / maple logit of token s, expert e (router input x), by one wave.
-__device__ void zz_logit_wave_f64(const ZzLogitArgs &a, int s, int e) {
+// -------------------------------------------------------------------------------
+// lfm / maple / ling logits. The reference sums the exact double products
+// p_i = (double)w_i * (double)x_i in order: one double chain (lfm25.c:650-653;
+// maple.c:744 through w_dot_f32, maple.c:400-410) or eight chains by i % 8 combined
+// pairwise (ling.c:722-727); the logit is the float of that sum. The first addition
+// (0 + p_0) is exact and each later one errs by at most u |v_i|, so the chain's sum
+// lies within u (1+u)^D sum_{i>=1} |S_i| of the exact prefix-sum end S_D. The wave
+// forms the products once, transposes them through LDS so that each lane owns a
+// contiguous run of the order, and joins the runs by a wave scan: that gives the
+// prefix sums S_i (to gamma_40 T, T = sum |p_i|) and the centre S_D (to gamma_30 T).
+// When every value the bound allows rounds to one float, that float is the
+// reference's logit; otherwise one lane replays the chain from the products staged
+// in LDS, chunk by chunk.
+#define ZZ_DPER 16                           // products per lane per chunk
+#define ZZ_DBUF (64 * (ZZ_DPER + 1))         // doubles of one wave's product buffer
+
+// The exact products of elements c0 .. c0 + 64*ZZ_DPER - 1 into the wave's buffer,
+// element c0 + q at tb[(q / ZZ_DPER) * (ZZ_DPER + 1) + q % ZZ_DPER] (0 past D).
+// Loads are coalesced (element c0 + 64 j + l on lane l). Ends synchronised.
+__device__ __forceinline__ void zz_stage_products(const float *w, const float *x, int D, int c0, double *tb) {
     const int l = threadIdx.x & 63;
-    const int D = a.D;
-    const float *w = a.router + (size_t)e * D;
-    const float *xv = a.x + (size_t)s * D;
-    const size_t o = (size_t)s * a.E + e;
-    double c = 0.0, t = 0.0;
-    for (int c0 = 0; c0 < D; c0 += 64 * 16) {
-        float wr[16], xr[16];
+    float wv[ZZ_DPER], xr[ZZ_DPER];
 #pragma unroll
-        for (int j = 0; j < 16; j++) {                        // clamped: loads stay in range
-            const int i = min(c0 + 64 * j + l, D - 1);
-            wr[j] = w[i];
-            xr[j] = xv[i];
-        }
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            if (c0 + 64 * j + l < D) {
-                const double p = (double)wr[j] * (double)xr[j];
-                c += p;
-                t += fabs(p);
-            }
-        }
+    for (int j = 0; j < ZZ_DPER; j++) {                   // clamped: loads stay in range
+        const int i = min(c0 + 64 * j + l, D - 1);
+        wv[j] = w[i];
+        xr[j] = x[i];
     }
-    c = zz_wave_sum(c);
-    t = zz_wave_sum(t);
-    if (l == 0) {
-        double m = (double)((D + 63) / 64 + 6);
-        double b = (zz_gamma(D - 1, ZZ_U64) + zz_gamma(m, ZZ_U64)) * t * 1.0000001 + 1e-300;
-        float lo = (float)(c - b), hi = (float)(c + b), v = lo;
-        if (lo != hi) {
-            double r = 0.0;                      // serial replay, reference order
-            if (a.gating == ZZ_GATE_GROUPED) {   // ling.c:722-727: 8 accumulators, D % 8 == 0
-                double q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-                for (int i = 0; i < D; i += 8)
-                    for (int k = 0; k < 8; k++) q[k] += (double)w[i + k] * (double)xv[i + k];
-                r = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
-            } else {
-                for (int i = 0; i < D; i++) r += (double)w[i] * (double)xv[i];
-            }
-            v = (float)r;
-            atomicAdd(a.diag + 1, 1u);
+#pragma unroll
+    for (int j = 0; j < ZZ_DPER; j++) {
+        const int q = 64 * j + l;
+        tb[(q / ZZ_DPER) * (ZZ_DPER + 1) + q % ZZ_DPER] =
+            c0 + q < D ? (double)wv[j] * (double)xr[j] : 0.0;
+    }
+    zz_wave_sync_lds();
+}
+
+// logit of token s, expert e (router input x), by one wave; tb: ZZ_DBUF doubles of
+// LDS owned by this wave. Lane 0 writes cen (the exact float logit) and bnd = 0.
+__device__ void zz_logit_wave_f64(const ZzLogitArgs &a, int s, int e, double *tb) {
+    const int l = threadIdx.x & 63, D = a.D;
+    const float *w = a.router + (size_t)e * D, *xv = a.x + (size_t)s * D;
+    const size_t o = (size_t)s * a.E + e;
+    const bool grp = a.gating == ZZ_GATE_GROUPED;
+    double carry = 0.0, sabs = 0.0, T = 0.0;
+    for (int c0 = 0; c0 < D; c0 += 64 * ZZ_DPER) {
+        zz_stage_products(w, xv, D, c0, tb);
+        const int i0 = c0 + l * ZZ_DPER;
+        double p[ZZ_DPER], loc = 0.0;
+#pragma unroll
+        for (int k = 0; k < ZZ_DPER; k++) {
+            p[k] = tb[l * (ZZ_DPER + 1) + k];
+            loc += p[k];
+            T += fabs(p[k]);
         }
+        double inc = loc;                                  // inclusive scan of the runs
+#pragma unroll
+        for (int q = 1; q < 64; q <<= 1) {
+            const double v = __shfl_up(inc, q, 64);
+            if (l >= q) inc += v;
+        }
+        if (!grp) {
+            double run = carry + (inc - loc);
+#pragma unroll
+            for (int k = 0; k < ZZ_DPER; k++) {
+                run += p[k];
+                if (i0 + k >= 1 && i0 + k < D) sabs += fabs(run);
+            }
+        }
+        carry += __shfl(inc, 63, 64);
+        zz_wave_sync_lds();                                // tb is rewritten next
+    }
+    sabs = zz_wave_sum(sabs);
+    T = zz_wave_sum(T);
+    // the centre's own error: runs of ZZ_DPER, 6 scan levels, one add per chunk
+    const double gc = zz_gamma(ZZ_DPER + 6 + (D + 64 * ZZ_DPER - 1) / (64 * ZZ_DPER) + 2, ZZ_U64) * T;
+    double b;
+    if (grp) {
+        // eight chains of D/8 terms, each within gamma_{D/8} of its exact sum, then
+        // three levels of pairwise adds: within gamma_{D/8 + 3} T in all
+        b = zz_gamma(D / 8 + 3, ZZ_U64) * T + gc;
+    } else {
+        // the prefix sums' slack: each S_i within gamma_{D + 40} T (far more than the
+        // run, scan and carry depth)
+        b = ZZ_U64 * (1.0 + zz_gamma(D + 2, ZZ_U64)) * (sabs + (double)D * zz_gamma(D + 40, ZZ_U64) * T) + gc;
+    }
+    b = b * 1.000001 + 1e-300;
+    const float lo = (float)(carry - b), hi = (float)(carry + b);
+    float v = lo;
+    if (__builtin_amdgcn_readfirstlane(lo != hi)) {
+        // replay, reference order, from the products staged chunk by chunk
+        double r = 0.0, q0 = 0.0, q1 = 0.0, q2 = 0.0, q3 = 0.0, q4 = 0.0, q5 = 0.0, q6 = 0.0, q7 = 0.0;
+        for (int c0 = 0; c0 < D; c0 += 64 * ZZ_DPER) {
+            zz_stage_products(w, xv, D, c0, tb);
+            if (l == 0) {
+                const int n = min(64 * ZZ_DPER, D - c0);
+                if (grp) {                                 // D % 8 == 0, c0 % 8 == 0
+                    for (int i = 0; i < n; i += 8) {
+                        const double *t = tb + (i / ZZ_DPER) * (ZZ_DPER + 1) + i % ZZ_DPER;
+                        q0 += t[0]; q1 += t[1]; q2 += t[2]; q3 += t[3];
+                        q4 += t[4]; q5 += t[5]; q6 += t[6]; q7 += t[7];
+                    }
+                } else {
+                    for (int i = 0; i < n; i += ZZ_DPER) {
+                        const double *t = tb + (i / ZZ_DPER) * (ZZ_DPER + 1);
+                        const int m = min(ZZ_DPER, n - i);
+#pragma unroll
+                        for (int k = 0; k < ZZ_DPER; k++)
+                            if (k < m) r += t[k];
+                    }
+                }
+            }
+            zz_wave_sync_lds();
+        }
+        if (grp) r = ((q0 + q1) + (q2 + q3)) + ((q4 + q5) + (q6 + q7));
+        v = (float)r;
+        if (l == 0) atomicAdd(a.diag + 1, 1u);
+    }
+    if (l == 0) {
         a.cen[o] = (double)v;                    // exact float logit
         a.bnd[o] = 0.0;
     }
