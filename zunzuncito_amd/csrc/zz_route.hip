@@ -505,27 +505,26 @@ __global__ __launch_bounds__(DP_T) void zz_dispatch_kernel(ZzDispatchArgs a) {
     }
     const int nm = __syncthreads_count(t < nu && nit > 1);
     if (t < 64 && nm > 0) {
-        // One wave, while the others write the sorted lists below. XCD x's key
-        // (load << 3) | x is a uniform value held in a scalar register (readfirstlane
-        // keeps it there); the keys are distinct, so the least one names the XCD.
-        // Lane i holds the batch's i-th entry.
-        unsigned k0 = 0, k1 = 1, k2 = 2, k3 = 3, k4 = 4, k5 = 5, k6 = 6, k7 = 7;
+        // One wave, while the others write the sorted lists below. Lane x < 8 holds
+        // XCD x's key (load << 3) | x, the other lanes ~0u; the keys are distinct, so
+        // the least one names the XCD. Per expert: a three-step DPP minimum over
+        // lanes 0-7 (swaps within quads, then the half-row mirror), read back as a
+        // uniform value, and the chosen lane adds the expert's cost. Lane i holds the
+        // batch's i-th entry.
+        unsigned key = t < 8 ? (unsigned)t : 0xffffffffu;
         for (int r0 = 0; r0 < nu; r0 += 64) {
             const int ec = r0 + t < nu ? xcost[r0 + t] : 0;
-            const int rn = min(64, nu - r0);
+            const int rn = (int)zz_uni((unsigned)min(64, nu - r0));
             int xo = 0;
             for (int i = 0; i < rn; i++) {
                 const unsigned c = (unsigned)__builtin_amdgcn_readlane(ec, i) << 3;
-                const unsigned m = zz_uni(min(min(min(k0, k1), min(k2, k3)), min(min(k4, k5), min(k6, k7))));
-                k0 = zz_uni(k0 + (m == k0 ? c : 0u));
-                k1 = zz_uni(k1 + (m == k1 ? c : 0u));
-                k2 = zz_uni(k2 + (m == k2 ? c : 0u));
-                k3 = zz_uni(k3 + (m == k3 ? c : 0u));
-                k4 = zz_uni(k4 + (m == k4 ? c : 0u));
-                k5 = zz_uni(k5 + (m == k5 ? c : 0u));
-                k6 = zz_uni(k6 + (m == k6 ? c : 0u));
-                k7 = zz_uni(k7 + (m == k7 ? c : 0u));
-                if (t == i) xo = (int)(m & 7u);
+                unsigned m = key;
+                m = min(m, (unsigned)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));
+                m = min(m, (unsigned)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));
+                m = min(m, (unsigned)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));
+                const unsigned mu = zz_uni(m);             // lane 0: the least of lanes 0-7
+                key += key == mu ? c : 0u;
+                if (t == i) xo = (int)(mu & 7u);
             }
             if (t < rn) xof[r0 + t] = xo;
         }
