@@ -557,3 +557,65 @@ def test_profile_sessions_do_not_share_events(dev, layer_cache):
             assert sum(ms for ms, _ in prof.values()) <= wall_ms
     finally:
         m.close()
+
+
+def _layer_from(L):
+    return zz.MoeLayer(L.D, L.MI, L.E, L.K, L.gating, L.act, L.fmts, L.router, L.router_scale,
+                       L.pes, L.bias, L.pre_ln, L.post_ln, norm_topk=L.norm_topk, use_bias=L.use_bias,
+                       eps=L.eps, routed_scaling=L.routed_scaling, clamp=L.clamp, n_group=L.n_group,
+                       topk_group=L.topk_group)
+
+
+def test_container_lfm_per_layer_formats(dev, tmp_path):
+    """An LFM-shaped container whose layers have different expert formats, one `eszl`
+    line each (lfm25.c:326-331): layer 0 q4_0, layer 1 q8_0. zz_moe_load_experts reads
+    each layer's records at its own size and format; a layer whose formats are not the
+    line's declines with the reason."""
+    say("container lfm eszl")
+    L0 = Z.make_layer("lfm", seed=31, D=512, MI=256, E=16, K=4, fmts=(Z.FMT_Q40,) * 3)
+    L1 = Z.make_layer("lfm", seed=32, D=512, MI=256, E=16, K=4, fmts=(Z.FMT_Q80,) * 3)
+    Z.write_moe_container(str(tmp_path), [L0, L1], per_layer=True)
+    for li, L in enumerate((L0, L1)):
+        m = _layer_from(L)
+        try:
+            m.load_experts(str(tmp_path), li)
+            x = Z.make_input(L, 6, 40 + li)
+            out, eidx, ewt = m.forward(x)
+            want = Z.oracle_moe(L, x)
+            assert np.array_equal(eidx, want.eidx) and Z.rel_l2(out, want.out) < 1e-3
+        finally:
+            m.close()
+    # the record size matches but the line names another format: a mixed layer (gate/up
+    # q4_0, down q8_0) under an eszl line that says q4_0 for all three
+    L0b = Z.make_layer("lfm", seed=31, D=512, MI=256, E=16, K=4, fmts=(Z.FMT_Q40, Z.FMT_Q40, Z.FMT_Q80))
+    Z.write_moe_container(str(tmp_path / "mixed"), [L0b], per_layer=False)
+    with open(tmp_path / "mixed" / "manifest.txt") as f:
+        text = f.read()
+    g, _, d = L0b.tensor_sizes()
+    text = text.replace(f"esz {L0b.esz} {g} {d}\n", f"eszl 0 {L0b.esz} {g} {d} 1\n")
+    with open(tmp_path / "mixed" / "manifest.txt", "w") as f:
+        f.write(text)
+    m = _layer_from(L0b)
+    try:
+        with pytest.raises(RuntimeError, match="format"):
+            m.load_experts(str(tmp_path / "mixed"), 0)
+    finally:
+        m.close()
+
+
+def test_container_maple_tq2(dev, tmp_path):
+    """A Maple-shaped tq2 container (one `esz` line, maple.c:255-258): the records load
+    into the slot table and the layer matches the oracle."""
+    say("container maple tq2")
+    L = Z.make_layer("maple", seed=33, D=512, MI=256, E=32, K=8)
+    Z.write_moe_container(str(tmp_path), [L], per_layer=False)
+    m = _layer_from(L)
+    try:
+        m.load_experts(str(tmp_path), 0)
+        for S in (1, 9):
+            x = Z.make_input(L, S, 50 + S)
+            out, eidx, ewt = m.forward(x)
+            want = Z.oracle_moe(L, x)
+            assert np.array_equal(eidx, want.eidx) and Z.rel_l2(out, want.out) < 1e-3
+    finally:
+        m.close()

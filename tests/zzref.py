@@ -805,3 +805,40 @@ def write_gemma_container(path, st, head_dim=64, n_heads=2, flash=None):
         for (l, e), o_ in eoff.items():
             m.write(f"expert {l} {e} {o_}\n")
     return eoff
+
+
+def write_moe_container(path, layers, per_layer):
+    """The expert part of a container directory for MoE layers `layers`: experts.bin
+    ([gate | up | down] records at 4096-aligned offsets, as tools/convert_*.py write
+    them) and a manifest.txt with the model cfg, the record size -- one `esz` line
+    (maple.c:255-258, gemma) or, with per_layer, one `eszl li esz gate down fmt` line
+    per layer with the layer's expert format (lfm25.c:328-331, convert_lfm25.py:490)
+    -- and one `expert li e off` line per record. Returns the offsets."""
+    os.makedirs(path, exist_ok=True)
+    eoff, off = {}, 0
+    with open(os.path.join(path, "experts.bin"), "wb") as f:
+        for li, L_ in enumerate(layers):
+            for e in range(L_.E):
+                pad = (-off) % 4096
+                f.write(b"\0" * pad)
+                off += pad
+                f.write(L_.experts[e * L_.esz:(e + 1) * L_.esz].tobytes())
+                eoff[(li, e)] = off
+                off += L_.esz
+    L0 = layers[0]
+    with open(os.path.join(path, "manifest.txt"), "w") as m:
+        for k, v in dict(hidden=L0.D, n_layers=len(layers), n_experts=L0.E, topk=L0.K,
+                         moe_inter=L0.MI).items():
+            m.write(f"cfg {k} {v}\n")
+        if per_layer:
+            for li, L_ in enumerate(layers):
+                g, _, d = L_.tensor_sizes()
+                m.write(f"eszl {li} {L_.esz} {g} {d} {L_.fmts[0]}\n")
+        else:
+            g, _, d = L0.tensor_sizes()
+            m.write(f"esz {L0.esz} {g} {d}\n")
+        m.write("ndense 0\n")
+        m.write(f"nexpert {len(eoff)}\n")
+        for (li, e), o in eoff.items():
+            m.write(f"expert {li} {e} {o}\n")
+    return eoff

@@ -7,6 +7,7 @@
 // HBM slot tables and per-layer workspaces.
 #include "zz_common.h"
 #include "zz_kernels.h"
+#include "zz_manifest.h"
 #include "../../include/zz_moe.h"
 
 #include <stdarg.h>
@@ -48,12 +49,7 @@ static __device__ __align__(256) unsigned char scratch[ZZ_SCRATCH_BYTES];
 static char *g_scratch[ZZ_MAX_DEVICES];     // scratch's address on device i
 static hipError_t g_scratch_err = hipSuccess;
 
-struct Mapping {
-    const uint8_t *host;
-    size_t n;
-    uint8_t *dev;
-};
-static std::vector<Mapping> g_maps;
+static ZzRanges g_maps;                      // gpu_map's host ranges (zz_manifest.h)
 
 // ----------------------------------------------------------------- gpu.h ABI
 extern "C" int gpu_init(void) {
@@ -89,14 +85,6 @@ extern "C" int gpu_init(void) {
 extern "C" int gpu_ready(void) { return g_ready; }
 extern "C" const char *gpu_name(void) { return g_name; }
 
-static const Mapping *find_map(const void *p, size_t n) {
-    const uint8_t *q = (const uint8_t *)p;
-    for (size_t i = g_maps.size(); i-- > 0;) {
-        const Mapping &m = g_maps[i];
-        if (q >= m.host && q + n <= m.host + m.n) return &m;
-    }
-    return nullptr;
-}
 
 // A range inside an existing mapping is re-uploaded in place (the refresh an
 // engine does after rewriting a mapped buffer). A range that only overlaps older
@@ -104,28 +92,18 @@ static const Mapping *find_map(const void *p, size_t n) {
 // dropped so a lookup can never return bytes from the previous owner.
 extern "C" int gpu_map(const void *p, size_t n) {
     if (!g_ready || !p || !n) ZZ_FAIL("gpu_map: not ready or empty range");
-    const uint8_t *q = (const uint8_t *)p;
-    for (size_t i = g_maps.size(); i-- > 0;) {
-        Mapping &m = g_maps[i];
-        if (q >= m.host && q + n <= m.host + m.n) {
-            ZZ_CHECK(hipMemcpy(m.dev + (q - m.host), p, n, hipMemcpyHostToDevice));
-            return 1;
-        }
+    if (ZzRange *m = g_maps.find(p, n)) {
+        ZZ_CHECK(hipMemcpy(m->dev + ((uintptr_t)p - m->host), p, n, hipMemcpyHostToDevice));
+        return 1;
     }
-    for (size_t i = g_maps.size(); i-- > 0;) {
-        Mapping &m = g_maps[i];
-        if (q < m.host + m.n && m.host < q + n) {
-            (void)hipFree(m.dev);
-            g_maps.erase(g_maps.begin() + i);
-        }
-    }
-    Mapping m{q, n, nullptr};
-    ZZ_CHECK(hipMalloc(&m.dev, n));
-    if (hipMemcpy(m.dev, p, n, hipMemcpyHostToDevice) != hipSuccess) {
-        (void)hipFree(m.dev);
+    g_maps.drop_overlaps(p, n, [](const ZzRange &m) { (void)hipFree(m.dev); });
+    uint8_t *dev = nullptr;
+    ZZ_CHECK(hipMalloc(&dev, n));
+    if (hipMemcpy(dev, p, n, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(dev);
         ZZ_FAIL("gpu_map: upload failed");
     }
-    g_maps.push_back(m);
+    g_maps.add(p, n, dev);
     return 1;
 }
 
@@ -157,9 +135,9 @@ extern "C" int gpu_matmul(int fmt, float *y, const uint8_t *W, const float *x, i
         ZZ_FAIL("gpu_matmul: fmt %d declined", fmt);
     const int grp = fmt == ZZ_FMT_TQ2 || fmt == ZZ_FMT_Q4A ? 64 : 32;
     if (O <= 0 || I <= 0 || S <= 0 || I % grp) ZZ_FAIL("gpu_matmul: bad shape");
-    const Mapping *m = find_map(W, (size_t)fmt_tensor_bytes(fmt, O, I));
+    const ZzRange *m = g_maps.find(W, (size_t)fmt_tensor_bytes(fmt, O, I));
     if (!m) ZZ_FAIL("gpu_matmul: W not inside a gpu_map'd range");
-    const uint8_t *dW = m->dev + (W - m->host);
+    const uint8_t *dW = m->dev + ((uintptr_t)W - m->host);
     if (!grow(&g_mx, &g_mxn, (size_t)S * I) || !grow(&g_my, &g_myn, (size_t)S * O)) return 0;
     ZZ_CHECK(hipMemcpyAsync(g_mx, x, sizeof(float) * (size_t)S * I, hipMemcpyHostToDevice, g_stream));
     if (!zz_launch_matmul_f32(fmt, g_my, dW, g_mx, O, I, S, g_stream)) ZZ_FAIL("gpu_matmul: launch failed");
@@ -898,8 +876,7 @@ extern "C" void gpu_shutdown(void) {
     zz_gemma_shutdown();
     for (Layer *&L : g_layers) { free_layer(L); L = nullptr; }
     g_layers.clear();
-    for (Mapping &m : g_maps) (void)hipFree(m.dev);
-    g_maps.clear();
+    g_maps.clear([](const ZzRange &m) { (void)hipFree(m.dev); });
     if (g_mx) (void)hipFree(g_mx);
     if (g_my) (void)hipFree(g_my);
     g_mx = g_my = nullptr;

@@ -8,6 +8,7 @@
 // f32 vectors) and experts.bin (4096-aligned [gate | up | down] records).
 #include "zz_common.h"
 #include "zz_kernels.h"
+#include "zz_manifest.h"
 #include "../../include/zz_gemma.h"
 
 #include <fcntl.h>
@@ -31,71 +32,13 @@ int zz_stack_adopt(int id, const std::vector<int> &layers, const std::vector<int
 
 namespace {
 
-struct DenseEnt {
-    int64_t off = 0, len = 0;
-    int fmt = 0, O = 0, I = 0;        // fmt: 0 f32, 1 q4_0, 5 i32 (convert_gemma4.py:404)
-};
+using zzm::DenseEnt;
+using zzm::Manifest;
+using zzm::RecSize;
 
-struct RecSize {
-    int64_t esz = 0, gate_b = 0, down_b = 0;
-    int fmt = 0;
-};
-
-struct Manifest {
-    std::map<std::string, std::string> cfg;
-    RecSize all;                                   // `esz` (gemma, maple)
-    std::map<int, RecSize> per_layer;              // `eszl` (lfm)
-    std::map<std::string, DenseEnt> dense;
-    std::map<std::pair<int, int>, int64_t> eoff;   // (layer, expert) -> experts.bin offset
-
-    int geti(const char *k, int dflt = -1) const {
-        auto it = cfg.find(k);
-        return it == cfg.end() ? dflt : atoi(it->second.c_str());
-    }
-    double getf(const char *k, double dflt = 0.0) const {
-        auto it = cfg.find(k);
-        return it == cfg.end() ? dflt : atof(it->second.c_str());
-    }
-    const RecSize *rec(int li) const {
-        auto it = per_layer.find(li);
-        if (it != per_layer.end()) return &it->second;
-        return all.esz > 0 ? &all : nullptr;
-    }
-};
-
-// The line grammar of gemma4.c:270-330 / lfm25.c:290-345.
 int parse_manifest(const std::string &dir, Manifest &m) {
-    const std::string p = dir + "/manifest.txt";
-    FILE *f = fopen(p.c_str(), "r");
-    if (!f) ZZ_FAIL("container: cannot open %s", p.c_str());
-    char line[4096];
-    while (fgets(line, sizeof line, f)) {
-        char k[128], nm[256];
-        long long a, b, c, off, len;
-        int li, e, fmt, O, I;
-        if (sscanf(line, "cfg %127s", k) == 1) {
-            const char *v = line + 4 + strlen(k);
-            while (*v == ' ') v++;
-            std::string val(v);
-            while (!val.empty() && (val.back() == '\n' || val.back() == '\r')) val.pop_back();
-            m.cfg[k] = val;
-        } else if (sscanf(line, "eszl %d %lld %lld %lld %d", &li, &a, &b, &c, &fmt) == 5) {
-            m.per_layer[li] = RecSize{a, b, c, fmt};
-        } else if (sscanf(line, "esz %lld %lld %lld", &a, &b, &c) == 3) {
-            m.all = RecSize{a, b, c, 1};
-        } else if (sscanf(line, "dense %255s %lld %lld %d %d %d", nm, &off, &len, &fmt, &O, &I) == 6) {
-            DenseEnt d;
-            d.off = off;
-            d.len = len;
-            d.fmt = fmt;
-            d.O = O;
-            d.I = I;
-            m.dense[nm] = d;
-        } else if (sscanf(line, "expert %d %d %lld", &li, &e, &off) == 3) {
-            m.eoff[{li, e}] = off;
-        }
-    }
-    fclose(f);
+    std::string err;
+    if (!zzm::parse_manifest(dir + "/manifest.txt", m, err)) ZZ_FAIL("container: %s", err.c_str());
     return 1;
 }
 
@@ -126,6 +69,11 @@ int load_experts(int layer, const std::string &dir, const Manifest &m, int li) {
     if (rs->esz != want)
         ZZ_FAIL("zz_moe_load_experts: container records are %lld bytes, the layer's %lld", (long long)rs->esz,
                 (long long)want);
+    // an eszl layer states its expert format, one for all three tensors (lfm25.c:328-331,
+    // convert_lfm25.py's expert_fmt): the layer must read its records that way
+    if (rs->fmt && (d->fmt_gate != rs->fmt || d->fmt_up != rs->fmt || d->fmt_down != rs->fmt))
+        ZZ_FAIL("zz_moe_load_experts: layer %d's records are format %d, the layer's (%d, %d, %d)", li, rs->fmt,
+                d->fmt_gate, d->fmt_up, d->fmt_down);
     Fd f(dir + "/experts.bin");
     if (f.fd < 0) ZZ_FAIL("zz_moe_load_experts: cannot open %s/experts.bin", dir.c_str());
     std::vector<uint8_t> rec((size_t)rs->esz);
