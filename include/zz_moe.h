@@ -135,8 +135,8 @@ int zz_moe_forward_end(int layer, float *out, int *eidx, float *ewt);
  * their top-k slots (offs[nu+1], rows[S*K], slots[S*K]); logits [S, E]: the
  * router logits, the reference's own float values for the lfm, maple and ling
  * routers at every S, and for gemma (after the bias) when S >= 16 and D % 64 == 0;
- * gemma's other batched logits are interval centres, and its decode path (S <= 4)
- * keeps none. */
+ * gemma's other batched logits are interval centres, and its decode path (S <= 2
+ * with q4_0 / q8_0 experts, S <= 4 with tq2) keeps none. */
 typedef struct zz_moe_dump {
     int8_t *xq; float *xs;
     int8_t *hq; float *hs;

@@ -498,7 +498,15 @@ extern "C" int zz_moe_profile_read(double *ms, int *launches, int n) {
 // One chunk of S <= chunk_tokens tokens: in/out device pointers.
 // decode-sized batches whose hidden rows fit the decode kernels' LDS take the GEMV
 // path; larger ones the matrix cores
-static bool takes_decode(const zz_moe_desc &d, int S) { return S <= g_dec_max_s && zz_dec_fits(S, d.K, d.MI); }
+// The decode kernels read each (token, slot) pair's expert rows, the matrix-core path
+// each distinct expert's once: measured on the MI355X (bench.py layers), decode wins
+// for q4_0 / q8_0 experts up to S = 2 (gemma S=2: 45.9 us against 55.1; S=3: 62.9
+// against 60.0; lfm S=4: 62.1 against 53.7) and for tq2's quarter-size rows up to S = 4
+// (maple S=4: 51.5 against 58.7).
+static bool takes_decode(const zz_moe_desc &d, int S) {
+    const int lim = d.fmt_gate == ZZ_FMT_TQ2 ? ZZ_DEC_MAXS : 2;
+    return S <= g_dec_max_s && S <= lim && zz_dec_fits(S, d.K, d.MI);
+}
 
 // Kernel arguments of one chunk of S <= chunk_tokens rows of layer L.
 struct ChunkArgs {
@@ -605,7 +613,10 @@ int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_
     Layer *L = get_layer(moe_id), *N = get_layer(dense_id);
     if (!L || !N || S <= 0) return -1;
     const zz_moe_desc &d = L->d, &dn = N->d;
-    if (d.gating != ZZ_GATE_SOFTMAX_PES || dn.gating != ZZ_GATE_DENSE || d.D != dn.D || !takes_decode(d, S) ||
+    // the fused block rows keep the decode kernels up to ZZ_DEC_MAXS: they also save
+    // the dense branch its own launches and stream
+    if (d.gating != ZZ_GATE_SOFTMAX_PES || dn.gating != ZZ_GATE_DENSE || d.D != dn.D || S > g_dec_max_s ||
+        !zz_dec_fits(S, d.K, d.MI) ||
         S > chunk_tokens(d) || d.fmt_down != dn.fmt_down || d.fmt_down == ZZ_FMT_TQ2 || dn.fmt_gate == ZZ_FMT_TQ2 ||
         dn.fmt_up == ZZ_FMT_TQ2 || d.fmt_gate == ZZ_FMT_TQ2 || !zz_dec_fits2(S, d.K, d.MI, dn.MI))
         return -1;

@@ -111,13 +111,14 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
 
     // intervals and keys; every load is issued before any is used
     double cv[EPL], bv[EPL];
-    float bi[EPL];
+    float bi[EPL], pv[EPL];
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
         const int e = min(l + 64 * j, E - 1);
         cv[j] = cen[e];
         bv[j] = sig ? 0.0 : bnd[e];
         bi[j] = sig && a.bias ? a.bias[e] : 0.0f;
+        pv[j] = a.gating == ZZ_GATE_SOFTMAX_PES ? a.pes[e] : 1.0f;    // the gate's scale, read now
     }
     double lo[EPL], hi[EPL];
     unsigned long long key[EPL];
@@ -360,11 +361,21 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
     // gate weights: per slot in parallel, their sum serially in slot order as the
     // reference adds them, then each slot's normalisation
     float wj = 0.0f, pj = 1.0f;
-    int ej = 0;
-    if (l < K) {
-        ej = h.idx[l];
-        wj = sig ? zz_sigmoid_score(cen[ej]) : zz_expf(h.topv[l] - h.topv[0]);
-        if (a.gating == ZZ_GATE_SOFTMAX_PES) pj = a.pes[ej];
+    const int ej = l < K ? h.idx[l] : 0;
+    {
+        // slot l's centre and scale from the lane that loaded them
+        const int own = ej & 63, jj = ej >> 6;
+        double cj = 0.0;
+#pragma unroll
+        for (int j = 0; j < EPL; j++) {
+            const double c = __shfl(cv[j], own, 64);
+            const float q = __shfl(pv[j], own, 64);
+            if (jj == j) {
+                cj = c;
+                pj = q;
+            }
+        }
+        if (l < K) wj = sig ? zz_sigmoid_score(cj) : zz_expf(h.topv[l] - h.topv[0]);
     }
     float sum = 0.0f;
     for (int j = 0; j < K; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wj), j));
