@@ -242,11 +242,15 @@ __global__ __launch_bounds__(256, 1) void zz_logits_exact_kernel(ZzLogitArgs a) 
     for (int v = 0; v < NV; v++) woff[v] = min(e0 + lr + RPP * v, a.E - 1) * D + lc;
     const float *R = a.router;
     zz_f4 wv4[NV];                                    // native vectors: kept in VGPRs
-    float xq[NX], xn[NX];
+    // the input of the chunk being summed and of the next one, in two register sets
+    // that swap roles each chunk: a copy from one set to the other would be placed by
+    // the compiler as soon as a register is free, early in the chunk, and wait there
+    // for the next chunk's loads
+    float xa[NX], xb[NX];
 #pragma unroll
     for (int v = 0; v < NV; v++) wv4[v] = *(const zz_f4 *)(R + woff[v]);
 #pragma unroll
-    for (int i = 0; i < NX; i++) xq[i] = xrow[16 * i];
+    for (int i = 0; i < NX; i++) xa[i] = xrow[16 * i];
     // L2 warm-up, issued behind chunk 0's loads: one dword per 64-byte sector of
     // (a) this XCD's share of the workgroup's router rows (workgroups are dealt to the
     // 8 XCDs round-robin, so those with the same blockIdx.x % 8 and blockIdx.y share
@@ -278,7 +282,7 @@ __global__ __launch_bounds__(256, 1) void zz_logits_exact_kernel(ZzLogitArgs a) 
 #pragma unroll
     for (int k = 0; k < (grp ? 8 : 1); k++) acc[k] = 0.0;
     int buf = 0;
-    for (int k0 = 0; k0 < D; k0 += KC) {
+    auto chunk = [&](int k0, const float (&xq)[NX], float (&xn)[NX]) {
         const int k1 = min(k0 + KC, D - KC);        // the last chunk reloads itself
 #pragma unroll
         for (int v = 0; v < NV; v++) wv4[v] = *(const zz_f4 *)(R + (woff[v] + k1));
@@ -325,11 +329,15 @@ __global__ __launch_bounds__(256, 1) void zz_logits_exact_kernel(ZzLogitArgs a) 
         }
 #pragma unroll
         for (int v = 0; v < NV; v++) *(zz_f4 *)&ws_t[buf ^ 1][lr + RPP * v][lc] = wv4[v];
-#pragma unroll
-        for (int i = 0; i < NX; i++) xq[i] = xn[i];
         __syncthreads();
         buf ^= 1;
+    };
+    int k0 = 0;
+    for (; k0 + 2 * KC <= D; k0 += 2 * KC) {
+        chunk(k0, xa, xb);
+        chunk(k0 + KC, xb, xa);
     }
+    if (k0 < D) chunk(k0, xa, xb);
 #pragma unroll
     for (int r = 0; r < 2 * LX_WARM; r++) asm volatile("" ::"v"(warm[r]));
     if (s < a.S && e < a.E) {
