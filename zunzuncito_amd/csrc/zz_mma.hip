@@ -132,12 +132,15 @@ __device__ __forceinline__ void mm_chunk(const MmA &A, int l, float (&acc)[NT][4
         // the 4 rows' d_w as f32 once per block, for every tile: the product d_w * d_x
         // is then a v_mul_f32, which ran the up kernel 3 % faster than the fused
         // mixed-precision form (v_fma_mix_f32) the compiler otherwise picks; the empty
-        // asm keeps it from folding them back together
-        float dwf[4];
+        // asm keeps it from folding them back together. tq2 has no block scale (its
+        // alpha is per row), and no asm: pinned, the constant 1 cost four moves a block.
+        float dwf[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (FMT != ZZ_FMT_TQ2) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            dwf[i] = FMT == ZZ_FMT_TQ2 ? 1.0f : (float)mm_dwh<FULL>(A.s0, A.s1, j, i);
-            asm volatile("" : "+v"(dwf[i]));
+            for (int i = 0; i < 4; i++) {
+                dwf[i] = (float)mm_dwh<FULL>(A.s0, A.s1, j, i);
+                asm volatile("" : "+v"(dwf[i]));
+            }
         }
 #pragma unroll
         for (int t = 0; t < NT; t++) {
