@@ -155,7 +155,7 @@ __global__ __launch_bounds__(256) void zz_logits_kernel(ZzLogitArgs a) {
 //   ling   eight double accumulators by k % 8, combined pairwise (ling.c:722-727).
 // The double product of two floats is exact, so v + (double)w * x rounds once and
 // equals fma((double)w, (double)x, v): the double chains take one fma per element.
-// A workgroup is 4 tokens x 64 experts: wave w holds token s0 + w, lane l expert
+// A workgroup is TT tokens x 64 experts: wave w holds token s0 + w, lane l expert
 // e0 + l. The 64 router rows are staged in LDS in K chunks of KC (256 where D allows,
 // else 64), double buffered, and each lane reads its own row as float4. The token's
 // input is wave-uniform: a chunk sits in KC/16 VGPRs, 16 values each, lane l holding
@@ -166,7 +166,6 @@ __global__ __launch_bounds__(256) void zz_logits_kernel(ZzLogitArgs a) {
 // latency, so KC = 64 (~200 ns of work) left every chunk waiting and KC = 256 does
 // not. The chain is serial per lane, so the VALU time of one wave per SIMD
 // (S * E / 64 waves) is the floor; LDS carries only the router operand.
-#define LX_T 4
 #define LX_E 64
 #define LX_WARM 3      // warm-up sectors per thread and operand
 // lane (l & ~15) + J's value of v, in every lane of its 16-lane row
@@ -222,11 +221,14 @@ __device__ __forceinline__ void zz_prod16(float *p, const zz_f4 *w4, float xq) {
 }
 // CH: the chain kind -- 0 gemma's fp32 chain, 1 one double chain (lfm, maple),
 // 2 ling's eight double accumulators; one instantiation each, so a chain carries only
-// its own registers. KC: the K chunk (D % KC == 0).
-template <int CH, int KC>
-__global__ __launch_bounds__(256, 1) void zz_logits_exact_kernel(ZzLogitArgs a) {
+// its own registers. KC: the K chunk (D % KC == 0). TT: tokens (waves) per workgroup,
+// which share each staged router row: 8 where there are E / 64 >= 4 expert blocks
+// (the grid still fills the chip at S = 512), else 4.
+template <int CH, int KC, int TT>
+__global__ __launch_bounds__(64 * TT, 1) void zz_logits_exact_kernel(ZzLogitArgs a) {
+    constexpr int NT = 64 * TT;                       // threads
     const int tid = threadIdx.x, lane = tid & 63;
-    const int s = blockIdx.x * LX_T + (tid >> 6), e0 = blockIdx.y * LX_E, e = e0 + lane, D = a.D;
+    const int s = blockIdx.x * TT + (tid >> 6), e0 = blockIdx.y * LX_E, e = e0 + lane, D = a.D;
     constexpr bool gem = CH == 0, grp = CH == 2;
     constexpr int NX = KC / 16;                       // input VGPRs per chunk
     const float *X = gem ? a.xn : a.x;
@@ -235,7 +237,7 @@ __global__ __launch_bounds__(256, 1) void zz_logits_exact_kernel(ZzLogitArgs a) 
     const float *xrow = X + (size_t)min(s, a.S - 1) * D + (lane & 15);
     __shared__ float ws_t[2][LX_E][KC + 4];
     // staging: TPR threads per router row, RPP rows per pass, NV passes (rows clamped)
-    constexpr int TPR = KC / 4, RPP = 256 / TPR, NV = LX_E / RPP;
+    constexpr int TPR = KC / 4, RPP = NT / TPR, NV = LX_E / RPP;
     const int lr = tid / TPR, lc = (tid % TPR) * 4;
     int woff[NV];                                     // element offsets into the router
 #pragma unroll
@@ -263,14 +265,14 @@ __global__ __launch_bounds__(256, 1) void zz_logits_exact_kernel(ZzLogitArgs a) 
         const int nr = min(LX_E, a.E - e0), J = ((int)gridDim.x + 7) >> 3, j = blockIdx.x >> 3;
         const long ns = (long)nr * D / 16;
         const float *rb = R + (size_t)e0 * D;
-        const int sx0 = blockIdx.x * LX_T, nx = min(LX_T, a.S - sx0);
+        const int sx0 = blockIdx.x * TT, nx = min(TT, a.S - sx0);
         const float *xb = X + (size_t)sx0 * D;
         const int nsx = nx * D / 16;
 #pragma unroll
         for (int r = 0; r < LX_WARM; r++) {
-            const long sr = j + (long)J * (tid + 256 * r);
+            const long sr = j + (long)J * (tid + NT * r);
             warm[r] = sr < ns ? rb[16 * sr] : 0.0f;
-            const int sx = tid + 256 * r;
+            const int sx = tid + NT * r;
             warm[LX_WARM + r] = sx < nsx ? xb[16 * sx] : 0.0f;
         }
     }
@@ -355,12 +357,17 @@ __global__ __launch_bounds__(256, 1) void zz_logits_exact_kernel(ZzLogitArgs a) 
     }
 }
 
+template <int KC, int TT>
+static void zz_launch_logits_exact_tt(const ZzLogitArgs &b, int S, hipStream_t st) {
+    const dim3 g((S + TT - 1) / TT, (b.E + LX_E - 1) / LX_E), t(64 * TT);
+    if (b.gating == ZZ_GATE_SOFTMAX_PES) hipLaunchKernelGGL((zz_logits_exact_kernel<0, KC, TT>), g, t, 0, st, b);
+    else if (b.gating == ZZ_GATE_GROUPED) hipLaunchKernelGGL((zz_logits_exact_kernel<2, KC, TT>), g, t, 0, st, b);
+    else hipLaunchKernelGGL((zz_logits_exact_kernel<1, KC, TT>), g, t, 0, st, b);
+}
 template <int KC>
 static void zz_launch_logits_exact(const ZzLogitArgs &b, int S, hipStream_t st) {
-    const dim3 g((S + LX_T - 1) / LX_T, (b.E + LX_E - 1) / LX_E);
-    if (b.gating == ZZ_GATE_SOFTMAX_PES) hipLaunchKernelGGL((zz_logits_exact_kernel<0, KC>), g, dim3(256), 0, st, b);
-    else if (b.gating == ZZ_GATE_GROUPED) hipLaunchKernelGGL((zz_logits_exact_kernel<2, KC>), g, dim3(256), 0, st, b);
-    else hipLaunchKernelGGL((zz_logits_exact_kernel<1, KC>), g, dim3(256), 0, st, b);
+    if (b.E >= 4 * LX_E) zz_launch_logits_exact_tt<KC, 8>(b, S, st);
+    else zz_launch_logits_exact_tt<KC, 4>(b, S, st);
 }
 
 // Top-k gating, one wave per token (zz_topk_wave.h), four tokens per workgroup.
