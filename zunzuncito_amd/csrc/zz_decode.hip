@@ -354,7 +354,9 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
 // down. First every (token, slot) pair's q8_0 hidden is staged in LDS. Wave w
 // takes the pairs w, w+8, ... and walks their units (pair,
 // chunk) in order, DD_C units' loads at a time; lane l = 16*qq + r as in the
-// gate/up kernel. A pair's partial dots are summed over the 4 k-quarters when its
+// gate/up kernel. With fewer pairs than waves (LFM's top-4 at S = 1), the 8 / P
+// waves w = p + P*sub of pair p take its chunks sub, sub + 8/P, ... and their
+// partial sums meet in LDS in wave order. A pair's partial dots are summed over the 4 k-quarters when its
 // last unit is done. The 16 x P expert outputs are then combined per token in slot
 // order, out = fma(w_j, y_j, out) as gemma4.c:652.
 #define DD_C 12
@@ -379,11 +381,15 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     const int MI = f.MI, nb = MI / ZZ_BLK, D = f.D, S = a.S, K = a.K, P = S * K;
     const int nch = FMT == ZZ_FMT_TQ2 ? (nb / 2 + 3) / 4 : (nb + 3) / 4;   // units per pair
     const int npw = (P - w + DD_W - 1) / DD_W;                  // this wave's pairs
-    const int U = npw * nch;
+    // split: nw waves per pair; wave w takes pair w % P, chunks w / P + nw * i
+    const int nw = P < DD_W ? DD_W / P : 1, sub = w / P;
+    const bool split = nw > 1, active = w < P * nw;
+    const int U = split ? (active ? (nch - sub + nw - 1) / nw : 0) : npw * nch;
     __shared__ ZzDecPairs pr;
     __shared__ float yv[DEC_MAXS * ZZ_MAXK][16];
     __shared__ float htot[DEC_MAXS * ZZ_MAXK];
     __shared__ float dpart[DD_W][DEC_MAXS][16];                 // fused dense branch, per wave
+    __shared__ float ypart[DD_W][16];                           // split pairs: per wave
     extern __shared__ __attribute__((aligned(16))) char dd_lds[];
     int8_t *sh_q = (int8_t *)dd_lds;                            // [P][MI] by flat pair
     float *sh_s = (float *)(dd_lds + (size_t)P * MI);           // [P][nb]
@@ -420,7 +426,8 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
 #pragma unroll
         for (int i = 0; i < DD_C; i++) {                        // clamped: loads stay in range
             const int u = min(u0 + i, max(U - 1, 0));
-            const int fp = w + DD_W * (u / nch), ch = u % nch;
+            const int fp = split ? w % P : w + DD_W * (u / nch);
+            const int ch = split ? min(sub + nw * u, nch - 1) : u % nch;
             const uint8_t *E = f.experts + (size_t)pr.e[min(fp, P - 1)] * f.estride;
             if (FMT == ZZ_FMT_TQ2) c[i] = ld16(E + zz_tq2off(T, 16 * g + r, min(qq + 4 * ch, nb / 2 - 1)));
             else k[i] = zz_load_chunk<FMT>(E, W, ch);
@@ -433,7 +440,8 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
         for (int i = 0; i < DD_C; i++) {
             const int u = u0 + i;
             if (u >= U) continue;
-            const int fp = w + DD_W * (u / nch), ch = u % nch;
+            const int fp = split ? w % P : w + DD_W * (u / nch);
+            const int ch = split ? sub + nw * u : u % nch;
             if (fp != cur) {                                    // wave-uniform
                 if (cur >= 0) {
                     acc += __shfl_xor(acc, 16, 64);
@@ -509,7 +517,13 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     if (cur >= 0) {
         acc += __shfl_xor(acc, 16, 64);
         acc += __shfl_xor(acc, 32, 64);
-        if (qq == 0) yv[cur][r] = FMT == ZZ_FMT_Q40 ? acc * 0.0625f : acc;   // 16*(q - 8) weights
+        const float y = FMT == ZZ_FMT_Q40 ? acc * 0.0625f : acc;   // 16*(q - 8) weights
+        if (qq == 0) {
+            if (split) ypart[w][r] = y;
+            else yv[cur][r] = y;
+        }
+    } else if (split && qq == 0) {
+        ypart[w][r] = 0.0f;                                     // a pair with fewer chunks than waves
     }
     if (nd) {                                                   // this wave's dense chunks
         float ad[DEC_MAXS] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -543,6 +557,15 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
         }
     }
     __syncthreads();
+    if (split) {                                                // uniform
+        if (tid < P * 16) {                                     // pair p's waves in order
+            const int q = tid >> 4, rr = tid & 15;
+            float v = ypart[q][rr];
+            for (int sb = 1; sb < nw; sb++) v += ypart[q + P * sb][rr];
+            yv[q][rr] = v;
+        }
+        __syncthreads();
+    }
     if (nd && tid < nd * 16) {                                  // dense rows 16g.., waves in order
         const int q = tid >> 4, rr = tid & 15;
         float v = dpart[0][q][rr];
