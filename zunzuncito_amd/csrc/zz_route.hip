@@ -156,18 +156,29 @@ __global__ __launch_bounds__(256) void zz_logits_kernel(ZzLogitArgs a) {
 // The double product of two floats is exact, so v + (double)w * x rounds once and
 // equals fma((double)w, (double)x, v): the double chains take one fma per element.
 // A workgroup is TT tokens x 64 experts: wave w holds token s0 + w, lane l expert
-// e0 + l. The 64 router rows are staged in LDS in K chunks of KC (256 where D allows,
-// else 64), double buffered, and each lane reads its own row as float4. The token's
-// input is wave-uniform: a chunk sits in KC/16 VGPRs, 16 values each, lane l holding
-// element l % 16 (every 16-lane row alike), and element j reaches all lanes by the
-// DPP row broadcast (row_newbcast:j) folded into the multiply. The next chunk's
-// loads (router rows and input) are issued before this chunk is summed and land in
-// LDS after it: a chunk's 2 * KC VALU operations per wave are what hide the L2 / HBM
-// latency, so KC = 64 (~200 ns of work) left every chunk waiting and KC = 256 does
-// not. The chain is serial per lane, so the VALU time of one wave per SIMD
-// (S * E / 64 waves) is the floor; LDS carries only the router operand.
+// e0 + l. The 64 router rows are loaded from L2 straight into LDS in K chunks of KC
+// (256 where D allows, else 64), double buffered, and each lane reads its own row as
+// float4. The token's input is wave-uniform: a chunk sits in KC/16 VGPRs, 16 values
+// each, lane l holding element l % 16 (every 16-lane row alike), and element j
+// reaches all lanes by the DPP row broadcast (row_newbcast:j) folded into the
+// multiply. The next chunk's loads (router rows and input) are issued before this
+// chunk is summed and waited for after it: a chunk's 2 * KC VALU operations per wave
+// are what hide the L2 / HBM latency, so KC = 64 (~200 ns of work) left every chunk
+// waiting and KC = 256 does not. The chain is serial per lane, so the VALU time of
+// one wave per SIMD (S * E / 64 waves) is the floor; LDS carries only the router
+// operand.
 #define LX_E 64
 #define LX_WARM 3      // warm-up sectors per thread and operand
+#define ZZ_WAIT_VM0 0x0F70   // s_waitcnt vmcnt(0), expcnt and lgkmcnt untouched (gfx9 fields)
+// one wave moves 64 * B bytes from global memory to LDS: lane l's B bytes at g go to
+// l_base + l * B (l_base wave-uniform); completion is counted by vmcnt
+template <int B>
+__device__ __forceinline__ void zz_load_lds(const float *g, float *l_base) {
+    static_assert(B == 4 || B == 16, "4 or 16 bytes per lane");
+    auto *l = (__attribute__((address_space(3))) void *)l_base;
+    if constexpr (B == 16) __builtin_amdgcn_global_load_lds((const void *)g, l, 16, 0, 0);
+    else __builtin_amdgcn_global_load_lds((const void *)g, l, 4, 0, 0);
+}
 // lane (l & ~15) + J's value of v, in every lane of its 16-lane row
 template <int J>
 __device__ __forceinline__ float zz_row_bcast(float v) {
@@ -235,22 +246,29 @@ __global__ __launch_bounds__(64 * TT, 1) void zz_logits_exact_kernel(ZzLogitArgs
     // this lane's elements of the wave's input row (rows past the end read the last
     // row; not stored)
     const float *xrow = X + (size_t)min(s, a.S - 1) * D + (lane & 15);
-    __shared__ float ws_t[2][LX_E][KC + 4];
-    // staging: TPR threads per router row, RPP rows per pass, NV passes (rows clamped)
-    constexpr int TPR = KC / 4, RPP = NT / TPR, NV = LX_E / RPP;
-    const int lr = tid / TPR, lc = (tid % TPR) * 4;
-    int woff[NV];                                     // element offsets into the router
-#pragma unroll
-    for (int v = 0; v < NV; v++) woff[v] = min(e0 + lr + RPP * v, a.E - 1) * D + lc;
+    __shared__ __attribute__((aligned(16))) float ws_t[2][LX_E][KC + 4];
+    // staging: wave w moves rows w, w + TT, ... of a chunk from L2 straight into LDS
+    // (global_load_lds: lane l's KC/64 floats land at the row start + l * KC/16 bytes),
+    // one row per instruction; rows past E repeat the last. Staged through registers,
+    // each row would cost a VGPR load and an LDS write per lane, and the chunk's
+    // register writes and LDS writes ran 1.7-1.9 us (of 34) slower at Gemma's S = 512.
+    constexpr int RPW = LX_E / TT;
     const float *R = a.router;
-    zz_f4 wv4[NV];                                    // native vectors: kept in VGPRs
+    const float *drow[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++)
+        drow[i] = R + (size_t)min(e0 + (tid >> 6) + TT * i, a.E - 1) * D + (KC / 64) * lane;
+    auto stage = [&](int b, int k) {
+#pragma unroll
+        for (int i = 0; i < RPW; i++)
+            zz_load_lds<KC / 16>(drow[i] + k, &ws_t[b][(tid >> 6) + TT * i][0]);
+    };
     // the input of the chunk being summed and of the next one, in two register sets
     // that swap roles each chunk: a copy from one set to the other would be placed by
     // the compiler as soon as a register is free, early in the chunk, and wait there
     // for the next chunk's loads
     float xa[NX], xb[NX];
-#pragma unroll
-    for (int v = 0; v < NV; v++) wv4[v] = *(const zz_f4 *)(R + woff[v]);
+    stage(0, 0);
 #pragma unroll
     for (int i = 0; i < NX; i++) xa[i] = xrow[16 * i];
     // L2 warm-up, issued behind chunk 0's loads: one dword per 64-byte sector of
@@ -276,8 +294,7 @@ __global__ __launch_bounds__(64 * TT, 1) void zz_logits_exact_kernel(ZzLogitArgs
             warm[LX_WARM + r] = sx < nsx ? xb[16 * sx] : 0.0f;
         }
     }
-#pragma unroll
-    for (int v = 0; v < NV; v++) *(zz_f4 *)&ws_t[0][lr + RPP * v][lc] = wv4[v];
+    __builtin_amdgcn_s_waitcnt(ZZ_WAIT_VM0);           // the staged rows have landed
     __syncthreads();
     float vf = 0.0f;
     double acc[grp ? 8 : 1];                          // grouped: ling.c's 8 accumulators
@@ -286,12 +303,11 @@ __global__ __launch_bounds__(64 * TT, 1) void zz_logits_exact_kernel(ZzLogitArgs
     int buf = 0;
     auto chunk = [&](int k0, const float (&xq)[NX], float (&xn)[NX]) {
         const int k1 = min(k0 + KC, D - KC);        // the last chunk reloads itself
-#pragma unroll
-        for (int v = 0; v < NV; v++) wv4[v] = *(const zz_f4 *)(R + (woff[v] + k1));
+        stage(buf ^ 1, k1);                          // free: every wave is past its reads
 #pragma unroll
         for (int i = 0; i < NX; i++) xn[i] = xrow[k1 + 16 * i];
-        // keep those loads here, a whole chunk ahead of their LDS writes (the
-        // scheduler would otherwise sink each to just before its write, and wait)
+        // keep those loads here, a whole chunk ahead of their use (the scheduler
+        // would otherwise sink each to just before it, and wait)
         __builtin_amdgcn_sched_barrier(0);
         const float *wr = ws_t[buf][lane];
         if constexpr (gem) {
@@ -329,8 +345,7 @@ __global__ __launch_bounds__(64 * TT, 1) void zz_logits_exact_kernel(ZzLogitArgs
                 zz_chain16<CH>(vf, acc, w4, xq[i]);
             }
         }
-#pragma unroll
-        for (int v = 0; v < NV; v++) *(zz_f4 *)&ws_t[buf ^ 1][lr + RPP * v][lc] = wv4[v];
+        __builtin_amdgcn_s_waitcnt(ZZ_WAIT_VM0);
         __syncthreads();
         buf ^= 1;
     };
