@@ -34,7 +34,9 @@ static constexpr uint64_t zz_exp2_tab32[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-__host__ __device__ inline float zz_expf(float x) {
+// TAB: the table's entry i (the table itself, or a copy of it nearer the caller)
+template <typename TAB>
+__host__ __device__ inline float zz_expf_tab(float x, TAB tab) {
     const uint32_t ux = __builtin_bit_cast(uint32_t, x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
     if (abstop >= 0x42bu) {                       // |x| >= 88 (the top 12 bits of 88.0f), or NaN
@@ -53,7 +55,7 @@ __host__ __device__ inline float zz_expf(float x) {
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd -= shift;
     const double r = fma(n_ln2, xd, -kd);
-    const uint64_t t = zz_exp2_tab32[ki % 32] + (ki << 47);
+    const uint64_t t = tab((int)(ki % 32)) + (ki << 47);
     const double s = __builtin_bit_cast(double, t);
     const double z = fma(c0, r, c1);
     const double r2 = r * r;
@@ -61,4 +63,8 @@ __host__ __device__ inline float zz_expf(float x) {
     y = fma(z, r2, y);
     y = y * s;
     return (float)y;
+}
+
+__host__ __device__ inline float zz_expf(float x) {
+    return zz_expf_tab(x, [](int i) { return zz_exp2_tab32[i]; });
 }

@@ -25,6 +25,7 @@
 #include "zz_route_dev.h"
 
 struct ZzTopkWaveHdr {
+    unsigned long long etab[32];    // expf's table (zz_exp2_tab32), staged with the inputs
     unsigned long long lmax[64];
     unsigned long long lk;
     int idx[ZZ_MAXK];           // the result: expert of each slot
@@ -74,11 +75,17 @@ __device__ __forceinline__ unsigned long long zz_lane_lt_mask() {
     return l ? (~0ull >> (64 - l)) : 0ull;
 }
 
+// expf with the wave's LDS copy of the table: read from device memory at the point
+// of use, the table cost a memory round trip in the middle of every top-k
+__device__ __forceinline__ float zz_expf_lds(float x, const unsigned long long *etab) {
+    return zz_expf_tab(x, [etab](int i) { return (uint64_t)etab[i]; });
+}
+
 // sigmoid score of an exact float logit, as lfm25.c:654 / ling.c:731 form it:
 // 1.0f / (1.0f + expf(-v)), bit for bit
-__device__ __forceinline__ float zz_sigmoid_score(double logit) {
+__device__ __forceinline__ float zz_sigmoid_score(double logit, const unsigned long long *etab) {
     const float v = (float)logit;
-    return 1.0f / (1.0f + zz_expf(-v));
+    return 1.0f / (1.0f + zz_expf_lds(-v, etab));
 }
 
 // The reference's gemma logit of expert e for router input xn: in-order fp32 sum
@@ -109,7 +116,9 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
     const bool sig = a.gating == ZZ_GATE_SIGMOID_BIAS || a.gating == ZZ_GATE_GROUPED;
     const unsigned long long ltm = zz_lane_lt_mask();
 
-    // intervals and keys; every load is issued before any is used
+    // intervals and keys; every load is issued before any is used (the expf table
+    // too: lane l moves its 32-bit word to the header's copy)
+    const unsigned tabw = ((const unsigned *)zz_exp2_tab32)[l];
     double cv[EPL], bv[EPL];
     float bi[EPL], pv[EPL];
 #pragma unroll
@@ -120,6 +129,8 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
         bi[j] = sig && a.bias ? a.bias[e] : 0.0f;
         pv[j] = a.gating == ZZ_GATE_SOFTMAX_PES ? a.pes[e] : 1.0f;    // the gate's scale, read now
     }
+    ((unsigned *)h.etab)[l] = tabw;
+    zz_wave_sync_lds();
     double lo[EPL], hi[EPL];
     unsigned long long key[EPL];
     int width = 0;
@@ -128,7 +139,7 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
         const int e = l + 64 * j;
         if (sig) {
             // the reference's selection score s + bias, exactly (lfm25.c:654-655)
-            const float sg = zz_sigmoid_score(cv[j]);
+            const float sg = zz_sigmoid_score(cv[j], h.etab);
             const float sel = a.bias ? sg + bi[j] : sg;
             lo[j] = hi[j] = (double)sel;
         } else {
@@ -375,7 +386,7 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
                 pj = q;
             }
         }
-        if (l < K) wj = sig ? zz_sigmoid_score(cj) : zz_expf(h.topv[l] - h.topv[0]);
+        if (l < K) wj = sig ? zz_sigmoid_score(cj, h.etab) : zz_expf_lds(h.topv[l] - h.topv[0], h.etab);
     }
     float sum = 0.0f;
     for (int j = 0; j < K; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wj), j));
