@@ -400,41 +400,63 @@ __global__ __launch_bounds__(256) void zz_topk_kernel(ZzTopkArgs a, int S) {
 // exactly rows[] of gemma4.c:779-786, ascending tokens. The smallest pair index
 // of each expert orders the union as first-seen (gemma4.c:756-761). Also emits
 // the FFN work list: per expert in union order, chunks of at most `tch` pairs.
-// exclusive prefix sum over the threads of a workgroup (up to 1024): a shuffle scan per wave,
-// then the wave totals (two barriers)
-__device__ __forceinline__ int zz_block_excl_scan(int v, int *tmp) {
-    const int t = threadIdx.x, l = t & 63, w = t >> 6;
-    int x = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int n = __shfl_up(x, off, 64);
-        if (l >= off) x += n;
+// inclusive prefix sum over a wave by DPP: shifts within each 16-lane row by 1, 2,
+// 4, 8 (lanes shifted in from outside the row add 0), then the rows' running totals
+// (row_bcast:15 adds row 0's total to row 1 and row 2's to row 3, row_bcast:31 the
+// total of rows 0-1 to rows 2 and 3). 32 or 64 bits (64: both halves move, one add).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ unsigned zz_dpp_u32(unsigned v) {
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, false);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ unsigned long long zz_dpp_u64(unsigned long long v) {
+    return ((unsigned long long)zz_dpp_u32<CTRL, ROWS>((unsigned)(v >> 32)) << 32) | zz_dpp_u32<CTRL, ROWS>((unsigned)v);
+}
+template <typename T>
+__device__ __forceinline__ T zz_wave_incl_scan(T x) {
+    if constexpr (sizeof(T) == 8) {
+        x += zz_dpp_u64<0x111, 0xF>(x);
+        x += zz_dpp_u64<0x112, 0xF>(x);
+        x += zz_dpp_u64<0x114, 0xF>(x);
+        x += zz_dpp_u64<0x118, 0xF>(x);
+        x += zz_dpp_u64<0x142, 0xA>(x);
+        x += zz_dpp_u64<0x143, 0xC>(x);
+    } else {
+        x += zz_dpp_u32<0x111, 0xF>(x);
+        x += zz_dpp_u32<0x112, 0xF>(x);
+        x += zz_dpp_u32<0x114, 0xF>(x);
+        x += zz_dpp_u32<0x118, 0xF>(x);
+        x += zz_dpp_u32<0x142, 0xA>(x);
+        x += zz_dpp_u32<0x143, 0xC>(x);
     }
+    return x;
+}
+
+// exclusive prefix sum over the threads of a workgroup (up to 1024; tmp: 16 entries
+// of LDS): the wave scans, then each thread adds the totals of the waves before its
+// own, all 15 read at once (a loop over them, one read after another, cost the last
+// wave ~0.5 us per scan). Two barriers.
+template <typename T>
+__device__ __forceinline__ T zz_block_excl_scan_t(T v, T *tmp) {
+    const int t = threadIdx.x, l = t & 63, w = t >> 6;
+    const T x = zz_wave_incl_scan(v);
     if (l == 63) tmp[w] = x;
     __syncthreads();
-    int base = 0;
-    for (int q = 0; q < w; q++) base += tmp[q];
+    T base = 0;
+#pragma unroll
+    for (int q = 0; q < 15; q++) base += q < w ? tmp[q] : (T)0;
     __syncthreads();                           // tmp is free again for the next scan
     return base + x - v;
+}
+__device__ __forceinline__ int zz_block_excl_scan(int v, int *tmp) {
+    return (int)zz_block_excl_scan_t<unsigned>((unsigned)v, (unsigned *)tmp);
 }
 
 __device__ __forceinline__ unsigned zz_uni(unsigned v) { return (unsigned)__builtin_amdgcn_readfirstlane((int)v); }
 
 // exclusive prefix sum of a 64-bit value over the workgroup (tmp: 16 entries of LDS)
 __device__ __forceinline__ unsigned long long zz_block_excl_scan64(unsigned long long v, unsigned long long *tmp) {
-    const int t = threadIdx.x, l = t & 63, w = t >> 6;
-    unsigned long long x = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const unsigned long long n = __shfl_up(x, off, 64);
-        if (l >= off) x += n;
-    }
-    if (l == 63) tmp[w] = x;
-    __syncthreads();
-    unsigned long long base = 0;
-    for (int q = 0; q < w; q++) base += tmp[q];
-    __syncthreads();
-    return base + x - v;
+    return zz_block_excl_scan_t<unsigned long long>(v, tmp);
 }
 
 #define DP_T 1024                     // threads
