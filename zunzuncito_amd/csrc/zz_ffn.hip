@@ -102,6 +102,68 @@ __global__ __launch_bounds__(256) void zz_combine_kernel(ZzCombineArgs a) {
     }
 }
 
+// The same combine for K <= 8 and D <= 1024 * NO with every load issued first: the
+// token's positions and weights, its 8 rows' values for all NO column slots of the
+// thread, the post-norm weights. The loop above waits out one memory round trip per
+// column slot; this one waits once (same sums, same order).
+template <int NO>
+__global__ __launch_bounds__(256) void zz_combine_fast_kernel(ZzCombineArgs a) {
+    const int s = blockIdx.x, D = a.D, K = a.K, t = threadIdx.x;
+    __shared__ double red[4];
+    int pos[8];
+    float wt[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {                // slots past K repeat the last (unused)
+        const int jj = min(j, K - 1);
+        pos[j] = a.ppos[(size_t)s * K + jj];
+        wt[j] = a.ewt[(size_t)s * K + jj];
+    }
+    float4 y[NO][8], pl[NO];
+#pragma unroll
+    for (int i = 0; i < NO; i++) {
+        const int o = min(4 * t + 1024 * i, D - 4);
+#pragma unroll
+        for (int j = 0; j < 8; j++) y[i][j] = *(const float4 *)(a.y + (size_t)pos[j] * D + o);
+        if (a.gemma) pl[i] = *(const float4 *)(a.post_ln + o);
+    }
+    float4 v[NO];
+    double ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < NO; i++) {
+        v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (j < K) {
+                v[i].x = fmaf(wt[j], y[i][j].x, v[i].x);
+                v[i].y = fmaf(wt[j], y[i][j].y, v[i].y);
+                v[i].z = fmaf(wt[j], y[i][j].z, v[i].z);
+                v[i].w = fmaf(wt[j], y[i][j].w, v[i].w);
+            }
+        }
+        if (4 * t + 1024 * i < D)
+            ss += (double)v[i].x * v[i].x + (double)v[i].y * v[i].y + (double)v[i].z * v[i].z +
+                  (double)v[i].w * v[i].w;
+    }
+    float r = 1.0f;
+    if (a.gemma) {
+        ss = zz_wave_sum(ss);
+        if ((t & 63) == 0) red[t >> 6] = ss;
+        __syncthreads();
+        const double tot = red[0] + red[1] + red[2] + red[3];
+        r = 1.0f / sqrtf((float)(tot / D) + a.eps);
+    }
+#pragma unroll
+    for (int i = 0; i < NO; i++) {
+        const int o = 4 * t + 1024 * i;
+        if (o < D) {
+            float4 u = v[i];
+            if (a.gemma)
+                u = make_float4((u.x * r) * pl[i].x, (u.y * r) * pl[i].y, (u.z * r) * pl[i].z, (u.w * r) * pl[i].w);
+            *(float4 *)(a.out + (size_t)s * D + o) = u;
+        }
+    }
+}
+
 // ------------------------------------------------------------------ debug dots
 // Exact int32 dot of one (row, block) against xq: q4_0 sum (q-8)*x, q8_0 sum q*x,
 // tq2 sum (c-1)*x, read from the slot table in its lane order.
@@ -142,7 +204,12 @@ int zz_launch_repack_n(const ZzRepackArgs &a, int n, hipStream_t st) {
 }
 
 int zz_launch_combine(const ZzCombineArgs &a, int S, hipStream_t st) {
-    hipLaunchKernelGGL(zz_combine_kernel, dim3(S), dim3(256), 0, st, a);
+    const int no = (a.D + 1023) / 1024;
+    if (a.K <= 8 && no <= 1) hipLaunchKernelGGL(zz_combine_fast_kernel<1>, dim3(S), dim3(256), 0, st, a);
+    else if (a.K <= 8 && no <= 2) hipLaunchKernelGGL(zz_combine_fast_kernel<2>, dim3(S), dim3(256), 0, st, a);
+    else if (a.K <= 8 && no <= 3) hipLaunchKernelGGL(zz_combine_fast_kernel<3>, dim3(S), dim3(256), 0, st, a);
+    else if (a.K <= 8 && no <= 4) hipLaunchKernelGGL(zz_combine_fast_kernel<4>, dim3(S), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(zz_combine_kernel, dim3(S), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess;
 }
 

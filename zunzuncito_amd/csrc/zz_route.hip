@@ -563,10 +563,11 @@ __global__ __launch_bounds__(DP_T) void zz_dispatch_kernel(ZzDispatchArgs a) {
         // each expert's rank within its batch (cost descending, then union order); the
         // batch's experts listed by rank, with their costs
         if (t < nu) {
-            const int b0 = t & ~7, b1 = min(b0 + 8, nu), my = xcost[t];
+            const int b0 = t & ~7, my = xcost[t];
             int rk = 0;
-            for (int j = b0; j < b1; j++) {
-                const int cj = xcost[j];
+#pragma unroll
+            for (int j = b0; j < b0 + 8; j++) {         // all 8 reads at once
+                const int cj = j < nu ? xcost[j] : -1;
                 rk += (cj > my) | ((cj == my) & (j < t));
             }
             xrank[b0 + rk] = t;
