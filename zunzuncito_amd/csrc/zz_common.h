@@ -163,26 +163,116 @@ __device__ __forceinline__ int zz_dot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);   // v_dot4_i32_i8
 }
 
-template <typename T>
-__device__ __forceinline__ T zz_wave_sum(T v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Cross-lane reductions without the LDS crossbar (a shuffle is a ds_bpermute, one
+// LDS round trip per step). Within a row of 16 lanes, DPP: quad_perm [1,0,3,2] and
+// [2,3,0,1] pair lane i with i ^ 1 and i ^ 2, row_half_mirror lane i of each 8 with
+// 7 - i, row_mirror lane i of the row with 15 - i. Across rows, gfx950's permlane
+// swaps with both operands v: lanes i and i ^ 16 (W = 16) or i ^ 32 (W = 32) both
+// receive (v of the lower lane, v of the upper lane).
+template <int CTRL>
+__device__ __forceinline__ unsigned zz_dpp_b32(unsigned v) {
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL, typename T>
+__device__ __forceinline__ T zz_dpp_x(T v) {
+    if constexpr (sizeof(T) == 8) {
+        const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+        return __builtin_bit_cast(T, ((unsigned long long)zz_dpp_b32<CTRL>((unsigned)(u >> 32)) << 32) |
+                                         zz_dpp_b32<CTRL>((unsigned)u));
+    } else {
+        return __builtin_bit_cast(T, zz_dpp_b32<CTRL>(__builtin_bit_cast(unsigned, v)));
+    }
+}
+template <int W>
+__device__ __forceinline__ void zz_swap_b32(unsigned v, unsigned &lo, unsigned &hi) {
+    if constexpr (W == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        lo = r[0];
+        hi = r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        lo = r[0];
+        hi = r[1];
+    }
+}
+template <int W, typename T>
+__device__ __forceinline__ void zz_swap_x(T v, T &lo, T &hi) {
+    if constexpr (sizeof(T) == 8) {
+        const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+        unsigned l0, h0, l1, h1;
+        zz_swap_b32<W>((unsigned)u, l0, h0);
+        zz_swap_b32<W>((unsigned)(u >> 32), l1, h1);
+        lo = __builtin_bit_cast(T, ((unsigned long long)l1 << 32) | l0);
+        hi = __builtin_bit_cast(T, ((unsigned long long)h1 << 32) | h0);
+    } else {
+        unsigned l, h;
+        zz_swap_b32<W>(__builtin_bit_cast(unsigned, v), l, h);
+        lo = __builtin_bit_cast(T, l);
+        hi = __builtin_bit_cast(T, h);
+    }
+}
+// v combined by op over aligned groups of N lanes (N a power of 2, 2..64); every lane
+// of a group gets the same result (each step combines two values, a op b == b op a
+// for the commutative ops used: IEEE add, fmaxf, integer add). Every lane of the
+// wave must take part.
+template <int N, typename T, typename OP>
+__device__ __forceinline__ T zz_group_reduce(T v, OP op) {
+    static_assert(N == 2 || N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "group of 2..64 lanes");
+    if constexpr (N >= 2) v = op(v, zz_dpp_x<0xB1>(v));
+    if constexpr (N >= 4) v = op(v, zz_dpp_x<0x4E>(v));
+    if constexpr (N >= 8) v = op(v, zz_dpp_x<0x141>(v));
+    if constexpr (N >= 16) v = op(v, zz_dpp_x<0x140>(v));
+    if constexpr (N >= 32) {
+        T a, b;
+        zz_swap_x<16>(v, a, b);
+        v = op(a, b);
+    }
+    if constexpr (N >= 64) {
+        T a, b;
+        zz_swap_x<32>(v, a, b);
+        v = op(a, b);
+    }
     return v;
+}
+template <int N, typename T>
+__device__ __forceinline__ T zz_group_sum(T v) {
+    return zz_group_reduce<N>(v, [](T x, T y) { return x + y; });
+}
+template <int N>
+__device__ __forceinline__ float zz_group_max(float v) {
+    return zz_group_reduce<N>(v, [](float x, float y) { return fmaxf(x, y); });
 }
 
-__device__ __forceinline__ float zz_wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+// v combined over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the same position in the
+// wave's four rows); every one of the four gets the result
+template <typename T, typename OP>
+__device__ __forceinline__ T zz_rows_reduce(T v, OP op) {
+    T a, b;
+    zz_swap_x<16>(v, a, b);
+    v = op(a, b);
+    zz_swap_x<32>(v, a, b);
+    return op(a, b);
 }
+template <typename T>
+__device__ __forceinline__ T zz_rows_sum(T v) {
+    return zz_rows_reduce(v, [](T x, T y) { return x + y; });
+}
+__device__ __forceinline__ float zz_rows_max(float v) {
+    return zz_rows_reduce(v, [](float x, float y) { return fmaxf(x, y); });
+}
+
+template <typename T>
+__device__ __forceinline__ T zz_wave_sum(T v) {
+    return zz_group_sum<64>(v);
+}
+
+__device__ __forceinline__ float zz_wave_max(float v) { return zz_group_max<64>(v); }
 
 // q40.h:124-138 activation quantisation of one 32-value block held one value per
 // lane of a 32-lane group (lanes 0..31 or 32..63 of a wave). d = amax/127 (IEEE
 // division), q = rint(v * (1/d)) clamped to +-127. Bit-exact with the reference.
 __device__ __forceinline__ int zz_quant_lane(float v, float *d_out) {
-    float a = fabsf(v);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+    const float a = zz_group_max<32>(fabsf(v));
     float d = a / 127.0f;
     float id = d != 0.0f ? 1.0f / d : 0.0f;
     float q = rintf(v * id);
@@ -219,19 +309,13 @@ __device__ __forceinline__ float zz_quant_block(const float (&v)[ZZ_BLK], int8_t
 // lane's 4 codes packed; d and the block's code sum go to every lane of the 8.
 // Every lane of the wave must call it.
 __device__ __forceinline__ unsigned zz_quant8(float4 v, float *d_out, int *sum_out) {
-    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    m = fmaxf(m, __shfl_xor(m, 1, 64));
-    m = fmaxf(m, __shfl_xor(m, 2, 64));
-    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    const float m = zz_group_max<8>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     const float d = m / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
     const int q0 = (int)fminf(fmaxf(rintf(v.x * id), -127.0f), 127.0f);
     const int q1 = (int)fminf(fmaxf(rintf(v.y * id), -127.0f), 127.0f);
     const int q2 = (int)fminf(fmaxf(rintf(v.z * id), -127.0f), 127.0f);
     const int q3 = (int)fminf(fmaxf(rintf(v.w * id), -127.0f), 127.0f);
-    int qs = q0 + q1 + q2 + q3;
-    qs += __shfl_xor(qs, 1, 64);
-    qs += __shfl_xor(qs, 2, 64);
-    qs += __shfl_xor(qs, 4, 64);
+    const int qs = zz_group_sum<8>(q0 + q1 + q2 + q3);
     *d_out = d;
     *sum_out = qs;
     return (unsigned)(q0 & 0xff) | (unsigned)(q1 & 0xff) << 8 | (unsigned)(q2 & 0xff) << 16 |

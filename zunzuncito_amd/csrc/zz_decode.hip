@@ -313,8 +313,7 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
     if (T.fmt == ZZ_FMT_Q40) acc = zz_dec_up_part<ZZ_FMT_Q40>(f, sr, st, E, T, g, h, l);
     else if (T.fmt == ZZ_FMT_Q80) acc = zz_dec_up_part<ZZ_FMT_Q80>(f, sr, st, E, T, g, h, l);
     else acc = zz_dec_up_part<ZZ_FMT_TQ2>(f, sr, st, E, T, g, h, l);
-    acc += __shfl_xor(acc, 16, 64);                             // sum over the 4 k-quarters
-    acc += __shfl_xor(acc, 32, 64);
+    acc = zz_rows_sum(acc);                                     // sum over the 4 k-quarters
     if (l < 16) part[h][q][l] = acc;
     if (T.fmt == ZZ_FMT_TQ2 && tid == 0) {          // tq2.h:101-106, serial
         const int nb = f.D / ZZ_BLK;
@@ -444,8 +443,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
             const int ch = split ? sub + nw * u : u % nch;
             if (fp != cur) {                                    // wave-uniform
                 if (cur >= 0) {
-                    acc += __shfl_xor(acc, 16, 64);
-                    acc += __shfl_xor(acc, 32, 64);
+                    acc = zz_rows_sum(acc);
                     if (qq == 0) yv[cur][r] = FMT == ZZ_FMT_Q40 ? acc * 0.0625f : acc;
                 }
                 cur = fp;
@@ -515,8 +513,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
         comp_units(u0);
     }
     if (cur >= 0) {
-        acc += __shfl_xor(acc, 16, 64);
-        acc += __shfl_xor(acc, 32, 64);
+        acc = zz_rows_sum(acc);
         const float y = FMT == ZZ_FMT_Q40 ? acc * 0.0625f : acc;   // 16*(q - 8) weights
         if (qq == 0) {
             if (split) ypart[w][r] = y;
@@ -551,8 +548,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
 #pragma unroll
         for (int q = 0; q < DEC_MAXS; q++) {
             float v = ad[q];
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
+            v = zz_rows_sum(v);
             if (qq == 0 && q < nd) dpart[w][q][r] = v;
         }
     }
@@ -574,8 +570,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
         if (FMT == ZZ_FMT_Q40) v *= 0.0625f;
         a.yd[(size_t)q * D + g * 16 + rr] = v;
         double t = (double)v * (double)v;
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1) t += __shfl_xor(t, m, 64);
+        t = zz_group_sum<16>(t);
         if (rr == 0) a.ssd[(size_t)q * gridDim.x + g] = t;
     }
     if (tid < S * 16) {
@@ -593,8 +588,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
         a.out[(size_t)s * D + o] = v;
         if (a.ss) {                               // this tile's sum of squares, for the post-norm
             double q = (double)v * (double)v;
-#pragma unroll
-            for (int m = 1; m < 16; m <<= 1) q += __shfl_xor(q, m, 64);
+            q = zz_group_sum<16>(q);
             if (rr == 0) a.ss[(size_t)s * gridDim.x + g] = q;
         }
     }
@@ -613,8 +607,7 @@ __global__ __launch_bounds__(256) void zz_dec_norm_kernel(float *out, const floa
     if (tid < 64) {
         double q = 0.0;
         for (int k = tid; k < G; k += 64) q += ss[(size_t)s * G + k];
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+        q = zz_group_sum<64>(q);
         if (tid == 0) rn = 1.0f / sqrtf((float)(q / D) + eps);
     }
     __syncthreads();
@@ -682,8 +675,7 @@ __global__ __launch_bounds__(256) void zz_dec_final_kernel(ZzDecFinalArgs a) {
         const double *ss = (which ? a.ssd : a.ss) + (size_t)s * G;
         double q = 0.0;
         for (int k = l; k < G; k += 64) q += ss[k];
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+        q = zz_group_sum<64>(q);
         if (l == 0) rn[which] = 1.0f / sqrtf((float)(q / D) + a.eps);
     }
     __syncthreads();

@@ -138,8 +138,7 @@ __global__ __launch_bounds__(256) void zz_head_kernel(const uint8_t *tb, ZzTenso
     for (int s = 0; s < ZZ_DEC_MAXS; s++) {
         if (s >= S) break;
         float v = acc[s];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
+        v = zz_rows_sum(v);
         v *= 0.0625f;                                    // the 16*(q - 8) weights
         if (cap > 0.0f) v = tanhf(v / cap) * cap;
         if (qq == 0) logits[(size_t)s * V + o] = v;

@@ -508,8 +508,7 @@ __device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &ite
                 acc[t][i] = h;
                 m = fmaxf(m, fabsf(h));
             }
-            m = fmaxf(m, __shfl_xor(m, 16, 64));
-            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            m = zz_rows_max(m);
             amx[t] = m;
             if (qq == 0) sm.e.amax[w][16 * t + l] = m;
         }
@@ -532,8 +531,7 @@ __device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &ite
                 s += qi;
                 pk |= (unsigned)(qi & 0xff) << (8 * i);
             }
-            s += __shfl_xor(s, 16, 64);
-            s += __shfl_xor(s, 32, 64);
+            s = zz_rows_sum(s);
             if (qq == 0) sm.e.qsum[w][tk] = s;
             if (tk < n) {
                 const size_t p = (size_t)item.p0 + tk;
