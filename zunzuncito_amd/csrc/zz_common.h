@@ -4,6 +4,7 @@
 // every fused multiply-add is written as fmaf(), so bit-level behaviour is
 // explicit wherever it matters (activation quantisation, router logits).
 #pragma once
+#include <type_traits>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stddef.h>
@@ -259,6 +260,41 @@ __device__ __forceinline__ T zz_rows_sum(T v) {
 }
 __device__ __forceinline__ float zz_rows_max(float v) {
     return zz_rows_reduce(v, [](float x, float y) { return fmaxf(x, y); });
+}
+
+// inclusive prefix sum over a wave: DPP shifts within each 16-lane row by 1, 2, 4,
+// 8 (lanes shifted in from outside the row add zero), then row_bcast:15 adds row 0's
+// total to row 1 and row 2's to row 3, row_bcast:31 the total of rows 0-1 to rows 2
+// and 3. Six levels of adds, as a shuffle scan. Every lane must take part.
+template <typename T>
+__device__ __forceinline__ T zz_wave_incl_scan_add(T x) {
+    auto sh = [](T v, auto ctrl, auto rows) {
+        constexpr int C = decltype(ctrl)::value, RW = decltype(rows)::value;
+        if constexpr (sizeof(T) == 8) {
+            const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+            const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)u, C, RW, 0xF, false);
+            const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(u >> 32), C, RW, 0xF, false);
+            return __builtin_bit_cast(T, ((unsigned long long)hi << 32) | lo);
+        } else {
+            return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), C, RW, 0xF, false));
+        }
+    };
+    using F = std::integral_constant<int, 0xF>;
+    x += sh(x, std::integral_constant<int, 0x111>(), F());
+    x += sh(x, std::integral_constant<int, 0x112>(), F());
+    x += sh(x, std::integral_constant<int, 0x114>(), F());
+    x += sh(x, std::integral_constant<int, 0x118>(), F());
+    x += sh(x, std::integral_constant<int, 0x142>(), std::integral_constant<int, 0xA>());
+    x += sh(x, std::integral_constant<int, 0x143>(), std::integral_constant<int, 0xC>());
+    return x;
+}
+
+// the value of lane q (q wave-uniform)
+__device__ __forceinline__ double zz_lane_f64(double v, int q) {
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)u, q);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(u >> 32), q);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
 }
 
 template <typename T>

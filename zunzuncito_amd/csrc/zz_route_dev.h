@@ -107,19 +107,14 @@ __device__ void zz_tight_wave(const float *w, const float *src, const float *rsc
                 loc += (double)p[k];
                 T[s] += fabs((double)p[k]);
             }
-            double inc = loc;                                 // inclusive scan of lane runs
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const double v = __shfl_up(inc, o, 64);
-                if (l >= o) inc += v;
-            }
+            const double inc = zz_wave_incl_scan_add(loc);    // inclusive scan of lane runs
             double run = carry[s] + (inc - loc);
 #pragma unroll
             for (int k = 0; k < ZZ_TPER; k++) {
                 run += (double)p[k];
                 if (i0 + k >= 1 && i0 + k < D) sabs[s] += fabs(run);
             }
-            carry[s] += __shfl(inc, 63, 64);
+            carry[s] += zz_lane_f64(inc, 63);
             zz_wave_sync_lds();                               // buf is rewritten next
         }
     }
@@ -155,12 +150,7 @@ __device__ void zz_tight_block_scan(const float *buf, int D, const float *bias, 
         loc += (double)p[k];
         T += fabs((double)p[k]);
     }
-    double inc = loc;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const double v = __shfl_up(inc, o, 64);
-        if (l >= o) inc += v;
-    }
+    const double inc = zz_wave_incl_scan_add(loc);
     if (l == 63) red[wv] = inc;
     __syncthreads();
     double run = inc - loc, sabs = 0.0;
@@ -240,12 +230,7 @@ __device__ void zz_logit_wave_f64(const ZzLogitArgs &a, int s, int e, double *tb
             loc += p[k];
             T += fabs(p[k]);
         }
-        double inc = loc;                                  // inclusive scan of the runs
-#pragma unroll
-        for (int q = 1; q < 64; q <<= 1) {
-            const double v = __shfl_up(inc, q, 64);
-            if (l >= q) inc += v;
-        }
+        const double inc = zz_wave_incl_scan_add(loc);     // inclusive scan of the runs
         if (!grp) {
             double run = carry + (inc - loc);
 #pragma unroll
@@ -254,7 +239,7 @@ __device__ void zz_logit_wave_f64(const ZzLogitArgs &a, int s, int e, double *tb
                 if (i0 + k >= 1 && i0 + k < D) sabs += fabs(run);
             }
         }
-        carry += __shfl(inc, 63, 64);
+        carry += zz_lane_f64(inc, 63);
         zz_wave_sync_lds();                                // tb is rewritten next
     }
     sabs = zz_wave_sum(sabs);
