@@ -274,29 +274,32 @@ __device__ __forceinline__ void mm_kloop(const uint8_t *E, const ZzTensor &T, in
 // B lane 4b+j = column j, D lane 4b+j, VGPR v = row v). The 4 waves split the K range
 // by chunks (c = w, w+4, ...) and their partial sums meet in LDS. Per 32-weight block
 // a lane spends 12 unpack and 12 epilogue operations for 64 rows x 4 tokens, where
-// the 16x16x32 path spends 4 x 15 for 64 rows x 16 padded tokens.
-#define MM4_K 4096                       // largest K whose 4 token rows are staged whole
+// the 16x16x32 path spends 4 x 15 for 64 rows x 16 padded tokens. Items of 5-8 tokens
+// take two token sets (NS = 2, q4_0; q8_0's twice-as-large weight registers would spill):
+// the same weight operand feeds both sets' MFMAs, so a block costs 12 unpack and 24
+// epilogue operations for 64 rows x 8 tokens.
+#define MM4_XB 24576                     // staged activation bytes: 4 rows of K <= 6144, 8 of K <= 3072
 struct Mm4Stage {
-    __attribute__((aligned(16))) int8_t x[4][MM4_K];
-    float s[4][MM4_K / ZZ_BLK];
+    __attribute__((aligned(16))) int8_t x[MM4_XB];      // token t's row at t * K
+    float s[MM4_XB / ZZ_BLK];                          // token t's block scales at t * K / 32
 };
 struct Mm4Red {
     float part[4][64][4];                // [wave][lane][row of the quad]
-    float res[64][5];                    // [row][token]
+    float res[64][9];                    // [row][token]
 };
 
-// The item's (up to) 4 token rows and block scales, whole. row(t) / srow(t) for
-// t < 4 (callers clamp t to the item's last token).
-template <typename RF, typename SF>
+// The item's (up to) 4 * NS token rows and block scales, whole. row(t) / srow(t) for
+// t < 4 * NS (callers clamp t to the item's last token).
+template <int NS, typename RF, typename SF>
 __device__ __forceinline__ void mm4_stage(Mm4Stage &st, RF row, SF srow, int K) {
     const int tid = threadIdx.x, nseg = K / 16, nb = K / ZZ_BLK;
-    for (int i = tid; i < 4 * nseg; i += 256) {
+    for (int i = tid; i < 4 * NS * nseg; i += 256) {
         const int t = i / nseg, sg = i - t * nseg;
-        *(uint4 *)&st.x[t][16 * sg] = ld16(row(t) + 16 * sg);
+        *(uint4 *)&st.x[t * K + 16 * sg] = ld16(row(t) + 16 * sg);
     }
-    for (int i = tid; i < 4 * nb; i += 256) {
+    for (int i = tid; i < 4 * NS * nb; i += 256) {
         const int t = i / nb, b = i - t * nb;
-        st.s[t][b] = srow(t)[b];
+        st.s[t * nb + b] = srow(t)[b];
     }
     __syncthreads();
 }
@@ -341,22 +344,33 @@ __device__ __forceinline__ int mm4_frag(const Mm4A &A, int j, int m) {
     return (int)((m & 1) ? u.y : u.x);
 }
 
-// acc[v]: row 4(l/4)+v of the 64, token l%4, over this wave's chunks c = w, w+4, ...
-template <int FMT, bool FULLC>
-__device__ __forceinline__ void mm4_chunk(const Mm4A &A, const Mm4Stage &st, int c, int l, float (&acc)[4]) {
-    const int t = l & 3;
+// acc[s][v]: row 4(l/4)+v of the 64, token 4s + l%4, over this wave's chunks c = w,
+// w+4, ... (K: the row length, the staged rows' stride)
+template <int FMT, bool FULLC, int NS>
+__device__ __forceinline__ void mm4_chunk(const Mm4A &A, const Mm4Stage &st, int c, int l, int K,
+                                          float (&acc)[NS][4]) {
+    const int nb = K / ZZ_BLK;
 #pragma unroll
     for (int j = 0; j < (FULLC ? 4 : 2); j++) {
         const int b = 4 * c + j;
-        const uint4 xa = *(const uint4 *)&st.x[t][b * ZZ_BLK], xb = *(const uint4 *)&st.x[t][b * ZZ_BLK + 16];
-        const unsigned xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-        zz_v4i d = {0, 0, 0, 0};
+        zz_v4i d[NS];
+        float sx[NS];
 #pragma unroll
-        for (int m = 0; m < 8; m++) d = __builtin_amdgcn_mfma_i32_4x4x4i8(mm4_frag<FMT>(A, j, m), (int)xw[m], d, 0, 0, 0);
-        const float sx = st.s[t][b];
+        for (int s = 0; s < NS; s++) {
+            const int t = 4 * s + (l & 3);
+            const uint4 xa = *(const uint4 *)&st.x[t * K + b * ZZ_BLK], xb = *(const uint4 *)&st.x[t * K + b * ZZ_BLK + 16];
+            const unsigned xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            d[s] = (zz_v4i){0, 0, 0, 0};
 #pragma unroll
-        for (int v = 0; v < 4; v++)
-            acc[v] = fmaf(fmaf((float)mm_dwh<FULLC>(A.s0, A.s1, j, v), sx, 0.0f), (float)d[v], acc[v]);
+            for (int m = 0; m < 8; m++) d[s] = __builtin_amdgcn_mfma_i32_4x4x4i8(mm4_frag<FMT>(A, j, m), (int)xw[m], d[s], 0, 0, 0);
+            sx[s] = st.s[t * nb + b];
+        }
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const float dw = (float)mm_dwh<FULLC>(A.s0, A.s1, j, v);
+#pragma unroll
+            for (int s = 0; s < NS; s++) acc[s][v] = fmaf(fmaf(dw, sx[s], 0.0f), (float)d[s][v], acc[s][v]);
+        }
     }
 }
 
@@ -382,18 +396,21 @@ __device__ __forceinline__ void mm4_first(Mm4Ring<FMT> &R, const uint8_t *E, con
 
 // acc[v]: row 4(l/4)+v of the 64, token l%4, over this wave's chunks. Every load is
 // unconditional (clamped past the end) so the compiler's load counters stay exact.
-template <int FMT>
+template <int FMT, int NS>
 __device__ __forceinline__ void mm4_kloop(Mm4Ring<FMT> &R, const uint8_t *E, int l, int w, const Mm4Stage &st,
-                                          float (&acc)[4]) {
+                                          int K, float (&acc)[NS][4]) {
     const int nch = R.nch;
 #pragma unroll
-    for (int v = 0; v < 4; v++) acc[v] = 0.0f;
+    for (int s = 0; s < NS; s++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[s][v] = 0.0f;
     auto chunk = [&](const Mm4A &A, int c) {
-        if (c < R.W.nfull) mm4_chunk<FMT, true>(A, st, c, l, acc);
-        else if (c < nch) mm4_chunk<FMT, false>(A, st, c, l, acc);
+        if (c < R.W.nfull) mm4_chunk<FMT, true, NS>(A, st, c, l, K, acc);
+        else if (c < nch) mm4_chunk<FMT, false, NS>(A, st, c, l, K, acc);
     };
-    if (FMT == ZZ_FMT_Q80) {
-        // q8_0 chunks are twice the registers: two sets, one chunk in flight
+    if (FMT == ZZ_FMT_Q80 || NS == 2) {
+        // q8_0 chunks are twice the registers, and two token sets twice the work per
+        // chunk: two sets, one chunk in flight
         for (int c = w; c < nch; c += 8) {
             chunk(R.r0, c);
             R.r0 = mm4_load<FMT>(E, R.W, min(c + 8, nch - 1));
@@ -412,24 +429,27 @@ __device__ __forceinline__ void mm4_kloop(Mm4Ring<FMT> &R, const uint8_t *E, int
     }
     if (FMT == ZZ_FMT_Q40)                       // the 16*(q - 8) weights
 #pragma unroll
-        for (int v = 0; v < 4; v++) acc[v] *= 0.0625f;
+        for (int s = 0; s < NS; s++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[s][v] *= 0.0625f;
 }
 
-// the four waves' partial sums into res[row][token] (fixed order)
-__device__ __forceinline__ void mm4_reduce(Mm4Red &rd, const float (&acc)[4]) {
+// the four waves' partial sums of token set s into res[row][4s + token] (fixed order)
+__device__ __forceinline__ void mm4_reduce(Mm4Red &rd, const float (&acc)[4], int s) {
     const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63;
 #pragma unroll
     for (int v = 0; v < 4; v++) rd.part[w][l][v] = acc[v];
     __syncthreads();
     const int L = tid >> 2, v = tid & 3;
-    rd.res[4 * (L >> 2) + v][L & 3] = ((rd.part[0][L][v] + rd.part[1][L][v]) + rd.part[2][L][v]) + rd.part[3][L][v];
+    rd.res[4 * (L >> 2) + v][4 * s + (L & 3)] =
+        ((rd.part[0][L][v] + rd.part[1][L][v]) + rd.part[2][L][v]) + rd.part[3][L][v];
     __syncthreads();
 }
 
 struct Mm4Shared {
     Mm4Stage st;
     Mm4Red rd;
-    float hb[4][ZZ_BLK];
+    float hb[8][ZZ_BLK];
 };
 
 // ------------------------------------------------------------------ up
@@ -592,9 +612,10 @@ __device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &i
     }
 }
 
-// Tiny items (<= 4 tokens): lanes 0..31 own gate rows 32rb.., lanes 32..63 the up rows
-// (gate and up in one format); then h = act(g, u) and its q8_0 quantisation per token.
-template <int FMT>
+// Tiny items (<= 4 NS tokens): lanes 0..31 own gate rows 32rb.., lanes 32..63 the up
+// rows (gate and up in one format); then h = act(g, u) and its q8_0 quantisation per
+// token.
+template <int FMT, int NS>
 __device__ __forceinline__ void mm4_up_body(const ZzFfnArgs &a, const ZzItem &item, int rb, Mm4Shared &sm) {
     const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, n = item.n, D = a.D, nb = D / ZZ_BLK;
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
@@ -602,18 +623,19 @@ __device__ __forceinline__ void mm4_up_body(const ZzFfnArgs &a, const ZzItem &it
     const ZzTensor &T = l < 32 ? a.lay.gate : a.lay.up;
     Mm4Ring<FMT> R;
     mm4_first<FMT>(R, E, T, 2 * rb + ((l >> 4) & 1), l, w);       // weights first
-    mm4_stage(sm.st, [&](int t) { return a.xq + (size_t)ptok[min(t, n - 1)] * D; },
-              [&](int t) { return a.xs + (size_t)ptok[min(t, n - 1)] * nb; }, D);
-    float acc[4];
-    mm4_kloop<FMT>(R, E, l, w, sm.st, acc);
+    mm4_stage<NS>(sm.st, [&](int t) { return a.xq + (size_t)ptok[min(t, n - 1)] * D; },
+                  [&](int t) { return a.xs + (size_t)ptok[min(t, n - 1)] * nb; }, D);
+    float acc[NS][4];
+    mm4_kloop<FMT, NS>(R, E, l, w, sm.st, D, acc);
     __syncthreads();                             // the stage is done with
-    mm4_reduce(sm.rd, acc);
-    if (tid < 4 * ZZ_BLK) {                      // token t, hidden row 32rb + r
+#pragma unroll
+    for (int s = 0; s < NS; s++) mm4_reduce(sm.rd, acc[s], s);
+    if (tid < 4 * NS * ZZ_BLK) {                 // token t, hidden row 32rb + r
         const int t = tid >> 5, r = tid & 31;
         sm.hb[t][r] = zz_act(a.act, sm.rd.res[r][t], sm.rd.res[32 + r][t], a.clamp);
     }
     __syncthreads();
-    if (tid < 32) {                              // q8_0 of each token's block (q40.h:124-138)
+    if (tid < 32 * NS) {                         // q8_0 of each token's block (q40.h:124-138)
         const int t = tid >> 3, m = tid & 7;
         float d;
         int qs;
@@ -630,21 +652,25 @@ __device__ __forceinline__ void mm4_up_body(const ZzFfnArgs &a, const ZzItem &it
     }
 }
 
-// Tiny items (<= 4 tokens), down: rows 64rt + l, the unweighted y of each token.
-template <int FMT>
+// Tiny items (<= 4 NS tokens), down: rows 64rt + l, the unweighted y of each token.
+template <int FMT, int NS>
 __device__ __forceinline__ void mm4_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, Mm4Shared &sm) {
     const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, n = item.n, MI = a.MI, nb = MI / ZZ_BLK;
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
     Mm4Ring<FMT> R;
     mm4_first<FMT>(R, E, a.lay.down, 4 * rt + (l >> 4), l, w);     // weights first
-    mm4_stage(sm.st, [&](int t) { return a.hq + ((size_t)item.p0 + min(t, n - 1)) * MI; },
-              [&](int t) { return a.hs + ((size_t)item.p0 + min(t, n - 1)) * nb; }, MI);
-    float acc[4];
-    mm4_kloop<FMT>(R, E, l, w, sm.st, acc);
+    mm4_stage<NS>(sm.st, [&](int t) { return a.hq + ((size_t)item.p0 + min(t, n - 1)) * MI; },
+                  [&](int t) { return a.hs + ((size_t)item.p0 + min(t, n - 1)) * nb; }, MI);
+    float acc[NS][4];
+    mm4_kloop<FMT, NS>(R, E, l, w, sm.st, MI, acc);
     __syncthreads();
-    mm4_reduce(sm.rd, acc);
-    const int t = tid >> 6, r = tid & 63;
-    if (t < n) a.y[((size_t)item.p0 + t) * a.D + 64 * rt + r] = sm.rd.res[r][t];
+#pragma unroll
+    for (int s = 0; s < NS; s++) mm4_reduce(sm.rd, acc[s], s);
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int t = 4 * s + (tid >> 6), r = tid & 63;
+        if (t < n) a.y[((size_t)item.p0 + t) * a.D + 64 * rt + r] = sm.rd.res[r][t];
+    }
 }
 
 // XCD-aware work order. Workgroup g of a launch runs on XCD g % 8 (round-robin
@@ -674,7 +700,8 @@ __global__ __launch_bounds__(256, 4) void zz_up_mma_kernel(ZzFfnArgs a) {
     __shared__ MmUpShared sm;
     __shared__ int tok[MM_TN];
     const int nt = (item.n + 15) / 16;
-    if (GF == UF && GF != ZZ_FMT_TQ2 && item.n <= 4 && a.D <= MM4_K) mm4_up_body<GF>(a, item, rb, sm.t4);
+    if (GF == UF && GF != ZZ_FMT_TQ2 && item.n <= 4 && a.D <= MM4_XB / 4) mm4_up_body<GF, 1>(a, item, rb, sm.t4);
+    else if (GF == UF && GF == ZZ_FMT_Q40 && item.n <= 8 && a.D <= MM4_XB / 8) mm4_up_body<GF, 2>(a, item, rb, sm.t4);
     else if (nt <= 1) mm_up_body<GF, UF, 1>(a, item, rb, sm, tok);
     else if (nt <= 2) mm_up_body<GF, UF, 2>(a, item, rb, sm, tok);
     else if (nt <= 3) mm_up_body<GF, UF, 3>(a, item, rb, sm, tok);
@@ -690,7 +717,8 @@ __global__ __launch_bounds__(256, 4) void zz_down_mma_kernel(ZzFfnArgs a) {
     if (item.n <= 0) return;
     __shared__ MmDownShared sm;
     const int nt = (item.n + 15) / 16;
-    if (FMT != ZZ_FMT_TQ2 && item.n <= 4 && a.MI <= MM4_K) mm4_down_body<FMT>(a, item, rt, sm.t4);
+    if (FMT != ZZ_FMT_TQ2 && item.n <= 4 && a.MI <= MM4_XB / 4) mm4_down_body<FMT, 1>(a, item, rt, sm.t4);
+    else if (FMT == ZZ_FMT_Q40 && item.n <= 8 && a.MI <= MM4_XB / 8) mm4_down_body<FMT, 2>(a, item, rt, sm.t4);
     else if (nt <= 1) mm_down_body<FMT, 1>(a, item, rt, sm);
     else if (nt <= 2) mm_down_body<FMT, 2>(a, item, rt, sm);
     else if (nt <= 3) mm_down_body<FMT, 3>(a, item, rt, sm);
