@@ -231,10 +231,12 @@ __device__ __forceinline__ float zz_dec_up_comp(const ZzChunk (&k)[DU_C], const 
     return acc;
 }
 
-// the wave's partial dot of row r of group g over its half h of the K range
-template <int FMT>
+// the wave's partial dot of row r of group g over its half h of the K range; hook()
+// runs once the wave's first weight loads are in flight
+template <int FMT, typename HOOK>
 __device__ __forceinline__ float zz_dec_up_part(const ZzFfnArgs &a, const ZzDecStageRegs &sr, ZzDecStage &st,
-                                                const uint8_t *E, const ZzTensor &T, int g, int h, int l) {
+                                                const uint8_t *E, const ZzTensor &T, int g, int h, int l,
+                                                HOOK hook) {
     const int nb = a.D / ZZ_BLK, r = l & 15, qq = l >> 4;
     float acc = 0.0f;
     // the first batch of loads, the staging commit (waits only for the activations,
@@ -261,6 +263,7 @@ __device__ __forceinline__ float zz_dec_up_part(const ZzFfnArgs &a, const ZzDecS
             }
         };
         load(0);
+        hook();
         zz_dec_stage_commit(a, sr, st);
         comp(0);
         for (int i0 = DU_C; 4 * h + 8 * i0 < ng; i0 += DU_C) {
@@ -277,6 +280,7 @@ __device__ __forceinline__ float zz_dec_up_part(const ZzFfnArgs &a, const ZzDecS
         for (int i = 0; i < DU_C; i++) k[i] = zz_load_chunk<FMT>(E, W, min(h + 2 * (i0 + i), nch - 1));
     };
     load(0);
+    hook();
     zz_dec_stage_commit(a, sr, st);
     acc = zz_dec_up_comp<FMT>(k, st, nb, h, 0, qq, acc);
     for (int i0 = DU_C; h + 2 * i0 < nch; i0 += DU_C) {
@@ -303,16 +307,23 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
     ZzDecStageRegs sr;
     zz_dec_stage_issue(f, s, sr);
     const bool routed = !a.dense && !dn;
-    if (w == 0 && routed) zz_topk_wave_any(a.tk, s, tk_lds, j == 0 && js == 0);
+    // wave 0 selects the token's experts; the gate weights, needed only by the down
+    // kernel, are formed by one workgroup per token (the writer) once its weight loads
+    // are in flight, so no workgroup waits for them before its own loads
+    const bool writer = j == 0 && js == 0;
+    if (w == 0 && routed) zz_topk_wave_any(a.tk, s, tk_lds, writer, false);
     __syncthreads();
     const int e = routed ? zz_clamp_e(((const ZzTopkWaveHdr *)tk_lds)->idx[js], a.tk.E) : 0;
     const ZzTensor &T = q >= 2 ? f.lay.up : f.lay.gate;
     const int g = 2 * j + (q & 1);
     const uint8_t *E = f.experts + (size_t)e * f.estride;
+    auto gates = [&] {
+        if (w == 0 && routed && writer) zz_topk_wave_gates(a.tk, s, tk_lds, true);
+    };
     float acc;
-    if (T.fmt == ZZ_FMT_Q40) acc = zz_dec_up_part<ZZ_FMT_Q40>(f, sr, st, E, T, g, h, l);
-    else if (T.fmt == ZZ_FMT_Q80) acc = zz_dec_up_part<ZZ_FMT_Q80>(f, sr, st, E, T, g, h, l);
-    else acc = zz_dec_up_part<ZZ_FMT_TQ2>(f, sr, st, E, T, g, h, l);
+    if (T.fmt == ZZ_FMT_Q40) acc = zz_dec_up_part<ZZ_FMT_Q40>(f, sr, st, E, T, g, h, l, gates);
+    else if (T.fmt == ZZ_FMT_Q80) acc = zz_dec_up_part<ZZ_FMT_Q80>(f, sr, st, E, T, g, h, l, gates);
+    else acc = zz_dec_up_part<ZZ_FMT_TQ2>(f, sr, st, E, T, g, h, l, gates);
     acc = zz_rows_sum(acc);                                     // sum over the 4 k-quarters
     if (l < 16) part[h][q][l] = acc;
     if (T.fmt == ZZ_FMT_TQ2 && tid == 0) {          // tq2.h:101-106, serial

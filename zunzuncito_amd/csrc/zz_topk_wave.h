@@ -103,10 +103,50 @@ __device__ float zz_gemma_chain(const float *w, const float *xn, int D, const fl
     return v;
 }
 
-// write: store the routing outputs (eidx, ewt, topv, counters); the result is in
-// the header's idx / wt either way
+// Gate weights of a selected set (the header's idx / topv): lane l < K holds slot l's
+// centre cj and scale pj. Per slot in parallel, their sum serially in slot order as the
+// reference adds them, then each slot's normalisation. write: store eidx, ewt, topv.
+__device__ __forceinline__ void zz_topk_gates(const ZzTopkArgs &a, int s, ZzTopkWaveHdr &h, double cj, float pj,
+                                              bool write) {
+    const int K = a.K, l = threadIdx.x & 63;
+    const bool sig = a.gating == ZZ_GATE_SIGMOID_BIAS || a.gating == ZZ_GATE_GROUPED;
+    const int ej = l < K ? h.idx[l] : 0;
+    float wj = 0.0f;
+    if (l < K) wj = sig ? zz_sigmoid_score(cj, h.etab) : zz_expf_lds(h.topv[l] - h.topv[0], h.etab);
+    float sum = 0.0f;
+    for (int j = 0; j < K; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wj), j));
+    if (l < K) {
+        float out;
+        if (a.gating == ZZ_GATE_SOFTMAX_PES) {                     // gemma4.c:609-612
+            out = (wj / sum) * pj;
+        } else if (a.gating == ZZ_GATE_GROUPED) {                  // ling.c:783-788
+            float t = wj;
+            if (a.norm_topk && K > 1) t /= (sum + 1e-20f);
+            out = t * a.routed_scaling;
+        } else if (sig) {                                          // lfm25.c:661-667
+            float t = wj;
+            if (a.norm_topk) t /= (sum + 1e-6f);
+            out = t * a.routed_scaling;
+        } else {                                                   // maple.c:596-600
+            float t = wj;
+            if (a.norm_topk) t /= (sum + 1e-20f);
+            out = t;
+        }
+        h.wt[l] = out;
+        if (write) {
+            a.eidx[(size_t)s * K + l] = ej;
+            a.ewt[(size_t)s * K + l] = out;
+            if (a.topv) a.topv[(size_t)s * K + l] = h.topv[l];
+        }
+    }
+    zz_wave_sync_lds();
+}
+
+// write: store the routing outputs (eidx, ewt, topv, counters); gates: form the gate
+// weights now (else only the selection, the header's idx and topv: the caller forms
+// them later with zz_topk_wave_gates, from the same LDS)
 template <int EPL>
-__device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) {
+__device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write, bool gates) {
     ZzTopkWaveHdr &h = *(ZzTopkWaveHdr *)lds;
     const int E = a.E, K = a.K, l = threadIdx.x & 63;
     unsigned long long *ck = (unsigned long long *)(lds + sizeof(ZzTopkWaveHdr));
@@ -369,14 +409,11 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
     }                                                    // general passes
     zz_wave_sync_lds();
 
-    // gate weights: per slot in parallel, their sum serially in slot order as the
-    // reference adds them, then each slot's normalisation
-    float wj = 0.0f, pj = 1.0f;
-    const int ej = l < K ? h.idx[l] : 0;
-    {
+    if (gates) {
         // slot l's centre and scale from the lane that loaded them
-        const int own = ej & 63, jj = ej >> 6;
+        const int ej = l < K ? h.idx[l] : 0, own = ej & 63, jj = ej >> 6;
         double cj = 0.0;
+        float pj = 1.0f;
 #pragma unroll
         for (int j = 0; j < EPL; j++) {
             const double c = __shfl(cv[j], own, 64);
@@ -386,47 +423,36 @@ __device__ void zz_topk_wave(const ZzTopkArgs &a, int s, char *lds, bool write) 
                 pj = q;
             }
         }
-        if (l < K) wj = sig ? zz_sigmoid_score(cj, h.etab) : zz_expf_lds(h.topv[l] - h.topv[0], h.etab);
+        zz_topk_gates(a, s, h, cj, pj, write);
     }
-    float sum = 0.0f;
-    for (int j = 0; j < K; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wj), j));
-    if (l < K) {
-        float out;
-        if (a.gating == ZZ_GATE_SOFTMAX_PES) {                     // gemma4.c:609-612
-            out = (wj / sum) * pj;
-        } else if (a.gating == ZZ_GATE_GROUPED) {                  // ling.c:783-788
-            float t = wj;
-            if (a.norm_topk && K > 1) t /= (sum + 1e-20f);
-            out = t * a.routed_scaling;
-        } else if (sig) {                                          // lfm25.c:661-667
-            float t = wj;
-            if (a.norm_topk) t /= (sum + 1e-6f);
-            out = t * a.routed_scaling;
-        } else {                                                   // maple.c:596-600
-            float t = wj;
-            if (a.norm_topk) t /= (sum + 1e-20f);
-            out = t;
-        }
-        h.wt[l] = out;
-        if (write) {
-            a.eidx[(size_t)s * K + l] = ej;
-            a.ewt[(size_t)s * K + l] = out;
-            if (a.topv) a.topv[(size_t)s * K + l] = h.topv[l];
-        }
-    }
-    zz_wave_sync_lds();
     if (l == 0 && ties && write) atomicAdd(a.diag + 3, 1u);
+}
+
+// The gate weights of a selection that zz_topk_wave(..., gates = false) left in lds:
+// each slot's centre and scale read again from memory.
+__device__ __forceinline__ void zz_topk_wave_gates(const ZzTopkArgs &a, int s, char *lds, bool write) {
+    ZzTopkWaveHdr &h = *(ZzTopkWaveHdr *)lds;
+    const int l = threadIdx.x & 63;
+    double cj = 0.0;
+    float pj = 1.0f;
+    if (l < a.K) {
+        const int ej = h.idx[l];
+        cj = a.cen[(size_t)s * a.E + ej];
+        if (a.gating == ZZ_GATE_SOFTMAX_PES) pj = a.pes[ej];
+    }
+    zz_topk_gates(a, s, h, cj, pj, write);
 }
 
 // experts per lane of zz_topk_wave for E experts
 __host__ __device__ inline int zz_topk_epl(int E) { return E <= 64 ? 1 : (E <= 128 ? 2 : (E <= 256 ? 4 : 8)); }
 
 // zz_topk_wave with the lane count chosen at run time
-__device__ __forceinline__ void zz_topk_wave_any(const ZzTopkArgs &a, int s, char *lds, bool write = true) {
+__device__ __forceinline__ void zz_topk_wave_any(const ZzTopkArgs &a, int s, char *lds, bool write = true,
+                                                 bool gates = true) {
     switch (zz_topk_epl(a.E)) {
-    case 1: zz_topk_wave<1>(a, s, lds, write); break;
-    case 2: zz_topk_wave<2>(a, s, lds, write); break;
-    case 4: zz_topk_wave<4>(a, s, lds, write); break;
-    default: zz_topk_wave<8>(a, s, lds, write); break;
+    case 1: zz_topk_wave<1>(a, s, lds, write, gates); break;
+    case 2: zz_topk_wave<2>(a, s, lds, write, gates); break;
+    case 4: zz_topk_wave<4>(a, s, lds, write, gates); break;
+    default: zz_topk_wave<8>(a, s, lds, write, gates); break;
     }
 }
