@@ -136,13 +136,18 @@ int zz_moe_forward_end(int layer, float *out, int *eidx, float *ewt);
  * router logits, the reference's own float values for the lfm, maple and ling
  * routers at every S, and for gemma (after the bias) when S >= 16 and D % 64 == 0;
  * gemma's other batched logits are interval centres, and its decode path (S <= 2
- * with q4_0 / q8_0 experts, S <= 4 with tq2) keeps none. */
+ * with q4_0 / q8_0 experts, S <= 4 with tq2) keeps none. items: the FFN work
+ * items of the batched path as 4 ints each (expert, union entry, first pair in
+ * the dispatch lists, pairs; 0 pairs: an empty slot), slot i runs on XCD i % 8;
+ * at most items_cap are copied and nitems is set to the slot count. */
 typedef struct zz_moe_dump {
     int8_t *xq; float *xs;
     int8_t *hq; float *hs;
     int *uniq, *offs, *rows, *slots;
     int nu;
     double *logits;
+    int *items;
+    int items_cap, nitems;
 } zz_moe_dump;
 int zz_moe_debug(int layer, zz_moe_dump *dump);
 

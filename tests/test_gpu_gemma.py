@@ -90,6 +90,28 @@ def test_dense_branch(dev, D, DI, S):
         m.close()
 
 
+def test_dense_items_spread_over_xcds(dev):
+    """The dense branch at S=512 is one expert of 8 work items: no placement of
+    whole experts balances 8 XCDs, so its items run one per XCD in union order."""
+    say("dense gemma shape S=512 items")
+    dn = Z.make_dense(2816, 2112, 8)
+    L = Z.make_layer("gemma", seed=1, E=8, D=2816, MI=64, K=2)
+    x = Z.make_input(L, 512, 9)
+    m = gpu_dense(dn)
+    try:
+        out, _, _ = m.forward(x)
+        err = Z.rel_l2(out, Z.oracle_dense(dn, 1e-6, x))
+        say(f"  rel L2 {err:.2e}")
+        assert err < OUT_TOL, err
+        d = m.debug(512)
+        xcds = Z.check_items(d)
+        used = [slot % 8 for slot, it in enumerate(d["items"]) if it[3] > 0]
+        assert len(used) == 8 and sorted(used) == list(range(8)), used
+        assert xcds[0] == set(range(8))
+    finally:
+        m.close()
+
+
 def test_block_golden(dev):
     g = np.load(Z.os.path.join(Z.ROOT, "tests", "golden", "gemma_block_stack.npz"))
     L, dn, H, table, fnorm, st, H0 = Z.gemma_block_case()

@@ -340,6 +340,9 @@ def test_config2_gemma_zipf_s512(dev, layer_cache):
         cnt = np.bincount(eidx, minlength=L.E)
         say(f"  nu {len(want.uniq)} max/min per-expert {cnt.max()}/{cnt.min()} rel L2 {err:.2e}")
         assert len(want.uniq) > 64 and cnt.max() > 4 * max(1, np.median(cnt))
+        # a skewed union of many experts is placed whole: each expert's items on one XCD
+        xcds = Z.check_items(m.debug(512))
+        assert all(len(x) == 1 for x in xcds.values()), xcds
     finally:
         m.close()
 

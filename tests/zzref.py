@@ -375,6 +375,30 @@ def rel_l2(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
+def check_items(d, tch=64):
+    """The FFN work items of a debug dump cover each union entry's pairs exactly:
+    the entry's items (expert uniq[u], at most tch pairs each) tile its list
+    [offs[u], offs[u+1]) in order without gaps or overlaps. Returns, per union
+    entry, the set of XCDs (slot % 8) its items run on."""
+    items, uniq, offs = d["items"], d["uniq"], d["offs"]
+    assert len(items) % 8 == 0 and len(items) > 0
+    xcds = {}
+    spans = {}
+    for slot, (e, u, p0, n) in enumerate(items):
+        if n == 0:
+            continue
+        assert 0 < n <= tch and 0 <= u < len(uniq) and e == uniq[u], (slot, e, u, n)
+        spans.setdefault(u, []).append((p0, n))
+        xcds.setdefault(u, set()).add(slot % 8)
+    assert sorted(spans) == list(range(len(uniq)))
+    for u, sp in spans.items():
+        sp.sort()
+        assert sum(n for _, n in sp) == offs[u + 1] - offs[u]
+        for (a, na), (b, _) in zip(sp, sp[1:]):
+            assert b == a + na
+    return xcds
+
+
 # ------------------------------------------- gemma around the MoE block
 class OrcDense(C.Structure):
     _fields_ = [("DI", C.c_int), ("mlp", u8p), ("pre_ffn_ln", f32p), ("post_ffn_ln1", f32p),

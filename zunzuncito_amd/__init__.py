@@ -62,7 +62,8 @@ class ZzMoeWeights(C.Structure):
 class ZzMoeDump(C.Structure):
     _fields_ = [("xq", _i8p), ("xs", _f32p), ("hq", _i8p), ("hs", _f32p),
                 ("uniq", _i32p), ("offs", _i32p), ("rows", _i32p), ("slots", _i32p),
-                ("nu", C.c_int), ("logits", C.POINTER(C.c_double))]
+                ("nu", C.c_int), ("logits", C.POINTER(C.c_double)),
+                ("items", _i32p), ("items_cap", C.c_int), ("nitems", C.c_int)]
 
 
 _lib = None
@@ -255,8 +256,11 @@ class MoeLayer:
 
     def debug(self, S, logits=False):
         """The last forward's dump (zz_moe_debug); logits=True adds the router
-        logits [S, E] as float64 (none for gemma's decode path)."""
+        logits [S, E] as float64 (none for gemma's decode path). items [n, 4]:
+        the batched path's FFN work items (expert, union entry, first pair, pairs),
+        slot i on XCD i % 8."""
         K, D, MI = self.K, self.D, self.MI
+        cap = 8 * (S * K + self.E + 16)
         d = dict(xq=np.zeros((S, D), np.int8), xs=np.zeros((S, D // 32), np.float32),
                  hq=np.zeros((S * K, MI), np.int8), hs=np.zeros((S * K, MI // 32), np.float32),
                  uniq=np.zeros(self.E, np.int32), offs=np.zeros(self.E + 1, np.int32),
@@ -267,8 +271,11 @@ class MoeLayer:
                          _p(d["hs"], _f32p), _p(d["uniq"], _i32p), _p(d["offs"], _i32p),
                          _p(d["rows"], _i32p), _p(d["slots"], _i32p), 0,
                          _p(d["logits"], C.POINTER(C.c_double)) if logits else None)
+        items = np.zeros((cap, 4), np.int32)
+        dump.items, dump.items_cap = _p(items, _i32p), cap
         if not lib().zz_moe_debug(self.id, C.byref(dump)):
             raise RuntimeError(last_error())
+        d["items"] = items[:min(dump.nitems, cap)]
         nu = dump.nu
         d["uniq"] = d["uniq"][:nu]
         d["offs"] = d["offs"][:nu + 1]

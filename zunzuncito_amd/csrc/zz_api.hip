@@ -810,6 +810,12 @@ extern "C" int zz_moe_debug(int id, zz_moe_dump *dp) {
     const int nu = meta[0];
     dp->nu = nu;
     if (dp->uniq) memcpy(dp->uniq, uniq.data(), sizeof(int) * nu);
+    dp->nitems = dec ? 0 : meta[1];
+    if (dp->items && dp->items_cap > 0 && dp->nitems > 0) {
+        const int ni = dp->nitems < dp->items_cap ? dp->nitems : dp->items_cap;
+        static_assert(sizeof(ZzItem) == 4 * sizeof(int), "items are copied as 4 ints");
+        ZZ_CHECK(hipMemcpy(dp->items, w.items, sizeof(ZzItem) * ni, hipMemcpyDeviceToHost));
+    }
     // lists in union order, as moe_apply_chunk walks them (gemma4.c:776-790)
     int n = 0;
     for (int u = 0; u < nu; u++) {
