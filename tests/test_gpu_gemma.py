@@ -297,6 +297,29 @@ def test_stack_runner_graph_equals_eager(dev):
         for graph, t, l in runs[1:]:
             assert np.array_equal(t, runs[0][1]), (graph, t, runs[0][1])
             assert np.array_equal(l.view(np.uint32), runs[0][2].view(np.uint32))
+        # the stack defers each block's combine into the next block's router; the
+        # blocks run one by one combine in their own kernel: equal bit for bit
+        h1 = torch.zeros((1, D), dtype=torch.float32, device="cuda")
+        dl = torch.zeros((1, V), dtype=torch.float32, device="cuda")
+        dtok = tok0.clone()
+        man = [int(tok0.item())]
+        for _ in range(n):
+            hd.embed_dev(dtok.data_ptr(), 1, h1.data_ptr(), s)
+            for B in blocks:
+                B.forward_dev(h1.data_ptr(), 1, stream=s)
+            hd.logits_dev(h1.data_ptr(), 1, dl.data_ptr(), dtok.data_ptr(), s)
+            man.append(int(dtok.item()))
+        assert man == runs[0][1].tolist(), (man, runs[0][1])
+        assert np.array_equal(dl.cpu().numpy()[0].view(np.uint32), runs[0][2].view(np.uint32))
+        # 3 rows through the stack (the deferred path holds up to 4) and one by one
+        a3 = torch.from_numpy(H0[:3]).cuda()
+        b3 = a3.clone()
+        t3 = torch.zeros(1, dtype=torch.int32, device="cuda")
+        stack.prefill_dev(a3.data_ptr(), 3, t3.data_ptr(), s)
+        for B in blocks:
+            B.forward_dev(b3.data_ptr(), 3, stream=s)
+        torch.cuda.synchronize()
+        assert torch.equal(a3.view(torch.int32), b3.view(torch.int32))
         # prefill's greedy token is the head of the last prefill row
         wl, wam = Z.oracle_head(st.table, V, D, st.fnorm, st.layers[0].eps, st.softcap,
                                 dH[-1:].cpu().numpy())

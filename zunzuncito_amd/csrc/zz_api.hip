@@ -608,18 +608,26 @@ static int run_chunk(Layer *L, Workspace &w, const float *d_in, float *d_out, in
 // both post-norms and the layer combine. H is updated in place; h1/h2 [S, D] hold
 // the dense and routed outputs before their norms. Returns 1 when done, 0 on a
 // failure, -1 when the layers or S do not take this path.
-int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_h2, const float *post_ln,
-                    float ls, int S, int *d_eidx, float *d_ewt, hipStream_t st) {
+int zz_block_decode_fits(int moe_id, int dense_id, int S) {
     Layer *L = get_layer(moe_id), *N = get_layer(dense_id);
-    if (!L || !N || S <= 0) return -1;
+    if (!L || !N || S <= 0) return 0;
     const zz_moe_desc &d = L->d, &dn = N->d;
     // the fused block rows keep the decode kernels up to ZZ_DEC_MAXS: they also save
     // the dense branch its own launches and stream
-    if (d.gating != ZZ_GATE_SOFTMAX_PES || dn.gating != ZZ_GATE_DENSE || d.D != dn.D || S > g_dec_max_s ||
-        !zz_dec_fits(S, d.K, d.MI) ||
-        S > chunk_tokens(d) || d.fmt_down != dn.fmt_down || d.fmt_down == ZZ_FMT_TQ2 || dn.fmt_gate == ZZ_FMT_TQ2 ||
-        dn.fmt_up == ZZ_FMT_TQ2 || d.fmt_gate == ZZ_FMT_TQ2 || !zz_dec_fits2(S, d.K, d.MI, dn.MI))
-        return -1;
+    return !(d.gating != ZZ_GATE_SOFTMAX_PES || dn.gating != ZZ_GATE_DENSE || d.D != dn.D || S > g_dec_max_s ||
+             !zz_dec_fits(S, d.K, d.MI) || S > chunk_tokens(d) || d.fmt_down != dn.fmt_down ||
+             d.fmt_down == ZZ_FMT_TQ2 || dn.fmt_gate == ZZ_FMT_TQ2 || dn.fmt_up == ZZ_FMT_TQ2 ||
+             d.fmt_gate == ZZ_FMT_TQ2 || !zz_dec_fits2(S, d.K, d.MI, dn.MI));
+}
+
+int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_h2, const float *post_ln,
+                    float ls, int S, int *d_eidx, float *d_ewt, hipStream_t st, const ZzDecFinalArgs *pend_in,
+                    ZzDecFinalArgs *pend_out) {
+    if (!zz_block_decode_fits(moe_id, dense_id, S)) return -1;
+    Layer *L = get_layer(moe_id), *N = get_layer(dense_id);
+    const zz_moe_desc &d = L->d, &dn = N->d;
+    if (pend_in && (pend_in->Hout != d_H || pend_in->D != d.D || !zz_dec_fin_fits(S, d.D)))
+        ZZ_FAIL("block: the deferred combine does not fit this block");
     if (L->n_present != d.E || N->n_present != dn.E) ZZ_FAIL("block: experts not uploaded");
     if (!ensure_ws(L, S) || !ensure_ws(N, S)) return 0;
     Workspace &w = L->ws, &wn = N->ws;
@@ -628,6 +636,10 @@ int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_
     ZzDecRouteArgs ra;
     memset(&ra, 0, sizeof ra);
     ra.prep = c.pa; ra.lg = c.la; ra.tk = c.ta; ra.dp = c.da; ra.S = S; ra.dual = 1; ra.prep2 = cn.pa;
+    if (pend_in) {
+        ra.fin = 1;
+        ra.fa = *pend_in;
+    }
     if (!(ProfScope(ZZ_K_DEC_ROUTE, st), zz_launch_dec_logits(ra, st))) ZZ_FAIL("block: router launch failed");
     ZzDecUpArgs ua;
     memset(&ua, 0, sizeof ua);
@@ -640,8 +652,13 @@ int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_
     if (!(ProfScope(ZZ_K_DEC_DOWN, st), zz_launch_dec_down(dd, st))) ZZ_FAIL("block: down launch failed");
     ZzDecFinalArgs fa;
     fa.D = d.D; fa.G = d.D / 16; fa.eps = d.eps; fa.ls = ls; fa.out = d_h2; fa.ss = w.ss; fa.post2 = L->post_ln;
-    fa.yd = d_h1; fa.ssd = wn.ss; fa.post1 = N->post_ln; fa.post = post_ln; fa.H = d_H;
-    if (!(ProfScope(ZZ_K_COMBINE, st), zz_launch_dec_final(fa, S, st))) ZZ_FAIL("block: final launch failed");
+    fa.yd = d_h1; fa.ssd = wn.ss; fa.post1 = N->post_ln; fa.post = post_ln; fa.H = d_H; fa.Hout = d_H;
+    if (pend_out) {
+        *pend_out = fa;
+        pend_out->Hout = nullptr;
+    } else if (!(ProfScope(ZZ_K_COMBINE, st), zz_launch_dec_final(fa, S, st))) {
+        ZZ_FAIL("block: final launch failed");
+    }
     if (d_eidx) ZZ_CHECK(hipMemcpyAsync(d_eidx, w.eidx, sizeof(int) * S * d.K, hipMemcpyDeviceToDevice, st));
     if (d_ewt) ZZ_CHECK(hipMemcpyAsync(d_ewt, w.ewt, sizeof(float) * S * d.K, hipMemcpyDeviceToDevice, st));
     L->last_S = S;

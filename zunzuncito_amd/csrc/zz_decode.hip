@@ -20,6 +20,80 @@
 // expert id kept inside the slot table whatever the router produced
 __device__ __forceinline__ int zz_clamp_e(int e, int E) { return e < 0 || e >= E ? 0 : e; }
 
+// The layer combine of token s (gemma4.c:807-808, 1020, 1022-1030): the two
+// post-norms from their per-tile sums, their sum t, then
+// Hout[s] = (H[s] + rmsnorm(t)·post)·ls. All 256 threads take part; row (LDS, D
+// floats) ends holding Hout[s], which `store` also writes to a.Hout. Each thread
+// reads H before it writes Hout, so H == Hout is allowed. The first 1024·NJ
+// elements' six operands are all loaded before the norms are formed; the rest of a
+// longer row streams.
+template <int NJ>
+__device__ void zz_dec_final_row(const ZzDecFinalArgs &a, int s, float *row, float *rn, double *red, bool store) {
+    const int tid = threadIdx.x, D = a.D, G = a.G;
+    const float *o2 = a.out + (size_t)s * D, *o1 = a.yd + (size_t)s * D, *hr = a.H + (size_t)s * D;
+    float4 y[NJ], w2[NJ], x[NJ], w1[NJ], h[NJ], wv[NJ], t[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int o = min(4 * tid + 1024 * j, D - 4);        // clamped: loads stay in range
+        y[j] = *(const float4 *)(o2 + o);
+        w2[j] = *(const float4 *)(a.post2 + o);
+        x[j] = *(const float4 *)(o1 + o);
+        w1[j] = *(const float4 *)(a.post1 + o);
+        h[j] = *(const float4 *)(hr + o);
+        wv[j] = *(const float4 *)(a.post + o);
+    }
+    if (tid < 128) {                                 // wave 0: routed, wave 1: dense
+        const int which = tid >> 6, l = tid & 63;
+        const double *ss = (which ? a.ssd : a.ss) + (size_t)s * G;
+        double q = 0.0;
+        for (int k = l; k < G; k += 64) q += ss[k];
+        q = zz_group_sum<64>(q);
+        if (l == 0) rn[which] = 1.0f / sqrtf((float)(q / D) + a.eps);
+    }
+    __syncthreads();
+    const float r2 = rn[0], r1 = rn[1];
+    auto tsum = [&](float4 yv, float4 v2, float4 xv, float4 v1) {
+        const float4 h2 = make_float4((yv.x * r2) * v2.x, (yv.y * r2) * v2.y, (yv.z * r2) * v2.z, (yv.w * r2) * v2.w);
+        const float4 h1 = make_float4((xv.x * r1) * v1.x, (xv.y * r1) * v1.y, (xv.z * r1) * v1.z, (xv.w * r1) * v1.w);
+        return make_float4(h1.x + h2.x, h1.y + h2.y, h1.z + h2.z, h1.w + h2.w);
+    };
+    double sq = 0.0;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        t[j] = tsum(y[j], w2[j], x[j], w1[j]);
+        if (4 * tid + 1024 * j < D)
+            sq += (double)t[j].x * t[j].x + (double)t[j].y * t[j].y + (double)t[j].z * t[j].z + (double)t[j].w * t[j].w;
+    }
+    for (int o = 4 * tid + 1024 * NJ; o < D; o += 1024) {
+        const float4 tv = tsum(*(const float4 *)(o2 + o), *(const float4 *)(a.post2 + o),
+                               *(const float4 *)(o1 + o), *(const float4 *)(a.post1 + o));
+        *(float4 *)&row[o] = tv;
+        sq += (double)tv.x * tv.x + (double)tv.y * tv.y + (double)tv.z * tv.z + (double)tv.w * tv.w;
+    }
+    sq = zz_block_sum(sq, red);
+    const float r = 1.0f / sqrtf((float)(sq / D) + a.eps);
+    float *ho = a.Hout + (size_t)s * D;
+    auto fin = [&](float4 tv, float4 w, float4 hv) {
+        return make_float4((hv.x + (tv.x * r) * w.x) * a.ls, (hv.y + (tv.y * r) * w.y) * a.ls,
+                           (hv.z + (tv.z * r) * w.z) * a.ls, (hv.w + (tv.w * r) * w.w) * a.ls);
+    };
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int o = 4 * tid + 1024 * j;
+        if (o < D) {
+            const float4 v = fin(t[j], wv[j], h[j]);
+            *(float4 *)&row[o] = v;
+            if (store) *(float4 *)(ho + o) = v;
+        }
+    }
+    for (int o = 4 * tid + 1024 * NJ; o < D; o += 1024) {
+        const float4 v = fin(*(const float4 *)&row[o], *(const float4 *)(a.post + o), *(const float4 *)(hr + o));
+        *(float4 *)&row[o] = v;
+        if (store) *(float4 *)(ho + o) = v;
+    }
+    __syncthreads();
+}
+
 // Decode router, part 1: one workgroup per expert e (the dense branch, which has
 // no router: 16 workgroups that only norm and quantise). Gemma: per token, one set of
 // loads (x row, router row e, router scale) gives both the rmsnorm factor and the
@@ -29,7 +103,9 @@ __device__ __forceinline__ int zz_clamp_e(int e, int E) { return e < 0 || e >= E
 // wave s computes token s's logit. Then the workgroup quantises its share of the
 // expert input (blocks e, e + E, ...).
 // RB >= ceil(D/256): loads per thread and token, all issued before any is used.
-template <int RB>
+// FIN: the input rows are first formed from the previous block's combine (a.fa)
+// in LDS, and read from there.
+template <int RB, bool FIN>
 __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
     const ZzPrepArgs &pp = a.prep;
     const ZzLogitArgs &lg = a.lg;
@@ -44,6 +120,13 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
     __shared__ double red[12];
     __shared__ float rr[DEC_MAXS];
     __shared__ float cert;
+    __shared__ __attribute__((aligned(16))) float hrow[FIN ? ZZ_DEC_FIN_MAXF : 4];
+    __shared__ float frn[2];
+    const float *xin = pp.in;
+    if (FIN) {
+        for (int s = 0; s < S; s++) zz_dec_final_row<4>(a.fa, s, hrow + (size_t)s * D, frn, red, e == 0);
+        xin = hrow;
+    }
     const float rs = 1.0f / sqrtf((float)D);
     if (a.dense && e == 0 && tid < S) {                      // one expert, weight 1
         pp.route_eidx[tid] = 0;
@@ -61,7 +144,7 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
 #pragma unroll
         for (int j = 0; j < RB; j++) sr[j] = sr[j] * rs;
         for (int s = 0; s < S; s++) {
-            const float *x = pp.in + (size_t)s * D;
+            const float *x = xin + (size_t)s * D;
             float xr[RB];
 #pragma unroll
             for (int j = 0; j < RB; j++) xr[j] = x[min(tid + 256 * j, D - 1)];
@@ -115,7 +198,7 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
         const bool two = g >= S * nb;
         const ZzPrepArgs &P = two ? a.prep2 : pp;
         const int gg = two ? g - S * nb : g, s = gg / nb, b = gg % nb;
-        float4 v = *(const float4 *)(pp.in + (size_t)s * D + b * ZZ_BLK + 4 * m);
+        float4 v = *(const float4 *)(xin + (size_t)s * D + b * ZZ_BLK + 4 * m);
         if (gem) {
             const float r = rr[s];
             const float4 w = *(const float4 *)(P.pre_ln + b * ZZ_BLK + 4 * m);
@@ -628,13 +711,22 @@ __global__ __launch_bounds__(256) void zz_dec_norm_kernel(float *out, const floa
 int zz_launch_dec_logits(const ZzDecRouteArgs &a, hipStream_t st) {
     const int R = (a.prep.D + 255) / 256;
     const dim3 g(a.dense ? 16 : a.lg.E);
-    if (R <= 4) hipLaunchKernelGGL(zz_dec_logits_kernel<4>, g, dim3(256), 0, st, a);
-    else if (R <= 8) hipLaunchKernelGGL(zz_dec_logits_kernel<8>, g, dim3(256), 0, st, a);
-    else if (R <= 12) hipLaunchKernelGGL(zz_dec_logits_kernel<12>, g, dim3(256), 0, st, a);
-    else if (R <= 16) hipLaunchKernelGGL(zz_dec_logits_kernel<16>, g, dim3(256), 0, st, a);
-    else if (R <= 24) hipLaunchKernelGGL(zz_dec_logits_kernel<24>, g, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(zz_dec_logits_kernel<32>, g, dim3(256), 0, st, a);
+    if (a.fin) {                                     // zz_dec_fin_fits holds
+        if (R <= 12) hipLaunchKernelGGL((zz_dec_logits_kernel<12, true>), g, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((zz_dec_logits_kernel<16, true>), g, dim3(256), 0, st, a);
+    }
+    else if (R <= 4) hipLaunchKernelGGL((zz_dec_logits_kernel<4, false>), g, dim3(256), 0, st, a);
+    else if (R <= 8) hipLaunchKernelGGL((zz_dec_logits_kernel<8, false>), g, dim3(256), 0, st, a);
+    else if (R <= 12) hipLaunchKernelGGL((zz_dec_logits_kernel<12, false>), g, dim3(256), 0, st, a);
+    else if (R <= 16) hipLaunchKernelGGL((zz_dec_logits_kernel<16, false>), g, dim3(256), 0, st, a);
+    else if (R <= 24) hipLaunchKernelGGL((zz_dec_logits_kernel<24, false>), g, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((zz_dec_logits_kernel<32, false>), g, dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess;
+}
+
+// a deferred combine fits the router's LDS rows (and its RB <= 16 forms)
+int zz_dec_fin_fits(int S, int D) {
+    return S > 0 && D % 4 == 0 && D <= 4096 && (long)S * D <= ZZ_DEC_FIN_MAXF;
 }
 
 int zz_launch_dec_up(const ZzDecUpArgs &a, int S, hipStream_t st) {
@@ -677,39 +769,10 @@ int zz_launch_dec_norm(float *out, const float *post_ln, const double *ss, int D
 // zz_dec_norm_kernel forms it), then the layer combine as zz_block_combine_kernel
 // forms it (gemma4.c:807-808, 1020, 1022-1030). One workgroup per token.
 __global__ __launch_bounds__(256) void zz_dec_final_kernel(ZzDecFinalArgs a) {
-    const int s = blockIdx.x, tid = threadIdx.x, D = a.D, G = a.G;
     __shared__ float rn[2];
     __shared__ __attribute__((aligned(16))) float row[ZZ_MAXD];
     __shared__ double red[4];
-    if (tid < 128) {                                 // wave 0: routed, wave 1: dense
-        const int which = tid >> 6, l = tid & 63;
-        const double *ss = (which ? a.ssd : a.ss) + (size_t)s * G;
-        double q = 0.0;
-        for (int k = l; k < G; k += 64) q += ss[k];
-        q = zz_group_sum<64>(q);
-        if (l == 0) rn[which] = 1.0f / sqrtf((float)(q / D) + a.eps);
-    }
-    __syncthreads();
-    const float r2 = rn[0], r1 = rn[1];
-    const float *o2 = a.out + (size_t)s * D, *o1 = a.yd + (size_t)s * D;
-    double sq = 0.0;
-    for (int o = 4 * tid; o < D; o += 1024) {
-        const float4 y = *(const float4 *)(o2 + o), w2 = *(const float4 *)(a.post2 + o);
-        const float4 x = *(const float4 *)(o1 + o), w1 = *(const float4 *)(a.post1 + o);
-        const float4 h2 = make_float4((y.x * r2) * w2.x, (y.y * r2) * w2.y, (y.z * r2) * w2.z, (y.w * r2) * w2.w);
-        const float4 h1 = make_float4((x.x * r1) * w1.x, (x.y * r1) * w1.y, (x.z * r1) * w1.z, (x.w * r1) * w1.w);
-        const float4 t = make_float4(h1.x + h2.x, h1.y + h2.y, h1.z + h2.z, h1.w + h2.w);
-        *(float4 *)&row[o] = t;
-        sq += (double)t.x * t.x + (double)t.y * t.y + (double)t.z * t.z + (double)t.w * t.w;
-    }
-    sq = zz_block_sum(sq, red);
-    const float r = 1.0f / sqrtf((float)(sq / D) + a.eps);
-    float *hr = a.H + (size_t)s * D;
-    for (int o = 4 * tid; o < D; o += 1024) {
-        const float4 t = *(const float4 *)&row[o], wv = *(const float4 *)(a.post + o), h = *(const float4 *)(hr + o);
-        *(float4 *)(hr + o) = make_float4((h.x + (t.x * r) * wv.x) * a.ls, (h.y + (t.y * r) * wv.y) * a.ls,
-                                          (h.z + (t.z * r) * wv.z) * a.ls, (h.w + (t.w * r) * wv.w) * a.ls);
-    }
+    zz_dec_final_row<4>(a, blockIdx.x, row, rn, red, true);
 }
 
 int zz_launch_dec_final(const ZzDecFinalArgs &a, int S, hipStream_t st) {

@@ -581,6 +581,7 @@ struct Stack {
     std::vector<int> blocks;
     int head, D, V;
     float *h = nullptr;             // [D] the decode row
+    float *alt = nullptr;           // [ZZ_DEC_MAXS, D] the residual stream's second buffer
     float *logits = nullptr;        // [V]
     int *cur = nullptr;             // the current token
     hipGraph_t graph = nullptr;
@@ -603,7 +604,7 @@ static void free_stack(Stack *k, bool owned = false) {
     }
     if (k->exec) (void)hipGraphExecDestroy(k->exec);
     if (k->graph) (void)hipGraphDestroy(k->graph);
-    void *ps[] = {k->h, k->logits, k->cur};
+    void *ps[] = {k->h, k->alt, k->logits, k->cur};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     delete k;
@@ -652,6 +653,7 @@ extern "C" int zz_stack_create(const int *blocks, int n, int head) {
     k->D = h->D;
     k->V = h->V;
     if (hipMalloc(&k->h, sizeof(float) * h->D) != hipSuccess ||
+        hipMalloc(&k->alt, sizeof(float) * ZZ_DEC_MAXS * h->D) != hipSuccess ||
         hipMalloc(&k->logits, sizeof(float) * h->V) != hipSuccess || hipMalloc(&k->cur, sizeof(int)) != hipSuccess) {
         zz_set_error("zz_stack_create: device allocation failed");
         free_stack(k);
@@ -680,12 +682,44 @@ int zz_stack_adopt(int id, const std::vector<int> &layers, const std::vector<int
     return 1;
 }
 
+// Decode rows through the blocks. Where every block takes the fused decode path and
+// the rows fit the router's LDS, each block's combine is deferred into the next
+// block's router kernel, which forms the combined rows in every workgroup and stores
+// them once: one launch less per block. The router cannot update the rows in place
+// (its other workgroups still read them), so the residual stream alternates between
+// d_H and k->alt; the last block's combine runs as its own kernel into d_H.
 static int stack_blocks(Stack *k, float *d_H, int S, hipStream_t st) {
+    bool chain = S <= ZZ_DEC_MAXS && zz_dec_fin_fits(S, k->D);
     for (int b : k->blocks) {
         FfnBlock *B = get_block(b);
         if (!B) ZZ_FAIL("zz_stack: block %d is gone", b);
-        if (!block_forward(B, d_H, S, nullptr, nullptr, st)) return 0;
+        chain = chain && B->fuse && zz_block_decode_fits(B->moe, B->dense, S);
     }
+    if (!chain) {
+        for (int b : k->blocks)
+            if (!block_forward(get_block(b), d_H, S, nullptr, nullptr, st)) return 0;
+        return 1;
+    }
+    ZzDecFinalArgs pend;
+    bool have = false;
+    for (int b : k->blocks) {
+        FfnBlock *B = get_block(b);
+        if (!block_grow(B, S, st)) return 0;
+        float *rows = d_H;
+        if (have) {
+            pend.Hout = pend.H == d_H ? k->alt : d_H;
+            rows = pend.Hout;
+        }
+        ZzDecFinalArgs next;
+        const int r = zz_block_decode(B->moe, B->dense, rows, B->h1, B->h2, B->post_ln, B->ls, S, nullptr,
+                                      nullptr, st, have ? &pend : nullptr, &next);
+        if (r < 0) ZZ_FAIL("zz_stack: block %d left the decode path", b);
+        if (r == 0) return 0;
+        pend = next;
+        have = true;
+    }
+    pend.Hout = d_H;
+    if (!zz_launch_dec_final(pend, S, st)) ZZ_FAIL("zz_stack: final combine launch failed");
     return 1;
 }
 

@@ -93,6 +93,26 @@ struct ZzCombineArgs {
 #define ZZ_DEC_MAXS 4   // largest batch of the fused decode path
 #define ZZ_DEC_LDS 49152  // LDS for the decode down kernel's quantised hidden rows
 
+// Decode tail of a gemma FFN block with the dense branch fused in: both post-norms
+// from their per-tile sums, then Hout = (H + rmsnorm(h1 + h2, post_ffn_ln)) * ls.
+struct ZzDecFinalArgs {
+    int D, G;                   // G = D/16 tiles
+    float eps, ls;
+    const float *out;           // [S, D] routed combine (before post_ffn_ln2)
+    const double *ss;
+    const float *post2;         // post_ffn_ln2
+    const float *yd;            // [S, D] dense down (before post_ffn_ln1)
+    const double *ssd;
+    const float *post1;         // post_ffn_ln1
+    const float *post;          // post_ffn_ln
+    const float *H;             // [S, D] the block's residual input
+    float *Hout;                // [S, D] the result (H itself, or another buffer)
+};
+
+// A block's combine deferred into the next block's router holds S*D <= this many
+// floats in each router workgroup's LDS
+#define ZZ_DEC_FIN_MAXF 12288
+
 // Decode router (two kernels): logits per expert workgroup, then top-k gating and
 // the small-batch dispatch in one workgroup.
 struct ZzDecRouteArgs {
@@ -104,6 +124,8 @@ struct ZzDecRouteArgs {
     int dense;                  // dense branch: norms and quantisation only, no logits
     int dual;                   // also quantise the dense branch's input into prep2
     ZzPrepArgs prep2;           // dual: the dense layer's pre-norm and input buffers
+    int fin;                    // first apply the previous block's combine `fa`: every
+    ZzDecFinalArgs fa;          // workgroup forms the rows, workgroup 0 stores fa.Hout
 };
 
 // Decode gate/up: the routing of each token and the expert GEMVs of its pairs.
@@ -129,21 +151,6 @@ struct ZzDecDownArgs {
     ZzFfnArgs fd;               // the dense layer (nd > 0)
     float *yd;                  // [S, D] its down projection
     double *ssd;                // [S, D/16] per-tile sums of squares of yd
-};
-
-// Decode tail of a gemma FFN block with the dense branch fused in: both post-norms
-// from their per-tile sums, then H = (H + rmsnorm(h1 + h2, post_ffn_ln)) * ls.
-struct ZzDecFinalArgs {
-    int D, G;                   // G = D/16 tiles
-    float eps, ls;
-    const float *out;           // [S, D] routed combine (before post_ffn_ln2)
-    const double *ss;
-    const float *post2;         // post_ffn_ln2
-    const float *yd;            // [S, D] dense down (before post_ffn_ln1)
-    const double *ssd;
-    const float *post1;         // post_ffn_ln1
-    const float *post;          // post_ffn_ln
-    float *H;                   // [S, D] in place
 };
 
 // FlashHead (zz_flash.hip): the tensors of tools/flashhead.py on the device, and one
@@ -183,9 +190,13 @@ int zz_lib_prof_set(int on);        // per-kernel event timing on/off; returns t
 unsigned long long zz_lib_mem_gen();
 void zz_lib_mem_bump();
 // a gemma FFN block's decode rows with the dense branch fused into the routed layer's
-// launches: 1 done, 0 failed, -1 not applicable
+// launches: 1 done, 0 failed, -1 not applicable. pend_in: the previous block's
+// combine, applied by this block's router (d_H must be pend_in->Hout); pend_out: this
+// block's combine is not launched but returned, with Hout left to the caller.
 int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_h2, const float *post_ln,
-                    float ls, int S, int *d_eidx, float *d_ewt, hipStream_t st);
+                    float ls, int S, int *d_eidx, float *d_ewt, hipStream_t st,
+                    const ZzDecFinalArgs *pend_in = nullptr, ZzDecFinalArgs *pend_out = nullptr);
+int zz_block_decode_fits(int moe_id, int dense_id, int S);   // the checks zz_block_decode makes
 // tensor in the slot-table layout at *cursor (advanced past it, 256-aligned)
 ZzTensor zz_make_tensor(int fmt, int O, int I, int64_t *cursor);
 
@@ -207,6 +218,7 @@ int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st);
 int zz_dec_fits(int S, int K, int MI);   // the decode path's LDS holds S*K hidden rows
 int zz_dec_fits2(int S, int K, int MI, int MID);   // ... and S dense hidden rows of MID
 int zz_launch_dec_final(const ZzDecFinalArgs &a, int S, hipStream_t st);
+int zz_dec_fin_fits(int S, int D);   // a deferred combine fits the decode router
 int zz_launch_dec_norm(float *out, const float *post_ln, const double *ss, int D, float eps, int S, hipStream_t st);
 // int8-MFMA grouped GEMM for work items of up to ZZ_MMA_TOKENS tokens
 #define ZZ_MMA_TOKENS 64
