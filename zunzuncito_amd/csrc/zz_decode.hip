@@ -28,7 +28,7 @@ __device__ __forceinline__ int zz_clamp_e(int e, int E) { return e < 0 || e >= E
 // elements' six operands are all loaded before the norms are formed; the rest of a
 // longer row streams.
 template <int NJ>
-__device__ void zz_dec_final_row(const ZzDecFinalArgs &a, int s, float *row, float *rn, double *red, bool store) {
+__device__ void zz_dec_final_row(const ZzDecFinalArgs &a, int s, float *row, double *red, bool store) {
     const int tid = threadIdx.x, D = a.D, G = a.G;
     const float *o2 = a.out + (size_t)s * D, *o1 = a.yd + (size_t)s * D, *hr = a.H + (size_t)s * D;
     float4 y[NJ], w2[NJ], x[NJ], w1[NJ], h[NJ], wv[NJ], t[NJ];
@@ -42,16 +42,17 @@ __device__ void zz_dec_final_row(const ZzDecFinalArgs &a, int s, float *row, flo
         h[j] = *(const float4 *)(hr + o);
         wv[j] = *(const float4 *)(a.post + o);
     }
-    if (tid < 128) {                                 // wave 0: routed, wave 1: dense
-        const int which = tid >> 6, l = tid & 63;
-        const double *ss = (which ? a.ssd : a.ss) + (size_t)s * G;
-        double q = 0.0;
-        for (int k = l; k < G; k += 64) q += ss[k];
-        q = zz_group_sum<64>(q);
-        if (l == 0) rn[which] = 1.0f / sqrtf((float)(q / D) + a.eps);
+    // every wave forms both norm factors itself: the same sums in the same order, whose
+    // totals every lane holds
+    const double *ss2 = a.ss + (size_t)s * G, *ss1 = a.ssd + (size_t)s * G;
+    double q2 = 0.0, q1 = 0.0;
+    for (int k = tid & 63; k < G; k += 64) {
+        q2 += ss2[k];
+        q1 += ss1[k];
     }
-    __syncthreads();
-    const float r2 = rn[0], r1 = rn[1];
+    q2 = zz_group_sum<64>(q2);
+    q1 = zz_group_sum<64>(q1);
+    const float r2 = 1.0f / sqrtf((float)(q2 / D) + a.eps), r1 = 1.0f / sqrtf((float)(q1 / D) + a.eps);
     auto tsum = [&](float4 yv, float4 v2, float4 xv, float4 v1) {
         const float4 h2 = make_float4((yv.x * r2) * v2.x, (yv.y * r2) * v2.y, (yv.z * r2) * v2.z, (yv.w * r2) * v2.w);
         const float4 h1 = make_float4((xv.x * r1) * v1.x, (xv.y * r1) * v1.y, (xv.z * r1) * v1.z, (xv.w * r1) * v1.w);
@@ -121,12 +122,10 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
     __shared__ float rr[DEC_MAXS];
     __shared__ float cert;
     __shared__ __attribute__((aligned(16))) float hrow[FIN ? ZZ_DEC_FIN_MAXF : 4];
-    __shared__ float frn[2];
-    const float *xin = pp.in;
-    if (FIN) {
-        for (int s = 0; s < S; s++) zz_dec_final_row<4>(a.fa, s, hrow + (size_t)s * D, frn, red, e == 0);
-        xin = hrow;
-    }
+    const float *xin = FIN ? hrow : pp.in;
+    auto combine = [&] {
+        for (int s = 0; s < S; s++) zz_dec_final_row<(RB + 3) / 4>(a.fa, s, hrow + (size_t)s * D, red, e == 0);
+    };
     const float rs = 1.0f / sqrtf((float)D);
     if (a.dense && e == 0 && tid < S) {                      // one expert, weight 1
         pp.route_eidx[tid] = 0;
@@ -143,6 +142,7 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < RB; j++) sr[j] = sr[j] * rs;
+        if (FIN) combine();                                   // the router rows are in flight
         for (int s = 0; s < S; s++) {
             const float *x = xin + (size_t)s * D;
             float xr[RB];
@@ -186,8 +186,9 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
             zz_tight_block_scan<RB>(buf, D, lg.bias, e, red, lg.cen + (size_t)s * lg.E + e,
                                 lg.bnd + (size_t)s * lg.E + e);
         }
-    } else if ((tid >> 6) < S) {
-        zz_logit_wave_f64(lg, tid >> 6, e, (double *)sbuf + (tid >> 6) * ZZ_DBUF);
+    } else {
+        if (FIN) combine();
+        if ((tid >> 6) < S) zz_logit_wave_f64(lg, tid >> 6, e, (double *)sbuf + (tid >> 6) * ZZ_DBUF);
     }
     // the expert input quantisation: block g on workgroup g % E, lanes 8(g / E)..+7;
     // dual: blocks S*nb.. are the dense branch's input (same rms factor, its own norm)
@@ -769,10 +770,9 @@ int zz_launch_dec_norm(float *out, const float *post_ln, const double *ss, int D
 // zz_dec_norm_kernel forms it), then the layer combine as zz_block_combine_kernel
 // forms it (gemma4.c:807-808, 1020, 1022-1030). One workgroup per token.
 __global__ __launch_bounds__(256) void zz_dec_final_kernel(ZzDecFinalArgs a) {
-    __shared__ float rn[2];
     __shared__ __attribute__((aligned(16))) float row[ZZ_MAXD];
     __shared__ double red[4];
-    zz_dec_final_row<4>(a, blockIdx.x, row, rn, red, true);
+    zz_dec_final_row<4>(a, blockIdx.x, row, red, true);
 }
 
 int zz_launch_dec_final(const ZzDecFinalArgs &a, int S, hipStream_t st) {
