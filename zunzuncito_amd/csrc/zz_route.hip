@@ -471,7 +471,7 @@ __global__ __launch_bounds__(DP_T) void zz_dispatch_kernel(ZzDispatchArgs a) {
     extern __shared__ unsigned dsm[];
     __shared__ int cnt[ZZ_MAXE], start[ZZ_MAXE], first[ZZ_MAXE], order[ZZ_MAXE], tmp[16];
     __shared__ int xcost[ZZ_MAXE], xof[ZZ_MAXE], xjb[ZZ_MAXE], xslot[9], xrank[ZZ_MAXE], xrc[ZZ_MAXE];
-    __shared__ unsigned xload[8];
+    __shared__ unsigned xload[8], uload[8];
     __shared__ unsigned long long tmp64[16];
     __shared__ int xtotal;
     __shared__ int fbase[DP_PT * DP_T / 32];      // first pairs before each bitmap word
@@ -531,6 +531,7 @@ __global__ __launch_bounds__(DP_T) void zz_dispatch_kernel(ZzDispatchArgs a) {
         const int f = first[t];
         order[fbase[f >> 5] + __popc(fb[f >> 5] & ((1u << (f & 31)) - 1u))] = t;
     }
+    if (t < 8) uload[t] = 0;
     const int nu = __syncthreads_count(present);
     const int ce = t < nu ? cnt[order[t]] : 0;
     const int nit = (ce + a.tch - 1) / a.tch;
@@ -548,14 +549,15 @@ __global__ __launch_bounds__(DP_T) void zz_dispatch_kernel(ZzDispatchArgs a) {
     // XCD balanced as well, max/mean load 1.019 against 1.018 over eight Zipf routings,
     // but took 8 µs of dependent steps; dealing experts in a fixed order, or running each
     // XCD's heavy experts first, measured slower.) Item slot j*8 + x is XCD x's j-th
-    // item. Without an expert of several items, or when no placement of whole experts
-    // balances the XCDs, the items keep union order, item i on XCD i % 8.
+    // item. Without an expert of several items, or when the placement's costliest XCD
+    // would carry more than union order's, the items keep union order, item i on XCD i % 8.
     int cost = 0;
     if (t < nu) {
         cost = a.wcost;
         for (int c = 0; c < nit; c++) {
-            const int n = min(a.tch, ce - c * a.tch);
-            cost += n <= 4 ? 4 : 16 * ((n + 15) >> 4);
+            const int n = min(a.tch, ce - c * a.tch), cols = n <= 4 ? 4 : 16 * ((n + 15) >> 4);
+            cost += cols;
+            atomicAdd(&uload[(i0 + c) & 7], (unsigned)(a.wcost + cols));   // the same in union order
         }
         xcost[t] = cost;
     }
@@ -631,19 +633,20 @@ __global__ __launch_bounds__(DP_T) void zz_dispatch_kernel(ZzDispatchArgs a) {
             xslot[x] = c;
         }
         // a count above 255 carries into the next byte (or out) and breaks the sum.
-        // A placement whose costliest XCD carries more than 5/4 of the mean load (an
-        // expert heavier than an eighth of the batch, as in a dense MLP's one expert,
-        // or fewer experts than XCDs) leaves XCDs idle: union order instead.
-        unsigned long long lmax = 0, lsum = 0;
+        // The placement is kept when its costliest XCD carries no more than union
+        // order's would, where an expert pays its weight stream on every XCD that
+        // runs one of its items. (A dense MLP's one expert of 8 items, or fewer
+        // experts than XCDs, would leave XCDs idle: union order.)
+        unsigned pmax = 0, umax = 0;
         for (int x = 0; nm > 0 && x < 8; x++) {
-            lmax = max(lmax, (unsigned long long)xload[x]);
-            lsum += xload[x];
+            pmax = max(pmax, xload[x]);
+            umax = max(umax, uload[x]);
         }
-        xslot[8] = sum == xtotal && nm > 0 && 32 * lmax <= 5 * lsum ? mx : 1 << 30;
+        xslot[8] = sum == xtotal && nm > 0 && pmax <= umax ? mx : 1 << 30;
     }
     __syncthreads();
-    // a placement past the grid's slots per XCD (never at realistic routings) or an
-    // unbalanced one: items in union order instead, item i on XCD i % 8, which always fits
+    // a placement past the grid's slots per XCD (never at realistic routings) or a
+    // costlier one: items in union order instead, item i on XCD i % 8, which always fits
     const int ms = xslot[8];
     const bool placed = ms <= a.xslots;
     if (t < nu) {
