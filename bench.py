@@ -210,6 +210,11 @@ def build_cfg_layers(zz, torch, name, n_layers, seed):
 def time_steps(torch, layers, xs, out, S, steps, warmup):
     st = torch.cuda.current_stream()
     L = len(layers)
+    # every rotated layer runs once before the timed loop, whatever `warmup` is: a
+    # layer's first forward at a batch size sizes its workspace (hipMalloc and two
+    # stream synchronisations), which must not fall between the timing events
+    for i, m in enumerate(layers):
+        m.forward_dev(xs[i % len(xs)].data_ptr(), out.data_ptr(), S, stream=st.cuda_stream)
     for i in range(warmup):
         layers[i % L].forward_dev(xs[i % len(xs)].data_ptr(), out.data_ptr(), S,
                                   stream=st.cuda_stream)
@@ -421,7 +426,9 @@ def cpu_baseline(zz, torch, host, seed, n_layers):
     main_ = r[f"t{cores}_s512"]
     return dict(value=main_["tokens_per_s"], unit="tokens/s", cores=cores, kind="reference",
                 variant=r["variant"],
-                sample=f"gemma4.c moe_start+moe_finish (oracle/_ref, {r['variant']} OpenMP), S=512, "
+                sample=f"gemma4.c moe_start+moe_finish (oracle/_ref, {r['variant']} OpenMP, built "
+                       f"gcc -O3 -march=x86-64-v3 -mavx2 -mfma -fopenmp: the reference's AVX2 kernel "
+                       f"path; its own Makefile's -march=native takes the same path), S=512, "
                        f"median of {main_['reps']} calls after 3 warm-ups, rotating over "
                        f"{n_layers} layers' experts preloaded in RAM; Zipf(1.1) routing via "
                        f"input column 0 (mean union {main_['mean_union_experts']:.1f} experts)",

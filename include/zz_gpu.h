@@ -9,18 +9,17 @@
  *
  * Differences forced by a discrete GPU, all inside the same contract:
  *  - gpu_map() cannot wrap host pages without a copy (gpu.h:66-69 "NO copy" is a
- *    unified-memory property). It uploads the range into HBM when called, and
- *    bytes written to the host range afterwards are not seen until that range is
- *    mapped again: mapping a range inside an existing mapping re-uploads those
- *    bytes; a range that only overlaps older mappings replaces them (the host
- *    memory was reused).
- *    The engines map each expert slot once, while it is still empty
- *    (gemma4.c:2051-2058, lfm25.c:1894, maple.c:1322, ling.c:1873), and then pread
- *    other experts into it (gemma4.c:484-491). Linked unchanged, their per-row
- *    expert matmuls (gemma4.c:670-684) would read the bytes the slot held at map
- *    time. Each engine therefore needs one added line: gpu_map(slot->buf, esz) on
- *    the main thread after a slot is refilled and before its first matmul. The
- *    dense blob (gemma4.c:348), mapped once after it is read, needs nothing.
+ *    unified-memory property). It uploads the range into HBM when called and keeps
+ *    a sampled fingerprint of it (the 8 bytes at every 256-byte step). The engines
+ *    map each expert slot once, while it is still empty (gemma4.c:2051-2058,
+ *    lfm25.c:1894, maple.c:1322, ling.c:1873), and then pread other experts into it
+ *    (gemma4.c:484-491). gpu_matmul() therefore compares the tensor's samples with
+ *    those of its last upload and, where the host bytes changed, uploads the tensor
+ *    again before computing: an engine linked unchanged computes on the expert it
+ *    just read. A rewrite that changes none of the sampled words is not seen (an
+ *    expert record read over another differs in essentially all of them); mapping
+ *    a range inside an existing mapping re-uploads it explicitly. A range that only
+ *    overlaps older mappings replaces them (the host memory was reused).
  *  - gpu_matmul() copies x in and y out per call (PCIe), then runs a dequantising
  *    GEMV with f32 activations: the *_dot_f32 semantics (gpu.h:25-27), checked to
  *    < 1e-4 relative like gemma4.c:2315-2368.

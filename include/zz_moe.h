@@ -193,6 +193,12 @@ int zz_router_expf(const float *d_x, float *d_y, int64_t n, void *stream);
 int zz_moe_profile(int on);
 int zz_moe_profile_read(double *ms, int *launches, int n);
 
+/* Diagnostic: how many times gpu_matmul (zz_gpu.h) found a mapped tensor rewritten
+ * on the host since its last upload (its sampled fingerprint changed) and uploaded
+ * it again before computing. The engines pread other experts into mapped slots
+ * (gemma4.c:484-491); this counts those refreshes. */
+long long zz_gpu_map_refreshes(void);
+
 /* Text of the last failure (a declined call), or "". */
 const char *zz_last_error(void);
 

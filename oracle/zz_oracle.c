@@ -139,10 +139,16 @@ void orc_q40_dequant_row(const uint8_t *src, float *w, int I) {
     }
 }
 
+/* Test-only planted mistakes (zz_oracle.h lists them); 0 everywhere else. */
+static int g_plant = 0;
+void orc_set_plant(int plant) { g_plant = plant; }
+
+/* q40.h:349-356: w = d * q per block. Pinned against the compiled reference's
+ * q80_dequant_row and against numpy's float16 decode of the scale times the codes. */
 void orc_q80_dequant_row(const uint8_t *src, float *w, int I) {
     for (int b = 0; b < I / BLK; b++) {
         const uint8_t *blk = src + (size_t)b * 34;
-        float d = blk_scale(blk);
+        float d = blk_scale(g_plant == 5 && b > 0 ? blk - 34 : blk);
         for (int j = 0; j < BLK; j++) w[b * BLK + j] = d * (float)(int8_t)blk[2 + j];
     }
 }
@@ -454,18 +460,33 @@ void orc_route(const orc_cfg *c, const orc_weights *w, const float *x,
         orc_rmsnorm(xn, x, NULL, D, c->eps);
         float rs = 1.0f / sqrtf((float)D);
         for (int i = 0; i < D; i++) xn[i] *= w->router_scale[i] * rs;
+        /* The harness's Zipf offset is one float add after the in-order
+         * chain, v = fl(chain + bias[e]); selection and softmax both see v. The
+         * reference router has no offset (gemma4.c:600-601). sel/soft differ only
+         * under a planted mistake. */
+        const int zb = c->use_bias && w->bias;
+        float *soft = (float *)malloc(sizeof(float) * (size_t)E);
         for (int e = 0; e < E; e++) {
             const float *r = w->router + (size_t)e * D;
-            float v = 0.0f;
-            for (int i = 0; i < D; i++) v += r[i] * xn[i];   /* in order, unfused */
-            if (c->use_bias && w->bias) v += w->bias[e];     /* harness Zipf offset */
-            if (logits_out) logits_out[e] = v;
-            topk_insert(v, e, K, topv, idx);
+            const float b = zb ? w->bias[e] : 0.0f;
+            float v = (zb && g_plant == 1) ? b : 0.0f;
+            for (int i = 0; i < D; i++) {
+                if (zb && g_plant == 2 && i == D - 1) v += b;
+                v += r[i] * xn[i];                           /* in order, unfused */
+            }
+            float sel = v, sv = v;
+            if (zb && g_plant == 0) sel = sv = v + b;
+            if (zb && g_plant == 3) sv = v + b;
+            if (zb && g_plant == 4) sel = v + b;
+            soft[e] = sv;
+            if (logits_out) logits_out[e] = sel;
+            topk_insert(sel, e, K, topv, idx);
         }
         free(xn);
-        float sum = 0.0f, mx = topv[0];
-        for (int j = 0; j < K; j++) { wts[j] = expf(topv[j] - mx); sum += wts[j]; }
+        float sum = 0.0f, mx = soft[idx[0]];
+        for (int j = 0; j < K; j++) { wts[j] = expf(soft[idx[j]] - mx); sum += wts[j]; }
         for (int j = 0; j < K; j++) wts[j] = (wts[j] / sum) * w->pes[idx[j]];
+        free(soft);
     } else if (c->gating == ORC_GATE_LFM) {
         /* lfm25.c:636-668 */
         float *sg = (float *)malloc(sizeof(float) * (size_t)E);

@@ -120,6 +120,14 @@ void  orc_rmsnorm(float *o, const float *x, const float *w, int D, float eps);
 float orc_act(int act, float g, float u, float clamp);
 
 /* ---- A10-A12: routers, one token ---- */
+/* Planted mistakes, for tests that show a pin rejects a plausible slip (0 = the
+ * faithful oracle; anything else is never used outside those tests):
+ *   1  gemma Zipf offset as the chain's starting value (added first, not last)
+ *   2  gemma Zipf offset added before the chain's last product
+ *   3  gemma Zipf offset in the softmax only (selection on unbiased logits)
+ *   4  gemma Zipf offset in the selection only (softmax on unbiased logits)
+ *   5  q8_0 dequantisation with the block scale of the previous block */
+void orc_set_plant(int plant);
 void orc_route(const orc_cfg *c, const orc_weights *w, const float *x,
                int *idx, float *wts, float *logits_out);
 

@@ -171,10 +171,24 @@ def flash_cases():
     np.savez(os.path.join(HERE, "gemma_flash_head.npz"), **out)
 
 
+def zipf_cases():
+    """configs[1]'s Zipf-offset router at the Gemma-4 shape. The reference router has
+    no offset (gemma4.c:600-601); zzref.zipf_pin_case carries it in the reference
+    layer's last router column, whose product is exactly the offset, so the
+    reference computes fl(chain + offset) as the configs[1] harness defines it."""
+    c = dict(Z.ZIPF_PIN)
+    Lo, Lr, x = Z.zipf_pin_case(**c)
+    r = Z.ref_moe(Lr, x)
+    np.savez(os.path.join(HERE, "gemma_zipf_e128_s8.npz"), digest=input_digest(Lr, x),
+             out=r.out, eidx=r.eidx, ewt=r.ewt, uniq=r.uniq, **{f"case_{k}": v for k, v in c.items()})
+    print("gemma_zipf_e128_s8 nu", len(r.uniq), "ids", r.eidx[:8].tolist())
+
+
+ALL = dict(kernels=kernel_cases, layers=layer_cases, gemma=gemma_cases, flash=flash_cases,
+           zipf=zipf_cases)
+
 if __name__ == "__main__":
     if Z.ref_lib("gemma4") is None:
         sys.exit("oracle/_ref is not built (needs /root/reference): run `make -C oracle`")
-    kernel_cases()
-    layer_cases()
-    gemma_cases()
-    flash_cases()
+    for name in (sys.argv[1:] or list(ALL)):      # e.g. `make_golden.py zipf`
+        ALL[name]()

@@ -134,6 +134,36 @@ static void ranges() {
     CHECK(n == 2 && g.size() == 0);
 }
 
+// the sampled fingerprint of a mapping: taken after an upload, compared before use
+static void fingerprints() {
+    static uint8_t buf[10000];
+    for (size_t i = 0; i < sizeof buf; i++) buf[i] = (uint8_t)(i * 131 + 7);
+    uint8_t *A = (uint8_t *)0x1000;
+    ZzRanges g;
+    ZzRange &m = g.add(buf, sizeof buf, A);
+    zz_fp_take(m, 0, sizeof buf);
+    CHECK(m.fp.size() == (sizeof buf - 8) / ZZ_FP_STRIDE + 1);
+    CHECK(!zz_fp_changed(m, 0, sizeof buf) && !zz_fp_changed(m, 300, 4000));
+    buf[5 * ZZ_FP_STRIDE + 3] ^= 1;                 // inside sample 5
+    CHECK(zz_fp_changed(m, 0, sizeof buf) && zz_fp_changed(m, 5 * ZZ_FP_STRIDE, 8));
+    CHECK(!zz_fp_changed(m, 6 * ZZ_FP_STRIDE, 3000));           // a tensor after it: untouched
+    CHECK(!zz_fp_changed(m, 5 * ZZ_FP_STRIDE + 1, 500));        // sample 5 not wholly inside
+    zz_fp_take(m, 4 * ZZ_FP_STRIDE, 2 * ZZ_FP_STRIDE);          // that sub-range re-uploaded
+    CHECK(!zz_fp_changed(m, 0, sizeof buf));
+    buf[sizeof buf - 1] ^= 1;                       // past the last sample: not seen
+    CHECK(!zz_fp_changed(m, 0, sizeof buf));
+    buf[(m.fp.size() - 1) * ZZ_FP_STRIDE] ^= 1;     // the last sample
+    CHECK(zz_fp_changed(m, 0, sizeof buf));
+    // empty and short ranges: no sample, nothing read out of bounds
+    CHECK(!zz_fp_changed(m, sizeof buf, 0) && !zz_fp_changed(m, sizeof buf - 7, 7));
+    zz_fp_take(m, sizeof buf - 4, 4);
+    static uint8_t tiny[5];
+    ZzRange &t = g.add(tiny, sizeof tiny, A);
+    zz_fp_take(t, 0, sizeof tiny);
+    CHECK(t.fp.empty() && !zz_fp_changed(t, 0, sizeof tiny));
+    g.clear([](const ZzRange &) {});
+}
+
 int main(int argc, char **argv) {
     if (argc != 2) {
         fprintf(stderr, "usage: %s <scratch directory>\n", argv[0]);
@@ -142,6 +172,7 @@ int main(int argc, char **argv) {
     g_dir = argv[1];
     manifests();
     ranges();
+    fingerprints();
     printf("host_check %s (%d failures)\n", fails ? "FAILED" : "ok", fails);
     return fails ? 1 : 0;
 }

@@ -257,12 +257,20 @@ def test_stack_prefill_and_greedy_decode_on_device(dev):
         close_all(*objs)
 
 
-def test_stack_runner_graph_equals_eager(dev):
+@pytest.mark.parametrize("n_blocks", [2, 3])
+def test_stack_runner_graph_equals_eager(dev, n_blocks):
     """zz_stack_*: prefill equals the blocks run one by one; greedy decode replayed
     from a captured HIP graph equals eager launches bit for bit, on every step of
-    three calls with eager work and host synchronisations between the replays."""
+    three calls with eager work and host synchronisations between the replays. The
+    residual stream alternates between two buffers as each block's combine is
+    deferred into the next block: with 3 blocks the last combine writes the caller's
+    buffer after it served as a router input, with 2 it ends in the second buffer."""
     import torch
     *_, st, H0 = Z.gemma_block_case()
+    if n_blocks != len(st.layers):
+        D_, MI_, E_, K_, DI_, V_, seed_ = Z.GEMMA_SHAPE
+        st = Z.make_stack(n_blocks, D_, MI_, E_, K_, DI_, V_, seed_)
+        st.embed_scale = Z.GEMMA_STACK["embed_scale"]
     D, V = st.layers[0].D, st.V
     blocks, objs = [], []
     for L_, dn in zip(st.layers, st.denses):

@@ -89,6 +89,29 @@ def test_golden_layer(dev, name, layer_cache):
         m.close()
 
 
+def test_golden_zipf_layer(dev):
+    """configs[1]'s Zipf-offset routing at the Gemma-4 shape against the fixture the
+    compiled reference wrote (its last router column carries the offset exactly,
+    zzref.zipf_pin_case): the batch on the matrix-core path and each token alone on
+    the decode path. Ids exact, outputs within the fp32 tier."""
+    g = np.load(os.path.join(Z.ROOT, "tests", "golden", "gemma_zipf_e128_s8.npz"))
+    Lo, _, x = Z.zipf_pin_case(**Z.ZIPF_PIN)
+    m = gpu_layer(Lo)
+    try:
+        K = Lo.K
+        want = Z.MoeResult(g["out"], g["eidx"], g["ewt"], g["uniq"])
+        say("case zipf S=8")
+        _, _, _, err = check_layer(m, Lo, x, want)
+        assert np.array_equal(m.debug(x.shape[0])["uniq"], g["uniq"])
+        say(f"  out rel L2 {err:.2e}")
+        for s in range(x.shape[0]):
+            say(f"case zipf token {s} (S=1)")
+            w1 = Z.MoeResult(g["out"][s:s + 1], g["eidx"][s * K:(s + 1) * K], g["ewt"][s * K:(s + 1) * K], None)
+            check_layer(m, Lo, x[s:s + 1], w1)
+    finally:
+        m.close()
+
+
 # D % 256 == 0 takes 256-wide K chunks, other D % 64 == 0 the 64-wide ones
 @pytest.mark.parametrize("kind,kw,S", [
     ("gemma", dict(), 64), ("gemma", dict(zipf=True, E=64), 37), ("gemma", dict(D=1088, E=64), 16),
@@ -188,8 +211,9 @@ def _lcg_check_gpu(O, I, t):
                                    (3, 2816, 2112), (4, 704, 2816), (5, 2816, 704)])
 def test_check_gpu_shapes(dev, t, O, I):
     """gemma4.c:2315-2368 --check-gpu: gpu_q40_matmul vs q40_dot_f32 at the engine's
-    shapes, max|d| / max|ref| < 1e-4 (rows whose random fp16 scale is NaN/inf drop
-    out of the reference's comparisons, here too)."""
+    shapes, max|d| / max|ref| < 1e-4 over the finite rows. Rows whose random fp16
+    scale is NaN or inf must be non-finite in the same way (NaN where the reference
+    has NaN, the same infinity otherwise): both scale each block's sum by d once."""
     say("check_gpu", O, I)
     W, x = _lcg_check_gpu(O, I, t)
     Wm = zz.gpu_map(W)
@@ -198,9 +222,13 @@ def test_check_gpu_shapes(dev, t, O, I):
                                    x.ctypes.data_as(zz._f32p), O, I, 1) == 1
     ref = np.zeros((1, O), np.float32)
     Z.oracle().orc_matmul_f32(Z.FMT_Q40, Z.ptr(ref), Z.ptr(Wm), Z.ptr(x), O, I, 1)
-    fin = np.isfinite(ref[0]) & np.isfinite(y[0])
+    fin = np.isfinite(ref[0])
+    assert np.array_equal(np.isfinite(y[0]), fin), "finite rows differ"
+    nan = np.isnan(ref[0])
+    assert np.array_equal(np.isnan(y[0]), nan), "NaN rows differ"
+    assert np.array_equal(y[0][~fin & ~nan], ref[0][~fin & ~nan]), "infinite rows differ"
     rel = np.abs(y[0] - ref[0])[fin].max() / (np.abs(ref[0][fin]).max() + 1e-9)
-    say(f"  max rel err {rel:.3e}")
+    say(f"  max rel err {rel:.3e}, {int((~fin).sum())} non-finite rows")
     assert rel < 1e-4
 
 
@@ -222,35 +250,47 @@ def test_gpu_matmul_other_formats(dev, fmt):
     assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-4
 
 
-def test_gpu_map_slot_refill_needs_a_remap(dev):
+def test_gpu_map_slot_refill_is_seen(dev):
     """The engines map an expert slot once, while empty (gemma4.c:2051-2058), then
-    pread other experts into the same bytes (gemma4.c:484-491). A discrete GPU
-    copies at map time, so gpu_matmul keeps using the bytes of the last upload until
-    the rewritten range is mapped again; mapping a sub-range of an existing mapping
-    re-uploads just that range."""
+    pread other experts into the same bytes (gemma4.c:484-491). A discrete GPU copies
+    at map time; gpu_matmul compares the tensor's sampled fingerprint with the one
+    of its last upload and uploads it again when the host bytes changed, so an
+    unchanged engine computes on the expert it just read. Unchanged bytes are not
+    uploaded again, and an explicit re-map still refreshes a sub-range."""
     rng = np.random.default_rng(43)
     O, I = 256, 512
     rb = O * (I // 32) * 18
     slot = np.zeros(2 * rb, np.uint8)               # two tensors in one mapped slot
     A = Z.quant_rows(Z.FMT_Q40, (rng.standard_normal((O, I)) * 0.02).astype(np.float32))
     Bw = Z.quant_rows(Z.FMT_Q40, (rng.standard_normal((O, I)) * 0.02).astype(np.float32))
+    Cw = Z.quant_rows(Z.FMT_Q40, (rng.standard_normal((O, I)) * 0.02).astype(np.float32))
     slot[:rb] = A
+    slot[rb:] = Cw
     Wm = zz.gpu_map(slot)
     x = rng.standard_normal((1, I)).astype(np.float32)
+    L = zz.lib()
 
     def ref(W):
         y = np.zeros((1, O), np.float32)
         Z.oracle().orc_matmul_f32(Z.FMT_Q40, Z.ptr(y), Z.ptr(np.ascontiguousarray(W)), Z.ptr(x), O, I, 1)
         return y
 
-    ya = zz.gpu_matmul(Z.FMT_Q40, Wm[:rb], x, O, I)
-    assert np.abs(ya - ref(A)).max() / np.abs(ref(A)).max() < 1e-4
+    def rel(y, W):
+        return np.abs(y - ref(W)).max() / np.abs(ref(W)).max()
+
+    n0 = L.zz_gpu_map_refreshes()
+    assert rel(zz.gpu_matmul(Z.FMT_Q40, Wm[:rb], x, O, I), A) < 1e-4
+    assert rel(zz.gpu_matmul(Z.FMT_Q40, Wm[rb:], x, O, I), Cw) < 1e-4
+    assert L.zz_gpu_map_refreshes() == n0            # unchanged: nothing uploaded again
     Wm[:rb] = Bw                                    # the "pread" of another expert
-    stale = zz.gpu_matmul(Z.FMT_Q40, Wm[:rb], x, O, I)
-    assert np.array_equal(stale, ya)                # not re-mapped: the old bytes
-    assert zz.lib().gpu_map(C.c_void_p(Wm.ctypes.data), rb) == 1   # refresh the sub-range
-    yb = zz.gpu_matmul(Z.FMT_Q40, Wm[:rb], x, O, I)
-    assert np.abs(yb - ref(Bw)).max() / np.abs(ref(Bw)).max() < 1e-4
+    assert rel(zz.gpu_matmul(Z.FMT_Q40, Wm[:rb], x, O, I), Bw) < 1e-4
+    assert L.zz_gpu_map_refreshes() == n0 + 1
+    assert rel(zz.gpu_matmul(Z.FMT_Q40, Wm[rb:], x, O, I), Cw) < 1e-4
+    assert L.zz_gpu_map_refreshes() == n0 + 1        # the other tensor was untouched
+    Wm[:rb] = A
+    assert L.gpu_map(C.c_void_p(Wm.ctypes.data), rb) == 1   # an explicit refresh
+    assert rel(zz.gpu_matmul(Z.FMT_Q40, Wm[:rb], x, O, I), A) < 1e-4
+    assert L.zz_gpu_map_refreshes() == n0 + 1
 
 
 def test_gpu_matmul_declines_unmapped_and_bad_shapes(dev):
@@ -304,24 +344,40 @@ def test_maple_check_gpu_shapes(dev, t, fmt, O, I):
     assert rel < 1e-4
 
 
-def test_every_token_tile_count(dev, layer_cache):
-    """Work items of every shape against the oracle: gemma with 8 experts and top-2 at
-    S = 12 .. 300 puts 3 .. 80 tokens on an expert, so the <= 4-token path, items of
-    1, 2, 3 and 4 token tiles of 16, and experts split over two items all run."""
-    L = layer_cache("gemma", seed=11, E=8, K=2)
+def _item_buckets(eidx, E):
+    """The FFN body each work item takes: <= 4 tokens "tiny" (4x4x4, one token set),
+    5-8 "two-set" (4x4x4 with two sets, q4_0; other formats the 16-token body), else
+    the number of 16-token tiles; experts of more than 64 tokens split into items."""
+    seen = set()
+    for c in np.bincount(eidx, minlength=E):
+        for n in [64] * (c // 64) + [c % 64]:
+            if n:
+                seen.add("tiny" if n <= 4 else "two-set" if n <= 8 else (n + 15) // 16)
+    return seen
+
+
+@pytest.mark.parametrize("kind,kw,sizes", [
+    ("gemma", dict(E=8, K=2), (12, 24, 100, 160, 200, 300)),
+    # q4_0 gate/up and q8_0 down: items of 5-8 tokens take the two-set body for
+    # gate/up and the 16-token body for down
+    ("lfm", dict(E=8, K=2, D=1024, MI=512), (12, 24, 100, 200))])
+def test_every_token_tile_count(dev, kind, kw, sizes, layer_cache):
+    """Work items of every shape against the oracle: 8 experts and top-2 at S = 12 ..
+    300 put 3 .. 80 tokens on an expert, so items of <= 4 tokens, of 5-8, of 1, 2, 3
+    and 4 token tiles of 16, and experts split over two items all run."""
+    L = layer_cache(kind, seed=11, **kw)
     m = gpu_layer(L)
     seen = set()
     try:
-        for S in (12, 24, 100, 160, 200, 300):
+        for S in sizes:
             x = Z.make_input(L, S, 7)
             want = Z.oracle_moe(L, x)
-            for c in np.bincount(want.eidx, minlength=L.E):
-                for n in [64] * (c // 64) + [c % 64]:
-                    if n:
-                        seen.add("tiny" if n <= 4 else (n + 15) // 16)
+            seen |= _item_buckets(want.eidx, L.E)
+            say(f"case {kind} S={S}")
             out, eidx, ewt, err = check_layer(m, L, x, want)
             say(f"  S={S} out rel L2 {err:.2e}")
-        assert seen >= {"tiny", 1, 2, 3, 4}, seen
+        need = {"tiny", "two-set", 1, 2, 3, 4} if kind == "gemma" else {"tiny", "two-set", 1}
+        assert seen >= need, seen
     finally:
         m.close()
 

@@ -475,7 +475,7 @@ def test_dispatch_is_stable_counting_sort(layer_cache):
 # whole-MoE-layer fixtures (the kernel vectors and the gemma block/stack fixture have
 # their own tests)
 CASES = sorted(f[:-4] for f in os.listdir(GOLDEN)
-               if f.endswith(".npz") and not f.startswith(("kernels", "gemma_block", "gemma_flash")))
+               if f.endswith(".npz") and not f.startswith(("kernels", "gemma_block", "gemma_flash", "gemma_zipf")))
 
 
 def load_case(name):
@@ -567,3 +567,166 @@ def test_tensor_sizes():
         assert L.orc_tensor_bytes(Z.FMT_Q80, 7, I) == 7 * (I // 32) * 34
         for f in (Z.FMT_Q40, Z.FMT_Q80, Z.FMT_TQ2, Z.FMT_Q4A):
             assert L.orc_tensor_bytes(f, 7, I) == Z.tensor_bytes(f, 7, I)
+
+
+# ------------------------------------------- the gemma Zipf offset
+def _route_oracle(D, E, K, router, rscale, pes, bias, x):
+    cfg = Z.OrcCfg(D, 64, E, K, Z.GATE_GEMMA, Z.ACT_GEGLU_TANH, 1, 1, 1, 1,
+                   0 if bias is None else 1, 0.0, 1.0, 7.0, 1, 1)
+    w = Z.OrcWeights(Z.ptr(router), Z.ptr(rscale), Z.ptr(pes), Z.ptr(bias), None, None, None, 0)
+    S = x.shape[0]
+    ids = np.zeros((S, K), np.int32)
+    wts = np.zeros((S, K), np.float32)
+    lg = np.zeros((S, E), np.float32)
+    for s in range(S):
+        Z.oracle().orc_route(C.byref(cfg), C.byref(w), Z.ptr(np.ascontiguousarray(x[s])), Z.ptr(ids[s]),
+                             Z.ptr(wts[s]), Z.ptr(lg[s]))
+    return ids, wts, lg
+
+
+def _route_ref(D, E, K, router, rscale, pes, x):
+    R = Z.ref_lib("gemma4")
+    R.ref_g4_route.argtypes = [C.c_int, C.c_int, C.c_int, C.c_float, Z.f32p, Z.f32p, Z.f32p, Z.f32p,
+                               Z.i32p, Z.f32p]
+    S = x.shape[0]
+    ids = np.zeros((S, K), np.int32)
+    wts = np.zeros((S, K), np.float32)
+    for s in range(S):
+        assert R.ref_g4_route(D, E, K, 0.0, Z.ptr(router), Z.ptr(rscale), Z.ptr(pes),
+                              Z.ptr(np.ascontiguousarray(x[s])), Z.ptr(ids[s]), Z.ptr(wts[s])) == 0
+    return ids, wts
+
+
+ZIPF_PAD = 32
+
+
+def _zipf_route_case(D=1024, E=32, K=8, S=24, seed=51):
+    """The oracle's biased router at D against the reference's unbiased route_row at
+    D' = D + 32 (gemma4.c:581-613), the offset carried by the last extra element.
+
+    With every input element +-1 and eps = 0 both rmsnorm factors are exactly 1
+    (gemma4.c:428). The reference's router inputs are c_i = fl(rscale'_i * rs') with
+    rs' = 1/sqrtf(D'); the oracle gets rscale_i = 32 c_i, so at rs = 1/sqrtf(1024)
+    = 1/32 its inputs are the same c_i. Extra elements D .. D'-2 have router weight 0
+    (each adds an exact +0). The last (x = 1, rscale' = 1) is rs' exactly, and its
+    router weight q_e = fl(zipf_e / rs') makes the reference's last product
+    bias_e = fl(q_e * rs'). The reference's logit is then fl(chain_D + bias_e): the
+    offset added once, after the chain. D' stays a multiple of 32: the compiled
+    reference adds its vectorised products unfused, but fuses the scalar remainder
+    of the loop (the last D' mod 4 products), which a D + 1 layout would hit."""
+    assert D == 1024
+    P = ZIPF_PAD
+    rng = np.random.default_rng(seed)
+    rsr = np.float32(1.0) / np.sqrt(np.float32(D + P))
+    rsc_ref = np.ones(D + P, np.float32)
+    rsc_ref[:D] = (1 + 0.05 * rng.standard_normal(D)).astype(np.float32)
+    c = (rsc_ref[:D] * rsr).astype(np.float32)
+    rsc = (c * np.float32(32)).astype(np.float32)
+    router = rng.standard_normal((E, D), dtype=np.float32)
+    zipf = (-1.1 * np.log(rng.permutation(E) + 1)).astype(np.float32)
+    q = (zipf / rsr).astype(np.float32)
+    bias = (q * rsr).astype(np.float32)
+    router_ref = np.zeros((E, D + P), np.float32)
+    router_ref[:, :D] = router
+    router_ref[:, D + P - 1] = q
+    pes = (1 + 0.1 * rng.random(E)).astype(np.float32)
+    x = Z.pm1_input(S, D, seed, last_one=False)
+    x_ref = np.ascontiguousarray(np.concatenate([x, np.ones((S, P), np.float32)], axis=1))
+    return D, E, K, router, rsc, pes, bias, x, router_ref, rsc_ref, x_ref
+
+
+def test_gemma_zipf_offset_equals_reference_last_product():
+    """The Zipf-offset branch (zz_oracle.c, gemma) equals the compiled reference bit for
+    bit: ids and softmax weights, which both see the offset logits. Its logits are
+    fl(unbiased chain + offset), and its ids a lower-index-tie argsort of them."""
+    if Z.ref_lib("gemma4") is None:
+        pytest.skip("oracle/_ref not built here")
+    D, E, K, router, rsc, pes, bias, x, router_ref, rsc_ref, x_ref = _zipf_route_case()
+    ids, wts, lg = _route_oracle(D, E, K, router, rsc, pes, bias, x)
+    rid, rwt = _route_ref(D + ZIPF_PAD, E, K, router_ref, rsc_ref, pes, x_ref)
+    assert np.array_equal(ids, rid)
+    assert np.array_equal(wts.view(np.uint32), rwt.view(np.uint32))
+    _, _, lg0 = _route_oracle(D, E, K, router, rsc, pes, None, x)
+    assert np.array_equal(lg.view(np.uint32), (lg0 + bias).astype(np.float32).view(np.uint32))
+    for s in range(x.shape[0]):
+        assert list(ids[s]) == sorted(range(E), key=lambda e: (-float(lg[s, e]), e))[:K]
+    # the offset moves the choice: the pin is not vacuous
+    ids0, _, _ = _route_oracle(D, E, K, router, rsc, pes, None, x)
+    assert not np.array_equal(ids0, ids)
+
+
+@pytest.mark.parametrize("plant", [1, 2, 3, 4])
+def test_gemma_zipf_offset_pin_rejects_planted_slips(plant):
+    """Each plausible slip in the offset branch fails the reference pin: the offset as
+    the chain's first term (1), before the chain's last product (2), in the softmax
+    only (3), in the selection only (4)."""
+    if Z.ref_lib("gemma4") is None:
+        pytest.skip("oracle/_ref not built here")
+    D, E, K, router, rsc, pes, bias, x, router_ref, rsc_ref, x_ref = _zipf_route_case()
+    rid, rwt = _route_ref(D + ZIPF_PAD, E, K, router_ref, rsc_ref, pes, x_ref)
+    Z.oracle().orc_set_plant(plant)
+    try:
+        ids, wts, _ = _route_oracle(D, E, K, router, rsc, pes, bias, x)
+    finally:
+        Z.oracle().orc_set_plant(0)
+    assert not (np.array_equal(ids, rid) and np.array_equal(wts.view(np.uint32), rwt.view(np.uint32)))
+
+
+def test_gemma_zipf_layer_golden():
+    """A whole Zipf-offset layer at the Gemma-4 shape (configs[1]: D=2816, 128 experts,
+    top-8) bit for bit against the fixture the compiled reference wrote, with the
+    offset in the reference's last router column (zzref.zipf_pin_case)."""
+    from golden.make_golden import input_digest
+    g = np.load(os.path.join(GOLDEN, "gemma_zipf_e128_s8.npz"))
+    Lo, Lr, x = Z.zipf_pin_case(**Z.ZIPF_PIN)
+    assert input_digest(Lr, x) == str(g["digest"]), "input generator drifted from the fixture"
+    r = Z.oracle_moe(Lo, x)
+    assert np.array_equal(r.eidx, g["eidx"])
+    assert np.array_equal(r.uniq, g["uniq"])
+    assert np.array_equal(r.ewt.view(np.uint32), g["ewt"].view(np.uint32))
+    assert np.array_equal(r.out.view(np.uint32), g["out"].view(np.uint32))
+    if Z.ref_lib("gemma4") is not None:        # and live
+        b = Z.ref_moe(Lr, x)
+        assert np.array_equal(b.eidx, g["eidx"]) and np.array_equal(b.out.view(np.uint32), g["out"].view(np.uint32))
+
+
+# ------------------------------------------------------------ q8_0 dequant (A7)
+def _q80_rows(rng, O, I):
+    q = Z.quant_rows(Z.FMT_Q80, (rng.standard_normal((O, I)) * 0.05).astype(np.float32)).reshape(-1, 34)
+    # special scales: NaN, +-inf, -0, subnormal halves
+    for k, h in enumerate([0x7e00, 0x7c00, 0xfc00, 0x8000, 0x0001, 0x03ff]):
+        q[3 * k + 1, 0], q[3 * k + 1, 1] = h & 255, h >> 8
+    return q.reshape(-1)
+
+
+def test_q80_dequant_matches_reference_and_closed_form():
+    """orc_q80_dequant_row (q40.h:349-356) against numpy (fp16 scale times the int8
+    code, one float rounding) and the compiled reference's q80_dequant_row."""
+    L = Z.oracle()
+    L.orc_q80_dequant_row.argtypes = [Z.u8p, Z.f32p, C.c_int]
+    rng = np.random.default_rng(61)
+    O, I = 8, 2816
+    q = _q80_rows(rng, O, I)
+    got = np.zeros(O * I, np.float32)
+    L.orc_q80_dequant_row(Z.ptr(q), Z.ptr(got), O * I)
+    blk = q.reshape(-1, 34)
+    d = blk[:, :2].copy().view(np.float16).astype(np.float32)
+    with np.errstate(invalid="ignore"):              # inf * 0
+        want = (d * blk[:, 2:].view(np.int8).astype(np.float32)).astype(np.float32).reshape(-1)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+    R = Z.ref_lib("kernels")
+    if R is not None:
+        ref = np.zeros(O * I, np.float32)
+        R.ref_q80_dequant_row.argtypes = [Z.u8p, Z.f32p, C.c_int]
+        R.ref_q80_dequant_row(Z.ptr(q), Z.ptr(ref), O * I)
+        assert np.array_equal(np.isnan(got), np.isnan(ref))
+        assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32))
+    L.orc_set_plant(5)
+    try:
+        bad = np.zeros(O * I, np.float32)
+        L.orc_q80_dequant_row(Z.ptr(q), Z.ptr(bad), O * I)
+    finally:
+        L.orc_set_plant(0)
+    assert not np.array_equal(bad[fin].view(np.uint32), want[fin].view(np.uint32))

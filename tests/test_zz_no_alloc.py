@@ -1,6 +1,7 @@
 """zz_moe_forward_dev_noalloc: the device-pointer forward on the library's fixed
 scratch array. Checked against zz_moe_forward_dev (the entry point it mirrors) on
-two calls in a row, the second smaller, bit for bit, and against the oracle at the
+three calls in a row, each smaller (matrix-core path, then two decode batches), bit
+for bit, and against the oracle at the
 parity bar (ids exact, rel L2 < 1e-3); a batch beyond the scratch is declined with
 its outputs untouched."""
 import sys
@@ -27,7 +28,9 @@ def test_noalloc_forward_equals_forward_dev():
     try:
         m.upload_all(L.experts)
         s = torch.cuda.current_stream().cuda_stream
-        for S in (200, 3):                       # the second call smaller (and a decode batch)
+        # each call smaller than the last: the matrix-core path, then the decode path
+        # (S <= 2 for q4_0 layers) twice, all on the same scratch array
+        for S in (200, 2, 1):
             say(f"noalloc vs forward_dev: gemma E=32, S={S}")
             x = Z.make_input(L, S, 40 + S)
             din = torch.from_numpy(x).cuda()

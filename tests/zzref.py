@@ -93,6 +93,7 @@ def oracle():
         L.orc_matmul_f32.argtypes = [C.c_int, f32p, u8p, f32p, C.c_int, C.c_int, C.c_int]
         L.orc_dispatch.argtypes = [i32p, f32p, C.c_int, C.c_int, i32p, C.c_int, i32p, i32p,
                                    f32p, i32p]
+        L.orc_set_plant.argtypes = [C.c_int]
         _oracle = L
     return _oracle
 
@@ -699,6 +700,47 @@ def _input_digest(L, x):
         if a is not None:
             h.update(np.ascontiguousarray(a).tobytes())
     return h.hexdigest()
+
+
+# ---------------------------------------------- the Zipf offset, through the reference
+# configs[1] adds a seeded Zipf(1.1) offset to each gemma logit after the in-order
+# chain: v = fl(chain + bias[e]). The reference router has no offset
+# (gemma4.c:600-601), but its chain's last product can carry one exactly: with every
+# input element +-1 and eps = 0 the rmsnorm factor is exactly 1 (gemma4.c:425-431),
+# so the router input of a last element x = 1 with router_scale 1 is exactly
+# rs = 1/sqrtf(D), and a router weight q = fl(zipf / rs) gives the product
+# fl(q * rs), which is taken as the offset. The reference's chain then ends with
+# "+ offset", which is the oracle's faithful form and none of the plausible slips.
+ZIPF_PIN = dict(seed=41, E=128, D=2816, MI=704, K=8, S=8, xseed=41)
+
+
+def pm1_input(S, D, seed, last_one=True):
+    """[S, D] of +-1 (the last element +1): the rmsnorm factor is exactly 1 at eps 0."""
+    rng = np.random.default_rng(20_000 + seed)
+    x = np.where(rng.random((S, D)) < 0.5, np.float32(-1), np.float32(1)).astype(np.float32)
+    if last_one:
+        x[:, D - 1] = 1.0
+    return x
+
+
+def zipf_pin_case(seed=41, E=128, D=2816, MI=704, K=8, S=8, xseed=41):
+    """(Lo, Lr, x): Lo a Zipf-offset gemma layer for the oracle and the GPU (its last
+    router column zero, so its chain over D elements is the chain over D - 1 plus an
+    exact +0), Lr the same layer for the reference with the offset in that column
+    and no offset of its own, x the +-1 input."""
+    import dataclasses
+    Lo = make_layer("gemma", seed=seed, E=E, D=D, MI=MI, K=K, zipf=True)
+    Lo.eps = 0.0
+    rs = np.float32(1.0) / np.sqrt(np.float32(D))
+    q = (Lo.bias / rs).astype(np.float32)
+    Lo.bias = (q * rs).astype(np.float32)
+    Lo.router_scale = Lo.router_scale.copy()
+    Lo.router_scale[D - 1] = 1.0
+    Lr = dataclasses.replace(Lo, use_bias=0, bias=None, router=Lo.router.copy(), _keep=[])
+    Lr.router[:, D - 1] = q
+    Lo.router = Lo.router.copy()
+    Lo.router[:, D - 1] = 0.0
+    return Lo, Lr, pm1_input(S, D, xseed)
 
 
 # gemma around the MoE block: (D, MI, E, K, DI, V, seed), the block's S, the stack's

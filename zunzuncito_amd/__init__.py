@@ -34,7 +34,7 @@ ABI_SYMBOLS = (
     "zz_head_embed", "zz_head_logits_dev", "zz_head_logits", "zz_stack_create",
     "zz_stack_destroy", "zz_stack_prefill_dev", "zz_stack_decode_dev", "zz_moe_load_experts",
     "zz_gemma_stack_load", "zz_head_flash", "zz_head_use_flash", "zz_head_flash_replays",
-    "zz_stack_use_flash", "zz_moe_forward_dev_noalloc", "zz_router_expf",
+    "zz_stack_use_flash", "zz_moe_forward_dev_noalloc", "zz_router_expf", "zz_gpu_map_refreshes",
 )
 KERNELS = ("prep", "logits", "topk", "dispatch", "ffn_up", "ffn_down", "combine", "dec_route",
            "dec_down")
@@ -108,6 +108,7 @@ def lib():
     L.zz_moe_profile.argtypes = [C.c_int]
     L.zz_moe_profile_read.argtypes = [C.POINTER(C.c_double), C.POINTER(C.c_int), C.c_int]
     L.zz_router_expf.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]
+    L.zz_gpu_map_refreshes.restype = C.c_longlong
     L.zz_quantize.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]
     L.zz_last_error.restype = C.c_char_p
     L.zz_ffn_block_create.argtypes = [C.c_int, C.c_int, _f32p, C.c_float]

@@ -93,7 +93,9 @@ extern "C" const char *gpu_name(void) { return g_name; }
 extern "C" int gpu_map(const void *p, size_t n) {
     if (!g_ready || !p || !n) ZZ_FAIL("gpu_map: not ready or empty range");
     if (ZzRange *m = g_maps.find(p, n)) {
-        ZZ_CHECK(hipMemcpy(m->dev + ((uintptr_t)p - m->host), p, n, hipMemcpyHostToDevice));
+        const size_t off = (uintptr_t)p - m->host;
+        ZZ_CHECK(hipMemcpy(m->dev + off, p, n, hipMemcpyHostToDevice));
+        zz_fp_take(*m, off, n);
         return 1;
     }
     g_maps.drop_overlaps(p, n, [](const ZzRange &m) { (void)hipFree(m.dev); });
@@ -103,9 +105,13 @@ extern "C" int gpu_map(const void *p, size_t n) {
         (void)hipFree(dev);
         ZZ_FAIL("gpu_map: upload failed");
     }
-    g_maps.add(p, n, dev);
+    zz_fp_take(g_maps.add(p, n, dev), 0, n);
     return 1;
 }
+
+// tensors gpu_matmul found rewritten on the host since their last upload
+static long long g_map_refreshes = 0;
+extern "C" long long zz_gpu_map_refreshes(void) { return g_map_refreshes; }
 
 static int64_t fmt_tensor_bytes(int fmt, int O, int I) {
     if (fmt == ZZ_FMT_Q40) return (int64_t)O * (I / ZZ_BLK) * 18;
@@ -135,9 +141,16 @@ extern "C" int gpu_matmul(int fmt, float *y, const uint8_t *W, const float *x, i
         ZZ_FAIL("gpu_matmul: fmt %d declined", fmt);
     const int grp = fmt == ZZ_FMT_TQ2 || fmt == ZZ_FMT_Q4A ? 64 : 32;
     if (O <= 0 || I <= 0 || S <= 0 || I % grp) ZZ_FAIL("gpu_matmul: bad shape");
-    const ZzRange *m = g_maps.find(W, (size_t)fmt_tensor_bytes(fmt, O, I));
+    const size_t wb = (size_t)fmt_tensor_bytes(fmt, O, I);
+    ZzRange *m = g_maps.find(W, wb);
     if (!m) ZZ_FAIL("gpu_matmul: W not inside a gpu_map'd range");
-    const uint8_t *dW = m->dev + ((uintptr_t)W - m->host);
+    const size_t off = (uintptr_t)W - m->host;
+    if (zz_fp_changed(*m, off, wb)) {            // refilled since its upload: refresh it
+        ZZ_CHECK(hipMemcpy(m->dev + off, W, wb, hipMemcpyHostToDevice));
+        zz_fp_take(*m, off, wb);
+        g_map_refreshes++;
+    }
+    const uint8_t *dW = m->dev + off;
     if (!grow(&g_mx, &g_mxn, (size_t)S * I) || !grow(&g_my, &g_myn, (size_t)S * O)) return 0;
     ZZ_CHECK(hipMemcpyAsync(g_mx, x, sizeof(float) * (size_t)S * I, hipMemcpyHostToDevice, g_stream));
     if (!zz_launch_matmul_f32(fmt, g_my, dW, g_mx, O, I, S, g_stream)) ZZ_FAIL("gpu_matmul: launch failed");

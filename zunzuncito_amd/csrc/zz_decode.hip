@@ -1,14 +1,18 @@
-// zz_decode.hip -- decode-sized batches (S <= 4 tokens):
+// zz_decode.hip -- decode-sized batches (S <= 4 tokens), four launches:
 //   1. zz_dec_logits_kernel: one workgroup per expert computes that expert's
 //      certified router logit for every token (gemma: with the input rmsnorm from
-//      the same loads) and quantises a share of the expert input;
-//   2. zz_dec_gate_kernel: one workgroup runs the top-k gating and builds the
-//      dispatch lists (gemma4.c:750-790 for a handful of rows);
-//   3. zz_dec_up_kernel: gate/up GEMV with the activation and the int8
-//      re-quantisation of the hidden, per expert work item;
+//      the same loads) and quantises a share of the expert input; in a stack it
+//      first forms the previous block's combined rows (the deferred combine);
+//   2. zz_dec_up_kernel: per (token, slot) pair and 32-row block of the hidden,
+//      wave 0 selects the token's experts (certified top-k); one workgroup per
+//      token then forms and writes the gate weights; gate/up GEMV of the chosen
+//      expert, the activation and the int8 re-quantisation of the hidden
+//      (a dense branch's rows ride in the same grid);
 //   3. zz_dec_down_kernel: down GEMV for all (token, slot) pairs of a row tile
-//      and the gate-weighted combine (gemma4.c:652); gemma's post-norm
-//      (gemma4.c:807-808) follows as a one-workgroup-per-token kernel.
+//      and the gate-weighted combine in slot order (gemma4.c:652), with per-tile
+//      sums of squares for the post-norm;
+//   4. zz_dec_norm_kernel (gemma's post-norm, gemma4.c:807-808) or, for a fused
+//      block, zz_dec_final_kernel (both post-norms and the block combine).
 #include "zz_common.h"
 #include "zz_kernels.h"
 #include "zz_route_dev.h"

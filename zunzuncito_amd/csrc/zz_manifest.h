@@ -130,11 +130,46 @@ inline bool parse_manifest(const std::string &path, Manifest &m, std::string &er
 // overlaps older mappings replaces them (the host memory was released and reused).
 // Arithmetic on addresses is done on uintptr_t with overflow checks: a range that
 // would wrap the address space is inside no mapping, and overlaps those up to the top.
+// Each mapping also keeps a sampled fingerprint of the host bytes it last uploaded:
+// the 8 bytes at every multiple of ZZ_FP_STRIDE from its start. The engines map an
+// expert slot once and later pread other experts into it (gemma4.c:2051-2058,
+// 484-491); a matmul whose tensor's samples no longer match re-uploads that tensor
+// first. An expert record read over another differs in essentially every sample; a
+// rewrite that changes none of them (or a tensor shorter than the stride holding no
+// sample) is not seen.
+#define ZZ_FP_STRIDE 256
 struct ZzRange {
     uintptr_t host;
     size_t n;
     uint8_t *dev;
+    std::vector<uint64_t> fp;      // sample k: host bytes [k*STRIDE, k*STRIDE + 8)
 };
+
+// sample indices [*k0, *k1) that lie wholly inside [off, off + len) of a mapping
+static inline void zz_fp_span(size_t off, size_t len, size_t *k0, size_t *k1) {
+    *k0 = off / ZZ_FP_STRIDE + (off % ZZ_FP_STRIDE != 0);
+    *k1 = len >= 8 ? (off + len - 8) / ZZ_FP_STRIDE + 1 : *k0;
+    if (*k1 < *k0) *k1 = *k0;
+}
+// record the samples of [off, off + len) from the host bytes (after an upload of them)
+static inline void zz_fp_take(ZzRange &m, size_t off, size_t len) {
+    if (m.fp.empty() && m.n >= 8) m.fp.resize((m.n - 8) / ZZ_FP_STRIDE + 1);
+    size_t k0, k1;
+    zz_fp_span(off, len, &k0, &k1);
+    for (size_t k = k0; k < k1 && k < m.fp.size(); k++)
+        memcpy(&m.fp[k], (const void *)(m.host + k * ZZ_FP_STRIDE), 8);
+}
+// whether a sample of [off, off + len) differs from the host bytes now
+static inline bool zz_fp_changed(const ZzRange &m, size_t off, size_t len) {
+    size_t k0, k1;
+    zz_fp_span(off, len, &k0, &k1);
+    for (size_t k = k0; k < k1 && k < m.fp.size(); k++) {
+        uint64_t w;
+        memcpy(&w, (const void *)(m.host + k * ZZ_FP_STRIDE), 8);
+        if (w != m.fp[k]) return true;
+    }
+    return false;
+}
 
 class ZzRanges {
     std::vector<ZzRange> v_;
@@ -169,7 +204,10 @@ public:
                 v_.erase(v_.begin() + (long)i);
             }
     }
-    void add(const void *p, size_t n, uint8_t *dev) { v_.push_back(ZzRange{(uintptr_t)p, n, dev}); }
+    ZzRange &add(const void *p, size_t n, uint8_t *dev) {
+        v_.push_back(ZzRange{(uintptr_t)p, n, dev, {}});
+        return v_.back();
+    }
     template <class F>
     void clear(F drop) {
         for (ZzRange &m : v_) drop(m);

@@ -619,7 +619,9 @@ __global__ __launch_bounds__(DP_T) void zz_dispatch_kernel(ZzDispatchArgs a) {
     // slot of each expert's first item: the items of earlier experts on its XCD, from
     // one exclusive scan of per-XCD item counts packed a byte per XCD
     if (t == nu - 1) xtotal = i0 + nit;                 // all items
-    const int xe = t < nu ? xof[t] : 0;
+    if (nu == 0 && t == 0) xtotal = 0;
+    // xof is written only by the placement (nm > 0); union order needs no XCD here
+    const int xe = t < nu && nm > 0 ? xof[t] : 0;
     const unsigned long long cnt8 = t < nu ? (unsigned long long)min(nit, 255) << (8 * xe) : 0ull;
     const unsigned long long pre8 = zz_block_excl_scan64(cnt8, tmp64);
     if (t < nu) xjb[t] = (int)((pre8 >> (8 * xe)) & 255u);
