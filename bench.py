@@ -128,12 +128,14 @@ def build_layers(zz, torch, n_layers, seed):
     return layers, host
 
 
-def layer_experts_host(zz, torch, seed, li):
-    """Gemma layer li's expert records regenerated on the device, copied to the host."""
+def layer_experts_host(zz, torch, seed, li, ids=None):
+    """Gemma layer li's expert records regenerated on the device, copied to the host
+    (only experts `ids` when given; the others stay zero)."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed * 1000 + li)
     per, chunk = 3 * MI * D, 16
-    out = np.empty(E * REC_B, np.uint8)
+    out = np.zeros(E * REC_B, np.uint8)
+    want = set(range(E)) if ids is None else {int(e) for e in ids}
     buf_f = torch.empty(chunk * per, dtype=torch.float32, device="cuda")
     buf_q = torch.empty(chunk * REC_B, dtype=torch.uint8, device="cuda")
     for e0 in range(0, E, chunk):
@@ -141,7 +143,11 @@ def layer_experts_host(zz, torch, seed, li):
         zz.quantize_dev(1, buf_f.data_ptr(), buf_q.data_ptr(), buf_f.numel(),
                         torch.cuda.current_stream().cuda_stream)
         torch.cuda.current_stream().synchronize()
-        out[e0 * REC_B:(e0 + chunk) * REC_B] = buf_q.cpu().numpy()
+        if want >= set(range(e0, e0 + chunk)):
+            out[e0 * REC_B:(e0 + chunk) * REC_B] = buf_q.cpu().numpy()
+        else:
+            for e in sorted(want & set(range(e0, e0 + chunk))):
+                out[e * REC_B:(e + 1) * REC_B] = buf_q[(e - e0) * REC_B:(e - e0 + 1) * REC_B].cpu().numpy()
     return out
 
 
@@ -482,25 +488,31 @@ def flash_tensors(zz, torch, table, seed, cluster_size=32, probe_fraction=512 / 
             np.arange(1, 1 + n_force, dtype=np.int32))
 
 
-def stack_bench(zz, torch, layers, seed, prefill_S, steps):
-    """the Gemma-4 stack of the MoE layers above, each with a q4_0
-    dense MLP (dense_inter 2112) and the layer combine, under a tied q4_0 embedding /
-    lm_head of Gemma-4's 262144 rows; attention is the identity. A prefill of
-    prefill_S N(0,1) rows, then greedy decode steps whose token ids stay on the
-    device, both timed with HIP events on the launching stream."""
+def build_stack(zz, torch, layers, seed, flash=True, keep_host=False):
+    """BASELINE config 5 around the MoE layers `layers`: per layer a q4_0 dense MLP
+    (dense_inter 2112) and the layer combine (gemma4.c:1003-1030), under a tied q4_0
+    embedding / lm_head of Gemma-4's 262144 rows; attention is the identity. Returns
+    a dict: blocks, head, stack, objs (to close), flash (Head.flash arguments, or
+    None), and with keep_host the dense branches' host weights per layer (mlp,
+    pre_ffn_ln, post_ffn_ln1, post_ffn_ln, layer_scalar) for a CPU check."""
     rng = np.random.default_rng(seed + 500)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed * 7919)
-    objs, blocks = [], []
+    objs, blocks, dense = [], [], []
     for li, m in enumerate(layers):
+        pre = (1 + 0.05 * rng.standard_normal(D)).astype(np.float32)
+        post1 = (1 + 0.05 * rng.standard_normal(D)).astype(np.float32)
         d = zz.MoeLayer(D, DI, 1, 1, zz.ZZ_GATE_DENSE, zz.ZZ_ACT_GEGLU_TANH, (1, 1, 1), None,
-                        pre_ln=(1 + 0.05 * rng.standard_normal(D)).astype(np.float32),
-                        post_ln=(1 + 0.05 * rng.standard_normal(D)).astype(np.float32), eps=1e-6)
+                        pre_ln=pre, post_ln=post1, eps=1e-6)
         q = device_q40(zz, torch, 3 * DI * D, gen)
         d.upload_dev(0, q.data_ptr(), DENSE_B)
+        post = (1 + 0.05 * rng.standard_normal(D)).astype(np.float32)
+        scalar = float(np.float32(0.5 + 0.5 * rng.random()))
+        if keep_host:
+            dense.append(dict(mlp=q.cpu().numpy(), pre_ffn_ln=pre, post_ffn_ln1=post1,
+                              post_ffn_ln=post, layer_scalar=scalar))
         del q
-        b = zz.FfnBlock(m, d, (1 + 0.05 * rng.standard_normal(D)).astype(np.float32),
-                        float(np.float32(0.5 + 0.5 * rng.random())))
+        b = zz.FfnBlock(m, d, post, scalar)
         objs += [b, d]
         blocks.append(b)
     parts = []
@@ -509,12 +521,21 @@ def stack_bench(zz, torch, layers, seed, prefill_S, steps):
     table = np.concatenate(parts)
     del parts
     torch.cuda.empty_cache()
-    head = zz.Head(table, V, D, (1 + 0.05 * rng.standard_normal(D)).astype(np.float32), 1e-6,
-                   float(np.sqrt(np.float32(D))), 30.0)
-    flash = flash_tensors(zz, torch, table, seed)
-    del table
+    fnorm = (1 + 0.05 * rng.standard_normal(D)).astype(np.float32)
+    head = zz.Head(table, V, D, fnorm, 1e-6, float(np.sqrt(np.float32(D))), 30.0)
+    fl = flash_tensors(zz, torch, table, seed) if flash else None
     stack = zz.Stack(blocks, head)
     objs += [stack, head]
+    return dict(blocks=blocks, head=head, stack=stack, objs=objs, flash=fl, dense=dense,
+                table=table if keep_host else None, fnorm=fnorm)
+
+
+def stack_bench(zz, torch, layers, seed, prefill_S, steps):
+    """BASELINE config 5 (build_stack): a prefill of prefill_S N(0,1) rows, then
+    greedy decode steps whose token ids stay on the device, both timed with HIP
+    events on the launching stream."""
+    c5 = build_stack(zz, torch, layers, seed)
+    stack, head, flash, objs = c5["stack"], c5["head"], c5["flash"], c5["objs"]
     st = torch.cuda.current_stream()
     g = torch.Generator(device="cuda")
     g.manual_seed(seed + 99)
