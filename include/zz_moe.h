@@ -193,6 +193,18 @@ int zz_router_expf(const float *d_x, float *d_y, int64_t n, void *stream);
 int zz_moe_profile(int on);
 int zz_moe_profile_read(double *ms, int *launches, int n);
 
+/* Diagnostic, for the integer tier: one forward of S host rows (synchronous, S within
+ * one chunk, at most 64 Mi dots in all) on diagnostics builds of the FFN kernels that
+ * store every per-block int32 dot before its fp32 scaling -- the integer dots of
+ * q40.h:179-186 (q4_0), q40.h:374-414 (q8_0) and tq2.h:134-155 (tq2), as the kernels
+ * that run the layer form them. By flat pair p = token*K + slot:
+ *   up[p][0 = gate, 1 = up][MI][D/32], down[p][D][MI/32].
+ * Values are the kernels' raw integers: q4_0 enters as 16*(q - 8), so its dots are 16
+ * times the reference's; tq2 on the matrix cores is sum (c - 1)*x, on the decode path
+ * (S <= 4) sum c*x with c in {0, 1, 2}. The timed kernels are separate builds without
+ * these stores. */
+int zz_moe_dots(int layer, const float *in, int S, int32_t *up, int32_t *down);
+
 /* Diagnostic: how many times gpu_matmul (zz_gpu.h) found a mapped tensor rewritten
  * on the host since its last upload (its sampled fingerprint changed) and uploaded
  * it again before computing. The engines pread other experts into mapped slots

@@ -34,7 +34,7 @@ ABI_SYMBOLS = (
     "zz_head_embed", "zz_head_logits_dev", "zz_head_logits", "zz_stack_create",
     "zz_stack_destroy", "zz_stack_prefill_dev", "zz_stack_decode_dev", "zz_moe_load_experts",
     "zz_gemma_stack_load", "zz_head_flash", "zz_head_use_flash", "zz_head_flash_replays",
-    "zz_stack_use_flash", "zz_moe_forward_dev_noalloc", "zz_router_expf", "zz_gpu_map_refreshes",
+    "zz_stack_use_flash", "zz_moe_forward_dev_noalloc", "zz_router_expf", "zz_gpu_map_refreshes", "zz_moe_dots",
 )
 KERNELS = ("prep", "logits", "topk", "dispatch", "ffn_up", "ffn_down", "combine", "dec_route",
            "dec_down")
@@ -104,6 +104,7 @@ def lib():
     L.zz_moe_forward_end.argtypes = [C.c_int, _f32p, _i32p, _f32p]
     L.zz_moe_debug.argtypes = [C.c_int, C.POINTER(ZzMoeDump)]
     L.zz_moe_blockdots.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _i8p, _i32p]
+    L.zz_moe_dots.argtypes = [C.c_int, _f32p, C.c_int, _i32p, _i32p]
     L.zz_moe_stats.argtypes = [C.POINTER(C.c_uint)]
     L.zz_moe_profile.argtypes = [C.c_int]
     L.zz_moe_profile_read.argtypes = [C.POINTER(C.c_double), C.POINTER(C.c_int), C.c_int]
@@ -281,6 +282,18 @@ class MoeLayer:
         d["uniq"] = d["uniq"][:nu]
         d["offs"] = d["offs"][:nu + 1]
         return d
+
+    def dots(self, x):
+        """One forward of host rows x [S, D] on the FFN kernels' diagnostics builds
+        (zz_moe_dots): their per-block int32 dots before scaling, by flat pair
+        (token*K + slot): up [S*K, 2, MI, D/32] (gate, up), down [S*K, D, MI/32]."""
+        x = np.ascontiguousarray(x, np.float32)
+        S, K, D, MI = x.shape[0], self.K, self.D, self.MI
+        up = np.zeros((S * K, 2, MI, D // 32), np.int32)
+        dn = np.zeros((S * K, D, MI // 32), np.int32)
+        if not lib().zz_moe_dots(self.id, _p(x, _f32p), S, _p(up, _i32p), _p(dn, _i32p)):
+            raise RuntimeError(f"zz_moe_dots declined: {last_error()}")
+        return up, dn
 
     def blockdots(self, eid, tensor, row0, nrows, xq):
         xq = np.ascontiguousarray(xq, np.int8)

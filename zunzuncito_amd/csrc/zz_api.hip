@@ -532,6 +532,9 @@ struct ChunkArgs {
     int P, max_items;
 };
 
+// zz_moe_dots: while it runs, the FFN kernels also store their per-block int32 dots
+static int32_t *g_dbg_up = nullptr, *g_dbg_dn = nullptr;
+
 static ChunkArgs chunk_args(Layer *L, Workspace &w, const float *d_in, int S) {
     const zz_moe_desc &d = L->d;
     ChunkArgs c;
@@ -574,6 +577,7 @@ static ChunkArgs chunk_args(Layer *L, Workspace &w, const float *d_in, int S) {
     fa.experts = L->slots; fa.estride = L->lay.bytes; fa.lay = L->lay; fa.items = w.items;
     fa.meta = w.meta; fa.ptok = w.ptok; fa.xq = w.xq; fa.xs = w.xs; fa.xsum = w.xsum; fa.xt = w.xt;
     fa.hq = w.hq; fa.hs = w.hs; fa.hsum = w.hsum; fa.y = w.y;
+    fa.pslot = w.pslot; fa.dbg_up = g_dbg_up; fa.dbg_dn = g_dbg_dn;
     c.max_items = 8 * da.xslots;
     return c;
 }
@@ -772,6 +776,39 @@ extern "C" int zz_moe_forward(int id, const float *in, float *out, int S, int *e
     Layer *L = get_layer(id);
     if (!L) ZZ_FAIL("zz_moe_forward: no such layer");
     return forward_host(L, in, out, S, eidx, ewt);
+}
+
+// One synchronous forward on the FFN kernels' diagnostics builds, which also store
+// every per-block int32 dot before its fp32 scaling. Unwritten entries keep the fill
+// 0x80808080.
+extern "C" int zz_moe_dots(int id, const float *in, int S, int32_t *up, int32_t *down) {
+    Layer *L = get_layer(id);
+    if (!L || !in || !up || !down || S <= 0) ZZ_FAIL("zz_moe_dots: bad arguments");
+    const zz_moe_desc &d = L->d;
+    if (S > chunk_tokens(d)) ZZ_FAIL("zz_moe_dots: S > %d", chunk_tokens(d));
+    const size_t P = (size_t)S * d.K;
+    const size_t nu = P * 2 * d.MI * (d.D / ZZ_BLK), nd = P * d.D * (d.MI / ZZ_BLK);
+    if (nu + nd > ((size_t)64 << 20)) ZZ_FAIL("zz_moe_dots: %zu dots exceed the limit of 64 Mi", nu + nd);
+    int32_t *du = nullptr, *dd = nullptr;
+    ZZ_CHECK(hipMalloc(&du, 4 * nu));
+    if (hipMalloc(&dd, 4 * nd) != hipSuccess) {
+        (void)hipFree(du);
+        ZZ_FAIL("zz_moe_dots: allocation failed");
+    }
+    std::vector<float> out(P / d.K * d.D);
+    int ok = hipMemset(du, 0x80, 4 * nu) == hipSuccess && hipMemset(dd, 0x80, 4 * nd) == hipSuccess;
+    if (ok) {
+        g_dbg_up = du;
+        g_dbg_dn = dd;
+        ok = forward_host(L, in, out.data(), S, nullptr, nullptr);
+        g_dbg_up = g_dbg_dn = nullptr;
+    }
+    ok = ok && hipMemcpy(up, du, 4 * nu, hipMemcpyDeviceToHost) == hipSuccess &&
+         hipMemcpy(down, dd, 4 * nd, hipMemcpyDeviceToHost) == hipSuccess;
+    (void)hipFree(du);
+    (void)hipFree(dd);
+    if (!ok) ZZ_FAIL("zz_moe_dots: forward failed");
+    return 1;
 }
 
 extern "C" int zz_moe_forward_begin(int id, const float *in, int S) {

@@ -279,9 +279,12 @@ __device__ __forceinline__ void zz_dec_stage_commit(const ZzFfnArgs &a, const Zz
 // The dots of one batch of a wave's chunks (h + 2i). The activation operands of a
 // chunk (4 blocks' 8 bytes and d_x) are read from LDS one chunk ahead, so LDS
 // latency overlaps the dots; no branch inside a chunk.
-template <int FMT>
+// dbg(b, d, whole): diagnostics hook with an int32 dot of block b before its scaling,
+// a quarter block of the lane (whole = false) or the whole block (tq2); the timed
+// build passes a hook that does nothing.
+template <int FMT, typename DF>
 __device__ __forceinline__ float zz_dec_up_comp(const ZzChunk (&k)[DU_C], const ZzDecStage &st, int nb, int h,
-                                                int i0, int qq, float acc) {
+                                                int i0, int qq, float acc, DF dbg) {
     const int nch = (nb + 3) / 4, nfull = nb / 4;
     auto ldx = [&](int c, uint2 (&xv)[4], float4 &xs) {
         c = min(c, nch - 1);               // a short chunk's extra slots stay inside the row
@@ -298,6 +301,7 @@ __device__ __forceinline__ float zz_dec_up_comp(const ZzChunk (&k)[DU_C], const 
             const uint2 w = zz_chunk_w<FMT>(kk, j);
             int d = zz_dot4(w.x, xv[j].x, 0);
             d = zz_dot4(w.y, xv[j].y, d);
+            dbg(4 * c + j, d, false);
             const float sx = j == 0 ? xs.x : j == 1 ? xs.y : j == 2 ? xs.z : xs.w;
             acc = fmaf(zz_chunk_dw(kk, j, full) * sx, (float)d, acc);
         }
@@ -321,10 +325,10 @@ __device__ __forceinline__ float zz_dec_up_comp(const ZzChunk (&k)[DU_C], const 
 
 // the wave's partial dot of row r of group g over its half h of the K range; hook()
 // runs once the wave's first weight loads are in flight
-template <int FMT, typename HOOK>
+template <int FMT, typename HOOK, typename DF>
 __device__ __forceinline__ float zz_dec_up_part(const ZzFfnArgs &a, const ZzDecStageRegs &sr, ZzDecStage &st,
                                                 const uint8_t *E, const ZzTensor &T, int g, int h, int l,
-                                                HOOK hook) {
+                                                HOOK hook, DF dbg) {
     const int nb = a.D / ZZ_BLK, r = l & 15, qq = l >> 4;
     float acc = 0.0f;
     // the first batch of loads, the staging commit (waits only for the activations,
@@ -346,6 +350,8 @@ __device__ __forceinline__ float zz_dec_up_part(const ZzFfnArgs &a, const ZzDecS
                 const int8_t *x = &st.xq[gp * 64];
                 const int d0 = zz_dot_tq2(c[i], 0, ld16(x), ld16(x + 16));
                 const int d1 = zz_dot_tq2(c[i], 1, ld16(x + 32), ld16(x + 48));
+                dbg(2 * gp, d0, true);
+                dbg(2 * gp + 1, d1, true);
                 acc = fmaf(st.xs[2 * gp], (float)d0, acc);
                 acc = fmaf(st.xs[2 * gp + 1], (float)d1, acc);
             }
@@ -370,14 +376,15 @@ __device__ __forceinline__ float zz_dec_up_part(const ZzFfnArgs &a, const ZzDecS
     load(0);
     hook();
     zz_dec_stage_commit(a, sr, st);
-    acc = zz_dec_up_comp<FMT>(k, st, nb, h, 0, qq, acc);
+    acc = zz_dec_up_comp<FMT>(k, st, nb, h, 0, qq, acc, dbg);
     for (int i0 = DU_C; h + 2 * i0 < nch; i0 += DU_C) {
         load(i0);
-        acc = zz_dec_up_comp<FMT>(k, st, nb, h, i0, qq, acc);
+        acc = zz_dec_up_comp<FMT>(k, st, nb, h, i0, qq, acc, dbg);
     }
     return FMT == ZZ_FMT_Q40 ? acc * 0.0625f : acc;            // the 16*(q - 8) weights
 }
 
+template <bool DBG>
 __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
     // workgroup (p, j) of the routed pairs is number p*(MI/32) + j; the fused dense
     // branch's rows (one per token, expert 0, no routing) follow, numbered the same way
@@ -408,10 +415,22 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
     auto gates = [&] {
         if (w == 0 && routed && writer) zz_topk_wave_gates(a.tk, s, tk_lds, true);
     };
+    // diagnostics: pair p, row 16g + r of the wave's tensor (gate for q < 2), block b;
+    // the quarters of a q4_0 / q8_0 block sit in lanes r, r + 16, r + 32, r + 48
+    auto dbg = [&](int b, int d, bool whole) {
+        if constexpr (DBG) {
+            if (!whole) {
+                d += __shfl_xor(d, 16);
+                d += __shfl_xor(d, 32);
+            }
+            if (routed && (whole || l < 16))
+                f.dbg_up[(((size_t)p * 2 + (q >= 2 ? 1 : 0)) * f.MI + 16 * g + (l & 15)) * (f.D / ZZ_BLK) + b] = d;
+        }
+    };
     float acc;
-    if (T.fmt == ZZ_FMT_Q40) acc = zz_dec_up_part<ZZ_FMT_Q40>(f, sr, st, E, T, g, h, l, gates);
-    else if (T.fmt == ZZ_FMT_Q80) acc = zz_dec_up_part<ZZ_FMT_Q80>(f, sr, st, E, T, g, h, l, gates);
-    else acc = zz_dec_up_part<ZZ_FMT_TQ2>(f, sr, st, E, T, g, h, l, gates);
+    if (T.fmt == ZZ_FMT_Q40) acc = zz_dec_up_part<ZZ_FMT_Q40>(f, sr, st, E, T, g, h, l, gates, dbg);
+    else if (T.fmt == ZZ_FMT_Q80) acc = zz_dec_up_part<ZZ_FMT_Q80>(f, sr, st, E, T, g, h, l, gates, dbg);
+    else acc = zz_dec_up_part<ZZ_FMT_TQ2>(f, sr, st, E, T, g, h, l, gates, dbg);
     acc = zz_rows_sum(acc);                                     // sum over the 4 k-quarters
     if (l < 16) part[h][q][l] = acc;
     if (T.fmt == ZZ_FMT_TQ2 && tid == 0) {          // tq2.h:101-106, serial
@@ -470,7 +489,7 @@ struct ZzDecPairs {                 // per (token, slot) pair, flat order s*K + 
 // LDS bytes of the staged hidden rows of P pairs: int8 codes, block scales and sums
 static inline size_t zz_dec_down_lds(int P, int MI) { return (size_t)P * MI + 8 * (size_t)P * (MI / ZZ_BLK); }
 
-template <int FMT>
+template <int FMT, bool DBG>
 __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     const ZzFfnArgs &f = a.f;
     const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, r = l & 15, qq = l >> 4;
@@ -531,6 +550,16 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
             else k[i] = zz_load_chunk<FMT>(E, W, ch);
         }
     };
+    // diagnostics: flat pair fp, row 16g + r of down, block b (quarters as in gate/up)
+    auto dbg = [&](int fp, int b, int d, bool whole) {
+        if constexpr (DBG) {
+            if (!whole) {
+                d += __shfl_xor(d, 16);
+                d += __shfl_xor(d, 32);
+            }
+            if (whole || qq == 0) f.dbg_dn[((size_t)fp * D + 16 * g + r) * nb + b] = d;
+        }
+    };
     float acc = 0.0f;
     int cur = -1;
     auto comp_units = [&](int u0) {
@@ -556,6 +585,8 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
                     const int8_t *x = hx + gp * 64;
                     const int d0 = zz_dot_tq2(c[i], 0, *(const uint4 *)x, *(const uint4 *)(x + 16));
                     const int d1 = zz_dot_tq2(c[i], 1, *(const uint4 *)(x + 32), *(const uint4 *)(x + 48));
+                    dbg(fp, 2 * gp, d0, true);
+                    dbg(fp, 2 * gp + 1, d1, true);
                     acc = fmaf(hsx[2 * gp], (float)d0, acc);
                     acc = fmaf(hsx[2 * gp + 1], (float)d1, acc);
                 }
@@ -569,6 +600,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
                     const uint2 xv = *(const uint2 *)(hx + b * ZZ_BLK + 8 * qq);
                     int d = zz_dot4(wv.x, xv.x, 0);
                     d = zz_dot4(wv.y, xv.y, d);
+                    dbg(fp, b, d, false);
                     acc = fmaf(zz_chunk_dw(k[i], j, cbs == 4) * hsx[b], (float)d, acc);
                 }
             }
@@ -736,7 +768,8 @@ int zz_dec_fin_fits(int S, int D) {
 
 int zz_launch_dec_up(const ZzDecUpArgs &a, int S, hipStream_t st) {
     const int n = S * a.tk.K * (a.f.MI / ZZ_BLK) + a.nd * (a.nd ? a.fd.MI / ZZ_BLK : 0);
-    hipLaunchKernelGGL(zz_dec_up_kernel, dim3(n), dim3(512), zz_topk_wave_bytes(a.tk.E), st, a);
+    if (a.f.dbg_up) hipLaunchKernelGGL(zz_dec_up_kernel<true>, dim3(n), dim3(512), zz_topk_wave_bytes(a.tk.E), st, a);
+    else hipLaunchKernelGGL(zz_dec_up_kernel<false>, dim3(n), dim3(512), zz_topk_wave_bytes(a.tk.E), st, a);
     return hipGetLastError() == hipSuccess;
 }
 
@@ -755,11 +788,16 @@ int zz_launch_dec_down(const ZzDecDownArgs &a, hipStream_t st) {
     const int nd = a.nd && a.f.lay.down.fmt != ZZ_FMT_TQ2 ? a.nd : 0;
     const size_t lds = zz_dec_down_lds(a.S * a.K, a.f.MI) + (nd ? zz_dec_dense_lds(nd, a.fd.MI) : 0);
     if (nd ? !zz_dec_fits2(a.S, a.K, a.f.MI, a.fd.MI) : !zz_dec_fits(a.S, a.K, a.f.MI)) return 0;
-    switch (a.f.lay.down.fmt) {
-    case ZZ_FMT_Q40: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q40>, grid, dim3(512), lds, st, a); break;
-    case ZZ_FMT_Q80: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_Q80>, grid, dim3(512), lds, st, a); break;
-    case ZZ_FMT_TQ2: hipLaunchKernelGGL(zz_dec_down_kernel<ZZ_FMT_TQ2>, grid, dim3(512), lds, st, a); break;
-    default: return 0;
+    const int fmt = a.f.lay.down.fmt;
+    if (fmt != ZZ_FMT_Q40 && fmt != ZZ_FMT_Q80 && fmt != ZZ_FMT_TQ2) return 0;
+    if (a.f.dbg_dn) {
+        if (fmt == ZZ_FMT_Q40) hipLaunchKernelGGL((zz_dec_down_kernel<ZZ_FMT_Q40, true>), grid, dim3(512), lds, st, a);
+        else if (fmt == ZZ_FMT_Q80) hipLaunchKernelGGL((zz_dec_down_kernel<ZZ_FMT_Q80, true>), grid, dim3(512), lds, st, a);
+        else hipLaunchKernelGGL((zz_dec_down_kernel<ZZ_FMT_TQ2, true>), grid, dim3(512), lds, st, a);
+    } else {
+        if (fmt == ZZ_FMT_Q40) hipLaunchKernelGGL((zz_dec_down_kernel<ZZ_FMT_Q40, false>), grid, dim3(512), lds, st, a);
+        else if (fmt == ZZ_FMT_Q80) hipLaunchKernelGGL((zz_dec_down_kernel<ZZ_FMT_Q80, false>), grid, dim3(512), lds, st, a);
+        else hipLaunchKernelGGL((zz_dec_down_kernel<ZZ_FMT_TQ2, false>), grid, dim3(512), lds, st, a);
     }
     return hipGetLastError() == hipSuccess;
 }

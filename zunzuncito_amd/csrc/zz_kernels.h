@@ -78,6 +78,11 @@ struct ZzFfnArgs {
     float *hs;                  // [P, MI/32]
     int *hsum;                  // [P, MI/32]
     float *y;                   // [P, D] expert outputs before weighting
+    // diagnostics (zz_moe_dots), null otherwise: the kernels' per-block integer dots
+    // before scaling, by flat pair p = token*K + slot (pslot: sorted pair -> slot)
+    const int *pslot;
+    int32_t *dbg_up;            // [P][gate, up][MI][D/32]
+    int32_t *dbg_dn;            // [P][D][MI/32]
 };
 
 struct ZzCombineArgs {

@@ -1,5 +1,7 @@
-// zz_mma.hip -- grouped expert FFN for batches (S >= 5) on the int8 matrix cores of
-// gfx950 (v_mfma_i32_16x16x32_i8).
+// zz_mma.h -- the grouped expert FFN for batches (S >= 5) on the int8 matrix cores
+// of gfx950 (v_mfma_i32_16x16x32_i8, v_mfma_i32_4x4x4_16b_i8): the K loops and
+// fragment code shared by the gate/up kernel (zz_mma_up.hip) and the down kernel
+// (zz_mma_down.hip).
 //
 // One MFMA step covers exactly one 32-weight block (K = 32), so its int32 results are
 // the reference's per-block integer dots (q40.h:27 <q_w - 8, q_x>, q8_0's <q_w, q_x>,
@@ -17,6 +19,7 @@
 // The K loop walks the slot table's chunks of 4 blocks. Weights go straight to
 // registers, two chunks ahead: the slot table holds each lane's bytes for a chunk
 // contiguously (zz_common.h). Activations are staged through LDS, one chunk ahead.
+#pragma once
 #include "zz_common.h"
 #include "zz_kernels.h"
 #include "zz_dot_dev.h"
@@ -111,8 +114,10 @@ __device__ __forceinline__ _Float16 mm_dwh(const uint4 &s0, const uint4 &s1, int
 // B operand of token tile t, block j; SX(t, j) that token's d_x.
 // Per product: d_w * d_x (a multiply by the block's d_w, converted once per block),
 // the int32 conversion, the accumulating FMA.
-template <int FMT, int NT, bool FULL, typename XF, typename SF>
-__device__ __forceinline__ void mm_chunk(const MmA &A, int l, float (&acc)[NT][4], XF X, SF SX) {
+// DF(j, r): called with block j's int32 results before their scaling (diagnostics
+// builds store them; the timed build passes a hook that does nothing).
+template <int FMT, int NT, bool FULL, typename XF, typename SF, typename DF>
+__device__ __forceinline__ void mm_chunk(const MmA &A, int l, float (&acc)[NT][4], XF X, SF SX, DF dbg) {
     const zz_v4i zero = {0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < (FULL ? 4 : 2); j++) {
@@ -129,6 +134,7 @@ __device__ __forceinline__ void mm_chunk(const MmA &A, int l, float (&acc)[NT][4
         zz_v4i r[NT];
 #pragma unroll
         for (int t = 0; t < NT; t++) r[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa, B[t], zero, 0, 0, 0);
+        dbg(j, r);
         // the 4 rows' d_w as f32 once per block, for every tile: the product d_w * d_x
         // is then a v_mul_f32, which ran the up kernel 3 % faster than the fused
         // mixed-precision form (v_fma_mix_f32) the compiler otherwise picks; the empty
@@ -212,9 +218,9 @@ __device__ __forceinline__ void mm_store_x(const MmX &x, MmStage &st) {
 //
 // Large items: activations one chunk ahead through the two LDS stages, one
 // workgroup barrier per chunk.
-template <int FMT, int NT, int RING>
+template <int FMT, int NT, int RING, typename DF>
 __device__ __forceinline__ void mm_kloop(const uint8_t *E, const ZzTensor &T, int g, const MmSrc &src,
-                                         MmStage (&st)[2], float (&acc)[NT][4]) {
+                                         MmStage (&st)[2], float (&acc)[NT][4], DF dbgc) {
     const int l = threadIdx.x & 63, nb = T.I / ZZ_BLK, nch = (nb + 3) / 4, nfull = nb / 4;
 #pragma unroll
     for (int t = 0; t < NT; t++)
@@ -239,7 +245,8 @@ __device__ __forceinline__ void mm_kloop(const uint8_t *E, const ZzTensor &T, in
         const MmStage &S = st[c & 1];
         mm_chunk<FMT, NT, decltype(full)::value>(
             A, l, acc, [&](int t, int j) { return *(const long *)&S.x[16 * t + (l & 15)][j * ZZ_BLK + 8 * (l >> 4)]; },
-            [&](int t, int j) { return S.s[j][16 * t + (l & 15)]; });
+            [&](int t, int j) { return S.s[j][16 * t + (l & 15)]; },
+            [&](int j, const zz_v4i (&rr)[NT]) { dbgc(c, j, rr); });
         mm_store_x<KP>(xr, st[(c + 1) & 1]);     // the last step refills the free stage: harmless
     };
     int c0 = 0;
@@ -347,9 +354,9 @@ __device__ __forceinline__ int mm4_frag(const Mm4A &A, int j, int m) {
 
 // acc[s][v]: row 4(l/4)+v of the 64, token 4s + l%4, over this wave's chunks c = w,
 // w+4, ... (K: the row length, the staged rows' stride)
-template <int FMT, bool FULLC, int NS>
+template <int FMT, bool FULLC, int NS, typename DF>
 __device__ __forceinline__ void mm4_chunk(const Mm4A &A, const Mm4Stage &st, int c, int l, int K,
-                                          float (&acc)[NS][4]) {
+                                          float (&acc)[NS][4], DF dbg) {
     const int nb = K / ZZ_BLK;
 #pragma unroll
     for (int j = 0; j < (FULLC ? 4 : 2); j++) {
@@ -366,6 +373,7 @@ __device__ __forceinline__ void mm4_chunk(const Mm4A &A, const Mm4Stage &st, int
             for (int m = 0; m < 8; m++) d[s] = __builtin_amdgcn_mfma_i32_4x4x4i8(mm4_frag<FMT>(A, j, m), (int)xw[m], d[s], 0, 0, 0);
             sx[s] = st.s[t * nb + b];
         }
+        dbg(c, j, d);
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const float dw = (float)mm_dwh<FULLC>(A.s0, A.s1, j, v);
@@ -397,17 +405,17 @@ __device__ __forceinline__ void mm4_first(Mm4Ring<FMT> &R, const uint8_t *E, con
 
 // acc[v]: row 4(l/4)+v of the 64, token l%4, over this wave's chunks. Every load is
 // unconditional (clamped past the end) so the compiler's load counters stay exact.
-template <int FMT, int NS>
+template <int FMT, int NS, typename DF>
 __device__ __forceinline__ void mm4_kloop(Mm4Ring<FMT> &R, const uint8_t *E, int l, int w, const Mm4Stage &st,
-                                          int K, float (&acc)[NS][4]) {
+                                          int K, float (&acc)[NS][4], DF dbg) {
     const int nch = R.nch;
 #pragma unroll
     for (int s = 0; s < NS; s++)
 #pragma unroll
         for (int v = 0; v < 4; v++) acc[s][v] = 0.0f;
     auto chunk = [&](const Mm4A &A, int c) {
-        if (c < R.W.nfull) mm4_chunk<FMT, true, NS>(A, st, c, l, K, acc);
-        else if (c < nch) mm4_chunk<FMT, false, NS>(A, st, c, l, K, acc);
+        if (c < R.W.nfull) mm4_chunk<FMT, true, NS>(A, st, c, l, K, acc, dbg);
+        else if (c < nch) mm4_chunk<FMT, false, NS>(A, st, c, l, K, acc, dbg);
     };
     if (FMT == ZZ_FMT_Q80 || NS == 2) {
         // q8_0 chunks are twice the registers, and two token sets twice the work per
@@ -453,225 +461,15 @@ struct Mm4Shared {
     float hb[8][ZZ_BLK];
 };
 
-// ------------------------------------------------------------------ up
-union MmUpShared {
-    MmStage st[2];
-    Mm4Shared t4;
-    struct {
-        float u[32][MM_TN + 1];              // up values, [hidden row][token]
-        float amax[2][MM_TN];
-        int qsum[2][MM_TN];
-    } e;
-};
-
-// GF, UF: the gate and up formats (gate and up are both tq2 or neither)
-template <int GF, int UF, int NT>
-__device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &item, int rb, MmUpShared &sm,
-                                           int *tok) {
-    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, qq = l >> 4;
-    const ZzTensor &T = w < 2 ? a.lay.gate : a.lay.up;
-    const int g = 2 * rb + (w & 1), n = item.n, D = a.D, nb = D / ZZ_BLK;
-    const uint8_t *E = a.experts + (size_t)item.e * a.estride;
-    if (tid < MM_TN) tok[tid] = a.ptok[item.p0 + min(tid, n - 1)];
-    __syncthreads();
-    MmSrc src;
-    src.xb = (const uint8_t *)a.xq;
-    src.sb = (const uint8_t *)a.xs;
-#pragma unroll
-    for (int k = 0; k < MM_XP; k++) {
-        const int i = tid + 256 * k, t = i >> 3;
-        src.row[k] = (uint32_t)tok[t] * (uint32_t)D;     // tok[t >= n]: token n - 1
-        src.seg[k] = i & 7;
-    }
-#pragma unroll
-    for (int k = 0; k < MM_SP; k++) {
-        const int i = tid + 256 * k, t = i % MM_TN;
-        src.srow[k] = (uint32_t)tok[t] * (uint32_t)(4 * nb);
-        src.kb[k] = i / MM_TN;
-    }
-
-    // gate and up may differ in format (q4_0 / q8_0); each wave runs its tensor's loop
-    // (the same number of chunks and barriers either way)
-    float acc[NT][4];
-    if (GF == UF || w < 2) mm_kloop<GF, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
-    else mm_kloop<UF, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
-    if ((w < 2 ? GF : UF) == ZZ_FMT_Q40)         // the 16*(q - 8) weights
-#pragma unroll
-        for (int t = 0; t < NT; t++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[t][i] *= 0.0625f;
-    if (GF == ZZ_FMT_TQ2) {                      // tq2.h:154, alpha of the row
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float al = ((const float *)(E + T.off_s))[16 * g + 4 * qq + i];
-#pragma unroll
-            for (int t = 0; t < NT; t++) acc[t][i] *= al;
-        }
-    }
-    __syncthreads();                             // the stages are done with
-    if (w >= 2) {
-#pragma unroll
-        for (int t = 0; t < NT; t++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) sm.e.u[16 * (w & 1) + 4 * qq + i][16 * t + (l & 15)] = acc[t][i];
-    }
-    __syncthreads();
-    // waves 0, 1: h = act(g, u) for hidden rows 16w + 4qq + i, then the q8_0
-    // quantisation of each token's 32-row block (q40.h:124-138)
-    float amx[NT];
-    if (w < 2) {
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            float m = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float h = zz_act(a.act, acc[t][i], sm.e.u[16 * w + 4 * qq + i][16 * t + (l & 15)], a.clamp);
-                acc[t][i] = h;
-                m = fmaxf(m, fabsf(h));
-            }
-            m = zz_rows_max(m);
-            amx[t] = m;
-            if (qq == 0) sm.e.amax[w][16 * t + l] = m;
-        }
-    }
-    __syncthreads();
-    if (w < 2) {
-        const int nbM = a.MI / ZZ_BLK;
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const int tk = 16 * t + (l & 15);
-            const float amax = fmaxf(amx[t], sm.e.amax[w ^ 1][tk]);
-            const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
-            unsigned pk = 0;
-            int s = 0;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float f = rintf(acc[t][i] * id);
-                f = fminf(fmaxf(f, -127.0f), 127.0f);
-                const int qi = (int)f;
-                s += qi;
-                pk |= (unsigned)(qi & 0xff) << (8 * i);
-            }
-            s = zz_rows_sum(s);
-            if (qq == 0) sm.e.qsum[w][tk] = s;
-            if (tk < n) {
-                const size_t p = (size_t)item.p0 + tk;
-                *(unsigned *)(a.hq + p * a.MI + rb * ZZ_BLK + 16 * w + 4 * qq) = pk;
-                if (w == 0 && qq == 0) a.hs[p * nbM + rb] = d;
-            }
-        }
-    }
-    __syncthreads();
-    if (tid < n) a.hsum[((size_t)item.p0 + tid) * (a.MI / ZZ_BLK) + rb] = sm.e.qsum[0][tid] + sm.e.qsum[1][tid];
+// Diagnostics store of one int32 block dot at flat pair (token*K + slot) of sorted
+// pair pos: up [P][gate/up][MI][D/32], down [P][D][MI/32].
+__device__ __forceinline__ void mm_dbg_up(const ZzFfnArgs &a, int pos, int tensor, int row, int b, int v) {
+    const int fl = a.ptok[pos] * a.K + a.pslot[pos];
+    a.dbg_up[(((size_t)fl * 2 + tensor) * a.MI + row) * (a.D / ZZ_BLK) + b] = v;
 }
-
-// ------------------------------------------------------------------ down
-union MmDownShared {
-    MmStage st[2];
-    Mm4Shared t4;
-};
-
-template <int FMT, int NT>
-__device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, MmDownShared &sm) {
-    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, qq = l >> 4;
-    const ZzTensor &T = a.lay.down;
-    const int g = 4 * rt + w, n = item.n, MI = a.MI, nb = MI / ZZ_BLK;
-    const uint8_t *E = a.experts + (size_t)item.e * a.estride;
-    MmSrc src;
-    src.xb = (const uint8_t *)a.hq;
-    src.sb = (const uint8_t *)a.hs;
-#pragma unroll
-    for (int k = 0; k < MM_XP; k++) {
-        const int i = tid + 256 * k, t = i >> 3;
-        src.row[k] = (uint32_t)(item.p0 + min(t, n - 1)) * (uint32_t)MI;
-        src.seg[k] = i & 7;
-    }
-#pragma unroll
-    for (int k = 0; k < MM_SP; k++) {
-        const int i = tid + 256 * k, t = i % MM_TN;
-        src.srow[k] = (uint32_t)(item.p0 + min(t, n - 1)) * (uint32_t)(4 * nb);
-        src.kb[k] = i / MM_TN;
-    }
-
-    float acc[NT][4];
-    mm_kloop<FMT, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc);
-    if (FMT == ZZ_FMT_Q40)                       // the 16*(q - 8) weights
-#pragma unroll
-        for (int t = 0; t < NT; t++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[t][i] *= 0.0625f;
-    const int row0 = 16 * g + 4 * qq;
-    float al[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-    if (FMT == ZZ_FMT_TQ2)
-        for (int i = 0; i < 4; i++) al[i] = ((const float *)(E + T.off_s))[row0 + i];
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        const int tk = 16 * t + (l & 15);
-        if (tk < n)
-            *(float4 *)(a.y + ((size_t)item.p0 + tk) * a.D + row0) =
-                make_float4(acc[t][0] * al[0], acc[t][1] * al[1], acc[t][2] * al[2], acc[t][3] * al[3]);
-    }
-}
-
-// Tiny items (<= 4 NS tokens): lanes 0..31 own gate rows 32rb.., lanes 32..63 the up
-// rows (gate and up in one format); then h = act(g, u) and its q8_0 quantisation per
-// token.
-template <int FMT, int NS>
-__device__ __forceinline__ void mm4_up_body(const ZzFfnArgs &a, const ZzItem &item, int rb, Mm4Shared &sm) {
-    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, n = item.n, D = a.D, nb = D / ZZ_BLK;
-    const uint8_t *E = a.experts + (size_t)item.e * a.estride;
-    const int *ptok = a.ptok + item.p0;
-    const ZzTensor &T = l < 32 ? a.lay.gate : a.lay.up;
-    Mm4Ring<FMT> R;
-    mm4_first<FMT>(R, E, T, 2 * rb + ((l >> 4) & 1), l, w);       // weights first
-    mm4_stage<NS>(sm.st, [&](int t) { return a.xq + (size_t)ptok[min(t, n - 1)] * D; },
-                  [&](int t) { return a.xs + (size_t)ptok[min(t, n - 1)] * nb; }, D);
-    float acc[NS][4];
-    mm4_kloop<FMT, NS>(R, E, l, w, sm.st, D, acc);
-    __syncthreads();                             // the stage is done with
-#pragma unroll
-    for (int s = 0; s < NS; s++) mm4_reduce(sm.rd, acc[s], s);
-    if (tid < 4 * NS * ZZ_BLK) {                 // token t, hidden row 32rb + r
-        const int t = tid >> 5, r = tid & 31;
-        sm.hb[t][r] = zz_act(a.act, sm.rd.res[r][t], sm.rd.res[32 + r][t], a.clamp);
-    }
-    __syncthreads();
-    if (tid < 32 * NS) {                         // q8_0 of each token's block (q40.h:124-138)
-        const int t = tid >> 3, m = tid & 7;
-        float d;
-        int qs;
-        const unsigned pk = zz_quant8(*(const float4 *)&sm.hb[t][4 * m], &d, &qs);
-        if (t < n) {
-            const size_t p = (size_t)item.p0 + t;
-            const int nbM = a.MI / ZZ_BLK;
-            *(unsigned *)(a.hq + p * a.MI + rb * ZZ_BLK + 4 * m) = pk;
-            if (m == 0) {
-                a.hs[p * nbM + rb] = d;
-                a.hsum[p * nbM + rb] = qs;
-            }
-        }
-    }
-}
-
-// Tiny items (<= 4 NS tokens), down: rows 64rt + l, the unweighted y of each token.
-template <int FMT, int NS>
-__device__ __forceinline__ void mm4_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, Mm4Shared &sm) {
-    const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, n = item.n, MI = a.MI, nb = MI / ZZ_BLK;
-    const uint8_t *E = a.experts + (size_t)item.e * a.estride;
-    Mm4Ring<FMT> R;
-    mm4_first<FMT>(R, E, a.lay.down, 4 * rt + (l >> 4), l, w);     // weights first
-    mm4_stage<NS>(sm.st, [&](int t) { return a.hq + ((size_t)item.p0 + min(t, n - 1)) * MI; },
-                  [&](int t) { return a.hs + ((size_t)item.p0 + min(t, n - 1)) * nb; }, MI);
-    float acc[NS][4];
-    mm4_kloop<FMT, NS>(R, E, l, w, sm.st, MI, acc);
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < NS; s++) mm4_reduce(sm.rd, acc[s], s);
-#pragma unroll
-    for (int s = 0; s < NS; s++) {
-        const int t = 4 * s + (tid >> 6), r = tid & 63;
-        if (t < n) a.y[((size_t)item.p0 + t) * a.D + 64 * rt + r] = sm.rd.res[r][t];
-    }
+__device__ __forceinline__ void mm_dbg_dn(const ZzFfnArgs &a, int pos, int row, int b, int v) {
+    const int fl = a.ptok[pos] * a.K + a.pslot[pos];
+    a.dbg_dn[((size_t)fl * a.D + row) * (a.MI / ZZ_BLK) + b] = v;
 }
 
 // XCD-aware work order. Workgroup g of a launch runs on XCD g % 8 (round-robin
@@ -687,62 +485,6 @@ __device__ __forceinline__ void zz_xcd_tile(int ntiles, int *item, int *tile) {
     *item = (k / ntiles) * ZZ_XCDS + x;
     *tile = k % ntiles;
 }
-static unsigned zz_xcd_grid(int max_items, int ntiles) {
+static inline unsigned zz_xcd_grid(int max_items, int ntiles) {
     return (unsigned)((max_items + ZZ_XCDS - 1) / ZZ_XCDS * ZZ_XCDS * ntiles);
-}
-
-template <int GF, int UF>
-__global__ __launch_bounds__(256, 4) void zz_up_mma_kernel(ZzFfnArgs a) {
-    int it, rb;
-    zz_xcd_tile(a.MI / 32, &it, &rb);
-    if (it >= a.meta[1]) return;
-    const ZzItem item = a.items[it];
-    if (item.n <= 0) return;
-    __shared__ MmUpShared sm;
-    __shared__ int tok[MM_TN];
-    const int nt = (item.n + 15) / 16;
-    if (GF == UF && GF != ZZ_FMT_TQ2 && item.n <= 4 && a.D <= MM4_XB / 4) mm4_up_body<GF, 1>(a, item, rb, sm.t4);
-    else if (GF == UF && GF == ZZ_FMT_Q40 && item.n <= 8 && a.D <= MM4_XB / 8) mm4_up_body<GF, 2>(a, item, rb, sm.t4);
-    else if (nt <= 1) mm_up_body<GF, UF, 1>(a, item, rb, sm, tok);
-    else if (nt <= 2) mm_up_body<GF, UF, 2>(a, item, rb, sm, tok);
-    else if (nt <= 3) mm_up_body<GF, UF, 3>(a, item, rb, sm, tok);
-    else mm_up_body<GF, UF, 4>(a, item, rb, sm, tok);
-}
-
-template <int FMT>
-__global__ __launch_bounds__(256, 4) void zz_down_mma_kernel(ZzFfnArgs a) {
-    int it, rt;
-    zz_xcd_tile(a.D / 64, &it, &rt);
-    if (it >= a.meta[1]) return;
-    const ZzItem item = a.items[it];
-    if (item.n <= 0) return;
-    __shared__ MmDownShared sm;
-    const int nt = (item.n + 15) / 16;
-    if (FMT != ZZ_FMT_TQ2 && item.n <= 4 && a.MI <= MM4_XB / 4) mm4_down_body<FMT, 1>(a, item, rt, sm.t4);
-    else if (FMT == ZZ_FMT_Q40 && item.n <= 8 && a.MI <= MM4_XB / 8) mm4_down_body<FMT, 2>(a, item, rt, sm.t4);
-    else if (nt <= 1) mm_down_body<FMT, 1>(a, item, rt, sm);
-    else if (nt <= 2) mm_down_body<FMT, 2>(a, item, rt, sm);
-    else if (nt <= 3) mm_down_body<FMT, 3>(a, item, rt, sm);
-    else mm_down_body<FMT, 4>(a, item, rt, sm);
-}
-
-int zz_launch_up_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st) {
-    const dim3 g(zz_xcd_grid(max_items, a.MI / 32));
-    const int gf = a.lay.gate.fmt, uf = a.lay.up.fmt;
-    if (gf == ZZ_FMT_TQ2) hipLaunchKernelGGL((zz_up_mma_kernel<ZZ_FMT_TQ2, ZZ_FMT_TQ2>), g, dim3(256), 0, st, a);
-    else if (gf == ZZ_FMT_Q40 && uf == ZZ_FMT_Q40) hipLaunchKernelGGL((zz_up_mma_kernel<ZZ_FMT_Q40, ZZ_FMT_Q40>), g, dim3(256), 0, st, a);
-    else if (gf == ZZ_FMT_Q80 && uf == ZZ_FMT_Q80) hipLaunchKernelGGL((zz_up_mma_kernel<ZZ_FMT_Q80, ZZ_FMT_Q80>), g, dim3(256), 0, st, a);
-    else if (gf == ZZ_FMT_Q40) hipLaunchKernelGGL((zz_up_mma_kernel<ZZ_FMT_Q40, ZZ_FMT_Q80>), g, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((zz_up_mma_kernel<ZZ_FMT_Q80, ZZ_FMT_Q40>), g, dim3(256), 0, st, a);
-    return hipGetLastError() == hipSuccess;
-}
-
-int zz_launch_down_mfma(const ZzFfnArgs &a, int max_items, hipStream_t st) {
-    dim3 g(zz_xcd_grid(max_items, a.D / 64));
-    switch (a.lay.down.fmt) {
-    case ZZ_FMT_Q40: hipLaunchKernelGGL(zz_down_mma_kernel<ZZ_FMT_Q40>, g, dim3(256), 0, st, a); break;
-    case ZZ_FMT_Q80: hipLaunchKernelGGL(zz_down_mma_kernel<ZZ_FMT_Q80>, g, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL(zz_down_mma_kernel<ZZ_FMT_TQ2>, g, dim3(256), 0, st, a); break;
-    }
-    return hipGetLastError() == hipSuccess;
 }
