@@ -432,14 +432,16 @@ def test_container_load(dev, tmp_path):
 def test_block_fused_decode_matches_two_stream_path(dev, S, layer_cache):
     """Decode rows run the dense branch fused into the routed layer's four launches;
     ZZ_BLOCK_FUSE=0 keeps it on its own stream. Both agree with the oracle (routing
-    exact, 1e-3) and with each other to float rounding (the dense down's chunks are
-    summed across waves in the fused path)."""
+    exact, 1e-3) and with each other to float rounding, except where the two paths'
+    different summation orders put a hidden element on opposite sides of a q8_0
+    rounding boundary: the int8 hidden codes of both layers then differ by 1 in
+    isolated elements, each of which moves the block's output by ~1e-4."""
     import os
     L = layer_cache("gemma", seed=2, zipf=True)
     dn = Z.make_dense(2816, 2112, 13)
     H = Z.make_input(L, S, 13 + S)
     want = Z.oracle_block(L, dn, H)
-    outs = []
+    outs, hqs = [], []
     for fuse in ("1", "0"):
         os.environ["ZZ_BLOCK_FUSE"] = fuse
         try:
@@ -455,9 +457,15 @@ def test_block_fused_decode_matches_two_stream_path(dev, S, layer_cache):
             say(f"block S={S} fuse={fuse}: rel L2 {err:.2e}")
             assert err < OUT_TOL
             outs.append(Hb)
+            hqs.append(np.concatenate([m.debug(S)["hq"].ravel(), d.debug(S)["hq"].ravel()]).astype(np.int32))
         finally:
             close_all(B, m, d)
-    assert Z.rel_l2(outs[0], outs[1]) < 1e-5
+    flips = np.abs(hqs[0] - hqs[1])
+    nf = int((flips > 0).sum())
+    d01 = Z.rel_l2(outs[0], outs[1])
+    say(f"  fused vs two-stream: {nf} hidden flips of {flips.size}, rel L2 {d01:.2e}")
+    assert flips.max() <= 1 and nf <= max(2, flips.size // 2000)
+    assert d01 < 1e-5 + 2e-4 * nf
 
 
 # ------------------------------------------------------------------- FlashHead

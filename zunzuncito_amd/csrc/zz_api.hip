@@ -196,7 +196,8 @@ struct Layer {
     std::vector<char> present;
     int n_present = 0;
     Workspace ws;
-    int last_S = 0;             // tokens of the first chunk of the last forward
+    int last_S = 0;             // tokens of the last chunk of the last forward
+    bool last_dec = false;      // whether that chunk ran the decode kernels (hidden by flat pair)
     int pending_S = -1;         // begin/end state
 };
 static std::vector<Layer *> g_layers;
@@ -602,6 +603,10 @@ static int run_chunk(Layer *L, Workspace &w, const float *d_in, float *d_out, in
         if (!(ProfScope(ZZ_K_DEC_DOWN, st), zz_launch_dec_down(dd, st))) ZZ_FAIL("decode down launch failed");
         if (c.gemma && !(ProfScope(ZZ_K_COMBINE, st), zz_launch_dec_norm(d_out, L->post_ln, w.ss, d.D, d.eps, S, st)))
             ZZ_FAIL("decode post-norm launch failed");
+        if (&w == &L->ws) {                      // what zz_moe_debug dumps
+            L->last_S = S;
+            L->last_dec = true;
+        }
         return 1;
     }
     if (!(ProfScope(ZZ_K_PREP, st), zz_launch_prep(c.pa, S, st))) ZZ_FAIL("prep launch failed");
@@ -615,6 +620,10 @@ static int run_chunk(Layer *L, Workspace &w, const float *d_in, float *d_out, in
     ca.D = d.D; ca.K = d.K; ca.gemma = c.gemma; ca.eps = d.eps; ca.y = w.y; ca.ppos = w.ppos;
     ca.ewt = w.ewt; ca.post_ln = L->post_ln; ca.out = d_out;
     if (!(ProfScope(ZZ_K_COMBINE, st), zz_launch_combine(ca, S, st))) ZZ_FAIL("combine launch failed");
+    if (&w == &L->ws) {
+        L->last_S = S;
+        L->last_dec = false;
+    }
     return 1;
 }
 
@@ -678,8 +687,8 @@ int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_
     }
     if (d_eidx) ZZ_CHECK(hipMemcpyAsync(d_eidx, w.eidx, sizeof(int) * S * d.K, hipMemcpyDeviceToDevice, st));
     if (d_ewt) ZZ_CHECK(hipMemcpyAsync(d_ewt, w.ewt, sizeof(float) * S * d.K, hipMemcpyDeviceToDevice, st));
-    L->last_S = S;
-    N->last_S = S;
+    L->last_S = N->last_S = S;                  // both layers' hidden rows by flat pair
+    L->last_dec = N->last_dec = true;
     return 1;
 }
 
@@ -704,7 +713,6 @@ static int forward_dev(Layer *L, const float *d_in, float *d_out, int S, int *d_
     const int CH = chunk_tokens(d);
     if (!ensure_ws(L, S < CH ? S : CH)) return 0;
     if (!run_chunks(L, L->ws, CH, d_in, d_out, S, d_eidx, d_ewt, st)) return 0;
-    L->last_S = S < CH ? S : CH;
     return 1;
 }
 
@@ -764,7 +772,6 @@ static int forward_host(Layer *L, const float *in, float *out, int S, int *eidx,
         ZZ_CHECK(hipMemcpyAsync(ix.data() + (size_t)s0 * d.K, w.eidx, sizeof(int) * n * d.K, hipMemcpyDeviceToHost, g_stream));
         ZZ_CHECK(hipMemcpyAsync(wt.data() + (size_t)s0 * d.K, w.ewt, sizeof(float) * n * d.K, hipMemcpyDeviceToHost, g_stream));
         ZZ_CHECK(hipStreamSynchronize(g_stream));
-        if (s0 == 0) L->last_S = n;
     }
     memcpy(out, o.data(), sizeof(float) * o.size());
     if (eidx) memcpy(eidx, ix.data(), sizeof(int) * ix.size());
@@ -822,7 +829,6 @@ extern "C" int zz_moe_forward_begin(int id, const float *in, int S) {
     ZZ_CHECK(hipMemcpyAsync(L->ws.in, in, sizeof(float) * S * d.D, hipMemcpyHostToDevice, g_stream));
     if (!run_chunk(L, L->ws, L->ws.in, L->ws.out, S, g_stream)) return 0;
     L->pending_S = S;
-    L->last_S = S;
     return 1;
 }
 
@@ -845,7 +851,7 @@ extern "C" int zz_moe_debug(int id, zz_moe_dump *dp) {
     const zz_moe_desc &d = L->d;
     Workspace &w = L->ws;
     const int S = L->last_S, P = S * d.K;
-    const bool dec = takes_decode(d, S);
+    const bool dec = L->last_dec;
     ZZ_CHECK(hipDeviceSynchronize());              // the forward may have run on any stream
     if (dec) {
         // the decode path routes inside its gate/up kernel and keeps the hidden by
@@ -901,6 +907,7 @@ extern "C" int zz_moe_debug(int id, zz_moe_dump *dp) {
         ZZ_CHECK(hipMemcpy(hs.data(), w.hs, sizeof(float) * hs.size(), hipMemcpyDeviceToHost));
         for (int f = 0; f < P; f++) {              // (token, slot) order
             int p = dec ? f : ppos[f];
+            if (p < 0 || p >= P) ZZ_FAIL("zz_moe_debug: pair %d of the last forward out of range", p);
             if (dp->hq) memcpy(dp->hq + (size_t)f * d.MI, hq.data() + (size_t)p * d.MI, d.MI);
             if (dp->hs) memcpy(dp->hs + (size_t)f * nbM, hs.data() + (size_t)p * nbM, sizeof(float) * nbM);
         }

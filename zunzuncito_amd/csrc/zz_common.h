@@ -358,12 +358,23 @@ __device__ __forceinline__ unsigned zz_quant8(float4 v, float *d_out, int *sum_o
            (unsigned)(q3 & 0xff) << 24;
 }
 
+// The activations (gemma4.c:432-437, lfm25.c:456-458, maple.c:607-611) in forms of one
+// hardware exp (v_exp_f32, 2^x) and one reciprocal (v_rcp_f32) per element, without
+// branches. gelu_tanh: 0.5 x (1 + tanh(y)) equals x / (1 + e^(-2y)) exactly in real
+// arithmetic, with y = sqrt(2/pi) (x + 0.044715 x^3); silu: x / (1 + e^(-x)). Each
+// result is within a few ulp of the reference's glibc tanhf / expf forms, except where
+// the reference's 1 + tanhf(y) cancels (y << 0), whose outputs are below any block's
+// q8_0 step. These feed the q8_0 hidden, which the reference quantises the same way.
+#define ZZ_LOG2E 1.4426950408889634f
 __device__ __forceinline__ float zz_gelu_tanh(float x) {
-    float inner = fmaf((0.044715f * x) * x, x, x);
-    return (0.5f * x) * (1.0f + tanhf(0.7978845608028654f * inner));
+    const float inner = fmaf((0.044715f * x) * x, x, x);
+    const float e = __builtin_amdgcn_exp2f(inner * (-2.0f * 0.7978845608028654f * ZZ_LOG2E));
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-__device__ __forceinline__ float zz_silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float zz_silu(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -ZZ_LOG2E));
+}
 
 __device__ __forceinline__ float zz_act(int act, float g, float u, float clamp) {
     if (act == ZZ_ACT_GEGLU_TANH) return zz_gelu_tanh(g) * u;
