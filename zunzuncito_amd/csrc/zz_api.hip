@@ -33,6 +33,7 @@ static int g_ready = 0;
 // batches of at most this many tokens take the three-launch decode path
 // (ZZ_DECODE_MAX_S, 0 turns it off; never above ZZ_DEC_MAXS)
 static int g_dec_max_s = ZZ_DEC_MAXS;
+static int g_exact_min_s = 16;          // ZZ_EXACT_LOGITS_MIN_S
 static char g_name[128] = "none";
 static hipStream_t g_stream = nullptr;
 static unsigned *g_diag = nullptr;          // device counters, see zz_moe_stats
@@ -76,6 +77,10 @@ extern "C" int gpu_init(void) {
     ZZ_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamDefault));
     ZZ_CHECK(hipMalloc(&g_diag, 16 * sizeof(unsigned)));
     ZZ_CHECK(hipMemset(g_diag, 0, 16 * sizeof(unsigned)));
+    // batches from this size on take the exact serial router chains, smaller ones the
+    // certified parallel logits with exact replay of contested chains
+    const char *em = getenv("ZZ_EXACT_LOGITS_MIN_S");
+    if (em) g_exact_min_s = atoi(em) < 1 ? 1 : atoi(em);
     const char *dm = getenv("ZZ_DECODE_MAX_S");
     if (dm) g_dec_max_s = atoi(dm) < 0 ? 0 : (atoi(dm) > ZZ_DEC_MAXS ? ZZ_DEC_MAXS : atoi(dm));
     g_ready = 1;
@@ -554,6 +559,7 @@ static ChunkArgs chunk_args(Layer *L, Workspace &w, const float *d_in, int S) {
     ZzLogitArgs &la = c.la;
     la.D = d.D; la.E = d.E; la.gating = d.gating; la.S = S; la.router = L->router; la.xn = w.xn; la.x = d_in;
     la.bias = c.gemma && d.use_bias ? L->bias : nullptr; la.cen = w.cen; la.bnd = w.bnd; la.diag = g_diag;
+    la.exact_min_s = g_exact_min_s;
 
     ZzTopkArgs &ta = c.ta;
     ta.D = d.D; ta.E = d.E; ta.K = d.K; ta.gating = d.gating; ta.norm_topk = d.norm_topk;

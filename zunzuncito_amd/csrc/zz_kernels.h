@@ -21,6 +21,7 @@ struct ZzPrepArgs {
 
 struct ZzLogitArgs {
     int D, E, gating, S;
+    int exact_min_s;            // batches of at least this many tokens take the exact chains
     const float *router;        // [E, D]
     const float *xn;            // [S, D] gemma
     const float *x;             // [S, D] lfm / maple

@@ -286,11 +286,19 @@ __device__ __forceinline__ void mm_kloop(const uint8_t *E, const ZzTensor &T, in
 // take two token sets (NS = 2, q4_0; q8_0's twice-as-large weight registers would spill):
 // the same weight operand feeds both sets' MFMAs, so a block costs 12 unpack and 24
 // epilogue operations for 64 rows x 8 tokens.
-#define MM4_XB 24576                     // staged activation bytes: 4 rows of K <= 6144, 8 of K <= 3072
+// Staged rows are K + 16 bytes apart and scale rows K/32 + 1 words apart: at the
+// unpadded strides (K a multiple of 128 bytes) every token's 16-byte read of block b
+// would fall on the same LDS banks, a 4- or 8-way conflict per read.
+#define MM4_K1 6144                      // K limit of one token set (4 rows)
+#define MM4_K2 3072                      // K limit of two token sets (8 rows)
+#define MM4_XB (8 * (MM4_K2 + 16))       // staged activation bytes (also >= 4 * (MM4_K1 + 16))
+#define MM4_XS(K) ((K) + 16)
+#define MM4_SS(K) ((K) / ZZ_BLK + 1)
 struct Mm4Stage {
-    __attribute__((aligned(16))) int8_t x[MM4_XB];      // token t's row at t * K
-    float s[MM4_XB / ZZ_BLK];                          // token t's block scales at t * K / 32
+    __attribute__((aligned(16))) int8_t x[MM4_XB];      // token t's row at t * MM4_XS(K)
+    float s[8 * MM4_SS(MM4_K2)];                       // token t's block scales at t * MM4_SS(K)
 };
+static_assert(4 * MM4_XS(MM4_K1) <= MM4_XB && 4 * MM4_SS(MM4_K1) <= 8 * MM4_SS(MM4_K2), "stage sizes");
 struct Mm4Red {
     float part[4][64][4];                // [wave][lane][row of the quad]
     float res[64][9];                    // [row][token]
@@ -303,11 +311,11 @@ __device__ __forceinline__ void mm4_stage(Mm4Stage &st, RF row, SF srow, int K) 
     const int tid = threadIdx.x, nseg = K / 16, nb = K / ZZ_BLK;
     for (int i = tid; i < 4 * NS * nseg; i += 256) {
         const int t = i / nseg, sg = i - t * nseg;
-        *(uint4 *)&st.x[t * K + 16 * sg] = ld16(row(t) + 16 * sg);
+        *(uint4 *)&st.x[t * MM4_XS(K) + 16 * sg] = ld16(row(t) + 16 * sg);
     }
     for (int i = tid; i < 4 * NS * nb; i += 256) {
         const int t = i / nb, b = i - t * nb;
-        st.s[t * nb + b] = srow(t)[b];
+        st.s[t * MM4_SS(K) + b] = srow(t)[b];
     }
     __syncthreads();
 }
@@ -353,11 +361,10 @@ __device__ __forceinline__ int mm4_frag(const Mm4A &A, int j, int m) {
 }
 
 // acc[s][v]: row 4(l/4)+v of the 64, token 4s + l%4, over this wave's chunks c = w,
-// w+4, ... (K: the row length, the staged rows' stride)
+// w+4, ... (K: the row length; the staged rows are MM4_XS(K) apart)
 template <int FMT, bool FULLC, int NS, typename DF>
 __device__ __forceinline__ void mm4_chunk(const Mm4A &A, const Mm4Stage &st, int c, int l, int K,
                                           float (&acc)[NS][4], DF dbg) {
-    const int nb = K / ZZ_BLK;
 #pragma unroll
     for (int j = 0; j < (FULLC ? 4 : 2); j++) {
         const int b = 4 * c + j;
@@ -366,12 +373,13 @@ __device__ __forceinline__ void mm4_chunk(const Mm4A &A, const Mm4Stage &st, int
 #pragma unroll
         for (int s = 0; s < NS; s++) {
             const int t = 4 * s + (l & 3);
-            const uint4 xa = *(const uint4 *)&st.x[t * K + b * ZZ_BLK], xb = *(const uint4 *)&st.x[t * K + b * ZZ_BLK + 16];
+            const int8_t *xr = &st.x[t * MM4_XS(K) + b * ZZ_BLK];
+            const uint4 xa = *(const uint4 *)xr, xb = *(const uint4 *)(xr + 16);
             const unsigned xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
             d[s] = (zz_v4i){0, 0, 0, 0};
 #pragma unroll
             for (int m = 0; m < 8; m++) d[s] = __builtin_amdgcn_mfma_i32_4x4x4i8(mm4_frag<FMT>(A, j, m), (int)xw[m], d[s], 0, 0, 0);
-            sx[s] = st.s[t * nb + b];
+            sx[s] = st.s[t * MM4_SS(K) + b];
         }
         dbg(c, j, d);
 #pragma unroll

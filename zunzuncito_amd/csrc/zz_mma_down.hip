@@ -102,8 +102,8 @@ __global__ __launch_bounds__(256, 4) void zz_down_mma_kernel(ZzFfnArgs a) {
     if (item.n <= 0) return;
     __shared__ MmDownShared sm;
     const int nt = (item.n + 15) / 16;
-    if (FMT != ZZ_FMT_TQ2 && item.n <= 4 && a.MI <= MM4_XB / 4) mm4_down_body<FMT, 1, DBG>(a, item, rt, sm.t4);
-    else if (FMT == ZZ_FMT_Q40 && item.n <= 8 && a.MI <= MM4_XB / 8) mm4_down_body<FMT, 2, DBG>(a, item, rt, sm.t4);
+    if (FMT != ZZ_FMT_TQ2 && item.n <= 4 && a.MI <= MM4_K1) mm4_down_body<FMT, 1, DBG>(a, item, rt, sm.t4);
+    else if (FMT == ZZ_FMT_Q40 && item.n <= 8 && a.MI <= MM4_K2) mm4_down_body<FMT, 2, DBG>(a, item, rt, sm.t4);
     else if (nt <= 1) mm_down_body<FMT, 1, DBG>(a, item, rt, sm);
     else if (nt <= 2) mm_down_body<FMT, 2, DBG>(a, item, rt, sm);
     else if (nt <= 3) mm_down_body<FMT, 3, DBG>(a, item, rt, sm);

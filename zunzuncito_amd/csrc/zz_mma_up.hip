@@ -189,8 +189,8 @@ __global__ __launch_bounds__(256, 4) void zz_up_mma_kernel(ZzFfnArgs a) {
     __shared__ MmUpShared sm;
     __shared__ int tok[MM_TN];
     const int nt = (item.n + 15) / 16;
-    if (GF == UF && GF != ZZ_FMT_TQ2 && item.n <= 4 && a.D <= MM4_XB / 4) mm4_up_body<GF, 1, DBG>(a, item, rb, sm.t4);
-    else if (GF == UF && GF == ZZ_FMT_Q40 && item.n <= 8 && a.D <= MM4_XB / 8) mm4_up_body<GF, 2, DBG>(a, item, rb, sm.t4);
+    if (GF == UF && GF != ZZ_FMT_TQ2 && item.n <= 4 && a.D <= MM4_K1) mm4_up_body<GF, 1, DBG>(a, item, rb, sm.t4);
+    else if (GF == UF && GF == ZZ_FMT_Q40 && item.n <= 8 && a.D <= MM4_K2) mm4_up_body<GF, 2, DBG>(a, item, rb, sm.t4);
     else if (nt <= 1) mm_up_body<GF, UF, 1, DBG>(a, item, rb, sm, tok);
     else if (nt <= 2) mm_up_body<GF, UF, 2, DBG>(a, item, rb, sm, tok);
     else if (nt <= 3) mm_up_body<GF, UF, 3, DBG>(a, item, rb, sm, tok);

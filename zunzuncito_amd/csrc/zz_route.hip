@@ -684,7 +684,7 @@ int zz_launch_prep(const ZzPrepArgs &a, int S, hipStream_t st) {
 }
 
 int zz_launch_logits(const ZzLogitArgs &a, int S, hipStream_t st) {
-    if (S >= 16 && a.D % 64 == 0) {
+    if (S >= a.exact_min_s && a.D % 64 == 0) {
         ZzLogitArgs b = a;
         b.S = S;
         if (a.D % 256 == 0) zz_launch_logits_exact<256>(b, S, st);
