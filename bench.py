@@ -600,7 +600,7 @@ def stack_bench(zz, torch, layers, seed, prefill_S, steps):
                     tokens_per_s=best["tokens_per_s"], hbm_bytes_per_token=step_bytes,
                     hbm_GBs=step_bytes * best["tokens_per_s"] / 1e9,
                     hbm_frac=step_bytes * best["tokens_per_s"] / 1e9 / HBM_PEAK_GBS,
-                    distinct_tokens=int(len(np.unique(toks)))),
+                    distinct_tokens=int(len(np.unique(toks))), first_tokens=toks[:12].tolist()),
         flash_decode=dict(head=f"FlashHead: {NC} balanced clusters of {CS} (random permutation, "
                                f"centroids the q4_0 member means), {NP} probed, {nforce} forced",
                           eager=fl["eager"], graph=fl["graph"], tokens_per_s=fbest["tokens_per_s"],
