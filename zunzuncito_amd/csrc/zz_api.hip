@@ -603,7 +603,7 @@ static int run_chunk(Layer *L, Workspace &w, const float *d_in, float *d_out, in
         ua.f = c.fa; ua.tk = c.ta; ua.dense = c.dense; ua.pk = c.P;
         ZzDecDownArgs dd;
         memset(&dd, 0, sizeof dd);
-        dd.f = c.fa; dd.S = S; dd.K = d.K; dd.E = d.E; dd.eidx = w.eidx; dd.ewt = w.ewt; dd.ppos = w.ppos;
+        dd.f = c.fa; dd.S = S; dd.K = d.K; dd.E = d.E; dd.eidx = w.eidx; dd.ewt = w.ewt;
         dd.out = d_out; dd.ss = c.gemma ? w.ss : nullptr;
         if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_dec_up(ua, S, st))) ZZ_FAIL("ffn_up launch failed");
         if (!(ProfScope(ZZ_K_DEC_DOWN, st), zz_launch_dec_down(dd, st))) ZZ_FAIL("decode down launch failed");
@@ -623,7 +623,7 @@ static int run_chunk(Layer *L, Workspace &w, const float *d_in, float *d_out, in
     if (!(ProfScope(ZZ_K_FFN_DOWN, st), zz_launch_down_mfma(c.fa, c.max_items, st))) ZZ_FAIL("ffn_down launch failed");
 
     ZzCombineArgs ca;
-    ca.D = d.D; ca.K = d.K; ca.gemma = c.gemma; ca.eps = d.eps; ca.y = w.y; ca.ppos = w.ppos;
+    ca.D = d.D; ca.K = d.K; ca.gemma = c.gemma; ca.eps = d.eps; ca.y = w.y;
     ca.ewt = w.ewt; ca.post_ln = L->post_ln; ca.out = d_out;
     if (!(ProfScope(ZZ_K_COMBINE, st), zz_launch_combine(ca, S, st))) ZZ_FAIL("combine launch failed");
     if (&w == &L->ws) {
@@ -679,7 +679,7 @@ int zz_block_decode(int moe_id, int dense_id, float *d_H, float *d_h1, float *d_
     if (!(ProfScope(ZZ_K_FFN_UP, st), zz_launch_dec_up(ua, S, st))) ZZ_FAIL("block: gate/up launch failed");
     ZzDecDownArgs dd;
     memset(&dd, 0, sizeof dd);
-    dd.f = c.fa; dd.S = S; dd.K = d.K; dd.E = d.E; dd.eidx = w.eidx; dd.ewt = w.ewt; dd.ppos = w.ppos;
+    dd.f = c.fa; dd.S = S; dd.K = d.K; dd.E = d.E; dd.eidx = w.eidx; dd.ewt = w.ewt;
     dd.out = d_h2; dd.ss = w.ss; dd.nd = S; dd.fd = cn.fa; dd.yd = d_h1; dd.ssd = wn.ss;
     if (!(ProfScope(ZZ_K_DEC_DOWN, st), zz_launch_dec_down(dd, st))) ZZ_FAIL("block: down launch failed");
     ZzDecFinalArgs fa;

@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void zz_combine_kernel(ZzCombineArgs a) {
     __shared__ int pos[ZZ_MAXK];
     __shared__ float wt[ZZ_MAXK];
     if (threadIdx.x < K) {
-        pos[threadIdx.x] = a.ppos[(size_t)s * K + threadIdx.x];
+        pos[threadIdx.x] = s * K + threadIdx.x;       // y rows are by flat pair
         wt[threadIdx.x] = a.ewt[(size_t)s * K + threadIdx.x];
     }
     __syncthreads();
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void zz_combine_kernel(ZzCombineArgs a) {
 }
 
 // The same combine for K <= 8 and D <= 1024 * NO with every load issued first: the
-// token's positions and weights, its 8 rows' values for all NO column slots of the
+// token's weights, its 8 rows' values for all NO column slots of the
 // thread, the post-norm weights. The loop above waits out one memory round trip per
 // column slot; this one waits once (same sums, same order).
 template <int NO>
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(256) void zz_combine_fast_kernel(ZzCombineArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; j++) {                // slots past K repeat the last (unused)
         const int jj = min(j, K - 1);
-        pos[j] = a.ppos[(size_t)s * K + jj];
+        pos[j] = s * K + jj;                     // y rows are by flat pair
         wt[j] = a.ewt[(size_t)s * K + jj];
     }
     float4 y[NO][8], pl[NO];

@@ -78,10 +78,10 @@ struct ZzFfnArgs {
     int8_t *hq;                 // [P, MI] by sorted pair
     float *hs;                  // [P, MI/32]
     int *hsum;                  // [P, MI/32]
-    float *y;                   // [P, D] expert outputs before weighting
+    float *y;                   // [P, D] expert outputs before weighting, row token*K + slot
+    const int *pslot;           // sorted pair -> slot
     // diagnostics (zz_moe_dots), null otherwise: the kernels' per-block integer dots
-    // before scaling, by flat pair p = token*K + slot (pslot: sorted pair -> slot)
-    const int *pslot;
+    // before scaling, by flat pair p = token*K + slot
     int32_t *dbg_up;            // [P][gate, up][MI][D/32]
     int32_t *dbg_dn;            // [P][D][MI/32]
 };
@@ -89,8 +89,7 @@ struct ZzFfnArgs {
 struct ZzCombineArgs {
     int D, K, gemma;
     float eps;
-    const float *y;             // [P, D]
-    const int *ppos;            // [S*K]
+    const float *y;             // [S*K, D] by flat pair token*K + slot
     const float *ewt;           // [S, K]
     const float *post_ln;       // [D] gemma
     float *out;                 // [S, D]
@@ -150,7 +149,6 @@ struct ZzDecDownArgs {
     int S, K, E;
     const int *eidx;            // [S, K]
     const float *ewt;           // [S, K]
-    const int *ppos;            // [S*K] -> sorted pair
     float *out;                 // [S, D]
     double *ss;                 // [S, D/16] per-tile sums of squares of out (gemma), or null
     int nd;                     // dense-branch rows fused in (0 or S)

@@ -1,6 +1,7 @@
 // zz_mma_down.hip -- the down half of the grouped expert FFN on the int8 matrix
-// cores: the unweighted expert outputs y of each pair (zz_mma.h holds the shared
-// K loops).
+// cores: the unweighted expert outputs y of each pair, stored at its flat index
+// token*K + slot so that the combine reads a token's K rows without a lookup
+// (zz_mma.h holds the shared K loops).
 #include "zz_mma.h"
 
 // ------------------------------------------------------------------ down
@@ -9,8 +10,11 @@ union MmDownShared {
     Mm4Shared t4;
 };
 
+// yrow[t]: the flat pair (token*K + slot) of the item's token t, the row of y that the
+// combine reads for that token and slot
 template <int FMT, int NT, bool DBG>
-__device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, MmDownShared &sm) {
+__device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, MmDownShared &sm,
+                                             const int *yrow) {
     const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, qq = l >> 4;
     const ZzTensor &T = a.lay.down;
     const int g = 4 * rt + w, n = item.n, MI = a.MI, nb = MI / ZZ_BLK;
@@ -56,14 +60,15 @@ __device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &i
     for (int t = 0; t < NT; t++) {
         const int tk = 16 * t + (l & 15);
         if (tk < n)
-            *(float4 *)(a.y + ((size_t)item.p0 + tk) * a.D + row0) =
+            *(float4 *)(a.y + (size_t)yrow[tk] * a.D + row0) =
                 make_float4(acc[t][0] * al[0], acc[t][1] * al[1], acc[t][2] * al[2], acc[t][3] * al[3]);
     }
 }
 
 // Tiny items (<= 4 NS tokens), down: rows 64rt + l, the unweighted y of each token.
 template <int FMT, int NS, bool DBG>
-__device__ __forceinline__ void mm4_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, Mm4Shared &sm) {
+__device__ __forceinline__ void mm4_down_body(const ZzFfnArgs &a, const ZzItem &item, int rt, Mm4Shared &sm,
+                                              const int *yrow) {
     const int tid = threadIdx.x, w = zz_wave_id(), l = tid & 63, n = item.n, MI = a.MI, nb = MI / ZZ_BLK;
     const uint8_t *E = a.experts + (size_t)item.e * a.estride;
     Mm4Ring<FMT> R;
@@ -89,7 +94,7 @@ __device__ __forceinline__ void mm4_down_body(const ZzFfnArgs &a, const ZzItem &
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         const int t = 4 * s + (tid >> 6), r = tid & 63;
-        if (t < n) a.y[((size_t)item.p0 + t) * a.D + 64 * rt + r] = sm.rd.res[r][t];
+        if (t < n) a.y[(size_t)yrow[t] * a.D + 64 * rt + r] = sm.rd.res[r][t];
     }
 }
 
@@ -101,13 +106,19 @@ __global__ __launch_bounds__(256, 4) void zz_down_mma_kernel(ZzFfnArgs a) {
     const ZzItem item = a.items[it];
     if (item.n <= 0) return;
     __shared__ MmDownShared sm;
+    __shared__ int yrow[MM_TN];
+    // read before the bodies' first barrier (the staging's), used after it
+    if ((int)threadIdx.x < item.n) {
+        const int p = item.p0 + (int)threadIdx.x;
+        yrow[threadIdx.x] = a.ptok[p] * a.K + a.pslot[p];
+    }
     const int nt = (item.n + 15) / 16;
-    if (FMT != ZZ_FMT_TQ2 && item.n <= 4 && a.MI <= MM4_K1) mm4_down_body<FMT, 1, DBG>(a, item, rt, sm.t4);
-    else if (FMT == ZZ_FMT_Q40 && item.n <= 8 && a.MI <= MM4_K2) mm4_down_body<FMT, 2, DBG>(a, item, rt, sm.t4);
-    else if (nt <= 1) mm_down_body<FMT, 1, DBG>(a, item, rt, sm);
-    else if (nt <= 2) mm_down_body<FMT, 2, DBG>(a, item, rt, sm);
-    else if (nt <= 3) mm_down_body<FMT, 3, DBG>(a, item, rt, sm);
-    else mm_down_body<FMT, 4, DBG>(a, item, rt, sm);
+    if (FMT != ZZ_FMT_TQ2 && item.n <= 4 && a.MI <= MM4_K1) mm4_down_body<FMT, 1, DBG>(a, item, rt, sm.t4, yrow);
+    else if (FMT == ZZ_FMT_Q40 && item.n <= 8 && a.MI <= MM4_K2) mm4_down_body<FMT, 2, DBG>(a, item, rt, sm.t4, yrow);
+    else if (nt <= 1) mm_down_body<FMT, 1, DBG>(a, item, rt, sm, yrow);
+    else if (nt <= 2) mm_down_body<FMT, 2, DBG>(a, item, rt, sm, yrow);
+    else if (nt <= 3) mm_down_body<FMT, 3, DBG>(a, item, rt, sm, yrow);
+    else mm_down_body<FMT, 4, DBG>(a, item, rt, sm, yrow);
 }
 
 template <bool DBG>
