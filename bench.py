@@ -213,6 +213,9 @@ def build_cfg_layers(zz, torch, name, n_layers, seed):
     return layers
 
 
+PREWARM_S = 0.2
+
+
 def time_steps(torch, layers, xs, out, S, steps, warmup):
     st = torch.cuda.current_stream()
     L = len(layers)
@@ -221,6 +224,15 @@ def time_steps(torch, layers, xs, out, S, steps, warmup):
     # stream synchronisations), which must not fall between the timing events
     for i, m in enumerate(layers):
         m.forward_dev(xs[i % len(xs)].data_ptr(), out.data_ptr(), S, stream=st.cuda_stream)
+    # then PREWARM_S seconds of untimed steps: on a GPU that was idle the first tens of
+    # milliseconds of load run a few percent slower (the same 20 timed steps took 228 us
+    # after 5 warm-up steps, 216 us after 200), which is not the steady state
+    t_end, i = time.perf_counter() + PREWARM_S, 0
+    while time.perf_counter() < t_end:
+        for _ in range(L):
+            layers[i % L].forward_dev(xs[i % len(xs)].data_ptr(), out.data_ptr(), S, stream=st.cuda_stream)
+            i += 1
+        torch.cuda.synchronize()
     for i in range(warmup):
         layers[i % L].forward_dev(xs[i % len(xs)].data_ptr(), out.data_ptr(), S,
                                   stream=st.cuda_stream)
