@@ -524,6 +524,29 @@ def test_begin_end_and_dev_paths(dev, layer_cache):
         m.close()
 
 
+def test_empty_and_bad_calls_decline(dev, layer_cache):
+    """An empty batch, a missing buffer, an unknown layer and an end with nothing begun
+    return 0 with a message and launch nothing; the layer then runs as before."""
+    L = layer_cache("gemma", seed=2, E=16)
+    x = Z.make_input(L, 5, 53)
+    m = gpu_layer(L)
+    try:
+        a, ea, _ = m.forward(x)
+        lib = zz.lib()
+        out = np.zeros_like(a)
+        xp, op = x.ctypes.data_as(zz._f32p), out.ctypes.data_as(zz._f32p)
+        assert lib.zz_moe_forward(m.id, xp, op, 0, None, None) == 0 and zz.last_error()
+        assert lib.zz_moe_forward(m.id, xp, None, 5, None, None) == 0
+        assert lib.zz_moe_forward(m.id + 1000, xp, op, 5, None, None) == 0
+        assert lib.zz_moe_forward_dev(m.id, None, None, 0, None, None, None) == 0
+        assert lib.zz_moe_forward_end(m.id, op, None, None) == 0
+        assert not out.any()
+        b, eb, _ = m.forward(x)
+        assert np.array_equal(b.view(np.uint32), a.view(np.uint32)) and np.array_equal(eb, ea)
+    finally:
+        m.close()
+
+
 def test_declines_until_all_experts_resident(dev, layer_cache):
     L = layer_cache("gemma", seed=2, E=16)
     m = zz.MoeLayer(L.D, L.MI, L.E, L.K, L.gating, L.act, L.fmts, L.router, L.router_scale,
