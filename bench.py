@@ -41,6 +41,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, HERE)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_PEAK_TOPS = 5000.0        # MI355X dense int8 matrix-core peak (5.0 POP/s)
 D, MI, E, K = 2816, 704, 128, 8
 
 
@@ -85,6 +86,20 @@ def measured_traffic(leg, kernel):
     for line in open(p):
         f = line.split()
         if len(f) == 4 and f[0] == "traffic_bytes_per_launch" and f[1] == leg and f[2] == kernel:
+            return float(f[3])
+    return None
+
+
+def measured_mfma_busy(leg, kernel):
+    """Fraction of the matrix cores' cycles busy in `kernel` of leg `leg` (e.g.
+    gemma512) from the committed SQ_VALU_MFMA_BUSY_CYCLES summary, or None where that
+    leg was not measured."""
+    p = os.path.join(HERE, "profiles", "ffn_mfma_gemma_s512_counters.md")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        f = line.split()
+        if len(f) == 4 and f[0] == "mfma_busy_frac" and f[1] == leg and f[2] == kernel:
             return float(f[3])
     return None
 
@@ -311,7 +326,26 @@ def run_leg(zz, torch, name, layers, S, steps, warmup, seed):
                           "kernel_us": kern[dom]},
                 layer_roofline={"bound": "hbm", "algorithmic_bytes": by["layer"],
                                 "achieved": by["layer"] / step / 1e9,
-                                "frac": by["layer"] / step / 1e9 / HBM_PEAK_GBS})
+                                "frac": by["layer"] / step / 1e9 / HBM_PEAK_GBS},
+                mfma=mfma_use(c, S, kern, f"{name}{S}"))
+
+
+def mfma_use(c, S, kern, leg):
+    """int8 matrix-core use of the batched FFN kernels (absent on the decode path):
+    the useful int8 operations (2 per multiply-add of the routed pairs' gate, up and
+    down products, padding excluded) per kernel second against the dense int8 peak,
+    and the busy fraction read by rocprofv3 where the counters were taken."""
+    if kern.get("dec_down"):                     # decode: dot4 GEMV kernels, no matrix cores
+        return None
+    P, D, MI = S * c["K"], c["D"], c["MI"]
+    ops = {"ffn_up": 2.0 * P * 2 * MI * D, "ffn_down": 2.0 * P * D * MI}
+    out = {}
+    for k, n in ops.items():
+        if kern.get(k):
+            a = n / (kern[k] * 1e-6) / 1e12
+            out[k] = {"achieved": a, "peak": MFMA_PEAK_TOPS, "unit": "TOP/s", "frac": a / MFMA_PEAK_TOPS,
+                      "int8_ops": n, "kernel_us": kern[k], "busy": measured_mfma_busy(leg, k)}
+    return out or None
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -718,6 +752,7 @@ def main():
                    "tokens_per_step": head_S, "mean_union_experts": r["mean_union_experts"]},
         "roofline": r["roofline"],
         "layer_roofline": r["layer_roofline"],
+        "mfma": r["mfma"],
         "kernels_us": r["kernels_us"],
     }
     if "gemma" in res and 1 in res["gemma"]:
