@@ -15,7 +15,7 @@
 //   up:   hidden rows 32*rb..+31: waves 0, 1 the gate groups, waves 2, 3 the up
 //         groups; then h = act(g, u) and its per-token q8_0 quantisation
 //         (gemma4.c:642-645, lfm25.c:712-723, maple.c:665-684) in registers;
-//   down: rows 64*rt..+63 of down; the unweighted y[pair][row] for the combine.
+//   down: rows 64*rt..+63 of down; the unweighted y[token*K + slot][row] for the combine.
 // The K loop walks the slot table's chunks of 4 blocks. Weights go straight to
 // registers, two chunks ahead: the slot table holds each lane's bytes for a chunk
 // contiguously (zz_common.h). Activations are staged through LDS, one chunk ahead.
