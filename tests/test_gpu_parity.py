@@ -461,6 +461,22 @@ def test_config1_gemma_s1_many_tokens(dev, layer_cache):
         m.close()
 
 
+@pytest.mark.parametrize("kind,kw", [("gemma", dict()), ("lfm", dict()), ("maple", dict(E=64))])
+def test_small_batches_both_paths(dev, kind, kw, layer_cache):
+    """S = 2, 3, 4, 5 against the oracle: the fused decode kernels take S <= 2 for q4_0 /
+    q8_0 weights and S <= 4 for tq2, the matrix-core path the rest, so each format
+    crosses from one path to the other inside this range."""
+    L = layer_cache(kind, seed=21, **kw)
+    m = gpu_layer(L)
+    try:
+        for S in (2, 3, 4, 5):
+            say(f"case {kind} S={S}")
+            x = Z.make_input(L, S, 60 + S)
+            check_layer(m, L, x, Z.oracle_moe(L, x))
+    finally:
+        m.close()
+
+
 # --------------------------------------------------------------- properties
 def test_batch_invariance(dev, layer_cache):
     """Tokens do not interact in a MoE layer: one S=96 call equals three S=32 calls
