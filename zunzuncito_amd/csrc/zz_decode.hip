@@ -484,6 +484,7 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
 
 struct ZzDecPairs {                 // per (token, slot) pair, flat order s*K + j
     int e[DEC_MAXS * ZZ_MAXK];      // expert (clamped into the table)
+    float w[DEC_MAXS * ZZ_MAXK];    // gate weight
 };
 
 // LDS bytes of the staged hidden rows of P pairs: int8 codes, block scales and sums
@@ -518,6 +519,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
     float *sh_sd = (float *)(sh_qd + (size_t)nd * MID);
     if (tid < P) {
         pr.e[tid] = zz_clamp_e(a.eidx[tid], a.E);
+        pr.w[tid] = a.ewt[tid];         // read now: the combine at the end would wait for it
     }
     __syncthreads();
     // the pairs' q8_0 hidden (codes, scales, sums by flat pair), requested before the
@@ -714,7 +716,7 @@ __global__ __launch_bounds__(512) void zz_dec_down_kernel(ZzDecDownArgs a) {
                 const float alpha = ((const float *)(f.experts + (size_t)pr.e[fp] * f.estride + T.off_s))[o];
                 y = alpha * (y - htot[fp]);        // tq2.h:154
             }
-            v = fmaf(a.ewt[fp], y, v);
+            v = fmaf(pr.w[fp], y, v);
         }
         a.out[(size_t)s * D + o] = v;
         if (a.ss) {                               // this tile's sum of squares, for the post-norm
