@@ -412,6 +412,12 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
     const ZzTensor &T = q >= 2 ? f.lay.up : f.lay.gate;
     const int g = 2 * j + (q & 1);
     const uint8_t *E = f.experts + (size_t)e * f.estride;
+    // tq2's row alphas of hidden row 32j + tid (tq2.h:154), read with the weights
+    float ag = 1.0f, au = 1.0f;
+    if (T.fmt == ZZ_FMT_TQ2 && tid < ZZ_BLK) {
+        ag = ((const float *)(E + f.lay.gate.off_s))[32 * j + tid];
+        au = ((const float *)(E + f.lay.up.off_s))[32 * j + tid];
+    }
     auto gates = [&] {
         if (w == 0 && routed && writer) zz_topk_wave_gates(a.tk, s, tk_lds, true);
     };
@@ -445,8 +451,8 @@ __global__ __launch_bounds__(512) void zz_dec_up_kernel(ZzDecUpArgs a) {
         float gv = part[0][gg][r] + part[1][gg][r];
         float uv = part[0][2 + gg][r] + part[1][2 + gg][r];
         if (T.fmt == ZZ_FMT_TQ2) {                              // tq2.h:154
-            gv = ((const float *)(E + f.lay.gate.off_s))[32 * j + tid] * (gv - st.xt);
-            uv = ((const float *)(E + f.lay.up.off_s))[32 * j + tid] * (uv - st.xt);
+            gv = ag * (gv - st.xt);
+            uv = au * (uv - st.xt);
         }
         hb[tid] = zz_act(f.act, gv, uv, f.clamp);
     }

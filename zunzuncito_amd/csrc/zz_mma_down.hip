@@ -46,16 +46,17 @@ __device__ __forceinline__ void mm_down_body(const ZzFfnArgs &a, const ZzItem &i
         }
     };
     float acc[NT][4];
+    const int row0 = 16 * g + 4 * qq;
+    float al[4] = {1.0f, 1.0f, 1.0f, 1.0f};     // tq2's row alpha: read now, used at the end
+    if (FMT == ZZ_FMT_TQ2)
+#pragma unroll
+        for (int i = 0; i < 4; i++) al[i] = ((const float *)(E + T.off_s))[row0 + i];
     mm_kloop<FMT, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc, dbgc);
     if (FMT == ZZ_FMT_Q40)                       // the 16*(q - 8) weights
 #pragma unroll
         for (int t = 0; t < NT; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[t][i] *= 0.0625f;
-    const int row0 = 16 * g + 4 * qq;
-    float al[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-    if (FMT == ZZ_FMT_TQ2)
-        for (int i = 0; i < 4; i++) al[i] = ((const float *)(E + T.off_s))[row0 + i];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const int tk = 16 * t + (l & 15);

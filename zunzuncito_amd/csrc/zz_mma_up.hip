@@ -54,6 +54,10 @@ __device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &ite
         }
     };
     float acc[NT][4];
+    float alr[4] = {1.0f, 1.0f, 1.0f, 1.0f};     // tq2.h:154, alpha of the row: read now,
+    if (GF == ZZ_FMT_TQ2)                        // used after the K loop
+#pragma unroll
+        for (int i = 0; i < 4; i++) alr[i] = ((const float *)(E + T.off_s))[16 * g + 4 * qq + i];
     if (GF == UF || w < 2) mm_kloop<GF, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc, dbgc);
     else mm_kloop<UF, NT, MM_RING(NT)>(E, T, g, src, sm.st, acc, dbgc);
     if ((w < 2 ? GF : UF) == ZZ_FMT_Q40)         // the 16*(q - 8) weights
@@ -61,13 +65,11 @@ __device__ __forceinline__ void mm_up_body(const ZzFfnArgs &a, const ZzItem &ite
         for (int t = 0; t < NT; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[t][i] *= 0.0625f;
-    if (GF == ZZ_FMT_TQ2) {                      // tq2.h:154, alpha of the row
+    if (GF == ZZ_FMT_TQ2) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float al = ((const float *)(E + T.off_s))[16 * g + 4 * qq + i];
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int t = 0; t < NT; t++) acc[t][i] *= al;
-        }
+            for (int t = 0; t < NT; t++) acc[t][i] *= alr[i];
     }
     __syncthreads();                             // the stages are done with
     if (w >= 2) {
