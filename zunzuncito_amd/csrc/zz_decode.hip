@@ -144,6 +144,8 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
             wr[j] = a.dense ? 0.0f : lg.router[(size_t)e * D + i];
             sr[j] = a.dense ? 0.0f : pp.router_scale[i];
         }
+        const bool hb = !a.dense && lg.bias;                  // the Zipf offset, read with them
+        const float bz = hb ? lg.bias[e] : 0.0f;
 #pragma unroll
         for (int j = 0; j < RB; j++) sr[j] = sr[j] * rs;
         if (FIN) combine();                                   // the router rows are in flight
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(256) void zz_dec_logits_kernel(ZzDecRouteArgs a) {
                 }
             }
             __syncthreads();
-            zz_tight_block_scan<RB>(buf, D, lg.bias, e, red, lg.cen + (size_t)s * lg.E + e,
+            zz_tight_block_scan<RB>(buf, D, hb, bz, red, lg.cen + (size_t)s * lg.E + e,
                                 lg.bnd + (size_t)s * lg.E + e);
         }
     } else {

@@ -246,6 +246,8 @@ __global__ __launch_bounds__(64 * TT, 1) void zz_logits_exact_kernel(ZzLogitArgs
     // this lane's elements of the wave's input row (rows past the end read the last
     // row; not stored)
     const float *xrow = X + (size_t)min(s, a.S - 1) * D + (lane & 15);
+    // gemma's harness logit offset, added after the chain: read now, not after it
+    const float bz = gem && a.bias ? a.bias[min(e, a.E - 1)] : 0.0f;
     __shared__ __attribute__((aligned(16))) float ws_t[2][LX_E][KC + 4];
     // staging: wave w moves rows w, w + TT, ... of a chunk from L2 straight into LDS
     // (global_load_lds: lane l's KC/64 floats land at the row start + l * KC/16 bytes),
@@ -360,7 +362,7 @@ __global__ __launch_bounds__(64 * TT, 1) void zz_logits_exact_kernel(ZzLogitArgs
     if (s < a.S && e < a.E) {
         const size_t o = (size_t)s * a.E + e;
         if constexpr (gem) {
-            if (a.bias) vf = vf + a.bias[e];       // harness logit offset, after the dot
+            if (a.bias) vf = vf + bz;              // harness logit offset, after the dot
             a.cen[o] = (double)vf;
         } else {
             double vd = acc[0];

@@ -43,10 +43,11 @@ __device__ __forceinline__ void zz_wave_sync_lds() {
     __builtin_amdgcn_wave_barrier();
 }
 
-// Centre and bound of a gemma logit from the exact-order prefix data; bias is the
-// harness's Zipf offset, v' = fl(v + bias_e).
+// Centre and bound of a gemma logit from the exact-order prefix data; with hb, bz is
+// the harness's Zipf offset bias_e (read by the caller when its loads are issued),
+// v' = fl(v + bias_e).
 __device__ __forceinline__ void zz_tight_finish(double sabs, double T, double tot, int D,
-                                                const float *bias, int e, double *cen_out,
+                                                bool hb, float bz, double *cen_out,
                                                 double *bnd_out) {
     const double gd = zz_gamma(D, ZZ_U64);
     // double-precision slack on every computed prefix (|S_k err| <= g_D^d T)
@@ -54,8 +55,8 @@ __device__ __forceinline__ void zz_tight_finish(double sabs, double T, double to
                (sabs + (double)D * gd * T + (double)(D - 1) * zz_gamma(D, ZZ_U32) * T);
     b = b * 1.000001 + gd * T + 1e-40;
     double cen = tot;
-    if (bias) {
-        cen += (double)bias[e];
+    if (hb) {
+        cen += (double)bz;
         b += 2.0 * ZZ_U32 * (fabs(cen) + b) + 1e-40;
     }
     *cen_out = cen;
@@ -73,6 +74,7 @@ __device__ void zz_tight_wave(const float *w, const float *src, const float *rsc
                               float rs, int D, const float *bias, int e, float *buf, double *cen,
                               double *bnd, int cstride, float *xn_out) {
     const int l = threadIdx.x & 63;
+    const float bz = bias ? bias[e] : 0.0f;
     double carry[NS], sabs[NS], T[NS];
 #pragma unroll
     for (int s = 0; s < NS; s++) carry[s] = sabs[s] = T[s] = 0.0;
@@ -121,7 +123,7 @@ __device__ void zz_tight_wave(const float *w, const float *src, const float *rsc
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         const double sa = zz_wave_sum(sabs[s]), t = zz_wave_sum(T[s]);
-        if (l == 0) zz_tight_finish(sa, t, carry[s], D, bias, e, cen + (size_t)s * cstride,
+        if (l == 0) zz_tight_finish(sa, t, carry[s], D, bias != nullptr, bz, cen + (size_t)s * cstride,
                                     bnd + (size_t)s * cstride);
     }
 }
@@ -135,7 +137,7 @@ __device__ void zz_tight_wave(const float *w, const float *src, const float *rsc
 __device__ __forceinline__ int zz_pad32(int i) { return i + (i >> 5); }
 
 template <int RB>
-__device__ void zz_tight_block_scan(const float *buf, int D, const float *bias, int e, double *red,
+__device__ void zz_tight_block_scan(const float *buf, int D, bool hb, float bz, double *red,
                                     double *cen, double *bnd) {
     const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6;
     const int R = (D + 255) >> 8;                             // R <= RB
@@ -170,7 +172,7 @@ __device__ void zz_tight_block_scan(const float *buf, int D, const float *bias, 
     if (tid == 0) {
         const double tot = ((red[0] + red[1]) + red[2]) + red[3];
         zz_tight_finish(((red[4] + red[5]) + red[6]) + red[7], ((red[8] + red[9]) + red[10]) + red[11],
-                        tot, D, bias, e, cen, bnd);
+                        tot, D, hb, bz, cen, bnd);
     }
     __syncthreads();
 }
